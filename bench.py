@@ -1,0 +1,256 @@
+"""Benchmark of the exact-fusions-v1 per-token layer path on one MI355X.
+
+Headline workload: one launch of the fused residual-add +
+RMSNorm + Q/K RMSNorm + NeoX RoPE + BF16 KV-store over a 2048-token prefill chunk
+(hidden 2048, 16 Q heads, 4 KV heads, head_dim 128, KV capacity 131072, positions 0..2047
+from a device PrefillState).  A step is one such launch.  Inputs are synthetic (seed 0,
+1% outlier channels x20), resident in HBM before timing.  Launches rotate over `--sets`
+independent buffer sets (> 512 MB in total) so the 256 MB Infinity Cache cannot serve
+them; K launches are captured in one HIP graph and replayed between HIP events.
+
+Output: one JSON line (rank 0).  value = achieved algorithmic HBM GB/s of the launch;
+roofline.frac = value / 8000 GB/s; cpu_baseline = the C oracle (a scalar port of the
+reference arithmetic) timed on a bounded sample of the same workload on the host.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+TOKENS, HIDDEN, HQ, HKV, D, CAPACITY = 2048, 2048, 16, 4, 128, 131072
+
+
+def chain_bytes(fmt: str) -> int:
+    """Algorithmic HBM bytes per token of the fused chain (BF16 device I/O):
+    residual-norm: read x, r; write x, y (4 * 2H);
+    Q/K: read q, k, v; write q, k in place; one cos|sin table row (2D);
+    cache: the K and V rows in `fmt` (BF16 2*1024; q8 1024 codes + 32 B scales;
+    q8_0 2*544)."""
+    norm = 4 * 2 * HIDDEN
+    qk = 2 * (2 * HQ * D) + 2 * (2 * HKV * D) + 2 * HKV * D + 2 * D
+    cache = {"bf16": 2 * 2 * HKV * D, "q8": 2 * HKV * D + 8 * HKV, "q8_0": 2 * 544,
+             "q8_0_norot": 2 * 544}[fmt]
+    return norm + qk + cache
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--sets", type=int, default=8)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--formats", default="bf16,q8_0,q8_0_norot,q8",
+                    help="KV formats measured (the first is the headline)")
+    return ap.parse_args()
+
+
+class ChainSet:
+    """One independent buffer set of the config-1 workload."""
+
+    def __init__(self, torch, host, table, fmt):
+        from padra_amd import abi, ops
+        dev = lambda a: torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).cuda()
+        self.x, self.r = dev(host["x"]), dev(host["residual"])
+        self.y = torch.empty_like(self.x)
+        self.q, self.k, self.v = dev(host["q"]), dev(host["k"]), dev(host["v"])
+        self.g, self.qn, self.kn = dev(host["gamma"]), dev(host["qn"]), dev(host["kn"])
+        self.table = table
+        code = {"bf16": abi.KV_BF16, "q8": abi.KV_Q8, "q8_0": abi.KV_Q8_0,
+                "q8_0_norot": abi.KV_Q8_0_NOROT}[fmt]
+        if fmt == "bf16":
+            self.kc = torch.empty((CAPACITY, HKV * D), dtype=torch.int16, device="cuda")
+            self.vc = torch.empty_like(self.kc)
+            self.sc = None
+        elif fmt == "q8":
+            self.kc = torch.empty((CAPACITY, HKV * D), dtype=torch.int8, device="cuda")
+            self.vc = torch.empty_like(self.kc)
+            self.sc = torch.empty((CAPACITY, HKV, 2), dtype=torch.float32, device="cuda")
+        else:
+            self.kc = torch.empty((CAPACITY, 544), dtype=torch.uint8, device="cuda")
+            self.vc = torch.empty_like(self.kc)
+            self.sc = None
+        self.state = torch.tensor([0, 0, TOKENS, CAPACITY, 0, 1, 1, 1], dtype=torch.int32,
+                                  device="cuda")
+        self.bad = torch.zeros(1, dtype=torch.int32, device="cuda")
+        self.pos = ops.positions_prefill(self.state, maximum=CAPACITY)
+        self.kv = ops.kv_cache(code, self.kc, self.vc, CAPACITY, scales=self.sc)
+        self.ops = ops
+
+    def launch(self):
+        self.ops.ResidualNormQKRopeStore(self.x, self.r, self.y, self.g, self.q, self.k, self.v,
+                                         self.qn, self.kn, self.table, self.pos, self.kv, self.bad)
+
+
+def time_graph(torch, sets, steps, warmup):
+    """Captures `steps` launches (rotating over sets) into one graph; returns ms/launch."""
+    for i in range(warmup):
+        sets[i % len(sets)].launch()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(graph, stream=stream):
+            for i in range(steps):
+                sets[i % len(sets)].launch()
+    torch.cuda.synchronize()
+    graph.replay()  # warm replay
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        torch.cuda.synchronize()
+        start.record(stream)
+        graph.replay()
+        end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def time_eager(torch, sets, steps):
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(steps):
+        sets[i % len(sets)].launch()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def copy_ceiling(torch, nbytes, reps=50):
+    """Device-to-device copy of `nbytes` (read + write), rotating over 8 buffer pairs."""
+    n = nbytes // 2 // 2
+    bufs = [(torch.empty(n, dtype=torch.int16, device="cuda").fill_(1),
+             torch.empty(n, dtype=torch.int16, device="cuda")) for _ in range(8)]
+    for s, d in bufs:
+        d.copy_(s)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(reps):
+        s, d = bufs[i % 8]
+        d.copy_(s)
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / reps
+    return 2 * n * 2 / (ms * 1e-3) / 1e9
+
+
+def cpu_baseline(host, seconds):
+    """The C oracle on the host: residual-norm (128-thread tree), Q/K norm + RoPE and the
+    BF16 store over the full 2048-token chunk, repeated until `seconds` have elapsed."""
+    from oracle import oracle
+    table = __import__("padra_amd").synth.bf16_bits(oracle.rope_table(TOKENS, D, 1e6))
+    pos = np.arange(TOKENS, dtype=np.int32)
+    kc = np.zeros((TOKENS, HKV * D), np.uint16)
+    vc = np.zeros_like(kc)
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        xn, y, _, _ = oracle.residual_rmsnorm(host["x"], host["residual"], host["gamma"], 1e-6,
+                                              128)
+        q, k, _ = oracle.qk_norm_rope(host["q"], host["k"], host["qn"], host["kn"], table, pos)
+        oracle.kv_store_bf16(k, host["v"], kc, vc, pos, TOKENS)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    per_chunk = el / reps
+    return {
+        "value": round(chain_bytes("bf16") * TOKENS / per_chunk / 1e9, 3),
+        "unit": "GB/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": f"{reps} full 2048-token config-1 chunks (BF16 KV) in {el:.1f} s, one thread",
+        "tokens_per_s": round(TOKENS / per_chunk, 1),
+        "us_per_token": round(per_chunk / TOKENS * 1e6, 3),
+    }
+
+
+def main():
+    args = parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(json.dumps({"error": "this path runs on one GPU only; --gpus must be 1"}))
+        sys.exit(2)
+    import torch
+
+    from padra_amd import abi, ops, synth
+
+    abi.lib()
+    host = synth.chain_inputs(TOKENS, HIDDEN, HQ, HKV, D, outliers=True, seed=0)
+    table = torch.from_numpy(ops.RopeTable(TOKENS, D, 1e6).view(torch.int16).numpy()).cuda()
+    formats = args.formats.split(",")
+    results = {}
+    for fmt in formats:
+        sets = [ChainSet(torch, host, table, fmt) for _ in range(args.sets)]
+        ms = time_graph(torch, sets, args.steps, args.warmup)
+        eager = time_eager(torch, sets, min(args.steps, 50))
+        nbytes = chain_bytes(fmt) * TOKENS
+        results[fmt] = {"ms": ms, "eager_ms": eager, "bytes": nbytes,
+                        "gbs": nbytes / (ms * 1e-3) / 1e9}
+        bad = sum(int(s.bad.item()) for s in sets)
+        if bad:
+            raise SystemExit(f"device error flag set for format {fmt}")
+        del sets
+        torch.cuda.empty_cache()
+    head = results[formats[0]]
+    ceiling = copy_ceiling(torch, head["bytes"])
+    achieved = head["gbs"]
+    line = {
+        "metric": "achieved HBM GB/s (% of peak) fused norm+RoPE+KV-store; tokens/s per layer",
+        "value": round(achieved, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(head["ms"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seed 0, N(0,1) with 1% outlier channels x20; gamma U(0.5,1.5))",
+        "config": {"workload": "config1: fused residual+RMSNorm+QK-norm+RoPE+BF16 KV store, "
+                               "2048-token prefill chunk, 1 layer",
+                   "tokens": TOKENS, "hidden": HIDDEN, "q_heads": HQ, "kv_heads": HKV,
+                   "head_dim": D, "kv_capacity": CAPACITY, "kv_format": formats[0],
+                   "norm_tree": 128, "buffer_sets": args.sets},
+        "tokens_per_s": round(TOKENS / (head["ms"] * 1e-3), 1),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": traffic_from_profiles(formats[0]),
+                     "kernel": "k_chain<128,16,fmt>", "bytes_per_launch": head["bytes"]},
+        "copy_ceiling_gbs": round(ceiling, 1),
+        "formats": {f: {"gbs": round(r["gbs"], 2), "us_per_launch": round(r["ms"] * 1e3, 3),
+                        "eager_us_per_launch": round(r["eager_ms"] * 1e3, 3),
+                        "bytes_per_launch": r["bytes"],
+                        "frac": round(r["gbs"] / HBM_PEAK_GBS, 4)} for f, r in results.items()},
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(host, args.cpu_seconds)
+    print(json.dumps(line), flush=True)
+
+
+def traffic_from_profiles(fmt):
+    """HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE (scaled by
+    the copy-kernel calibration), read from the committed profile summary if present."""
+    path = os.path.join(ROOT, "profiles", "chain_config1_traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        data = json.load(f)
+    return data.get(fmt, {}).get("bytes_per_launch")
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,161 @@
+/*
+ * padra_hip.h -- C-ABI of the MI355X (gfx950) kernels for Padra's exact-fusions-v1
+ * per-token layer path: residual-add + RMSNorm, Q/K RMSNorm + NeoX RoPE + KV-cache
+ * store (BF16, q8, q8_0), SwiGLU at the expert boundary and the embedding gather.
+ *
+ * The reference launches these as __global__ functions from RunCudaInferenceCore
+ * (/root/reference/src/cuda/inference.cu:2988-3166 decode, :3421-3950 prefill); it
+ * has no FFI of its own.  Each entry point below replaces one reference kernel family
+ * (cited per function) with the same arithmetic, the same KV-cache byte layout
+ * (/root/reference/docs/kv-cache.md, src/runtime/kv_cache_layout.h) and the same two
+ * error channels:
+ *   - a host-checkable shape/pointer problem returns a nonzero status and launches
+ *     nothing (the reference throws std::runtime_error, prefill_kv_commit.cuh:6-9);
+ *   - a device-detected problem (invalid DecodeState/PrefillState, non-finite value,
+ *     token id out of range, -128 code) stores 1 to the caller's device int `bad`
+ *     and the affected unit writes nothing (reference: atomicExch(bad, 1)).
+ *
+ * Conventions: every pointer except `stream` and the descriptor structs is a device
+ * pointer owned by the caller.  Nothing here allocates, frees or synchronizes; all
+ * work is ordered on `stream` (a hipStream_t, NULL = default stream) and may be
+ * captured into a HIP graph: positions are read on the device when a state pointer
+ * is given, so replays at new positions need no host update.
+ * Activations (x, residual, normalized, q, k, v, gate, up) are BF16 bit patterns
+ * (uint16_t) unless a function takes `act`; with act = PADRA_ACT_F32 they are fp32
+ * words holding BF16-exact values, the reference's own buffer convention
+ * (inference.cu:52-54).  16-byte alignment is required for every row base.
+ */
+#ifndef PADRA_HIP_H
+#define PADRA_HIP_H
+#include <stddef.h>
+#include <stdint.h>
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes, numbered as mellum16::StatusCode (include/mellum16/status.h:11-21). */
+enum {
+  PADRA_OK = 0,
+  PADRA_INVALID_ARGUMENT = 1,
+  PADRA_UNSUPPORTED = 5,
+  PADRA_INTERNAL = 8
+};
+
+/* Activation storage. */
+enum { PADRA_ACT_BF16 = 0, PADRA_ACT_F32 = 1 };
+
+/* Reduction tree of the row norms (which reference kernel's bits to reproduce):
+ * 128 = Norm / NormFP8Exact / NormFP8WideExact (inference.cu:188-214), 128 threads,
+ *       thread t sums elements t, t+128, ...;
+ * 256 = ResidualPostNormWideExact (residual_norm_wide_exact.cuh:6-80), 256 threads. */
+enum { PADRA_TREE_128 = 128, PADRA_TREE_256 = 256 };
+
+/* KV cache formats (src/runtime/kv_cache_layout.h:6). */
+enum {
+  PADRA_KV_BF16 = 0,       /* "bf16": K [cap][F] bf16, V [cap][F] bf16 */
+  PADRA_KV_Q8 = 1,         /* "q8_token_head128_f32scale_v1": codes K [cap][F] int8,
+                              codes V [cap][F] int8, scales [cap][Hkv] {float k, v} */
+  PADRA_KV_Q8_0 = 2,       /* "q8_0_token512_block32_f16scale_rot_k128_v64_v2": K and V
+                              [cap] rows of {fp16 d[F/32]; int8 qs[F]} (544 B for F=512) */
+  PADRA_KV_Q8_0_NOROT = 3  /* the same row layout without the Hadamard rotation */
+};
+
+/* Device control state, byte-identical to the reference's structs. */
+typedef struct padra_DecodeState { /* decode_control.cuh:3-6 */
+  int32_t token, position, capacity, remaining, global_valid, local_valid, eos, stopped;
+} padra_DecodeState;
+typedef struct padra_PrefillState { /* src/runtime/prefill_state.h:8-11 */
+  int32_t base, prompt_offset, tokens, capacity, committed;
+  uint32_t binding_epoch, request_epoch, valid;
+} padra_PrefillState;
+typedef struct padra_Q8KVScalePair { float k, v; } padra_Q8KVScalePair; /* kv_cache_layout.h:48-51 */
+
+/* Where token t's position comes from. */
+enum {
+  PADRA_POS_BASE = 0,     /* position = base + t (host-known chunk base; QKNormRope `position`) */
+  PADRA_POS_PREFILL = 1,  /* position = prefill->base + t after ValidPrefillState
+                             (prefill_state.h:16-24) with tokens = chunk rows */
+  PADRA_POS_DECODE = 2    /* one token per sequence: position = decode[t].position after
+                             DecodeReadyAtLimit (context_admission.cuh:5-11) */
+};
+typedef struct padra_Positions {
+  int32_t mode;
+  int32_t base;                        /* PADRA_POS_BASE */
+  const padra_PrefillState *prefill;   /* device, PADRA_POS_PREFILL */
+  const padra_DecodeState *decode;     /* device array [tokens], PADRA_POS_DECODE */
+  int32_t maximum;                     /* context limit for state validation, <= 131072 */
+  int32_t vocab;                       /* DecodeState token bound (reference: 98304) */
+  uint32_t binding_epoch;              /* expected PrefillState.binding_epoch (reference: 1) */
+} padra_Positions;
+
+/* A KV cache binding for one layer (KVCacheView, kv_cache_layout.h:42-47). */
+typedef struct padra_KVCache {
+  int32_t format;        /* PADRA_KV_* */
+  void *k, *v;           /* device */
+  void *scales;          /* PADRA_KV_Q8 only */
+  int32_t cap;           /* ring rows: capacity (global layer) or min(1024, capacity) (local) */
+  int32_t first;         /* chunk rows before `first` are not stored: max(0, tokens-cap) for a
+                            local ring narrower than the chunk, else 0 */
+  int64_t seq_stride;    /* rows between consecutive sequences' caches (PADRA_POS_DECODE with
+                            several sequences); 0 for one sequence */
+} padra_KVCache;
+
+/* ---- residual + RMSNorm / RMSNorm -------------------------------------------------
+ * Replaces ResidualPostNormWideExact (residual_norm_wide_exact.cuh:6-80),
+ * ResidualPostNormBF16 (residual_norm_bf16.cuh:3-40) and the prefill pair Add + Norm
+ * (inference.cu:475-481, :188-214) fused in one pass:
+ *   x[r][i] <- B(x + residual);  normalized[r][i] <- B(B(x*inv) * gamma[i]),
+ *   inv = 1/sqrt(S/H + eps), S the compensated sum of squares in `tree` order.
+ * residual may be NULL: then x is read only (Norm, and the norm half of NormFP8Exact /
+ * NormFP8WideExact, norm_fp8_exact.cuh:6-45).  statistics (nullable, device float
+ * [rows][2]) receives {variance, inv}.  gamma: BF16 [hidden].  hidden % tree == 0,
+ * hidden / tree <= 36. */
+int padra_ResidualPostNorm(void *stream, void *x, const void *residual, void *normalized,
+                           const uint16_t *gamma, int rows, int hidden, float eps, int tree,
+                           float *statistics, int *bad, int act);
+
+/* ---- RoPE table (host) --------------------------------------------------------------
+ * Replaces RopeTable (inference.cu:764-785): fills the HOST buffer table[positions][D]
+ * with BF16 bit patterns of cos (first D/2) and sin (last D/2), theta a parameter;
+ * yarn != 0 selects the reference's global-layer ramp (factor, original_context).
+ * The caller uploads it (the reference copies its table host-to-device once). */
+int padra_RopeTable(uint16_t *table, int positions, int head_dim, float theta, int yarn,
+                    float factor, int original_context);
+
+/* ---- Q/K RMSNorm + RoPE (+ KV store) ------------------------------------------------
+ * Replaces QKNormRope (qknorm_rope.cuh:4-50), QKNormRopePair64 (qknorm_rope_pair64.cuh:
+ * 3-83), QKNormRopeControlled (decode_control.cuh:80-126) and, when kv != NULL,
+ * QKNormRopeStoreControlled (qk_rope_store_exact.cuh:4-49) together with the cache
+ * writers that follow it: StorePrefillControlled / Store (prefill_control.cuh:24-38,
+ * inference.cu:248-256), kv_q8::Encode + Commit (kv_q8.cuh:28-98) and
+ * q8_native::EncodeKV + Commit (kv_q8_native.cuh:52-101, :440-463).
+ * q [T][Hq][D] and k [T][Hkv][D] are normalized and rotated in place (qn, kn: BF16 [D]);
+ * table: BF16 [table_rows][D] from padra_RopeTable.  With kv: for every token t >= first
+ * the rotated K row and the V row (v: [T][Hkv][D]) are stored at cache slot
+ * position % cap in kv->format.  D must be 128 (the reference's block shape). */
+int padra_QKNormRopeStore(void *stream, void *q, void *k, const void *v, const uint16_t *qn,
+                          const uint16_t *kn, const uint16_t *table, int table_rows,
+                          const padra_Positions *pos, int tokens, int q_heads, int kv_heads,
+                          int head_dim, float eps, const padra_KVCache *kv, int *bad, int act);
+
+/* ---- fused per-token chain ----------------------------------------------------------
+ * One launch of padra_ResidualPostNorm over `tokens` rows and padra_QKNormRopeStore over
+ * the same tokens (the two have no data dependence; exact-fusions-v1 runs them as
+ * separate kernels).  Arguments mean what they mean there; results are bit-identical to
+ * the two calls. */
+int padra_ResidualNormQKRopeStore(void *stream, void *x, const void *residual,
+                                  void *normalized, const uint16_t *gamma, int hidden,
+                                  int tree, float *statistics, void *q, void *k,
+                                  const void *v, const uint16_t *qn, const uint16_t *kn,
+                                  const uint16_t *table, int table_rows,
+                                  const padra_Positions *pos, int tokens, int q_heads,
+                                  int kv_heads, int head_dim, float eps,
+                                  const padra_KVCache *kv, int *bad);
+
+/* ---- version / capability ----------------------------------------------------------- */
+const char *padra_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

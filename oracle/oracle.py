@@ -1,0 +1,192 @@
+"""ctypes binding of the CPU parity oracle (oracle/libpadra_oracle.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and bench.py's
+cpu_baseline leg, as the checker.  The product (padra_amd) never imports it.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB = os.path.join(HERE, "libpadra_oracle.so")
+
+
+def build() -> str:
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+    return LIB
+
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB):
+            build()
+        _lib = ctypes.CDLL(LIB)
+        P, I, F = ctypes.c_void_p, ctypes.c_int, ctypes.c_float
+        sig = {
+            "po_bf16_round": ([F], F), "po_f32_to_f16": ([F], ctypes.c_uint16),
+            "po_f16_to_f32": ([ctypes.c_uint16], F),
+            "po_sumsq_tree": ([P, I, I], F),
+            "po_residual_rmsnorm": ([P, P, P, P, I, I, F, I, P, P], None),
+            "po_rmsnorm": ([P, P, P, I, I, F, I, P, P], None),
+            "po_rope_table": ([P, I, I, F, I, F, I], None),
+            "po_qk_norm_rope": ([P, P, P, P, P, P, I, I, I, I, F, P], None),
+            "po_kv_store_bf16": ([P, P, P, P, P, I, I, I, I], None),
+            "po_kv_q8_encode": ([P, P, P, P, P, P, I, I, I, I, I, P], None),
+            "po_hadamard": ([P, I, F], None),
+            "po_q8_0_row_bytes": ([I], I),
+            "po_kv_q8_0_encode": ([P, P, P, P, P, I, I, I, I, I, I, P], None),
+            "po_kv_q8_0_dequantize": ([P, P, P, P, I, I, P], None),
+            "po_silu_bf16": ([ctypes.c_uint16], ctypes.c_uint16),
+            "po_silu_table": ([P], None),
+            "po_swiglu": ([P, P, P, ctypes.c_longlong, P], None),
+            "po_embed": ([P, P, P, I, I, I, P], None),
+            "po_decode_ready": ([P, I, I], I),
+            "po_valid_prefill_state": ([P, I, I, ctypes.c_uint32, I], I),
+        }
+        for name, (args, res) in sig.items():
+            fn = getattr(_lib, name)
+            fn.argtypes = args
+            fn.restype = res
+    return _lib
+
+
+def _p(a: np.ndarray | None):
+    if a is None:
+        return None
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+class Bad:
+    def __init__(self):
+        self.v = ctypes.c_int(0)
+
+    @property
+    def ptr(self):
+        return ctypes.byref(self.v)
+
+    def __bool__(self):
+        return bool(self.v.value)
+
+
+def residual_rmsnorm(x, residual, gamma, eps=1e-6, threads=128):
+    """Returns (x_new, y, stats, bad) for BF16-bit arrays x, residual [rows][H]."""
+    x = np.array(x, dtype=np.uint16, copy=True, order="C")
+    rows, hidden = x.shape
+    y = np.empty_like(x)
+    stats = np.empty((rows, 2), np.float32)
+    bad = Bad()
+    lib().po_residual_rmsnorm(_p(x), _p(np.ascontiguousarray(residual, np.uint16)), _p(y),
+                              _p(np.ascontiguousarray(gamma, np.uint16)), rows, hidden, eps,
+                              threads, _p(stats), bad.ptr)
+    return x, y, stats, bool(bad)
+
+
+def rmsnorm(x, gamma, eps=1e-6, threads=128):
+    x = np.ascontiguousarray(x, np.uint16)
+    rows, hidden = x.shape
+    y = np.empty_like(x)
+    stats = np.empty((rows, 2), np.float32)
+    bad = Bad()
+    lib().po_rmsnorm(_p(x), _p(y), _p(np.ascontiguousarray(gamma, np.uint16)), rows, hidden,
+                     eps, threads, _p(stats), bad.ptr)
+    return y, stats, bool(bad)
+
+
+def rope_table(positions, head_dim=128, theta=1e6, yarn=False, factor=16.0,
+               original_context=8192) -> np.ndarray:
+    """float32 [positions][head_dim] (BF16-exact values)."""
+    t = np.empty((positions, head_dim), np.float32)
+    lib().po_rope_table(_p(t), positions, head_dim, theta, int(yarn), factor, original_context)
+    return t
+
+
+def qk_norm_rope(q, k, qn, kn, table_bits, positions, eps=1e-6):
+    q = np.array(q, dtype=np.uint16, copy=True, order="C")
+    k = np.array(k, dtype=np.uint16, copy=True, order="C")
+    tokens, hq, d = q.shape
+    hkv = k.shape[1]
+    pos = np.ascontiguousarray(positions, np.int32)
+    bad = Bad()
+    lib().po_qk_norm_rope(_p(q), _p(k), _p(np.ascontiguousarray(qn, np.uint16)),
+                          _p(np.ascontiguousarray(kn, np.uint16)),
+                          _p(np.ascontiguousarray(table_bits, np.uint16)), _p(pos), tokens, hq,
+                          hkv, d, eps, bad.ptr)
+    return q, k, bool(bad)
+
+
+def kv_store_bf16(k, v, kc, vc, positions, cap, first=0):
+    tokens = k.shape[0]
+    features = int(np.prod(k.shape[1:]))
+    lib().po_kv_store_bf16(_p(np.ascontiguousarray(k, np.uint16)),
+                           _p(np.ascontiguousarray(v, np.uint16)), _p(kc), _p(vc),
+                           _p(np.ascontiguousarray(positions, np.int32)), tokens, features, cap,
+                           first)
+
+
+def kv_q8_encode(k, v, codes_k, codes_v, scales, positions, cap, first=0):
+    tokens, hkv, d = k.shape
+    bad = Bad()
+    lib().po_kv_q8_encode(_p(np.ascontiguousarray(k, np.uint16)),
+                          _p(np.ascontiguousarray(v, np.uint16)), _p(codes_k), _p(codes_v),
+                          _p(scales), _p(np.ascontiguousarray(positions, np.int32)), tokens,
+                          hkv, d, cap, first, bad.ptr)
+    return bool(bad)
+
+
+def kv_q8_0_encode(k, v, rows_k, rows_v, positions, cap, first=0, rotate=True):
+    tokens, hkv, d = k.shape
+    bad = Bad()
+    lib().po_kv_q8_0_encode(_p(np.ascontiguousarray(k, np.uint16)),
+                            _p(np.ascontiguousarray(v, np.uint16)), _p(rows_k), _p(rows_v),
+                            _p(np.ascontiguousarray(positions, np.int32)), tokens, hkv, d, cap,
+                            first, int(rotate), bad.ptr)
+    return bool(bad)
+
+
+def kv_q8_0_dequantize(rows_k, rows_v, rows, features):
+    out_k = np.empty((rows, features), np.uint16)
+    out_v = np.empty((rows, features), np.uint16)
+    bad = Bad()
+    lib().po_kv_q8_0_dequantize(_p(rows_k), _p(rows_v), _p(out_k), _p(out_v), rows, features,
+                                bad.ptr)
+    return out_k, out_v, bool(bad)
+
+
+def hadamard(x, scale):
+    x = np.array(x, dtype=np.float32, copy=True)
+    lib().po_hadamard(_p(x), x.size, scale)
+    return x
+
+
+def silu_table() -> np.ndarray:
+    t = np.empty(65536, np.uint16)
+    lib().po_silu_table(_p(t))
+    return t
+
+
+def swiglu(gate, up):
+    gate = np.ascontiguousarray(gate, np.uint16)
+    out = np.zeros_like(gate)
+    bad = Bad()
+    lib().po_swiglu(_p(gate), _p(np.ascontiguousarray(up, np.uint16)), _p(out), gate.size,
+                    bad.ptr)
+    return out, bool(bad)
+
+
+def embed(table, ids, vocab=None):
+    ids = np.ascontiguousarray(ids, np.int32)
+    vocab = table.shape[0] if vocab is None else vocab
+    out = np.zeros((ids.size, table.shape[1]), np.uint16)
+    bad = Bad()
+    lib().po_embed(_p(np.ascontiguousarray(table, np.uint16)), _p(ids), _p(out), ids.size,
+                   table.shape[1], vocab, bad.ptr)
+    return out, bool(bad)

@@ -1,0 +1,119 @@
+/*
+ * padra_oracle.h -- CPU restatement of Padra's exact-fusions-v1 per-token layer
+ * arithmetic (the parity oracle).
+ *
+ * TEST INFRASTRUCTURE ONLY.  This library is the checker for the HIP product in
+ * padra_amd/: only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg
+ * may load it.  The product never links, loads or falls back to it.
+ *
+ * Every function restates the reference CUDA source in plain C11, operation by
+ * operation (same rounding points, same reduction tree), citing the file:line of
+ * /root/reference it follows.  Activations cross this interface as BF16 bit
+ * patterns (uint16_t), the device I/O format of the product; the reference keeps
+ * the same values in fp32 buffers (BF16-exact), which changes no arithmetic.
+ *
+ * Pinning (what checks each function against something other than itself) is
+ * listed per function in tests/test_oracle.py.
+ */
+#ifndef PADRA_ORACLE_H
+#define PADRA_ORACLE_H
+#include <stdint.h>
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- A1 numeric primitives ------------------------------------------------ */
+float po_bf16_round(float x);           /* B(x): inference.cu:52-54, BHost :742-748 */
+uint16_t po_f32_to_bf16(float x);       /* __float2bfloat16_rn */
+float po_bf16_to_f32(uint16_t h);
+uint16_t po_f32_to_f16(float x);        /* __float2half_rn (RNE, subnormals) */
+float po_f16_to_f32(uint16_t h);
+void po_accumulate(float value, float *sum, float *error); /* inference.cu:103-109 */
+/* Compensated sum of squares of n values with a block of `threads` threads
+ * (128: AccurateReduce inference.cu:110-135 / Rms128In256Exact rms_wide_exact.cuh:3-31;
+ *  256: ResidualPostNormWideExact residual_norm_wide_exact.cuh:24-63). */
+float po_sumsq_tree(const float *v, int n, int threads);
+/* variance and 1/sqrt(variance+eps), each step correctly rounded (inference.cu:203-205). */
+void po_rms_inv(float sumsq, int n, float eps, float *variance, float *inv);
+float po_exp_rn(float x);               /* ExpRN: inference.cu:57-59 */
+
+/* ---- A2 residual + RMSNorm, A3 RMSNorm ------------------------------------ */
+/* x <- B(x + r); y <- B(B(x*inv)*gamma).  stats (nullable) gets {variance, inv} per row. */
+void po_residual_rmsnorm(uint16_t *x, const uint16_t *residual, uint16_t *y,
+                         const uint16_t *gamma, int rows, int hidden, float eps,
+                         int threads, float *stats, int *bad);
+void po_rmsnorm(const uint16_t *x, uint16_t *y, const uint16_t *gamma, int rows, int hidden,
+                float eps, int threads, float *stats, int *bad);
+
+/* ---- A5 RoPE table --------------------------------------------------------- */
+/* table[p][i] = B(cos(p*f_i)*scale), table[p][D/2+i] = B(sin(p*f_i)*scale), fp32 values.
+ * yarn=0: plain NeoX f_i = 1/theta^(2i/D).  yarn=1: the reference's global-layer ramp
+ * (inference.cu:764-785) with factor, original context, beta_fast 32, beta_slow 1. */
+void po_rope_table(float *table, int positions, int head_dim, float theta, int yarn,
+                   float factor, int original_context);
+
+/* ---- A4 Q/K norm + RoPE (+ A6 BF16 store) ---------------------------------- */
+/* One head vector in place: RMSNorm over D then NeoX half-split rotation with the
+ * table row (D BF16 values, cos then sin).  qk_rope_store_exact.cuh:27-44,
+ * qknorm_rope_pair64.cuh:30-82. */
+void po_qk_norm_rope_head(uint16_t *x, const uint16_t *weight, const uint16_t *table_row,
+                          int head_dim, float eps, int *bad);
+/* q [T][Hq][D], k [T][Hkv][D] in place; positions[t] selects the table row. */
+void po_qk_norm_rope(uint16_t *q, uint16_t *k, const uint16_t *qn, const uint16_t *kn,
+                     const uint16_t *table, const int *positions, int tokens, int q_heads,
+                     int kv_heads, int head_dim, float eps, int *bad);
+/* kc[(pos_t % cap)][f] = k[t][f] (and v) for t >= first; prefill_control.cuh:24-38,
+ * qk_rope_store_exact.cuh:45-48, prefill_kv_commit.cuh:4-13. */
+void po_kv_store_bf16(const uint16_t *k, const uint16_t *v, uint16_t *kc, uint16_t *vc,
+                      const int *positions, int tokens, int features, int cap, int first);
+
+/* ---- A7 Q8 KV (q8_token_head128_f32scale_v1) -------------------------------- */
+/* kv_q8.cuh:28-74 (Encode) + :75-98 (Commit), written straight to slot pos%cap.
+ * scales: [cap][kv_heads] {k,v} pairs (fp32). */
+void po_kv_q8_encode(const uint16_t *k, const uint16_t *v, int8_t *codes_k, int8_t *codes_v,
+                     float *scales, const int *positions, int tokens, int kv_heads,
+                     int head_dim, int cap, int first, int *bad);
+int po_kv_q8_decode(int8_t code, float scale, uint16_t *out); /* kv_q8.cuh:15-27 */
+
+/* ---- A8 Q8_0 KV (q8_0_token512_block32_f16scale_rot_k128_v64_v2) ------------ */
+void po_hadamard(float *x, int n, float scale); /* kv_q8_native.cuh:22-45, stages bit0..bitlog2(n)-1 */
+/* Row layout: uint16 d[F/32] (fp16), int8 qs[F], padded to 16 B (544 B for F=512).
+ * rotate=1 is the reference v2 format (K: 128-point, V: 64-point transforms);
+ * rotate=0 quantizes the BF16 values directly (no Hadamard). kv_q8_native.cuh:52-101. */
+int po_q8_0_row_bytes(int features);
+void po_kv_q8_0_encode(const uint16_t *k, const uint16_t *v, uint8_t *rows_k, uint8_t *rows_v,
+                       const int *positions, int tokens, int kv_heads, int head_dim, int cap,
+                       int first, int rotate, int *bad);
+/* bf16(code * fp16 d) for rows [0, rows); kv_q8_native.cuh:366-390. */
+void po_kv_q8_0_dequantize(const uint8_t *rows_k, const uint8_t *rows_v, uint16_t *out_k,
+                           uint16_t *out_v, int rows, int features, int *bad);
+
+/* ---- A10 SwiGLU -------------------------------------------------------------- */
+uint16_t po_silu_bf16(uint16_t gate);   /* exl3_silu_lut.cuh:5-8 */
+void po_silu_table(uint16_t *table);    /* 65536 entries, exl3_silu_lut.cuh:9-14 */
+/* out = B(s*u), s = silu LUT of the BF16 gate; exl3_silu_lut.cuh:15-31, inference.cu:575-579. */
+void po_swiglu(const uint16_t *gate, const uint16_t *up, uint16_t *out, long long count,
+               int *bad);
+
+/* ---- A11 embedding gather --------------------------------------------------- */
+/* out[t][:] = table[ids[t]][:]; ids outside [0, vocab) set bad and leave the row.
+ * decode_control.cuh:68-79, prefill_control.cuh:3-22. */
+void po_embed(const uint16_t *table, const int32_t *ids, uint16_t *out, int tokens, int hidden,
+              int vocab, int *bad);
+
+/* ---- A12 device state predicates ------------------------------------------- */
+typedef struct {
+  int32_t token, position, capacity, remaining, global_valid, local_valid, eos, stopped;
+} po_DecodeState;
+typedef struct {
+  int32_t base, prompt_offset, tokens, capacity, committed;
+  uint32_t binding_epoch, request_epoch, valid;
+} po_PrefillState;
+int po_decode_ready(const po_DecodeState *s, int maximum, int vocab); /* context_admission.cuh:5-11 */
+int po_valid_prefill_state(const po_PrefillState *s, int active_tokens, int capacity,
+                           uint32_t binding_epoch, int maximum); /* prefill_state.h:16-24 */
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,44 @@
+"""Builds libpadra_hip.so in-tree for gfx950 (python -m padra_amd.build).
+
+One hipcc invocation over every source in padra_amd/csrc.  Flags:
+  -ffp-contract=off  every float op rounds once, as the reference's __f*_rn intrinsics;
+  -Xclang -target-feature -Xclang -packed-fp32-ops  no packed-FP32 instructions.
+"""
+from __future__ import annotations
+
+import os
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+SOURCES = ["csrc/kernels.hip", "csrc/rope_table.cpp"]
+OUT = os.path.join(HERE, "libpadra_hip.so")
+
+
+def hipcc() -> str:
+    rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
+    return os.path.join(rocm, "bin", "hipcc")
+
+
+def command(out: str = OUT) -> list[str]:
+    return [hipcc(), "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",
+            "-ffp-contract=off", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+            "-Wall", "-I", os.path.join(ROOT, "include"), "-o", out] + \
+           [os.path.join(HERE, s) for s in SOURCES]
+
+
+def build(out: str = OUT, verbose: bool = False) -> str:
+    cmd = command(out)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    noise = ("packed-fp32-ops", "warning: argument unused")
+    msgs = [l for l in (res.stdout + res.stderr).splitlines() if l and not any(n in l for n in noise)]
+    if res.returncode != 0:
+        raise RuntimeError("hipcc failed:\n" + "\n".join(msgs))
+    if verbose and msgs:
+        print("\n".join(msgs), file=sys.stderr)
+    return out
+
+
+if __name__ == "__main__":
+    print(build(verbose=True))

@@ -1,0 +1,156 @@
+// Device primitives shared by the gfx950 kernels of the per-token layer path.
+//
+// Arithmetic contract (reference: /root/reference/src/cuda/inference.cu:52-59, 103-135):
+//  - B(x): round-to-nearest-even to BF16 and back.  gfx950 has a native RNE
+//    conversion (v_cvt_pk_bf16_f32), two values per instruction.
+//  - every + - * / sqrt is one correctly rounded binary32 operation: the build uses
+//    -ffp-contract=off and HIP's default correctly rounded division and sqrt.
+//  - compensated (Neumaier) accumulation with the reference's exact step and tree
+//    order, so sums of squares match bit for bit.
+#pragma once
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "padra_hip.h"
+
+namespace padra {
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+// BF16 halves of a packed word (element 2w in the low half, 2w+1 in the high half).
+__device__ __forceinline__ float lo16(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float hi16(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// RNE-convert two floats to one packed BF16 word (one v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+  const f32x2_t f = {a, b};
+  const bf16x2_t h = __builtin_convertvector(f, bf16x2_t);
+  return __builtin_bit_cast(uint32_t, h);
+}
+// B(x) of inference.cu:52-54.
+__device__ __forceinline__ float B(float x) { return (float)(__bf16)x; }
+
+// Neumaier step, inference.cu:103-109: the larger magnitude leads the Fast2Sum.
+__device__ __forceinline__ void acc(float value, float &sum, float &error) {
+  const float next = sum + value;
+  const bool lead = fabsf(sum) >= fabsf(value);
+  const float big = lead ? sum : value, small = lead ? value : sum;
+  error = error + ((big - next) + small);
+  sum = next;
+}
+// The same step when sum >= 0 and value >= 0 (squares and their partial sums): then
+// |sum| >= |value| <=> sum >= value, so max/min pick the same operands.
+// (AccumulatePositiveExact, positive_accumulate_exact.cuh:3-9, is this form.)
+__device__ __forceinline__ void acc_pos(float value, float &sum, float &error) {
+  const float next = sum + value;
+  error = error + ((fmaxf(sum, value) - next) + fminf(sum, value));
+  sum = next;
+}
+// Fold partner partial (s2, e2) into (s, e) as one shuffle-down step does
+// (inference.cu:113-117): first the partner's sum, then its error.
+__device__ __forceinline__ void fold(float s2, float e2, float &s, float &e) {
+  acc_pos(s2, s, e);
+  acc(e2, s, e);
+}
+
+__device__ __forceinline__ float shfl_down(float v, int d) { return __shfl_down(v, d, 64); }
+__device__ __forceinline__ float shfl_xor(float v, int m) { return __shfl_xor(v, m, 64); }
+
+// 16-byte vector loads/stores of activations.  Eight consecutive elements map to one
+// uint4 of BF16 or two uint4 of fp32.
+template <class T> struct ActIO;
+template <> struct ActIO<uint16_t> {
+  static __device__ __forceinline__ void load8(const uint16_t *p, float (&v)[8]) {
+    const uint4 w = *reinterpret_cast<const uint4 *>(p);
+    v[0] = lo16(w.x); v[1] = hi16(w.x); v[2] = lo16(w.y); v[3] = hi16(w.y);
+    v[4] = lo16(w.z); v[5] = hi16(w.z); v[6] = lo16(w.w); v[7] = hi16(w.w);
+  }
+  static __device__ __forceinline__ void store8(uint16_t *p, const uint32_t (&w)[4]) {
+    *reinterpret_cast<uint4 *>(p) = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+};
+template <> struct ActIO<float> {
+  static __device__ __forceinline__ void load8(const float *p, float (&v)[8]) {
+    const float4 a = *reinterpret_cast<const float4 *>(p);
+    const float4 b = *reinterpret_cast<const float4 *>(p + 4);
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+  }
+  static __device__ __forceinline__ void store8(float *p, const uint32_t (&w)[4]) {
+    *reinterpret_cast<float4 *>(p) = make_float4(lo16(w[0]), hi16(w[0]), lo16(w[1]), hi16(w[1]));
+    *reinterpret_cast<float4 *>(p + 4) =
+        make_float4(lo16(w[2]), hi16(w[2]), lo16(w[3]), hi16(w[3]));
+  }
+};
+__device__ __forceinline__ void load8_bf16(const uint16_t *p, float (&v)[8]) {
+  ActIO<uint16_t>::load8(p, v);
+}
+
+// Sets the caller's sticky error flag (reference: atomicExch(bad, 1)).
+__device__ __forceinline__ void raise_bad(int *bad) {
+  if (bad)
+    atomicExch(bad, 1);
+}
+
+// DecodeReadyAtLimit (context_admission.cuh:5-11) with the vocabulary bound a parameter.
+__device__ __forceinline__ bool decode_ready(const padra_DecodeState *s, int maximum, int vocab) {
+  return maximum > 0 && maximum <= 131072 && s && !s->stopped && !s->eos && s->remaining > 0 &&
+         s->token >= 0 && s->token < vocab && s->capacity > 0 && s->capacity <= maximum &&
+         s->position >= 0 && s->position < s->capacity && s->global_valid == s->position &&
+         s->local_valid == min(s->position, 1024);
+}
+// ValidPrefillState (src/runtime/prefill_state.h:16-24).
+__device__ __forceinline__ bool prefill_valid(const padra_PrefillState &s, int active_tokens,
+                                              int capacity, uint32_t binding_epoch,
+                                              int maximum) {
+  return s.valid == 1 && s.binding_epoch == binding_epoch && s.request_epoch != 0 &&
+         maximum > 0 && maximum <= 131072 && s.capacity == capacity && capacity > 0 &&
+         capacity <= maximum && s.tokens == active_tokens && active_tokens > 0 &&
+         active_tokens <= 2048 && s.base >= 0 && s.base <= capacity - active_tokens &&
+         s.committed == s.base && s.prompt_offset >= 0 &&
+         s.prompt_offset <= capacity - active_tokens;
+}
+
+// Position source passed by value to kernels.
+struct PosSrc {
+  int mode, base, maximum, vocab, tokens;
+  uint32_t epoch;
+  const padra_PrefillState *prefill;
+  const padra_DecodeState *decode;
+};
+
+// Resolves token t's absolute position; `ok` false means the unit must write nothing
+// and the caller raises the flag.  With a cache binding (cap > 0) the state must admit
+// the ring: cap <= capacity (StorePrefillControlled prefill_control.cuh:27-29,
+// QKNormRopeStoreControlled qk_rope_store_exact.cuh:8), and for the quantized formats
+// (`ring_exact`) cap is the capacity or the 1024-row local ring and `first` is the
+// chunk rows that do not fit (kv_q8.cuh:36-38, 80-82; kv_q8_native.cuh:447-450).
+__device__ __forceinline__ int resolve_position(const PosSrc &p, int t, int cap, int first,
+                                                bool ring_exact, bool &ok) {
+  ok = true;
+  if (p.mode == PADRA_POS_BASE)
+    return p.base + t;
+  if (p.mode == PADRA_POS_PREFILL) {
+    const padra_PrefillState s = *p.prefill;
+    ok = prefill_valid(s, p.tokens, s.capacity, p.epoch, p.maximum);
+    if (cap > 0) {
+      ok = ok && cap <= s.capacity;
+      if (ring_exact)
+        ok = ok && (cap == s.capacity || cap == min(1024, s.capacity)) &&
+             first == (cap == s.capacity ? 0 : max(0, p.tokens - cap));
+    }
+    return s.base + t;
+  }
+  const padra_DecodeState *s = p.decode + t;
+  ok = decode_ready(s, p.maximum, p.vocab);
+  if (ok && cap > 0) {
+    ok = cap <= s->capacity;
+    if (ring_exact)
+      ok = ok && (cap == s->capacity || cap == min(1024, s->capacity));
+  }
+  return ok ? s->position : 0;
+}
+
+} // namespace padra

@@ -1,0 +1,306 @@
+// gfx950 kernels and the extern "C" entry points of include/padra_hip.h for the
+// residual-norm, Q/K-norm + RoPE + KV-store and fused chain paths.
+//
+// Launch geometry: one 64-lane wavefront per workgroup.  A residual-norm wave covers
+// 64/(VT/8) rows (4 rows for the 128-thread tree, 2 for the 256-thread tree); a Q/K wave
+// covers 32 head vectors.  Every wave streams its inputs with 16-byte loads issued
+// before any arithmetic, and there is no inter-wave communication, so the grid is a
+// flat list of independent waves (thousands for a 2048-token chunk: >> 256 CUs).
+#include <stdio.h>
+
+#include <type_traits>
+
+#include "norm_rows.h"
+#include "qk_heads.h"
+
+using namespace padra;
+
+namespace {
+
+template <int VT, int J, class T, bool RES>
+__global__ __launch_bounds__(64) void k_norm(NormArgs<T> a) {
+  norm_rows_wave<VT, J, T, RES>(a, blockIdx.x);
+}
+
+template <class T, int FMT> __global__ __launch_bounds__(64) void k_qk(QKArgs<T> a) {
+  qk_heads_wave<T, FMT>(a, blockIdx.x);
+}
+
+// Residual-norm waves and Q/K waves interleaved evenly over the grid, so every CU gets
+// the same mix of the (VALU-heavier) norm rows and the (store-heavier) head vectors.
+template <int VT, int J, int FMT>
+__global__ __launch_bounds__(64) void k_chain(NormArgs<uint16_t> n, QKArgs<uint16_t> q,
+                                              long long norm_waves, long long waves) {
+  const long long b = blockIdx.x;
+  const long long n0 = b * norm_waves / waves, n1 = (b + 1) * norm_waves / waves;
+  if (n1 > n0)
+    norm_rows_wave<VT, J, uint16_t, true>(n, (int)n0);
+  else
+    qk_heads_wave<uint16_t, FMT>(q, b - n1);
+}
+
+bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int launched() {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    fprintf(stderr, "padra: kernel launch failed: %s\n", hipGetErrorString(e));
+    return PADRA_INTERNAL;
+  }
+  return PADRA_OK;
+}
+
+// Residual-norm dispatch over the supported (tree, hidden/tree) pairs.
+#define PADRA_NORM_J(VT, JV)                                                                 \
+  case JV:                                                                                   \
+    return f(std::integral_constant<int, VT>{}, std::integral_constant<int, JV>{});
+template <class F> int norm_shape(int tree, int j, F &&f) {
+  if (tree == 128) {
+    switch (j) {
+      PADRA_NORM_J(128, 8)
+      PADRA_NORM_J(128, 9)
+      PADRA_NORM_J(128, 16)
+      PADRA_NORM_J(128, 18)
+      PADRA_NORM_J(128, 32)
+      PADRA_NORM_J(128, 36)
+    }
+  } else if (tree == 256) {
+    switch (j) {
+      PADRA_NORM_J(256, 4)
+      PADRA_NORM_J(256, 8)
+      PADRA_NORM_J(256, 9)
+      PADRA_NORM_J(256, 16)
+      PADRA_NORM_J(256, 18)
+    }
+  }
+  return PADRA_UNSUPPORTED;
+}
+#undef PADRA_NORM_J
+
+int check_norm(const void *x, const void *normalized, const uint16_t *gamma, int rows,
+               int hidden, float eps, int tree, int *bad, int act) {
+  if (!x || !normalized || !gamma || !bad || x == normalized || rows < 1 || hidden < 1 ||
+      !(eps >= 0.f) || (tree != 128 && tree != 256) || (act != PADRA_ACT_BF16 && act != PADRA_ACT_F32))
+    return PADRA_INVALID_ARGUMENT;
+  if (!aligned16(x) || !aligned16(normalized) || !aligned16(gamma))
+    return PADRA_INVALID_ARGUMENT;
+  if (hidden % tree != 0)
+    return PADRA_UNSUPPORTED;
+  return PADRA_OK;
+}
+
+int rows_per_wave(int tree) { return 64 / (tree / 8); }
+
+PosSrc make_pos(const padra_Positions &p, int tokens) {
+  PosSrc s;
+  s.mode = p.mode;
+  s.base = p.base;
+  s.maximum = p.maximum;
+  s.vocab = p.vocab;
+  s.tokens = tokens;
+  s.epoch = p.binding_epoch;
+  s.prefill = p.prefill;
+  s.decode = p.decode;
+  return s;
+}
+
+int check_qk(const void *q, const void *k, const void *v, const uint16_t *qn, const uint16_t *kn,
+             const uint16_t *table, int table_rows, const padra_Positions *pos, int tokens,
+             int q_heads, int kv_heads, int head_dim, float eps, const padra_KVCache *kv,
+             int *bad, int act) {
+  if (!q || !k || !qn || !kn || !table || !pos || !bad || table_rows < 1 || tokens < 1 ||
+      q_heads < 1 || kv_heads < 1 || !(eps >= 0.f) ||
+      (act != PADRA_ACT_BF16 && act != PADRA_ACT_F32))
+    return PADRA_INVALID_ARGUMENT;
+  if (head_dim != 128)
+    return PADRA_UNSUPPORTED;
+  if (!aligned16(q) || !aligned16(k) || !aligned16(qn) || !aligned16(kn) || !aligned16(table))
+    return PADRA_INVALID_ARGUMENT;
+  switch (pos->mode) {
+  case PADRA_POS_BASE:
+    if (pos->base < 0 || (long long)pos->base + tokens > 0x7fffffffLL)
+      return PADRA_INVALID_ARGUMENT;
+    break;
+  case PADRA_POS_PREFILL:
+    if (!pos->prefill || tokens > 2048 || pos->maximum < 1 || pos->maximum > 131072)
+      return PADRA_INVALID_ARGUMENT;
+    break;
+  case PADRA_POS_DECODE:
+    if (!pos->decode || pos->maximum < 1 || pos->maximum > 131072 || pos->vocab < 1)
+      return PADRA_INVALID_ARGUMENT;
+    break;
+  default:
+    return PADRA_INVALID_ARGUMENT;
+  }
+  if (kv) {
+    if (!v || !kv->k || !kv->v || !aligned16(v) || !aligned16(kv->k) || !aligned16(kv->v) ||
+        kv->cap < 1 || kv->first < 0 || kv->first >= tokens || kv->seq_stride < 0)
+      return PADRA_INVALID_ARGUMENT;
+    if (kv->format < PADRA_KV_BF16 || kv->format > PADRA_KV_Q8_0_NOROT)
+      return PADRA_INVALID_ARGUMENT;
+    if (kv->format == PADRA_KV_Q8 && (!kv->scales || (reinterpret_cast<uintptr_t>(kv->scales) & 7u)))
+      return PADRA_INVALID_ARGUMENT;
+    if (pos->mode == PADRA_POS_DECODE && tokens > 1 && kv->seq_stride < kv->cap)
+      return PADRA_INVALID_ARGUMENT;
+    if (pos->mode != PADRA_POS_DECODE && tokens - kv->first > kv->cap)
+      return PADRA_INVALID_ARGUMENT; // a local ring stores at most its last `cap` rows
+  }
+  return PADRA_OK;
+}
+
+template <class T>
+QKArgs<T> make_qk(void *q, void *k, const void *v, const uint16_t *qn, const uint16_t *kn,
+                  const uint16_t *table, int table_rows, const padra_Positions *pos, int tokens,
+                  int q_heads, int kv_heads, float eps, const padra_KVCache *kv, int *bad) {
+  QKArgs<T> a;
+  a.q = static_cast<T *>(q);
+  a.k = static_cast<T *>(k);
+  a.v = static_cast<const T *>(v);
+  a.qn = qn;
+  a.kn = kn;
+  a.table = table;
+  a.table_rows = table_rows;
+  a.tokens = tokens;
+  a.hq = q_heads;
+  a.hkv = kv_heads;
+  a.eps = eps;
+  a.pos = make_pos(*pos, tokens);
+  a.kc = kv ? kv->k : nullptr;
+  a.vc = kv ? kv->v : nullptr;
+  a.scales = kv ? kv->scales : nullptr;
+  a.cap = kv ? kv->cap : 0;
+  a.first = kv ? kv->first : 0;
+  a.seq_stride = kv ? kv->seq_stride : 0;
+  a.bad = bad;
+  return a;
+}
+
+template <class F> int with_format(const padra_KVCache *kv, F &&f) {
+  if (!kv)
+    return f(std::integral_constant<int, -1>{});
+  switch (kv->format) {
+  case PADRA_KV_BF16:
+    return f(std::integral_constant<int, PADRA_KV_BF16>{});
+  case PADRA_KV_Q8:
+    return f(std::integral_constant<int, PADRA_KV_Q8>{});
+  case PADRA_KV_Q8_0:
+    return f(std::integral_constant<int, PADRA_KV_Q8_0>{});
+  case PADRA_KV_Q8_0_NOROT:
+    return f(std::integral_constant<int, PADRA_KV_Q8_0_NOROT>{});
+  }
+  return PADRA_INVALID_ARGUMENT;
+}
+
+long long qk_waves(int tokens, int q_heads, int kv_heads) {
+  return ((long long)tokens * (q_heads + kv_heads) + 31) / 32;
+}
+
+} // namespace
+
+extern "C" int padra_ResidualPostNorm(void *stream, void *x, const void *residual,
+                                      void *normalized, const uint16_t *gamma, int rows,
+                                      int hidden, float eps, int tree, float *statistics,
+                                      int *bad, int act) {
+  int st = check_norm(x, normalized, gamma, rows, hidden, eps, tree, bad, act);
+  if (st)
+    return st;
+  if (residual && (!aligned16(residual) || residual == x))
+    return PADRA_INVALID_ARGUMENT;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const int grid = (rows + rows_per_wave(tree) - 1) / rows_per_wave(tree);
+  auto launch = [&](auto tag) -> int {
+    using T = decltype(tag);
+    NormArgs<T> a;
+    a.x = static_cast<T *>(x);
+    a.residual = static_cast<const T *>(residual);
+    a.y = static_cast<T *>(normalized);
+    a.gamma = gamma;
+    a.stats = statistics;
+    a.bad = bad;
+    a.rows = rows;
+    a.eps = eps;
+    return norm_shape(tree, hidden / tree, [&](auto vt, auto j) -> int {
+      if (residual)
+        hipLaunchKernelGGL((k_norm<vt.value, j.value, T, true>), dim3(grid), dim3(64), 0, s, a);
+      else
+        hipLaunchKernelGGL((k_norm<vt.value, j.value, T, false>), dim3(grid), dim3(64), 0, s, a);
+      return launched();
+    });
+  };
+  return act == PADRA_ACT_BF16 ? launch(uint16_t{}) : launch(float{});
+}
+
+extern "C" int padra_QKNormRopeStore(void *stream, void *q, void *k, const void *v,
+                                     const uint16_t *qn, const uint16_t *kn,
+                                     const uint16_t *table, int table_rows,
+                                     const padra_Positions *pos, int tokens, int q_heads,
+                                     int kv_heads, int head_dim, float eps,
+                                     const padra_KVCache *kv, int *bad, int act) {
+  const int st = check_qk(q, k, v, qn, kn, table, table_rows, pos, tokens, q_heads, kv_heads,
+                          head_dim, eps, kv, bad, act);
+  if (st)
+    return st;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const long long grid = qk_waves(tokens, q_heads, kv_heads);
+  auto launch = [&](auto tag) -> int {
+    using T = decltype(tag);
+    const QKArgs<T> a =
+        make_qk<T>(q, k, v, qn, kn, table, table_rows, pos, tokens, q_heads, kv_heads, eps, kv, bad);
+    return with_format(kv, [&](auto fmt) -> int {
+      hipLaunchKernelGGL((k_qk<T, fmt.value>), dim3((unsigned)grid), dim3(64), 0, s, a);
+      return launched();
+    });
+  };
+  return act == PADRA_ACT_BF16 ? launch(uint16_t{}) : launch(float{});
+}
+
+extern "C" int padra_ResidualNormQKRopeStore(
+    void *stream, void *x, const void *residual, void *normalized, const uint16_t *gamma,
+    int hidden, int tree, float *statistics, void *q, void *k, const void *v,
+    const uint16_t *qn, const uint16_t *kn, const uint16_t *table, int table_rows,
+    const padra_Positions *pos, int tokens, int q_heads, int kv_heads, int head_dim, float eps,
+    const padra_KVCache *kv, int *bad) {
+  int st = check_norm(x, normalized, gamma, tokens, hidden, eps, tree, bad, PADRA_ACT_BF16);
+  if (st)
+    return st;
+  if (!residual || !aligned16(residual) || residual == x)
+    return PADRA_INVALID_ARGUMENT;
+  st = check_qk(q, k, v, qn, kn, table, table_rows, pos, tokens, q_heads, kv_heads, head_dim, eps,
+                kv, bad, PADRA_ACT_BF16);
+  if (st)
+    return st;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  NormArgs<uint16_t> n;
+  n.x = static_cast<uint16_t *>(x);
+  n.residual = static_cast<const uint16_t *>(residual);
+  n.y = static_cast<uint16_t *>(normalized);
+  n.gamma = gamma;
+  n.stats = statistics;
+  n.bad = bad;
+  n.rows = tokens;
+  n.eps = eps;
+  const QKArgs<uint16_t> a = make_qk<uint16_t>(q, k, v, qn, kn, table, table_rows, pos, tokens,
+                                               q_heads, kv_heads, eps, kv, bad);
+  const long long norm_waves = (tokens + rows_per_wave(tree) - 1) / rows_per_wave(tree);
+  const long long waves = norm_waves + qk_waves(tokens, q_heads, kv_heads);
+  const int j = hidden / tree;
+  if (!((tree == 128 && (j == 16 || j == 18)) || (tree == 256 && (j == 8 || j == 9))))
+    return PADRA_UNSUPPORTED;
+  return with_format(kv, [&](auto fmt) -> int {
+    if (tree == 128 && j == 16)
+      hipLaunchKernelGGL((k_chain<128, 16, fmt.value>), dim3((unsigned)waves), dim3(64), 0, s, n, a,
+                         norm_waves, waves);
+    else if (tree == 128)
+      hipLaunchKernelGGL((k_chain<128, 18, fmt.value>), dim3((unsigned)waves), dim3(64), 0, s, n, a,
+                         norm_waves, waves);
+    else if (j == 8)
+      hipLaunchKernelGGL((k_chain<256, 8, fmt.value>), dim3((unsigned)waves), dim3(64), 0, s, n, a,
+                         norm_waves, waves);
+    else
+      hipLaunchKernelGGL((k_chain<256, 9, fmt.value>), dim3((unsigned)waves), dim3(64), 0, s, n, a,
+                         norm_waves, waves);
+    return launched();
+  });
+}
+
+extern "C" const char *padra_version(void) { return "padra-mi355x 0.1 gfx950 exact-fusions-v1"; }

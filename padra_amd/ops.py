@@ -1,0 +1,141 @@
+"""Torch-tensor front end of the C-ABI (the host-side mirror of the reference launches).
+
+Names follow the reference kernels each call replaces.  Tensors must live on the GPU
+(except RopeTable, which builds a host table as the reference does); BF16 activations
+are torch.bfloat16 (or int16 views of BF16 bits), fp32 activations torch.float32.
+Every call is asynchronous on the current torch stream and raises PadraError on a
+nonzero status.  Device-detected problems set the caller's `bad` flag (int32 tensor).
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import abi
+
+_BF16_DTYPES = (torch.bfloat16, torch.int16, torch.uint16)
+
+
+def _act(t: torch.Tensor) -> int:
+    if t.dtype in _BF16_DTYPES:
+        return abi.ACT_BF16
+    if t.dtype == torch.float32:
+        return abi.ACT_F32
+    raise TypeError(f"activation dtype {t.dtype} (want bfloat16 or float32)")
+
+
+def _p(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(t: torch.Tensor):
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def _need_cuda(*ts):
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise ValueError("padra_amd ops take GPU tensors")
+
+
+def ResidualPostNorm(x, residual, normalized, gamma, bad, eps=1e-6, tree=abi.TREE_128,
+                     statistics=None):
+    """x <- B(x + residual); normalized <- B(B(x*inv)*gamma).  residual=None: RMSNorm only.
+
+    Replaces ResidualPostNormWideExact (tree=256), Add+Norm (tree=128)
+    (residual_norm_wide_exact.cuh:6-80, inference.cu:188-214, 475-481).
+    """
+    _need_cuda(x, residual, normalized, gamma, bad, statistics)
+    rows, hidden = x.shape[0], x.shape[-1]
+    abi.call("padra_ResidualPostNorm", _stream(x), _p(x), _p(residual), _p(normalized),
+             _p(gamma), rows, hidden, float(eps), int(tree), _p(statistics), _p(bad), _act(x))
+
+
+def RopeTable(positions, head_dim=128, theta=1e6, yarn=False, factor=16.0,
+              original_context=8192) -> torch.Tensor:
+    """Host BF16 cos|sin table [positions][head_dim] (RopeTable, inference.cu:764-785)."""
+    out = torch.empty((positions, head_dim), dtype=torch.int16)
+    abi.call("padra_RopeTable", _p(out), int(positions), int(head_dim), float(theta),
+             int(bool(yarn)), float(factor), int(original_context))
+    return out.view(torch.bfloat16)
+
+
+def positions_base(base: int = 0) -> abi.Positions:
+    return abi.Positions(mode=abi.POS_BASE, base=int(base), prefill=None, decode=None,
+                         maximum=131072, vocab=98304, binding_epoch=1)
+
+
+def positions_prefill(state: torch.Tensor, maximum=131072, binding_epoch=1) -> abi.Positions:
+    """state: device int32[8] holding a PrefillState."""
+    return abi.Positions(mode=abi.POS_PREFILL, base=0, prefill=state.data_ptr(), decode=None,
+                         maximum=int(maximum), vocab=98304, binding_epoch=int(binding_epoch))
+
+
+def positions_decode(states: torch.Tensor, maximum=131072, vocab=98304) -> abi.Positions:
+    """states: device int32[n][8] holding one DecodeState per sequence."""
+    return abi.Positions(mode=abi.POS_DECODE, base=0, prefill=None, decode=states.data_ptr(),
+                         maximum=int(maximum), vocab=int(vocab), binding_epoch=1)
+
+
+def kv_cache(fmt, k, v, cap, scales=None, first=0, seq_stride=0) -> abi.KVCache:
+    return abi.KVCache(format=int(fmt), k=k.data_ptr(), v=v.data_ptr(),
+                       scales=None if scales is None else scales.data_ptr(), cap=int(cap),
+                       first=int(first), seq_stride=int(seq_stride))
+
+
+def q8_0_row_bytes(features: int) -> int:
+    """CacheRow size: fp16 d[F/32] + int8 qs[F], 16-byte aligned (kv_q8_layout.cuh:6-12)."""
+    return (2 * (features // 32) + features + 15) // 16 * 16
+
+
+def kv_cache_layout(fmt: int, rows: int, features: int = 512) -> dict:
+    """Byte offsets of one layer's cache, KVCacheLayout::Make (kv_cache_layout.h:12-33)."""
+    if not 1 <= rows <= 131072:
+        raise ValueError("unsupported KV row capacity")
+    if fmt == abi.KV_BF16:
+        return {"v_offset": rows * 2 * features, "scales_offset": 0, "bytes": rows * 4 * features}
+    if fmt == abi.KV_Q8:
+        heads = features // 128
+        return {"v_offset": rows * features, "scales_offset": rows * 2 * features,
+                "bytes": rows * (2 * features + 8 * heads)}
+    if fmt in (abi.KV_Q8_0, abi.KV_Q8_0_NOROT):
+        rb = q8_0_row_bytes(features)
+        return {"v_offset": rows * rb, "scales_offset": 0, "bytes": rows * 2 * rb}
+    raise ValueError("unknown KV format")
+
+
+def _shape_qk(q, k):
+    tokens, q_heads, head_dim = q.shape
+    if k.shape[0] != tokens or k.shape[2] != head_dim:
+        raise ValueError("q [T][Hq][D] and k [T][Hkv][D] disagree")
+    return tokens, q_heads, k.shape[1], head_dim
+
+
+def QKNormRopeStore(q, k, qn, kn, table, positions: abi.Positions, bad, eps=1e-6, v=None,
+                    kv: abi.KVCache | None = None):
+    """Per-head RMSNorm + NeoX RoPE of q [T][Hq][D], k [T][Hkv][D] in place; with kv, the
+    rotated K rows and V rows are stored at slot position % cap.
+
+    Replaces QKNormRope / QKNormRopePair64 / QKNormRopeControlled /
+    QKNormRopeStoreControlled and the cache writers after them (see padra_hip.h).
+    """
+    _need_cuda(q, k, v, qn, kn, table, bad)
+    tokens, q_heads, kv_heads, head_dim = _shape_qk(q, k)
+    abi.call("padra_QKNormRopeStore", _stream(q), _p(q), _p(k), _p(v), _p(qn), _p(kn),
+             _p(table), table.shape[0], ctypes.byref(positions), tokens, q_heads, kv_heads,
+             head_dim, float(eps), None if kv is None else ctypes.byref(kv), _p(bad), _act(q))
+
+
+def ResidualNormQKRopeStore(x, residual, normalized, gamma, q, k, v, qn, kn, table,
+                            positions: abi.Positions, kv: abi.KVCache | None, bad, eps=1e-6,
+                            tree=abi.TREE_128, statistics=None):
+    """ResidualPostNorm and QKNormRopeStore over the same tokens in one launch."""
+    _need_cuda(x, residual, normalized, gamma, q, k, v, qn, kn, table, bad, statistics)
+    tokens, q_heads, kv_heads, head_dim = _shape_qk(q, k)
+    if x.shape[0] != tokens:
+        raise ValueError("x rows must equal the token count")
+    abi.call("padra_ResidualNormQKRopeStore", _stream(x), _p(x), _p(residual), _p(normalized),
+             _p(gamma), x.shape[-1], int(tree), _p(statistics), _p(q), _p(k), _p(v), _p(qn),
+             _p(kn), _p(table), table.shape[0], ctypes.byref(positions), tokens, q_heads,
+             kv_heads, head_dim, float(eps), None if kv is None else ctypes.byref(kv), _p(bad))

@@ -1,0 +1,348 @@
+"""GPU parity: the HIP library (through its C-ABI) against the CPU oracle, bit for bit.
+
+Every output here is BF16, integer codes or fp16/fp32 scales: the bar is exact equality.
+The reduction-order golden rows (tests/golden/reduction_order.npz) make the tree order
+observable, so a GPU tree that differs from the reference's fails here.
+"""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from padra_amd import abi, ops, synth
+
+pytestmark = pytest.mark.gpu
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+
+
+@pytest.fixture(scope="module", autouse=True)
+def gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    abi.lib()
+    yield
+    torch.cuda.synchronize()
+
+
+def dev(a):
+    a = np.ascontiguousarray(a)
+    if a.dtype == np.uint16:
+        return torch.from_numpy(a.view(np.int16)).cuda()
+    return torch.from_numpy(a).cuda()
+
+
+def host16(t):
+    return t.cpu().numpy().view(np.uint16)
+
+
+def flag():
+    return torch.zeros(1, dtype=torch.int32, device="cuda")
+
+
+def table_bits(oracle, n, theta=1e6):
+    return synth.bf16_bits(oracle.rope_table(n, 128, theta))
+
+
+# ---- residual + RMSNorm ------------------------------------------------------------------
+
+@pytest.mark.parametrize("tree", [128, 256])
+@pytest.mark.parametrize("hidden", [2048, 2304])
+@pytest.mark.parametrize("rows", [1, 5, 37])
+@pytest.mark.parametrize("residual", [True, False])
+def test_residual_norm_bf16(oracle, tree, hidden, rows, residual):
+    print(f"[case] norm tree={tree} hidden={hidden} rows={rows} residual={residual}", flush=True)
+    d = synth.chain_inputs(rows, hidden=hidden, outliers=True, seed=rows + hidden + tree)
+    if residual:
+        want_x, want_y, want_st, want_bad = oracle.residual_rmsnorm(d["x"], d["residual"],
+                                                                    d["gamma"], threads=tree)
+    else:
+        want_y, want_st, want_bad = oracle.rmsnorm(d["x"], d["gamma"], threads=tree)
+        want_x = d["x"]
+    x, r, g = dev(d["x"]), dev(d["residual"]), dev(d["gamma"])
+    y = torch.empty_like(x)
+    st = torch.empty((rows, 2), dtype=torch.float32, device="cuda")
+    bad = flag()
+    ops.ResidualPostNorm(x, r if residual else None, y, g, bad, tree=tree, statistics=st)
+    torch.cuda.synchronize()
+    assert np.array_equal(host16(x), want_x)
+    assert np.array_equal(host16(y), want_y)
+    assert np.array_equal(st.cpu().numpy(), want_st)
+    assert bool(bad.item()) == want_bad
+
+
+@pytest.mark.parametrize("tree", [128, 256])
+def test_residual_norm_f32_activations(oracle, tree):
+    print(f"[case] norm f32 tree={tree}", flush=True)
+    d = synth.chain_inputs(9, outliers=True, seed=77)
+    want_x, want_y, want_st, _ = oracle.residual_rmsnorm(d["x"], d["residual"], d["gamma"],
+                                                         threads=tree)
+    x = torch.from_numpy(synth.bf16_to_f32(d["x"])).cuda()
+    r = torch.from_numpy(synth.bf16_to_f32(d["residual"])).cuda()
+    y = torch.empty_like(x)
+    bad = flag()
+    ops.ResidualPostNorm(x, r, y, dev(d["gamma"]), bad, tree=tree)
+    torch.cuda.synchronize()
+    assert np.array_equal(x.cpu().numpy(), synth.bf16_to_f32(want_x))
+    assert np.array_equal(y.cpu().numpy(), synth.bf16_to_f32(want_y))
+    assert not bad.item()
+
+
+def test_residual_norm_golden_order_rows(oracle):
+    """Rows built from the order-sensitive golden vector: the two trees give different
+    variances, and the GPU must give each tree's own."""
+    g = np.load(os.path.join(HERE, "golden", "reduction_order.npz"))
+    row = np.zeros(2048, np.float32)
+    row[:512] = g["v512"]
+    bits = synth.bf16_bits(np.stack([row, row * 0.5]))
+    gamma = synth.bf16_bits(np.ones(2048))
+    for tree, key in ((128, "v512_tree128"), (256, "v512_tree256")):
+        print(f"[case] golden order tree={tree}", flush=True)
+        x = dev(bits)
+        y = torch.empty_like(x)
+        st = torch.empty((2, 2), dtype=torch.float32, device="cuda")
+        ops.ResidualPostNorm(x, None, y, dev(gamma), flag(), tree=tree, statistics=st)
+        torch.cuda.synchronize()
+        assert st[0, 0].item() == np.float32(g[key] / np.float32(2048))
+        want_y, want_st, _ = oracle.rmsnorm(bits, gamma, threads=tree)
+        assert np.array_equal(host16(y), want_y)
+        assert np.array_equal(st.cpu().numpy(), want_st)
+
+
+def test_residual_norm_nonfinite_sets_bad():
+    d = synth.chain_inputs(4, seed=3)
+    xb = d["x"].copy()
+    xb[2, 100] = 0x7F80
+    x = dev(xb)
+    y = torch.empty_like(x)
+    bad = flag()
+    ops.ResidualPostNorm(x, dev(d["residual"]), y, dev(d["gamma"]), bad)
+    torch.cuda.synchronize()
+    assert bad.item() == 1
+
+
+# ---- Q/K norm + RoPE + KV store -------------------------------------------------------------
+
+def _qk_oracle(oracle, d, tb, positions):
+    return oracle.qk_norm_rope(d["q"], d["k"], d["qn"], d["kn"], tb, positions)
+
+
+@pytest.mark.parametrize("tokens,base", [(1, 4097), (7, 0), (300, 123)])
+def test_qk_rope_no_store(oracle, tokens, base):
+    print(f"[case] qk tokens={tokens} base={base}", flush=True)
+    d = synth.chain_inputs(tokens, outliers=True, seed=tokens)
+    tb = table_bits(oracle, base + tokens)
+    wq, wk, _ = _qk_oracle(oracle, d, tb, np.arange(base, base + tokens, dtype=np.int32))
+    q, k = dev(d["q"]), dev(d["k"])
+    bad = flag()
+    ops.QKNormRopeStore(q, k, dev(d["qn"]), dev(d["kn"]), dev(tb), ops.positions_base(base), bad)
+    torch.cuda.synchronize()
+    assert np.array_equal(host16(q), wq) and np.array_equal(host16(k), wk)
+    assert not bad.item()
+
+
+def test_qk_rope_golden_order_heads(oracle):
+    g = np.load(os.path.join(HERE, "golden", "reduction_order.npz"))
+    heads = synth.bf16_bits(g["head128"])  # [2][128]
+    q = np.stack([heads] * 8, axis=1).reshape(2, 16, 128)[:, :16]
+    k = np.stack([heads] * 2, axis=1).reshape(2, 4, 128)
+    ones = synth.bf16_bits(np.ones(128))
+    tb = table_bits(oracle, 4)
+    wq, wk, _ = oracle.qk_norm_rope(q, k, ones, ones, tb, np.array([1, 3], np.int32))
+    tq, tk = dev(q), dev(k)
+    ops.QKNormRopeStore(tq, tk, dev(ones), dev(ones), dev(tb), ops.positions_base(1), flag())
+    torch.cuda.synchronize()
+    assert np.array_equal(host16(tq), wq) and np.array_equal(host16(tk), wk)
+
+
+def _prefill_state(base, tokens, capacity, **kw):
+    s = dict(base=base, prompt_offset=base, tokens=tokens, capacity=capacity, committed=base,
+             binding_epoch=1, request_epoch=1, valid=1)
+    s.update(kw)
+    return torch.tensor([s[k] for k in ("base", "prompt_offset", "tokens", "capacity",
+                                        "committed", "binding_epoch", "request_epoch", "valid")],
+                        dtype=torch.int32, device="cuda")
+
+
+def _expected_cache(oracle, fmt, wk, v, positions, cap, first):
+    tokens = wk.shape[0]
+    if fmt == abi.KV_BF16:
+        kc = np.zeros((cap, 512), np.uint16)
+        vc = np.zeros((cap, 512), np.uint16)
+        oracle.kv_store_bf16(wk, v, kc, vc, positions, cap, first)
+        return kc, vc, None
+    if fmt == abi.KV_Q8:
+        kc = np.zeros((cap, 512), np.int8)
+        vc = np.zeros((cap, 512), np.int8)
+        sc = np.zeros((cap, 4, 2), np.float32)
+        assert not oracle.kv_q8_encode(wk, v, kc, vc, sc, positions, cap, first)
+        return kc, vc, sc
+    kc = np.zeros((cap, 544), np.uint8)
+    vc = np.zeros((cap, 544), np.uint8)
+    assert not oracle.kv_q8_0_encode(wk, v, kc, vc, positions, cap, first,
+                                     rotate=(fmt == abi.KV_Q8_0))
+    return kc, vc, None
+
+
+def _alloc_cache(fmt, rows):
+    if fmt == abi.KV_BF16:
+        return (torch.zeros((rows, 512), dtype=torch.int16, device="cuda"),
+                torch.zeros((rows, 512), dtype=torch.int16, device="cuda"), None)
+    if fmt == abi.KV_Q8:
+        return (torch.zeros((rows, 512), dtype=torch.int8, device="cuda"),
+                torch.zeros((rows, 512), dtype=torch.int8, device="cuda"),
+                torch.zeros((rows, 4, 2), dtype=torch.float32, device="cuda"))
+    return (torch.zeros((rows, 544), dtype=torch.uint8, device="cuda"),
+            torch.zeros((rows, 544), dtype=torch.uint8, device="cuda"), None)
+
+
+def _np(t, fmt):
+    a = t.cpu().numpy()
+    return a.view(np.uint16) if fmt == abi.KV_BF16 else a
+
+
+FORMATS = [abi.KV_BF16, abi.KV_Q8, abi.KV_Q8_0, abi.KV_Q8_0_NOROT]
+
+
+@pytest.mark.parametrize("fmt", FORMATS)
+@pytest.mark.parametrize("tokens,base,cap", [(64, 0, 4096), (300, 1000, 4096), (1500, 100, 1024)])
+def test_qk_rope_store_prefill(oracle, fmt, tokens, base, cap):
+    print(f"[case] store fmt={fmt} tokens={tokens} base={base} cap={cap}", flush=True)
+    d = synth.chain_inputs(tokens, outliers=True, seed=fmt * 7 + tokens)
+    capacity = 4096
+    first = 0 if cap == capacity else max(0, tokens - cap)
+    tb = table_bits(oracle, capacity)
+    positions = np.arange(base, base + tokens, dtype=np.int32)
+    wq, wk, _ = _qk_oracle(oracle, d, tb, positions)
+    ek, ev, es = _expected_cache(oracle, fmt, wk, d["v"], positions, cap, first)
+    kc, vc, sc = _alloc_cache(fmt, cap)
+    q, k = dev(d["q"]), dev(d["k"])
+    state = _prefill_state(base, tokens, capacity)
+    bad = flag()
+    kv = ops.kv_cache(fmt, kc, vc, cap, scales=sc, first=first)
+    ops.QKNormRopeStore(q, k, dev(d["qn"]), dev(d["kn"]), dev(tb),
+                        ops.positions_prefill(state, maximum=capacity), bad, v=dev(d["v"]), kv=kv)
+    torch.cuda.synchronize()
+    assert not bad.item()
+    assert np.array_equal(host16(q), wq) and np.array_equal(host16(k), wk)
+    assert np.array_equal(_np(kc, fmt), ek)
+    assert np.array_equal(_np(vc, fmt), ev)
+    if es is not None:
+        assert np.array_equal(sc.cpu().numpy(), es)
+
+
+@pytest.mark.parametrize("fmt", FORMATS)
+def test_qk_rope_store_decode_batch(oracle, fmt):
+    """Ragged positions, one token per sequence, per-sequence caches (seq_stride rows)."""
+    print(f"[case] decode batch fmt={fmt}", flush=True)
+    seqs, cap, capacity = 16, 256, 256
+    rng = np.random.default_rng(fmt)
+    positions = rng.integers(0, capacity, seqs).astype(np.int32)
+    d = synth.chain_inputs(seqs, outliers=True, seed=40 + fmt)
+    tb = table_bits(oracle, capacity)
+    states = np.zeros((seqs, 8), np.int32)
+    for s, p in enumerate(positions):
+        states[s] = [5, p, capacity, 10, p, min(p, 1024), 0, 0]
+    states[3, 7] = 1  # stopped: this sequence must write nothing and raise the flag
+    wq, wk, _ = _qk_oracle(oracle, d, tb, positions)
+    kc, vc, sc = _alloc_cache(fmt, seqs * cap)
+    q, k = dev(d["q"]), dev(d["k"])
+    bad = flag()
+    kv = ops.kv_cache(fmt, kc, vc, cap, scales=sc, seq_stride=cap)
+    ops.QKNormRopeStore(q, k, dev(d["qn"]), dev(d["kn"]), dev(tb),
+                        ops.positions_decode(torch.from_numpy(states).cuda(), maximum=capacity),
+                        bad, v=dev(d["v"]), kv=kv)
+    torch.cuda.synchronize()
+    assert bad.item() == 1
+    gq, gk = host16(q).copy(), host16(k).copy()
+    assert np.array_equal(gq[3], d["q"][3]) and np.array_equal(gk[3], d["k"][3])
+    keep = [s for s in range(seqs) if s != 3]
+    assert np.array_equal(gq[keep], wq[keep]) and np.array_equal(gk[keep], wk[keep])
+    kca, vca = _np(kc, fmt).reshape(seqs, cap, -1), _np(vc, fmt).reshape(seqs, cap, -1)
+    for s in range(seqs):
+        ek, ev, es = _expected_cache(oracle, fmt, wk[s:s + 1], d["v"][s:s + 1],
+                                     positions[s:s + 1], cap, 0)
+        if s == 3:
+            assert not kca[s].any() and not vca[s].any()
+            continue
+        assert np.array_equal(kca[s], ek) and np.array_equal(vca[s], ev)
+        if es is not None:
+            assert np.array_equal(sc.cpu().numpy().reshape(seqs, cap, 4, 2)[s], es)
+
+
+def test_invalid_prefill_state_writes_nothing(oracle):
+    d = synth.chain_inputs(8, seed=9)
+    tb = table_bits(oracle, 64)
+    for field in ({"committed": 1}, {"valid": 0}, {"tokens": 7}, {"base": 60}):
+        q, k = dev(d["q"]), dev(d["k"])
+        kc, vc, _ = _alloc_cache(abi.KV_BF16, 64)
+        state = _prefill_state(0, 8, 64, **field)
+        bad = flag()
+        ops.QKNormRopeStore(q, k, dev(d["qn"]), dev(d["kn"]), dev(tb),
+                            ops.positions_prefill(state, maximum=64), bad, v=dev(d["v"]),
+                            kv=ops.kv_cache(abi.KV_BF16, kc, vc, 64))
+        torch.cuda.synchronize()
+        assert bad.item() == 1, field
+        assert np.array_equal(host16(q), d["q"]) and not kc.any().item(), field
+
+
+# ---- fused chain -----------------------------------------------------------------------------
+
+@pytest.mark.parametrize("fmt", FORMATS)
+@pytest.mark.parametrize("tree", [128, 256])
+def test_fused_chain_matches_oracle(oracle, fmt, tree):
+    print(f"[case] chain fmt={fmt} tree={tree}", flush=True)
+    tokens, capacity = 333, 4096
+    d = synth.chain_inputs(tokens, outliers=True, seed=fmt + tree)
+    tb = table_bits(oracle, capacity)
+    positions = np.arange(tokens, dtype=np.int32) + 17
+    wx, wy, wst, _ = oracle.residual_rmsnorm(d["x"], d["residual"], d["gamma"], threads=tree)
+    wq, wk, _ = _qk_oracle(oracle, d, tb, positions)
+    ek, ev, es = _expected_cache(oracle, fmt, wk, d["v"], positions, capacity, 0)
+    x, r, g = dev(d["x"]), dev(d["residual"]), dev(d["gamma"])
+    y = torch.empty_like(x)
+    st = torch.empty((tokens, 2), dtype=torch.float32, device="cuda")
+    q, k = dev(d["q"]), dev(d["k"])
+    kc, vc, sc = _alloc_cache(fmt, capacity)
+    bad = flag()
+    ops.ResidualNormQKRopeStore(x, r, y, g, q, k, dev(d["v"]), dev(d["qn"]), dev(d["kn"]),
+                                dev(tb), ops.positions_base(17),
+                                ops.kv_cache(fmt, kc, vc, capacity, scales=sc), bad, tree=tree,
+                                statistics=st)
+    torch.cuda.synchronize()
+    assert not bad.item()
+    assert np.array_equal(host16(x), wx) and np.array_equal(host16(y), wy)
+    assert np.array_equal(st.cpu().numpy(), wst)
+    assert np.array_equal(host16(q), wq) and np.array_equal(host16(k), wk)
+    assert np.array_equal(_np(kc, fmt), ek) and np.array_equal(_np(vc, fmt), ev)
+    if es is not None:
+        assert np.array_equal(sc.cpu().numpy(), es)
+
+
+def test_config1_full_chunk(oracle):
+    """Config 1 at full size: 2048-token prefill chunk, BF16 KV, cap 131072, outliers."""
+    print("[case] config1 full", flush=True)
+    tokens, capacity = 2048, 131072
+    d = synth.chain_inputs(tokens, outliers=True, seed=0)
+    tb = table_bits(oracle, tokens)
+    positions = np.arange(tokens, dtype=np.int32)
+    wx, wy, _, _ = oracle.residual_rmsnorm(d["x"], d["residual"], d["gamma"], threads=128)
+    wq, wk, _ = _qk_oracle(oracle, d, tb, positions)
+    x, r, g = dev(d["x"]), dev(d["residual"]), dev(d["gamma"])
+    y = torch.empty_like(x)
+    q, k = dev(d["q"]), dev(d["k"])
+    kc = torch.zeros((capacity, 512), dtype=torch.int16, device="cuda")
+    vc = torch.zeros_like(kc)
+    state = _prefill_state(0, tokens, capacity)
+    bad = flag()
+    ops.ResidualNormQKRopeStore(x, r, y, g, q, k, dev(d["v"]), dev(d["qn"]), dev(d["kn"]),
+                                dev(tb), ops.positions_prefill(state),
+                                ops.kv_cache(abi.KV_BF16, kc, vc, capacity), bad)
+    torch.cuda.synchronize()
+    assert not bad.item()
+    assert np.array_equal(host16(x), wx) and np.array_equal(host16(y), wy)
+    assert np.array_equal(host16(q), wq) and np.array_equal(host16(k), wk)
+    assert np.array_equal(host16(kc[:tokens]), wk.reshape(tokens, -1))
+    assert np.array_equal(host16(vc[:tokens]), d["v"].reshape(tokens, -1))
+    assert not kc[tokens:].any().item()

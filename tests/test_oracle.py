@@ -1,0 +1,454 @@
+"""Pins the CPU oracle (oracle/padra_oracle.c) against things other than itself.
+
+Per oracle function, what checks it:
+  po_f32_to_bf16 / po_bf16_round  torch's RNE float->bfloat16 cast, specials
+  po_f32_to_f16                   numpy's float32->float16 cast (RNE, subnormals), all
+                                  2^16 half values round trip
+  po_accumulate / po_sumsq_tree   tests/refsim.py (thread-level simulation of the CUDA
+                                  kernels) on order-sensitive golden inputs and random
+                                  rows; exact rational sums (|error| <= 1 ulp)
+  po_rms_inv                      numpy float32 arithmetic (correctly rounded)
+  po_residual_rmsnorm/po_rmsnorm  refsim rows (bitwise), closed forms (zero row,
+                                  constant row), float64 formula within 1 BF16 ulp
+  po_rope_table                   identity row at p=0, float64 cos/sin of the same
+                                  float32 angle, YaRN ramp constants of the reference
+  po_qk_norm_rope                 pos 0 = plain norm, float64 rotation within 1 ulp,
+                                  refsim norm of a head (bitwise)
+  po_kv_store_bf16                ring addressing: last `cap` rows win, rows < first skipped
+  po_kv_q8_encode                 numpy float32 division + rint, |code|<=127, max 127
+  po_hadamard                     scipy.linalg.hadamard on integer inputs (exact)
+  po_kv_q8_0_encode               roundf half-away ties, fp16 scale via numpy, decode error
+                                  bound, rotation self-inverse
+  po_kv_q8_0_dequantize           bf16(code * fp16 d) via torch
+  po_silu_table                   all 65536 gates against a long-double evaluation
+  po_embed / state predicates     numpy indexing; reference truth tables
+"""
+import numpy as np
+import pytest
+import torch
+from fractions import Fraction
+
+from padra_amd import synth
+
+import refsim
+
+F32 = np.float32
+
+
+def f32bits(x):
+    return np.asarray(x, np.float32).view(np.uint32)
+
+
+# ---- A1 -------------------------------------------------------------------------------
+
+def test_bf16_round_matches_torch(oracle):
+    rng = np.random.default_rng(0)
+    x = np.concatenate([
+        rng.standard_normal(20000).astype(np.float32) * np.exp2(rng.integers(-130, 127, 20000)),
+        np.array([0.0, -0.0, np.inf, -np.inf, 3.3895314e38, 3.3961514e38, 3.39615e38,
+                  1e-40, -1e-41, 1.0 + 2**-8, 1.0 + 3 * 2**-8], np.float32)]).astype(np.float32)
+    ref = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    got = synth.bf16_bits(x)
+    assert np.array_equal(got, ref)
+    lib = oracle.lib()
+    for v in x[::97]:
+        assert F32(lib.po_bf16_round(float(v))).tobytes() == synth.bf16_to_f32(
+            synth.bf16_bits(np.array([v])))[0].tobytes()
+
+
+def test_f16_conversion_matches_numpy(oracle):
+    lib = oracle.lib()
+    rng = np.random.default_rng(1)
+    x = np.concatenate([
+        rng.standard_normal(5000).astype(np.float32) * np.exp2(rng.integers(-30, 18, 5000)),
+        np.array([65504, 65519.99, 65520, 2**-24, 2**-25, 3 * 2**-26, 2**-14, 0.0, -0.0],
+                 np.float32)]).astype(np.float32)
+    for v in x:
+        assert lib.po_f32_to_f16(float(v)) == int(np.float16(v).view(np.uint16)), v
+    halves = np.arange(65536, dtype=np.uint16).view(np.float16)
+    finite = np.isfinite(halves)
+    for h, v in zip(np.nonzero(finite)[0][::7], halves[finite][::7]):
+        assert F32(lib.po_f16_to_f32(int(h))) == F32(v)
+
+
+# ---- reduction order ----------------------------------------------------------------
+
+def test_sumsq_tree_golden_order_sensitive(oracle):
+    g = np.load(__import__("os").path.join(__import__("os").path.dirname(__file__), "golden",
+                                           "reduction_order.npz"))
+    lib = oracle.lib()
+    v = np.ascontiguousarray(g["v512"])
+    ptr = v.ctypes.data_as(__import__("ctypes").c_void_p)
+    t128, t256 = F32(lib.po_sumsq_tree(ptr, 512, 128)), F32(lib.po_sumsq_tree(ptr, 512, 256))
+    assert t128 == g["v512_tree128"] and t256 == g["v512_tree256"]
+    assert t128 != t256  # the fixture separates the two trees
+    # the 128-thread tree is the correctly rounded one here; the 256 tree drops 2^-18
+    exact = sum(Fraction(float(x)) ** 2 for x in v)
+    assert abs(Fraction(float(t128)) - exact) < abs(Fraction(float(t256)) - exact)
+    for h, want in zip(g["head128"], g["head128_tree128"]):
+        h = np.ascontiguousarray(h)
+        assert F32(lib.po_sumsq_tree(h.ctypes.data_as(__import__("ctypes").c_void_p), 128,
+                                     128)) == want
+
+
+@pytest.mark.parametrize("threads", [128, 256])
+def test_sumsq_tree_matches_refsim_random(oracle, threads):
+    import ctypes
+    lib = oracle.lib()
+    rng = np.random.default_rng(threads)
+    for n in (256, 512, 768):
+        v = synth.bf16_to_f32(synth.bf16_bits(rng.standard_normal(n) * np.exp2(
+            rng.integers(-8, 8, n))))
+        got = F32(lib.po_sumsq_tree(v.ctypes.data_as(ctypes.c_void_p), n, threads))
+        assert got == refsim.block_sumsq(v, threads)
+        exact = sum(Fraction(float(x)) ** 2 for x in v)
+        ulp = np.spacing(got)
+        assert abs(Fraction(float(got)) - exact) <= Fraction(float(ulp))
+
+
+def test_rms_inv_numpy(oracle):
+    import ctypes
+    lib = oracle.lib()
+    rng = np.random.default_rng(3)
+    _, st, _ = oracle.rmsnorm(np.zeros((1, 128), np.uint16), np.zeros(128, np.uint16))
+    assert st[0, 0] == 0 and st[0, 1] == F32(F32(1) / np.sqrt(F32(1e-6)))
+    # direct: variance and inv of a random row follow numpy float32 arithmetic
+    x = synth.bf16_bits(rng.standard_normal((4, 2048)))
+    _, st, _ = oracle.rmsnorm(x, synth.bf16_bits(np.ones(2048)))
+    for r in range(4):
+        xv = synth.bf16_to_f32(x[r])
+        s = F32(lib.po_sumsq_tree(np.ascontiguousarray(xv).ctypes.data_as(ctypes.c_void_p),
+                                  2048, 128))
+        var = F32(s / F32(2048))
+        assert st[r, 0] == var
+        assert st[r, 1] == F32(F32(1) / np.sqrt(F32(var + F32(1e-6))))
+
+
+# ---- A2 / A3 -------------------------------------------------------------------------
+
+@pytest.mark.parametrize("threads", [128, 256])
+def test_residual_norm_matches_refsim(oracle, threads):
+    rng = np.random.default_rng(10 + threads)
+    hidden = 512
+    x = synth.bf16_bits(rng.standard_normal((2, hidden)))
+    r = synth.bf16_bits(rng.standard_normal((2, hidden)) * 3)
+    g = synth.bf16_bits(rng.uniform(0.5, 1.5, hidden))
+    xn, y, st, bad = oracle.residual_rmsnorm(x, r, g, threads=threads)
+    assert not bad
+    for row in range(2):
+        v = [refsim.bf16(F32(a + b)) for a, b in zip(synth.bf16_to_f32(x[row]),
+                                                    synth.bf16_to_f32(r[row]))]
+        assert np.array_equal(synth.bf16_to_f32(xn[row]), np.array(v, np.float32))
+        want, var, inv = refsim.norm_row(v, synth.bf16_to_f32(g), threads)
+        assert np.array_equal(synth.bf16_to_f32(y[row]), np.array(want, np.float32))
+        assert st[row, 0] == var and st[row, 1] == inv
+
+
+def test_residual_norm_closed_forms(oracle):
+    hidden = 2048
+    zero = np.zeros((1, hidden), np.uint16)
+    g = synth.bf16_bits(np.linspace(0.5, 1.5, hidden))
+    xn, y, st, bad = oracle.residual_rmsnorm(zero, zero, g)
+    assert not bad and not y.any() and st[0, 0] == 0
+    c = F32(0.75)
+    row = synth.bf16_bits(np.full((1, hidden), c))
+    ones = synth.bf16_bits(np.ones(hidden))
+    y, st, _ = oracle.rmsnorm(row, ones)
+    inv = F32(F32(1) / np.sqrt(F32(F32(c * c) + F32(1e-6))))  # S/H = c^2 exactly
+    assert st[0, 1] == inv
+    assert np.all(synth.bf16_to_f32(y) == refsim.bf16(F32(c * inv)))
+
+
+@pytest.mark.parametrize("threads", [128, 256])
+def test_residual_norm_float64_within_1p5_ulp(oracle, threads):
+    d = synth.chain_inputs(64, outliers=True, seed=4)
+    xn, y, st, bad = oracle.residual_rmsnorm(d["x"], d["residual"], d["gamma"], threads=threads)
+    assert not bad
+    v = (synth.bf16_to_f32(d["x"]).astype(np.float64) + synth.bf16_to_f32(d["residual"]))
+    v = synth.bf16_to_f32(synth.bf16_bits(v.astype(np.float32))).astype(np.float64)
+    inv = 1 / np.sqrt((v * v).mean(axis=1, keepdims=True) + 1e-6)
+    ref = v * inv * synth.bf16_to_f32(d["gamma"])
+    got = synth.bf16_to_f32(y).astype(np.float64)
+    ulp = np.exp2(np.floor(np.log2(np.maximum(np.abs(ref), 1e-30))) - 7)
+    # two BF16 roundings (B(v*inv), then B(.*gamma)): within 1.5 ulp of the exact value
+    assert np.all(np.abs(got - ref) <= 1.5 * ulp)
+
+
+def test_residual_norm_nonfinite_sets_bad(oracle):
+    d = synth.chain_inputs(2, seed=5)
+    x = d["x"].copy()
+    x[1, 7] = 0x7F80  # +inf
+    _, _, _, bad = oracle.residual_rmsnorm(x, d["residual"], d["gamma"])
+    assert bad
+
+
+# ---- A5 --------------------------------------------------------------------------------
+
+def test_rope_table_plain(oracle):
+    t = oracle.rope_table(4096, 128, 1e6)
+    assert np.all(t[0, :64] == 1) and np.all(t[0, 64:] == 0)
+    i = np.arange(64)
+    freq = (F32(1) / np.power(F32(1e6), (2 * i).astype(np.float32) / F32(128))).astype(np.float32)
+    mismatch = 0
+    for p in (1, 7, 4097 % 4096, 4095):
+        ang = (F32(p) * freq).astype(np.float32).astype(np.float64)
+        c = synth.bf16_to_f32(synth.bf16_bits(np.cos(ang).astype(np.float32)))
+        s = synth.bf16_to_f32(synth.bf16_bits(np.sin(ang).astype(np.float32)))
+        mismatch += int((t[p, :64] != c).sum() + (t[p, 64:] != s).sum())
+        assert np.all(np.abs(t[p, :64] - c) <= 2 ** -8) and np.all(np.abs(t[p, 64:] - s) <= 2 ** -8)
+    assert mismatch <= 2
+    norm = t[:, :64].astype(np.float64) ** 2 + t[:, 64:].astype(np.float64) ** 2
+    assert np.all(np.abs(norm - 1) < 2 ** -6)
+
+
+def test_rope_table_yarn_ramp(oracle):
+    # reference constants: theta 5e5, factor 16, original context 8192 -> low 18, high 35
+    t = oracle.rope_table(2, 128, 5e5, yarn=True, factor=16.0, original_context=8192)
+    scale = F32(1 + 0.1 * np.log(16.0))
+    i = np.arange(64)
+    freq = np.power(F32(5e5), (2 * i).astype(np.float32) / F32(128)).astype(np.float32)
+    ramp = np.clip((i - 18.0) / (35.0 - 18.0), 0, 1)
+    f = (1 / (16 * freq.astype(np.float64))) * ramp + (1 / freq.astype(np.float64)) * (1 - ramp)
+    c = np.cos(f) * scale
+    assert np.all(np.abs(t[1, :64] - c) <= np.abs(c) * 2 ** -7 + 1e-6)
+    assert np.all(t[0, :64] == synth.bf16_to_f32(synth.bf16_bits(np.full(64, scale))))
+
+
+# ---- A4 / A6 ----------------------------------------------------------------------------
+
+def _table_bits(oracle, n, theta=1e6):
+    return synth.bf16_bits(oracle.rope_table(n, 128, theta))
+
+
+def test_qk_rope_position_zero_is_norm(oracle):
+    d = synth.chain_inputs(3, seed=6)
+    tb = _table_bits(oracle, 8)
+    q, k, bad = oracle.qk_norm_rope(d["q"], d["k"], d["qn"], d["kn"], tb, np.zeros(3, np.int32))
+    assert not bad
+    yq, _, _ = oracle.rmsnorm(d["q"].reshape(-1, 128), d["qn"])
+    yk, _, _ = oracle.rmsnorm(d["k"].reshape(-1, 128), d["kn"])
+    assert np.array_equal(q.reshape(-1, 128), yq) and np.array_equal(k.reshape(-1, 128), yk)
+
+
+def test_qk_rope_head_refsim_and_float64(oracle):
+    d = synth.chain_inputs(4, seed=7, outliers=True)
+    tb = _table_bits(oracle, 5000)
+    pos = np.array([0, 1, 4097, 4999], np.int32)
+    q, k, bad = oracle.qk_norm_rope(d["q"], d["k"], d["qn"], d["kn"], tb, pos)
+    assert not bad
+    tf = synth.bf16_to_f32(tb)
+    for t in range(4):
+        head = synth.bf16_to_f32(d["k"][t, 2])
+        o, _, _ = refsim.norm_row(head, synth.bf16_to_f32(d["kn"]), 128)
+        o = np.array(o, np.float32)
+        c, s = tf[pos[t], :64], tf[pos[t], 64:]
+        lo = [refsim.bf16(F32(refsim.bf16(F32(a * cc)) + refsim.bf16(F32(-b * ss))))
+              for a, b, cc, ss in zip(o[:64], o[64:], c, s)]
+        hi = [refsim.bf16(F32(refsim.bf16(F32(b * cc)) + refsim.bf16(F32(a * ss))))
+              for a, b, cc, ss in zip(o[:64], o[64:], c, s)]
+        assert np.array_equal(synth.bf16_to_f32(k[t, 2]), np.array(lo + hi, np.float32))
+        # float64 rotation of the normalized head agrees to BF16 rounding
+        ref = np.concatenate([o[:64] * c - o[64:] * s, o[64:] * c + o[:64] * s]).astype(np.float64)
+        got = synth.bf16_to_f32(k[t, 2])
+        # each product is rounded to BF16 before the add: bound by the term magnitudes
+        terms = np.concatenate([np.abs(o[:64] * c) + np.abs(o[64:] * s),
+                                np.abs(o[64:] * c) + np.abs(o[:64] * s)]).astype(np.float64)
+        assert np.all(np.abs(got - ref) <= 2 ** -8 * terms + 2 ** -8 * 1.01 * np.abs(ref) + 1e-30)
+
+
+def test_qk_head_golden_order(oracle):
+    import os
+    g = np.load(os.path.join(os.path.dirname(__file__), "golden", "reduction_order.npz"))
+    for h, want in zip(g["head128"], g["head128_tree128"]):
+        bits = synth.bf16_bits(h).reshape(1, 1, 128)
+        ones = synth.bf16_bits(np.ones(128))
+        tb = _table_bits(oracle, 1)
+        q, _, _ = oracle.qk_norm_rope(bits, bits.copy(), ones, ones, tb, np.zeros(1, np.int32))
+        var = F32(want / F32(128))
+        inv = F32(F32(1) / np.sqrt(F32(var + F32(1e-6))))
+        exp = np.array([refsim.bf16(F32(refsim.bf16(F32(x * inv)))) for x in h], np.float32)
+        assert np.array_equal(synth.bf16_to_f32(q[0, 0]), exp)
+
+
+def test_kv_store_ring(oracle):
+    d = synth.chain_inputs(10, seed=8)
+    cap = 4
+    kc = np.zeros((cap, 512), np.uint16)
+    vc = np.zeros((cap, 512), np.uint16)
+    pos = np.arange(100, 110, dtype=np.int32)
+    oracle.kv_store_bf16(d["k"], d["v"], kc, vc, pos, cap, first=10 - cap)
+    for t in range(6, 10):
+        assert np.array_equal(kc[pos[t] % cap], d["k"][t].reshape(-1))
+        assert np.array_equal(vc[pos[t] % cap], d["v"][t].reshape(-1))
+
+
+# ---- A7 ---------------------------------------------------------------------------------
+
+def test_kv_q8_codes(oracle):
+    d = synth.chain_inputs(6, seed=9, outliers=True)
+    cap = 8
+    ck = np.zeros((cap, 512), np.int8)
+    cv = np.zeros((cap, 512), np.int8)
+    sc = np.zeros((cap, 4, 2), np.float32)
+    pos = np.arange(6, dtype=np.int32) + 3
+    assert not oracle.kv_q8_encode(d["k"], d["v"], ck, cv, sc, pos, cap)
+    for t in range(6):
+        for h in range(4):
+            for src, codes, j in ((d["k"], ck, 0), (d["v"], cv, 1)):
+                x = synth.bf16_to_f32(src[t, h])
+                am = np.abs(x).max()
+                s = F32(am / F32(127)) if am else F32(1)
+                assert sc[pos[t] % cap, h, j] == s
+                want = np.clip(np.rint(x / s), -127, 127).astype(np.int8)
+                got = codes[pos[t] % cap, h * 128:(h + 1) * 128]
+                assert np.array_equal(got, want)
+                assert np.abs(got).max() == 127
+                assert np.all(np.abs(got * s - x) <= s / 2 * (1 + 2 ** -20))
+
+
+# ---- A8 ---------------------------------------------------------------------------------
+
+def test_hadamard_matches_sylvester(oracle):
+    from scipy.linalg import hadamard
+    rng = np.random.default_rng(11)
+    for n, scale in ((128, 1.0), (64, 1.0)):
+        x = rng.integers(-50, 50, n).astype(np.float32)
+        assert np.array_equal(oracle.hadamard(x, scale), (hadamard(n) @ x).astype(np.float32))
+    x = rng.standard_normal(128).astype(np.float32)
+    twice = oracle.hadamard(oracle.hadamard(x, .08838834764831845), .08838834764831845)
+    assert np.allclose(twice, x, atol=1e-5)
+
+
+def _row_fields(rows, features=512):
+    nd = features // 32
+    d = rows[:, :2 * nd].copy().view(np.float16)
+    qs = rows[:, 2 * nd:2 * nd + features].view(np.int8)
+    return d, qs
+
+
+@pytest.mark.parametrize("rotate", [True, False])
+def test_kv_q8_0_encode(oracle, rotate):
+    d = synth.chain_inputs(5, seed=12, outliers=True)
+    cap = 8
+    rb = 544
+    rk = np.zeros((cap, rb), np.uint8)
+    rv = np.zeros((cap, rb), np.uint8)
+    pos = np.arange(5, dtype=np.int32)
+    assert not oracle.kv_q8_0_encode(d["k"], d["v"], rk, rv, pos, cap, rotate=rotate)
+    dk, qk = _row_fields(rk)
+    for t in range(5):
+        for h in range(4):
+            x = synth.bf16_to_f32(d["k"][t, h])
+            if rotate:
+                x = oracle.hadamard(x, .08838834764831845)
+            for r in range(4):
+                blk = x[32 * r:32 * r + 32]
+                ad = F32(np.abs(blk).max() / F32(127))
+                assert dk[t, h * 4 + r] == np.float16(ad)
+                inv = F32(F32(1) / ad)
+                prod = (blk * inv).astype(np.float32)
+                want = np.clip(np.sign(prod) * np.floor(np.abs(prod) + 0.5), -127, 127)
+                got = qk[t, h * 128 + 32 * r:h * 128 + 32 * r + 32]
+                assert np.array_equal(got, want.astype(np.int8))
+                assert np.abs(got).max() == 127
+    # decode error bound on K: |code*d - x| <= d/2 (+ fp16 scale rounding)
+    out_k, out_v, bad = oracle.kv_q8_0_dequantize(rk, rv, 5, 512)
+    assert not bad
+    ref = torch.from_numpy(qk[:5].astype(np.float32) *
+                           np.repeat(dk[:5].astype(np.float32), 32, axis=1))
+    assert np.array_equal(out_k, ref.to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16))
+
+
+def test_q8_0_roundf_ties_away():
+    # roundf, not rint: 2.5 -> 3, -2.5 -> -3 (kv_q8_native.cuh:46-48)
+    from oracle import oracle as o
+    # block with amax 127 -> ad = 1, inverse = 1, so codes are roundf of the values
+    vals = np.zeros((1, 4, 128), np.float32)
+    vals[0, 0, 0] = 127
+    vals[0, 0, 1] = 2.5
+    vals[0, 0, 2] = -2.5
+    vals[0, 0, 3] = 0.5
+    bits = synth.bf16_bits(vals)
+    rk = np.zeros((1, 544), np.uint8)
+    rv = np.zeros((1, 544), np.uint8)
+    o.kv_q8_0_encode(bits, bits, rk, rv, np.zeros(1, np.int32), 1, rotate=False)
+    _, qk = _row_fields(rk)
+    assert list(qk[0, :4]) == [127, 3, -3, 1]
+
+
+def test_q8_0_layout_bytes(oracle):
+    assert oracle.lib().po_q8_0_row_bytes(512) == 544
+    from padra_amd import ops, abi
+    assert ops.kv_cache_layout(abi.KV_Q8_0, 131072)["v_offset"] == 131072 * 544
+    assert ops.kv_cache_layout(abi.KV_Q8_0, 131072)["bytes"] == 131072 * 1088
+    q8 = ops.kv_cache_layout(abi.KV_Q8, 8192)
+    assert (q8["v_offset"], q8["scales_offset"], q8["bytes"]) == (8192 * 512, 8192 * 1024,
+                                                                 8192 * 1056)
+    assert ops.kv_cache_layout(abi.KV_BF16, 1024)["bytes"] == 1024 * 2048
+
+
+# ---- A10 --------------------------------------------------------------------------------
+
+def test_silu_table_exhaustive_long_double(oracle):
+    table = oracle.silu_table()
+    g = synth.bf16_to_f32(np.arange(65536, dtype=np.uint16))
+    finite = np.isfinite(g)
+    gl = g[finite].astype(np.longdouble)
+    e = np.exp(-gl)  # 64-bit mantissa
+    with np.errstate(over="ignore"):
+        e32 = e.astype(np.float32)  # one rounding from extended precision
+    den = (F32(1) + e32).astype(np.float32)
+    with np.errstate(invalid="ignore", divide="ignore"):
+        s = (g[finite] / den).astype(np.float32)
+    want = synth.bf16_bits(s)
+    got = table[finite]
+    assert np.array_equal(got, want)
+
+
+def test_swiglu(oracle):
+    d = synth.swiglu_inputs(tokens=4, width=64, seed=13)
+    out, bad = oracle.swiglu(d["gate"], d["up"])
+    assert not bad
+    table = oracle.silu_table()
+    want = synth.bf16_bits(synth.bf16_to_f32(table[d["gate"]]) * synth.bf16_to_f32(d["up"]))
+    assert np.array_equal(out, want)
+    g = d["gate"].copy()
+    g[0, 0] = 0x7FC0
+    assert oracle.swiglu(g, d["up"])[1]
+
+
+# ---- A11 / A12 ----------------------------------------------------------------------------
+
+def test_embed(oracle):
+    rng = np.random.default_rng(14)
+    table = synth.bf16_bits(rng.standard_normal((100, 64)) * 0.02)
+    ids = np.array([0, 99, 5, 5], np.int32)
+    out, bad = oracle.embed(table, ids)
+    assert not bad and np.array_equal(out, table[ids])
+    _, bad = oracle.embed(table, np.array([100], np.int32))
+    assert bad
+
+
+def test_state_predicates(oracle):
+    import ctypes
+    from padra_amd.abi import DecodeState, PrefillState
+    lib = oracle.lib()
+    s = DecodeState(token=5, position=2000, capacity=4096, remaining=3, global_valid=2000,
+                    local_valid=1024, eos=0, stopped=0)
+    assert lib.po_decode_ready(ctypes.byref(s), 8192, 98304)
+    for field, value in (("local_valid", 2000), ("stopped", 1), ("remaining", 0),
+                         ("position", 4096), ("token", 98304)):
+        bad = DecodeState.from_buffer_copy(s)
+        setattr(bad, field, value)
+        if field == "position":
+            bad.global_valid = 4096
+        assert not lib.po_decode_ready(ctypes.byref(bad), 8192, 98304), field
+    assert not lib.po_decode_ready(ctypes.byref(s), 2048, 98304)  # capacity above maximum
+    p = PrefillState(base=0, prompt_offset=0, tokens=2048, capacity=131072, committed=0,
+                     binding_epoch=1, request_epoch=1, valid=1)
+    assert lib.po_valid_prefill_state(ctypes.byref(p), 2048, 131072, 1, 131072)
+    for field, value in (("committed", 1), ("valid", 0), ("tokens", 2047), ("request_epoch", 0),
+                         ("base", 131072 - 2047)):
+        bad = PrefillState.from_buffer_copy(p)
+        setattr(bad, field, value)
+        assert not lib.po_valid_prefill_state(ctypes.byref(bad), 2048, 131072, 1, 131072), field
