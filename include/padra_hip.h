@@ -152,6 +152,14 @@ int padra_ResidualNormQKRopeStore(void *stream, void *x, const void *residual,
                                   int kv_heads, int head_dim, float eps,
                                   const padra_KVCache *kv, int *bad);
 
+/* ---- launch tuning ------------------------------------------------------------------
+ * No counterpart in the reference (its launch shapes are fixed).  Process-wide launch
+ * parameters for measurement sweeps; defaults need no call.
+ * PADRA_TUNE_NORM_WAVES_PER_CU: residual-norm rows run on value * CU-count waves that
+ * pipeline their rows (0, the default: one wave per row). */
+enum { PADRA_TUNE_NORM_WAVES_PER_CU = 0 };
+int padra_Tune(int knob, int value);
+
 /* ---- version / capability ----------------------------------------------------------- */
 const char *padra_version(void);
 

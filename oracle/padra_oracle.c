@@ -139,7 +139,8 @@ static int finite_f(float x) { return isfinite(x) != 0; }
 
 /* Add (inference.cu:475-481) followed by Norm (inference.cu:188-214) for threads=128,
  * or ResidualPostNormWideExact (residual_norm_wide_exact.cuh:6-80) for threads=256:
- * v = B(x + r) is written back to x, y = B(B(v*inv) * gamma). */
+ * v = B(x + r) is written back to x, y = B(B(v*inv) * gamma).  bad: a non-finite v
+ * (Add, inference.cu:479) or row sum; with threads=256 also a non-finite output. */
 void po_residual_rmsnorm(uint16_t *x, const uint16_t *residual, uint16_t *y,
                          const uint16_t *gamma, int rows, int hidden, float eps, int threads,
                          float *stats, int *bad) {
@@ -166,7 +167,7 @@ void po_residual_rmsnorm(uint16_t *x, const uint16_t *residual, uint16_t *y,
     for (int i = 0; i < hidden; ++i) {
       const float o = po_bf16_round(po_bf16_round(v[i] * inv) * po_bf16_to_f32(gamma[i]));
       yr[i] = po_f32_to_bf16(o);
-      if (!finite_f(o))
+      if (!finite_f(o) && threads == 256) /* residual_norm_wide_exact.cuh:77 */
         set_bad(bad);
     }
   }

@@ -72,6 +72,7 @@ SIGNATURES = {
     "padra_ResidualNormQKRopeStore": [_P, _P, _P, _P, _P, _I, _I, _P, _P, _P, _P, _P, _P, _P, _I,
                                       ctypes.POINTER(Positions), _I, _I, _I, _I, _F,
                                       ctypes.POINTER(KVCache), _P],
+    "padra_Tune": [_I, _I],
     "padra_version": [],
 }
 RESTYPES = {"padra_version": ctypes.c_char_p}

@@ -50,38 +50,77 @@ __device__ __forceinline__ void acc_pos(float value, float &sum, float &error) {
 }
 // Fold partner partial (s2, e2) into (s, e) as one shuffle-down step does
 // (inference.cu:113-117): first the partner's sum, then its error.
+//
+// For sums of squares the second step never needs the reference's magnitude test
+// (inference.cu:105): every residual of a step is at most 2^-24 of the partial sum it
+// came from, partial sums only grow (non-negative terms, monotone rounding), and no
+// partial takes more than ~40 steps, so |e2| < 2^-18 * s2 <= s after the first step.
+// The test would always pick its first arm, (s - next) + e2, which is what is computed.
 __device__ __forceinline__ void fold(float s2, float e2, float &s, float &e) {
   acc_pos(s2, s, e);
-  acc(e2, s, e);
+  const float next = s + e2;
+  e = e + ((s - next) + e2);
+  s = next;
 }
 
 __device__ __forceinline__ float shfl_down(float v, int d) { return __shfl_down(v, d, 64); }
 __device__ __forceinline__ float shfl_xor(float v, int m) { return __shfl_xor(v, m, 64); }
+
+// Streaming (non-temporal) global accesses for data each launch touches once: the
+// activations, the KV rows.  On gfx950 these bypass the normal cache allocation policy;
+// a plain store stream loses up to half its bandwidth to cache write-allocation when
+// every load of a wave is issued before its stores.  Norm weights and the RoPE table
+// are re-read by many waves and use ordinary loads.
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint32_t ld_nt(const uint32_t *p) { return __builtin_nontemporal_load(p); }
+__device__ __forceinline__ uint2 ld_nt(const uint2 *p) {
+  const u32x2_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x2_t *>(p));
+  return make_uint2(v.x, v.y);
+}
+__device__ __forceinline__ uint4 ld_nt(const uint4 *p) {
+  const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t *>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ void st_nt(uint32_t *p, uint32_t v) { __builtin_nontemporal_store(v, p); }
+__device__ __forceinline__ void st_nt(uint2 *p, uint2 v) {
+  const u32x2_t t = {v.x, v.y};
+  __builtin_nontemporal_store(t, reinterpret_cast<u32x2_t *>(p));
+}
+__device__ __forceinline__ void st_nt(uint4 *p, uint4 v) {
+  const u32x4_t t = {v.x, v.y, v.z, v.w};
+  __builtin_nontemporal_store(t, reinterpret_cast<u32x4_t *>(p));
+}
+__device__ __forceinline__ float ld_nt(const float *p) { return __builtin_nontemporal_load(p); }
+__device__ __forceinline__ void st_nt(float *p, float v) { __builtin_nontemporal_store(v, p); }
 
 // 16-byte vector loads/stores of activations.  Eight consecutive elements map to one
 // uint4 of BF16 or two uint4 of fp32.
 template <class T> struct ActIO;
 template <> struct ActIO<uint16_t> {
   static __device__ __forceinline__ void load8(const uint16_t *p, float (&v)[8]) {
-    const uint4 w = *reinterpret_cast<const uint4 *>(p);
+    const uint4 w = ld_nt(reinterpret_cast<const uint4 *>(p));
     v[0] = lo16(w.x); v[1] = hi16(w.x); v[2] = lo16(w.y); v[3] = hi16(w.y);
     v[4] = lo16(w.z); v[5] = hi16(w.z); v[6] = lo16(w.w); v[7] = hi16(w.w);
   }
   static __device__ __forceinline__ void store8(uint16_t *p, const uint32_t (&w)[4]) {
-    *reinterpret_cast<uint4 *>(p) = make_uint4(w[0], w[1], w[2], w[3]);
+    st_nt(reinterpret_cast<uint4 *>(p), make_uint4(w[0], w[1], w[2], w[3]));
   }
 };
 template <> struct ActIO<float> {
   static __device__ __forceinline__ void load8(const float *p, float (&v)[8]) {
-    const float4 a = *reinterpret_cast<const float4 *>(p);
-    const float4 b = *reinterpret_cast<const float4 *>(p + 4);
-    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
-    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    const uint4 a = ld_nt(reinterpret_cast<const uint4 *>(p));
+    const uint4 b = ld_nt(reinterpret_cast<const uint4 *>(p + 4));
+    v[0] = __uint_as_float(a.x); v[1] = __uint_as_float(a.y);
+    v[2] = __uint_as_float(a.z); v[3] = __uint_as_float(a.w);
+    v[4] = __uint_as_float(b.x); v[5] = __uint_as_float(b.y);
+    v[6] = __uint_as_float(b.z); v[7] = __uint_as_float(b.w);
   }
   static __device__ __forceinline__ void store8(float *p, const uint32_t (&w)[4]) {
-    *reinterpret_cast<float4 *>(p) = make_float4(lo16(w[0]), hi16(w[0]), lo16(w[1]), hi16(w[1]));
-    *reinterpret_cast<float4 *>(p + 4) =
-        make_float4(lo16(w[2]), hi16(w[2]), lo16(w[3]), hi16(w[3]));
+    st_nt(reinterpret_cast<uint4 *>(p), make_uint4(w[0] << 16, w[0] & 0xffff0000u, w[1] << 16,
+                                                   w[1] & 0xffff0000u));
+    st_nt(reinterpret_cast<uint4 *>(p + 4), make_uint4(w[2] << 16, w[2] & 0xffff0000u,
+                                                       w[3] << 16, w[3] & 0xffff0000u));
   }
 };
 __device__ __forceinline__ void load8_bf16(const uint16_t *p, float (&v)[8]) {

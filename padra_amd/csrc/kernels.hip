@@ -1,9 +1,8 @@
 // gfx950 kernels and the extern "C" entry points of include/padra_hip.h for the
 // residual-norm, Q/K-norm + RoPE + KV-store and fused chain paths.
 //
-// Launch geometry: one 64-lane wavefront per workgroup.  A residual-norm wave covers
-// 64/(VT/8) rows (4 rows for the 128-thread tree, 2 for the 256-thread tree); a Q/K wave
-// covers 32 head vectors.  Every wave streams its inputs with 16-byte loads issued
+// Launch geometry: one 64-lane wavefront per workgroup.  A residual-norm wave covers one
+// row; a Q/K wave covers 32 head vectors (two lanes per head).  Every wave streams its inputs with 16-byte loads issued
 // before any arithmetic, and there is no inter-wave communication, so the grid is a
 // flat list of independent waves (thousands for a 2048-token chunk: >> 256 CUs).
 #include <stdio.h>
@@ -19,24 +18,48 @@ namespace {
 
 template <int VT, int J, class T, bool RES>
 __global__ __launch_bounds__(64) void k_norm(NormArgs<T> a) {
-  norm_rows_wave<VT, J, T, RES>(a, blockIdx.x);
+  norm_row_wave<VT, J, T, RES>(a, blockIdx.x);
 }
 
-template <class T, int FMT> __global__ __launch_bounds__(64) void k_qk(QKArgs<T> a) {
+// Fewer waves than rows, each pipelining its rows (row loads in flight during the
+// previous row's arithmetic).
+template <int VT, int J, class T, bool RES>
+__global__ __launch_bounds__(64) void k_norm_pipe(NormArgs<T> a) {
+  norm_rows_pipelined<VT, J, T, RES>(a, blockIdx.x, gridDim.x);
+}
+
+template <class T, int FMT> __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4, 8))) void k_qk(QKArgs<T> a) {
   qk_heads_wave<T, FMT>(a, blockIdx.x);
 }
 
 // Residual-norm waves and Q/K waves interleaved evenly over the grid, so every CU gets
 // the same mix of the (VALU-heavier) norm rows and the (store-heavier) head vectors.
 template <int VT, int J, int FMT>
-__global__ __launch_bounds__(64) void k_chain(NormArgs<uint16_t> n, QKArgs<uint16_t> q,
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4, 8))) void k_chain(NormArgs<uint16_t> n, QKArgs<uint16_t> q,
                                               long long norm_waves, long long waves) {
   const long long b = blockIdx.x;
   const long long n0 = b * norm_waves / waves, n1 = (b + 1) * norm_waves / waves;
   if (n1 > n0)
-    norm_rows_wave<VT, J, uint16_t, true>(n, (int)n0);
+    norm_row_wave<VT, J, uint16_t, true>(n, (int)n0);
   else
     qk_heads_wave<uint16_t, FMT>(q, b - n1);
+}
+
+// Launch tuning (padra_Tune): waves per CU for the pipelined row kernel, 0 = one wave
+// per row.
+int g_norm_waves_per_cu = 0;
+int g_cu_count = 0;
+
+int cu_count() {
+  if (!g_cu_count) {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess)
+      g_cu_count = n;
+    else
+      g_cu_count = 256;
+  }
+  return g_cu_count;
 }
 
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -89,7 +112,7 @@ int check_norm(const void *x, const void *normalized, const uint16_t *gamma, int
   return PADRA_OK;
 }
 
-int rows_per_wave(int tree) { return 64 / (tree / 8); }
+int rows_per_wave(int) { return 1; }
 
 PosSrc make_pos(const padra_Positions &p, int tokens) {
   PosSrc s;
@@ -191,8 +214,9 @@ template <class F> int with_format(const padra_KVCache *kv, F &&f) {
   return PADRA_INVALID_ARGUMENT;
 }
 
-long long qk_waves(int tokens, int q_heads, int kv_heads) {
-  return ((long long)tokens * (q_heads + kv_heads) + 31) / 32;
+// Q/K waves (32 head vectors each) plus, with a cache binding, the V-row waves.
+long long qk_waves(int tokens, int q_heads, int kv_heads, bool store) {
+  return ((long long)tokens * (q_heads + kv_heads * (store ? 2 : 1)) + 31) / 32;
 }
 
 } // namespace
@@ -219,11 +243,18 @@ extern "C" int padra_ResidualPostNorm(void *stream, void *x, const void *residua
     a.bad = bad;
     a.rows = rows;
     a.eps = eps;
+    const int pipe_waves = g_norm_waves_per_cu * cu_count();
     return norm_shape(tree, hidden / tree, [&](auto vt, auto j) -> int {
-      if (residual)
+      if (pipe_waves > 0 && pipe_waves < rows) {
+        if (residual)
+          hipLaunchKernelGGL((k_norm_pipe<vt.value, j.value, T, true>), dim3(pipe_waves), dim3(64), 0, s, a);
+        else
+          hipLaunchKernelGGL((k_norm_pipe<vt.value, j.value, T, false>), dim3(pipe_waves), dim3(64), 0, s, a);
+      } else if (residual) {
         hipLaunchKernelGGL((k_norm<vt.value, j.value, T, true>), dim3(grid), dim3(64), 0, s, a);
-      else
+      } else {
         hipLaunchKernelGGL((k_norm<vt.value, j.value, T, false>), dim3(grid), dim3(64), 0, s, a);
+      }
       return launched();
     });
   };
@@ -241,7 +272,7 @@ extern "C" int padra_QKNormRopeStore(void *stream, void *q, void *k, const void 
   if (st)
     return st;
   const hipStream_t s = static_cast<hipStream_t>(stream);
-  const long long grid = qk_waves(tokens, q_heads, kv_heads);
+  const long long grid = qk_waves(tokens, q_heads, kv_heads, kv != nullptr);
   auto launch = [&](auto tag) -> int {
     using T = decltype(tag);
     const QKArgs<T> a =
@@ -282,7 +313,7 @@ extern "C" int padra_ResidualNormQKRopeStore(
   const QKArgs<uint16_t> a = make_qk<uint16_t>(q, k, v, qn, kn, table, table_rows, pos, tokens,
                                                q_heads, kv_heads, eps, kv, bad);
   const long long norm_waves = (tokens + rows_per_wave(tree) - 1) / rows_per_wave(tree);
-  const long long waves = norm_waves + qk_waves(tokens, q_heads, kv_heads);
+  const long long waves = norm_waves + qk_waves(tokens, q_heads, kv_heads, kv != nullptr);
   const int j = hidden / tree;
   if (!((tree == 128 && (j == 16 || j == 18)) || (tree == 256 && (j == 8 || j == 9))))
     return PADRA_UNSUPPORTED;
@@ -301,6 +332,14 @@ extern "C" int padra_ResidualNormQKRopeStore(
                          norm_waves, waves);
     return launched();
   });
+}
+
+extern "C" int padra_Tune(int knob, int value) {
+  if (knob == PADRA_TUNE_NORM_WAVES_PER_CU && value >= 0 && value <= 64) {
+    g_norm_waves_per_cu = value;
+    return PADRA_OK;
+  }
+  return PADRA_INVALID_ARGUMENT;
 }
 
 extern "C" const char *padra_version(void) { return "padra-mi355x 0.1 gfx950 exact-fusions-v1"; }

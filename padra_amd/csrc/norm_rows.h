@@ -1,16 +1,21 @@
-// Residual-add + RMSNorm over hidden rows, one 64-lane wavefront per VT/8-lane row group.
+// Residual-add + RMSNorm over hidden rows: one 64-lane wavefront per row.
 //
 // Reference: Add + Norm (inference.cu:475-481, 188-214) for VT = 128 and
 // ResidualPostNormWideExact (residual_norm_wide_exact.cuh:6-80) for VT = 256.  The
 // reference block has VT threads; thread t owns elements t, t+VT, t+2VT, ... and sums
 // their squares in that order, then a 32-lane shuffle-down tree per warp and one more
-// tree over the warp partials.  Here each lane owns EIGHT consecutive "threads"
-// (8*lr .. 8*lr+7), so every 16-byte load lands exactly the elements those threads own
-// for one j, and the same tree is replayed: tree levels 16 and 8 cross lanes (shuffle
-// down by 2 and 1 lanes), levels 4, 2, 1 stay inside the lane, and the warp partials
-// sit in lanes 0, 4, 8, ... of the row group.  Levels of the final tree that only add
-// zero lanes are exact no-ops and are skipped.  The result is bit-identical to the
-// reference's fadd(sum, error).
+// tree over the warp partials.  Here lane l owns the K = VT/64 consecutive threads
+// K*l .. K*l+K-1, so one K-element load per j lands exactly the elements those threads
+// own, and the same tree is replayed: tree levels d >= K cross lanes (lane l folds lane
+// l + d/K, a DPP row shift), levels d < K stay inside the lane, and the warp partials
+// sit in lanes 0, 32/K, 64/K, ... .  Levels of the final tree that only add zero lanes
+// are exact no-ops and are skipped.  The result is bit-identical to the reference's
+// fadd(sum, error).
+//
+// Memory schedule: every load of the row (x, residual, gamma) is issued before the first
+// store, so the wave pays one HBM round trip, not one per 16-byte slice (an in-place
+// store to x may alias the residual for all the compiler knows, which would otherwise
+// pin each load behind the previous store).
 #pragma once
 #include "common.h"
 
@@ -33,98 +38,228 @@ __device__ __forceinline__ bool bf16_finite_after_round(float y) {
   return fabsf(y) < __uint_as_float(0x7f7f8000u);
 }
 
-template <int VT, int J, class T, bool RES>
-__device__ __forceinline__ void norm_rows_wave(const NormArgs<T> &a, int wave) {
-  constexpr int LPR = VT / 8, RPW = 64 / LPR, H = VT * J, WARPS = VT / 32;
-  const int lane = threadIdx.x & 63, lr = lane % LPR, rsub = lane / LPR;
-  const int row = wave * RPW + rsub;
-  const bool live = row < a.rows;
-  const size_t off = (size_t)(live ? row : 0) * H;
+// K consecutive activations: K BF16 (K*2 bytes) or K fp32.
+template <class T, int K> struct Lanes;
+template <int K> struct Lanes<uint16_t, K> {
+  uint32_t w[K / 2];
+  template <bool NT = true> __device__ __forceinline__ void load(const uint16_t *p) {
+    if constexpr (K == 2) {
+      w[0] = NT ? ld_nt(reinterpret_cast<const uint32_t *>(p)) : *reinterpret_cast<const uint32_t *>(p);
+    } else {
+      const uint2 v = NT ? ld_nt(reinterpret_cast<const uint2 *>(p)) : *reinterpret_cast<const uint2 *>(p);
+      w[0] = v.x;
+      w[1] = v.y;
+    }
+  }
+  __device__ __forceinline__ float get(int i) const { return i & 1 ? hi16(w[i / 2]) : lo16(w[i / 2]); }
+  static __device__ __forceinline__ void store(uint16_t *p, const uint32_t *w) {
+    if constexpr (K == 2)
+      st_nt(reinterpret_cast<uint32_t *>(p), w[0]);
+    else
+      st_nt(reinterpret_cast<uint2 *>(p), make_uint2(w[0], w[1]));
+  }
+};
+template <int K> struct Lanes<float, K> {
+  float f[K];
+  template <bool NT = true> __device__ __forceinline__ void load(const float *p) {
+    if constexpr (K == 2) {
+      const uint2 v = ld_nt(reinterpret_cast<const uint2 *>(p));
+      f[0] = __uint_as_float(v.x);
+      f[1] = __uint_as_float(v.y);
+    } else {
+      const uint4 v = ld_nt(reinterpret_cast<const uint4 *>(p));
+      f[0] = __uint_as_float(v.x);
+      f[1] = __uint_as_float(v.y);
+      f[2] = __uint_as_float(v.z);
+      f[3] = __uint_as_float(v.w);
+    }
+  }
+  __device__ __forceinline__ float get(int i) const { return f[i]; }
+  static __device__ __forceinline__ void store(float *p, const uint32_t *w) {
+    if constexpr (K == 2)
+      st_nt(reinterpret_cast<uint2 *>(p), make_uint2(w[0] << 16, w[0] & 0xffff0000u));
+    else
+      st_nt(reinterpret_cast<uint4 *>(p), make_uint4(w[0] << 16, w[0] & 0xffff0000u, w[1] << 16,
+                                                     w[1] & 0xffff0000u));
+  }
+};
 
-  uint32_t vp[J][4];
-  float s[8], e[8];
+// Value of lane (lane + L) for L < 16 inside the same 16-lane DPP row (row_shl:L), and
+// through the LDS crossbar (ds_bpermute) for longer strides.  Lanes whose source falls
+// outside the row read garbage; the trees below never consume those lanes.
+template <int L> __device__ __forceinline__ float lane_down(float v) {
+  if constexpr (L < 16)
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x100 + L, 0xf, 0xf, false));
+  else
+    return __shfl_down(v, L, 64);
+}
+
+// Folds lane + L's partial into this lane's for every slot (one tree level).
+template <int L, int K>
+__device__ __forceinline__ void fold_lanes(float (&s)[K], float (&e)[K]) {
+  float s2[K], e2[K];
 #pragma unroll
-  for (int k = 0; k < 8; ++k) {
+  for (int k = 0; k < K; ++k) {
+    s2[k] = lane_down<L>(s[k]);
+    e2[k] = lane_down<L>(e[k]);
+  }
+#pragma unroll
+  for (int k = 0; k < K; ++k)
+    fold(s2[k], e2[k], s[k], e[k]);
+}
+
+// One level of the 32-thread warp tree (inference.cu:111-119) for lanes owning K
+// consecutive threads: d >= K folds lane + d/K, d < K folds slot k + d into slot k.
+template <int D, int K>
+__device__ __forceinline__ void warp_level(float (&s)[K], float (&e)[K]) {
+  if constexpr (D >= K) {
+    fold_lanes<D / K, K>(s, e);
+  } else {
+#pragma unroll
+    for (int k = 0; k < D; ++k)
+      fold(s[k + D], e[k + D], s[k], e[k]);
+  }
+}
+template <int K> __device__ __forceinline__ void warp_tree(float (&s)[K], float (&e)[K]) {
+  warp_level<16, K>(s, e);
+  warp_level<8, K>(s, e);
+  warp_level<4, K>(s, e);
+  warp_level<2, K>(s, e);
+  warp_level<1, K>(s, e);
+}
+// Tree over WARPS warp partials held by lanes 0, LPW, 2*LPW, ... (inference.cu:120-135).
+template <int WARPS, int LPW>
+__device__ __forceinline__ void partials_tree(float &S, float &E) {
+  if constexpr (WARPS >= 2) {
+    constexpr int D = WARPS / 2;
+    const float s2 = lane_down<D * LPW>(S), e2 = lane_down<D * LPW>(E);
+    fold(s2, e2, S, E);
+    partials_tree<D, LPW>(S, E);
+  }
+}
+
+// One row's raw inputs in registers (x, residual), as loaded by norm_load.
+template <int VT, int J, class T> struct RowIn {
+  Lanes<T, VT / 64> x[J], r[J];
+};
+
+template <int VT, int J, class T, bool RES>
+__device__ __forceinline__ void norm_load(const NormArgs<T> &a, int row, RowIn<VT, J, T> &in) {
+  constexpr int K = VT / 64, H = VT * J;
+  const size_t off = (size_t)row * H + K * (threadIdx.x & 63);
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    in.x[j].load(a.x + off + VT * j);
+    if constexpr (RES)
+      in.r[j].load(a.residual + off + VT * j);
+  }
+}
+
+template <int VT, int J>
+__device__ __forceinline__ void norm_load_gamma(const uint16_t *gamma,
+                                                Lanes<uint16_t, VT / 64> (&gr)[J]) {
+  constexpr int K = VT / 64;
+#pragma unroll
+  for (int j = 0; j < J; ++j)
+    gr[j].template load<false>(gamma + K * (threadIdx.x & 63) + VT * j);
+}
+
+// Everything after the loads: v = B(x + r), the reference reduction tree, the outputs.
+template <int VT, int J, class T, bool RES>
+__device__ __forceinline__ void norm_compute(const NormArgs<T> &a, int row,
+                                             const RowIn<VT, J, T> &in,
+                                             const Lanes<uint16_t, VT / 64> (&gr)[J]) {
+  constexpr int K = VT / 64, H = VT * J, LPW = 32 / K, WARPS = VT / 32;
+  const int lane = threadIdx.x & 63;
+  const size_t off = (size_t)row * H + K * lane;
+  uint32_t vp[J][K / 2];
+  float s[K], e[K];
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
     s[k] = 0.f;
     e[k] = 0.f;
   }
 #pragma unroll
   for (int j = 0; j < J; ++j) {
-    const int col = VT * j + 8 * lr;
-    float xv[8];
-    ActIO<T>::load8(a.x + off + col, xv);
-    if constexpr (RES) {
-      float rv[8];
-      ActIO<T>::load8(a.residual + off + col, rv);
 #pragma unroll
-      for (int w = 0; w < 4; ++w)
-        vp[j][w] = pack2(xv[2 * w] + rv[2 * w], xv[2 * w + 1] + rv[2 * w + 1]);
-      if (live)
-        ActIO<T>::store8(a.x + off + col, vp[j]);
-    } else {
-#pragma unroll
-      for (int w = 0; w < 4; ++w)
-        vp[j][w] = pack2(xv[2 * w], xv[2 * w + 1]);
-    }
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
+    for (int w = 0; w < K / 2; ++w) {
+      const float a0 = RES ? in.x[j].get(2 * w) + in.r[j].get(2 * w) : in.x[j].get(2 * w);
+      const float a1 =
+          RES ? in.x[j].get(2 * w + 1) + in.r[j].get(2 * w + 1) : in.x[j].get(2 * w + 1);
+      vp[j][w] = pack2(a0, a1);
       const float v0 = lo16(vp[j][w]), v1 = hi16(vp[j][w]);
       acc_pos(v0 * v0, s[2 * w], e[2 * w]);
       acc_pos(v1 * v1, s[2 * w + 1], e[2 * w + 1]);
     }
   }
-  // Warp tree level 16: threads 8*lr+k with (lr%4) < 2 fold threads 16 further on,
-  // i.e. the same slot two lanes down; level 8: one lane down.
+  if constexpr (RES) {
 #pragma unroll
-  for (int k = 0; k < 8; ++k) {
-    const float s2 = shfl_down(s[k], 2), e2 = shfl_down(e[k], 2);
-    fold(s2, e2, s[k], e[k]);
+    for (int j = 0; j < J; ++j)
+      Lanes<T, K>::store(a.x + off + VT * j, vp[j]);
   }
-#pragma unroll
-  for (int k = 0; k < 8; ++k) {
-    const float s2 = shfl_down(s[k], 1), e2 = shfl_down(e[k], 1);
-    fold(s2, e2, s[k], e[k]);
-  }
-  // Levels 4, 2, 1 inside the lane.
-#pragma unroll
-  for (int k = 0; k < 4; ++k)
-    fold(s[k + 4], e[k + 4], s[k], e[k]);
-#pragma unroll
-  for (int k = 0; k < 2; ++k)
-    fold(s[k + 2], e[k + 2], s[k], e[k]);
-  fold(s[1], e[1], s[0], e[0]);
-  // Final tree over the WARPS partials held by lanes 0, 4, 8, ... of the row group.
-#pragma unroll
-  for (int d = WARPS / 2; d >= 1; d /= 2) {
-    const float s2 = shfl_down(s[0], 4 * d), e2 = shfl_down(e[0], 4 * d);
-    fold(s2, e2, s[0], e[0]);
-  }
-  const float total = __shfl(s[0] + e[0], rsub * LPR, 64);
+  warp_tree<K>(s, e);
+  float S = s[0], E = e[0];
+  partials_tree<WARPS, LPW>(S, E);
+  const float total = __shfl(S + E, 0, 64);
   const float variance = total / (float)H;
   const float inv = 1.f / sqrtf(variance + a.eps);
-  bool fine = isfinite(total);
-  if (a.stats && live && lr == 0) {
+  if (a.stats && lane == 0) {
     a.stats[2 * row] = variance;
     a.stats[2 * row + 1] = inv;
   }
+  // Error flag, as the reference kernels set it: with a residual, a non-finite v (Add,
+  // inference.cu:479) shows as a non-finite row sum, and the 256-thread decode kernel also
+  // checks the sum and every output (residual_norm_wide_exact.cuh:30, 61, 77); without a
+  // residual, NormFP8Exact / NormFP8WideExact check every output (norm_fp8_exact.cuh:42).
+  constexpr bool CHECK_Y = VT == 256 || !RES;
+  bool fine = !RES || isfinite(total);
 #pragma unroll
   for (int j = 0; j < J; ++j) {
-    const int col = VT * j + 8 * lr;
-    float g[8];
-    load8_bf16(a.gamma + col, g);
-    uint32_t out[4];
+    uint32_t out[K / 2];
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      const float y0 = B(lo16(vp[j][w]) * inv) * g[2 * w];
-      const float y1 = B(hi16(vp[j][w]) * inv) * g[2 * w + 1];
-      fine = fine && bf16_finite_after_round(y0) && bf16_finite_after_round(y1);
+    for (int w = 0; w < K / 2; ++w) {
+      const uint32_t p = pack2(lo16(vp[j][w]) * inv, hi16(vp[j][w]) * inv);
+      const float y0 = lo16(p) * gr[j].get(2 * w), y1 = hi16(p) * gr[j].get(2 * w + 1);
+      if constexpr (CHECK_Y)
+        fine = fine && bf16_finite_after_round(y0) && bf16_finite_after_round(y1);
       out[w] = pack2(y0, y1);
     }
-    if (live)
-      ActIO<T>::store8(a.y + off + col, out);
+    Lanes<T, K>::store(a.y + off + VT * j, out);
   }
-  if (__ballot(live && !fine) != 0 && lane == 0)
+  if (__ballot(!fine) != 0 && lane == 0)
     raise_bad(a.bad);
+}
+
+// One row per wave: all loads of the row, then compute and stores.
+template <int VT, int J, class T, bool RES>
+__device__ __forceinline__ void norm_row_wave(const NormArgs<T> &a, int row) {
+  if (row >= a.rows)
+    return; // wave-uniform
+  RowIn<VT, J, T> in;
+  Lanes<uint16_t, VT / 64> gr[J];
+  norm_load<VT, J, T, RES>(a, row, in);
+  norm_load_gamma<VT, J>(a.gamma, gr);
+  norm_compute<VT, J, T, RES>(a, row, in, gr);
+}
+
+// Rows first, first + stride, ... with the next row's loads in flight while the current
+// row computes (software pipelining across the wave's rows).
+template <int VT, int J, class T, bool RES>
+__device__ __forceinline__ void norm_rows_pipelined(const NormArgs<T> &a, int first, int stride) {
+  if (first >= a.rows)
+    return;
+  Lanes<uint16_t, VT / 64> gr[J];
+  RowIn<VT, J, T> cur;
+  norm_load<VT, J, T, RES>(a, first, cur);
+  norm_load_gamma<VT, J>(a.gamma, gr);
+  for (int row = first; row < a.rows; row += stride) {
+    RowIn<VT, J, T> nxt;
+    const int next = row + stride;
+    if (next < a.rows)
+      norm_load<VT, J, T, RES>(a, next, nxt);
+    norm_compute<VT, J, T, RES>(a, row, cur, gr);
+    cur = nxt;
+  }
 }
 
 } // namespace padra

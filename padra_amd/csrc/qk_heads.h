@@ -113,24 +113,256 @@ __device__ __forceinline__ uint32_t q8_0_code(float value, float inverse) {
   return (uint32_t)(c & 0xff);
 }
 __device__ __forceinline__ void store_codes32(int8_t *p, const uint32_t (&w)[8]) {
-  reinterpret_cast<uint4 *>(p)[0] = make_uint4(w[0], w[1], w[2], w[3]);
-  reinterpret_cast<uint4 *>(p)[1] = make_uint4(w[4], w[5], w[6], w[7]);
+  st_nt(reinterpret_cast<uint4 *>(p), make_uint4(w[0], w[1], w[2], w[3]));
+  st_nt(reinterpret_cast<uint4 *>(p) + 1, make_uint4(w[4], w[5], w[6], w[7]));
 }
 
+// Q8 / Q8_0 encoding of one head vector of the K cache (ISV false: the rotated K row)
+// or the V cache (ISV true), held by the two lanes of a pair: this lane has features
+// 32*half + i in xa and 64 + 32*half + i in xb.  Writes codes and scales to row `slot`.
+// The reference encodes K and V of a head in one warp (kv_q8.cuh:41-73,
+// kv_q8_native.cuh:70-100); here they are encoded by different waves, so when one of them
+// is invalid (non-finite input, the error flag is raised) the other is still written.
+template <int FMT, bool ISV, class A>
+__device__ __forceinline__ void encode_head_q(const A &a, float (&xa)[32], float (&xb)[32],
+                                              long long slot, int h, int half) {
+  constexpr int D = 128;
+  const int features = a.hkv * D;
+  bool invalid = false;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) {
+    invalid |= !isfinite(xa[i]) || !isfinite(xb[i]);
+    if constexpr (FMT == PADRA_KV_Q8) // q8 also rejects values that are not BF16-exact
+      invalid |= (__float_as_uint(xa[i]) & 0xffffu) != 0 || (__float_as_uint(xb[i]) & 0xffffu) != 0;
+  }
+  invalid = invalid || __shfl_xor((int)invalid, 1, 64);
+  if (invalid) {
+    if (half == 0)
+      raise_bad(a.bad);
+    return;
+  }
+  if constexpr (FMT == PADRA_KV_Q8) {
+    // kv_q8::Encode (kv_q8.cuh:56-73): scale = amax/127 (1 for an all-zero head), codes
+    // RNE(x / scale) clamped to +-127.
+    float m = 0.f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i)
+      m = fmaxf(m, fmaxf(fabsf(xa[i]), fabsf(xb[i])));
+    m = fmaxf(m, shfl_xor(m, 1));
+    const float scale = m == 0.f ? 1.f : m / 127.f;
+    int8_t *codes = static_cast<int8_t *>(ISV ? a.vc : a.kc) + slot * features + h * D;
+    uint32_t w0[8], w1[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      w0[i] = w1[i] = 0u;
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        w0[i] |= q8_code(xa[4 * i + b], scale) << (8 * b);
+        w1[i] |= q8_code(xb[4 * i + b], scale) << (8 * b);
+      }
+    }
+    store_codes32(codes + 32 * half, w0);
+    store_codes32(codes + 64 + 32 * half, w1);
+    if (half == 0)
+      reinterpret_cast<float *>(a.scales)[(slot * a.hkv + h) * 2 + (ISV ? 1 : 0)] = scale;
+  } else {
+    if constexpr (FMT == PADRA_KV_Q8_0) {
+      // q8_native::Rotate (kv_q8_native.cuh:22-45): stages on feature bits 0..4 in lane,
+      // bit 5 across the pair, and for K bit 6 between the lane's two groups.
+      hadamard32(xa);
+      hadamard32(xb);
+      hadamard_cross(xa, half);
+      hadamard_cross(xb, half);
+      if constexpr (!ISV) {
+#pragma unroll
+        for (int i = 0; i < 32; ++i) {
+          const float lower = xa[i], upper = xb[i];
+          xa[i] = (lower + upper) * .08838834764831845f;
+          xb[i] = (lower - upper) * .08838834764831845f;
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 32; ++i) {
+          xa[i] = xa[i] * .125f;
+          xb[i] = xb[i] * .125f;
+        }
+      }
+    }
+    // Blocks (kv_q8_native.cuh:84-99): this lane holds block `half` (xa) and block
+    // `half + 2` (xb); d = half(amax/127), codes roundf(x * (1/d_fp32)).
+    float am = 0.f, bm = 0.f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+      am = fmaxf(am, fabsf(xa[i]));
+      bm = fmaxf(bm, fabsf(xb[i]));
+    }
+    const float ad = am / 127.f, bd = bm / 127.f;
+    const __half ah = __float2half(ad), bh = __float2half(bd);
+    // A failing block stops the reference at that block: blocks before the first failing
+    // one are written, later ones are not.
+    const bool fa = !isfinite(am) || !isfinite(__half2float(ah));
+    const bool fb = !isfinite(bm) || !isfinite(__half2float(bh));
+    const int mine = fa ? half : (fb ? half + 2 : 4);
+    const int stop = min(mine, __shfl_xor(mine, 1, 64)); // first failing block, 4 = none
+    if (stop < 4 && half == 0)
+      raise_bad(a.bad);
+    const int row_bytes = ((2 * (features / 32) + features) + 15) / 16 * 16;
+    uint8_t *row = static_cast<uint8_t *>(ISV ? a.vc : a.kc) + slot * row_bytes;
+    int8_t *qs = reinterpret_cast<int8_t *>(row + 2 * (features / 32) + h * D);
+    uint16_t *d = reinterpret_cast<uint16_t *>(row) + h * 4;
+    const float ai = ad == 0.f ? 0.f : 1.f / ad, bi = bd == 0.f ? 0.f : 1.f / bd;
+    uint32_t w0[8], w1[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      w0[i] = w1[i] = 0u;
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        w0[i] |= q8_0_code(xa[4 * i + b], ai) << (8 * b);
+        w1[i] |= q8_0_code(xb[4 * i + b], bi) << (8 * b);
+      }
+    }
+    const uint16_t a16 = __half_as_ushort(ah), b16 = __half_as_ushort(bh);
+    if (stop == 4) {
+      // The head's four block scales go out as one 8-byte store from lane 0 of the pair:
+      // d[0] = block 0 (lane 0, a), d[1] = block 1 (lane 1, a), d[2], d[3] the b blocks.
+      const uint32_t mine_d = (uint32_t)a16 | ((uint32_t)b16 << 16);
+      const uint32_t other = __shfl_xor(mine_d, 1, 64);
+      if (half == 0)
+        *reinterpret_cast<uint2 *>(d) = make_uint2((mine_d & 0xffffu) | (other << 16),
+                                                   (mine_d >> 16) | (other & 0xffff0000u));
+      store_codes32(qs + 32 * half, w0);
+      store_codes32(qs + 64 + 32 * half, w1);
+    } else {
+      if (half < stop) {
+        d[half] = a16;
+        store_codes32(qs + 32 * half, w0);
+      }
+      if (half + 2 < stop) {
+        d[half + 2] = b16;
+        store_codes32(qs + 64 + 32 * half, w1);
+      }
+    }
+  }
+}
+
+// 32 consecutive activations of one lane, kept packed: 4 x 16 B of BF16 or 8 x 16 B of
+// fp32.  get(i) unpacks on use, so the packed words are all that stays live.
+template <class T> struct Act32;
+template <> struct Act32<uint16_t> {
+  uint4 w[4];
+  __device__ __forceinline__ void load(const uint16_t *p) {
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+      w[m] = ld_nt(reinterpret_cast<const uint4 *>(p) + m);
+  }
+  __device__ __forceinline__ uint32_t word(int i) const {
+    const uint4 &v = w[i / 4];
+    return (i & 3) == 0 ? v.x : (i & 3) == 1 ? v.y : (i & 3) == 2 ? v.z : v.w;
+  }
+  __device__ __forceinline__ float get(int i) const {
+    return i & 1 ? hi16(word(i / 2)) : lo16(word(i / 2));
+  }
+};
+template <> struct Act32<float> {
+  float4 f[8];
+  __device__ __forceinline__ void load(const float *p) {
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+      const uint4 v = ld_nt(reinterpret_cast<const uint4 *>(p) + m);
+      f[m] = make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z),
+                         __uint_as_float(v.w));
+    }
+  }
+  __device__ __forceinline__ float get(int i) const {
+    const float4 &v = f[i / 4];
+    return (i & 3) == 0 ? v.x : (i & 3) == 1 ? v.y : (i & 3) == 2 ? v.z : v.w;
+  }
+};
+
+// Eight consecutive BF16 values of a cached (re-read) vector: norm weights, table rows.
+struct Bf8 {
+  uint4 w;
+  __device__ __forceinline__ void load(const uint16_t *p) { w = *reinterpret_cast<const uint4 *>(p); }
+  __device__ __forceinline__ float get(int i) const {
+    const uint32_t v = (i / 2) == 0 ? w.x : (i / 2) == 1 ? w.y : (i / 2) == 2 ? w.z : w.w;
+    return i & 1 ? hi16(v) : lo16(v);
+  }
+};
+
+template <class X>
+__device__ __forceinline__ void group_sumsq(const X &x, float &S, float &E) {
+  float v[32];
+#pragma unroll
+  for (int i = 0; i < 32; ++i)
+    v[i] = x.get(i);
+  warp_sumsq32(v, S, E);
+}
+
+// One wave = 32 head vectors, two lanes each.  The flat index space is the T*Hq query
+// heads, then the T*Hkv key heads, then (with a cache binding) the T*Hkv value heads,
+// whose waves only move the V row into the cache.
 template <class T, int FMT>
 __device__ __forceinline__ void qk_heads_wave(const QKArgs<T> &a, long long wave) {
   constexpr int D = 128;
   const int lane = threadIdx.x & 63, half = lane & 1;
-  const long long hv = wave * 32 + (lane >> 1);
-  const long long nq = (long long)a.tokens * a.hq;
-  const long long total = nq + (long long)a.tokens * a.hkv;
+  const unsigned hv = (unsigned)wave * 32u + (unsigned)(lane >> 1);
+  const unsigned nq = (unsigned)a.tokens * (unsigned)a.hq;
+  const unsigned nk = (unsigned)a.tokens * (unsigned)a.hkv;
+  const unsigned total = nq + nk + (FMT >= 0 ? nk : 0u);
   if (hv >= total)
     return; // both lanes of a pair leave together
-  const bool isk = hv >= nq;
-  const long long kvi = hv - nq;
-  const int t = isk ? (int)(kvi / a.hkv) : (int)(hv / a.hq);
-  const int h = isk ? (int)(kvi % a.hkv) : (int)(hv % a.hq);
-  T *const base = isk ? a.k + kvi * D : a.q + hv * D;
+  const int role = hv < nq ? 0 : (hv < nq + nk ? 1 : 2); // 0 q, 1 k, 2 v
+  const unsigned idx = role == 0 ? hv : (role == 1 ? hv - nq : hv - nq - nk);
+  const unsigned heads = role == 0 ? (unsigned)a.hq : (unsigned)a.hkv;
+  const int t = (int)(idx / heads), h = (int)(idx % heads);
+
+  if constexpr (FMT >= 0) {
+    if (role == 2) {
+      // V row: the unchanged values go to the cache (StorePrefillControlled,
+      // prefill_control.cuh:36-37; QKNormRopeStoreControlled, qk_rope_store_exact.cuh:47).
+      bool ok;
+      const int pos = resolve_position(a.pos, t, a.cap, a.first, FMT > PADRA_KV_BF16, ok);
+      if (!ok || pos < 0 || pos >= a.table_rows) {
+        if (half == 0)
+          raise_bad(a.bad);
+        return;
+      }
+      if (t < a.first)
+        return;
+      const long long seq = a.pos.mode == PADRA_POS_DECODE ? t : 0;
+      const long long slot = seq * a.seq_stride + pos % a.cap;
+      const T *src = a.v + (size_t)idx * D;
+      Act32<T> va, vb;
+      va.load(src + 32 * half);
+      vb.load(src + 64 + 32 * half);
+      if constexpr (FMT == PADRA_KV_BF16) {
+        uint16_t *vc = static_cast<uint16_t *>(a.vc) + slot * (a.hkv * D) + h * D;
+        uint32_t pa[16], pb[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          pa[i] = pack2(va.get(2 * i), va.get(2 * i + 1));
+          pb[i] = pack2(vb.get(2 * i), vb.get(2 * i + 1));
+        }
+        store32_bf16(vc + 32 * half, pa);
+        store32_bf16(vc + 64 + 32 * half, pb);
+      } else {
+        float fa[32], fb[32];
+#pragma unroll
+        for (int i = 0; i < 32; ++i) {
+          fa[i] = va.get(i);
+          fb[i] = vb.get(i);
+        }
+        encode_head_q<FMT, true>(a, fa, fb, slot, h, half);
+      }
+      return;
+    }
+  }
+
+  const bool isk = role == 1;
+  T *const base = isk ? a.k + (size_t)idx * D : a.q + (size_t)idx * D;
+  Act32<T> xa, xb;
+  xa.load(base + 32 * half);
+  xb.load(base + 64 + 32 * half);
 
   bool ok;
   const int pos = resolve_position(a.pos, t, FMT >= 0 ? a.cap : 0, a.first,
@@ -140,13 +372,12 @@ __device__ __forceinline__ void qk_heads_wave(const QKArgs<T> &a, long long wave
       raise_bad(a.bad);
     return;
   }
+  const uint16_t *w = isk ? a.kn : a.qn;
+  const uint16_t *row = a.table + (size_t)pos * D;
 
-  float xa[32], xb[32];
-  load32<T>(base + 32 * half, xa);
-  load32<T>(base + 64 + 32 * half, xb);
   float S, E, S2, E2;
-  warp_sumsq32(xa, S, E);
-  warp_sumsq32(xb, S2, E2);
+  group_sumsq(xa, S, E);
+  group_sumsq(xb, S2, E2);
   fold(S2, E2, S, E); // w_half + w_{half+2}
   const float So = shfl_xor(S, 1), Eo = shfl_xor(E, 1);
   float bs = half ? So : S, be = half ? Eo : E;
@@ -154,31 +385,34 @@ __device__ __forceinline__ void qk_heads_wave(const QKArgs<T> &a, long long wave
   const float sum = bs + be;
   const float inv = 1.f / sqrtf(sum / (float)D + a.eps);
 
-  const uint16_t *w = isk ? a.kn : a.qn;
-  const uint16_t *row = a.table + (size_t)pos * D;
+  // Normalize and rotate pairs (i, i + 64), eight at a time: every BF16 rounding of the
+  // reference is one half of a packed conversion of the pair.
   uint32_t lo[16], hi[16];
-  bool fine = true;
+  bool fine = isfinite(sum);
 #pragma unroll
   for (int m = 0; m < 4; ++m) {
-    float wa[8], wb[8], c[8], sn[8];
-    load8_bf16(w + 32 * half + 8 * m, wa);
-    load8_bf16(w + 64 + 32 * half + 8 * m, wb);
-    load8_bf16(row + 32 * half + 8 * m, c);
-    load8_bf16(row + 64 + 32 * half + 8 * m, sn);
+    Bf8 wa, wb, c8, s8;
+    wa.load(w + 32 * half + 8 * m);
+    wb.load(w + 64 + 32 * half + 8 * m);
+    c8.load(row + 32 * half + 8 * m);
+    s8.load(row + 64 + 32 * half + 8 * m);
 #pragma unroll
-    for (int p = 0; p < 4; ++p) {
+    for (int q = 0; q < 8; q += 2) {
       float l2[2], h2[2];
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
-        const int i = 8 * m + 2 * p + u, ii = 2 * p + u;
-        const float A = B(B(xa[i] * inv) * wa[ii]);
-        const float Bv = B(B(xb[i] * inv) * wb[ii]);
-        l2[u] = B(A * c[ii]) + B((-Bv) * sn[ii]);
-        h2[u] = B(Bv * c[ii]) + B(A * sn[ii]);
+        const int i = 8 * m + q + u;
+        const uint32_t p1 = pack2(xa.get(i) * inv, xb.get(i) * inv);
+        const uint32_t p2 = pack2(lo16(p1) * wa.get(q + u), hi16(p1) * wb.get(q + u));
+        const float A = lo16(p2), Bv = hi16(p2), c = c8.get(q + u), sn = s8.get(q + u);
+        const uint32_t p3 = pack2(A * c, Bv * c);
+        const uint32_t p4 = pack2((-Bv) * sn, A * sn);
+        l2[u] = lo16(p3) + lo16(p4);
+        h2[u] = hi16(p3) + hi16(p4);
         fine = fine && bf16_finite_after_round(l2[u]) && bf16_finite_after_round(h2[u]);
       }
-      lo[4 * m + p] = pack2(l2[0], l2[1]);
-      hi[4 * m + p] = pack2(h2[0], h2[1]);
+      lo[(8 * m + q) / 2] = pack2(l2[0], l2[1]);
+      hi[(8 * m + q) / 2] = pack2(h2[0], h2[1]);
     }
   }
   store32<T>(base + 32 * half, lo);
@@ -189,29 +423,14 @@ __device__ __forceinline__ void qk_heads_wave(const QKArgs<T> &a, long long wave
   if constexpr (FMT >= 0) {
     if (!isk || t < a.first)
       return;
-    const int features = a.hkv * D;
     const long long seq = a.pos.mode == PADRA_POS_DECODE ? t : 0;
     const long long slot = seq * a.seq_stride + pos % a.cap;
-    const T *vsrc = a.v + kvi * D;
     if constexpr (FMT == PADRA_KV_BF16) {
-      uint16_t *kc = static_cast<uint16_t *>(a.kc) + slot * features + h * D;
-      uint16_t *vc = static_cast<uint16_t *>(a.vc) + slot * features + h * D;
+      uint16_t *kc = static_cast<uint16_t *>(a.kc) + slot * (a.hkv * D) + h * D;
       store32_bf16(kc + 32 * half, lo);
       store32_bf16(kc + 64 + 32 * half, hi);
-      float va[32], vb[32];
-      load32<T>(vsrc + 32 * half, va);
-      load32<T>(vsrc + 64 + 32 * half, vb);
-      uint32_t pa[16], pb[16];
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        pa[i] = pack2(va[2 * i], va[2 * i + 1]);
-        pb[i] = pack2(vb[2 * i], vb[2 * i + 1]);
-      }
-      store32_bf16(vc + 32 * half, pa);
-      store32_bf16(vc + 64 + 32 * half, pb);
     } else {
-      // Rotated K (BF16-exact) and V values of this lane's two feature groups.
-      float ka[32], kb[32], va[32], vb[32];
+      float ka[32], kb[32];
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         ka[2 * i] = lo16(lo[i]);
@@ -219,157 +438,7 @@ __device__ __forceinline__ void qk_heads_wave(const QKArgs<T> &a, long long wave
         kb[2 * i] = lo16(hi[i]);
         kb[2 * i + 1] = hi16(hi[i]);
       }
-      load32<T>(vsrc + 32 * half, va);
-      load32<T>(vsrc + 64 + 32 * half, vb);
-      // The encoders reject heads with non-finite values (kv_q8.cuh:49-54,
-      // kv_q8_native.cuh:79-83); q8 also rejects values that are not BF16-exact.
-      bool invalid = false;
-#pragma unroll
-      for (int i = 0; i < 32; ++i) {
-        invalid |= !isfinite(ka[i]) || !isfinite(kb[i]) || !isfinite(va[i]) || !isfinite(vb[i]);
-        if constexpr (FMT == PADRA_KV_Q8)
-          invalid |= (__float_as_uint(va[i]) & 0xffffu) != 0 ||
-                     (__float_as_uint(vb[i]) & 0xffffu) != 0;
-      }
-      invalid = invalid || __shfl_xor((int)invalid, 1, 64);
-      if (invalid) {
-        if (half == 0)
-          raise_bad(a.bad);
-        return;
-      }
-      if constexpr (FMT == PADRA_KV_Q8) {
-        float km = 0.f, vm = 0.f;
-#pragma unroll
-        for (int i = 0; i < 32; ++i) {
-          km = fmaxf(km, fmaxf(fabsf(ka[i]), fabsf(kb[i])));
-          vm = fmaxf(vm, fmaxf(fabsf(va[i]), fabsf(vb[i])));
-        }
-        km = fmaxf(km, shfl_xor(km, 1));
-        vm = fmaxf(vm, shfl_xor(vm, 1));
-        const float ks = km == 0.f ? 1.f : km / 127.f, vs = vm == 0.f ? 1.f : vm / 127.f;
-        int8_t *ck = static_cast<int8_t *>(a.kc) + slot * features + h * D;
-        int8_t *cv = static_cast<int8_t *>(a.vc) + slot * features + h * D;
-        uint32_t w0[8], w1[8], w2[8], w3[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          w0[i] = w1[i] = w2[i] = w3[i] = 0u;
-#pragma unroll
-          for (int b = 0; b < 4; ++b) {
-            w0[i] |= q8_code(ka[4 * i + b], ks) << (8 * b);
-            w1[i] |= q8_code(kb[4 * i + b], ks) << (8 * b);
-            w2[i] |= q8_code(va[4 * i + b], vs) << (8 * b);
-            w3[i] |= q8_code(vb[4 * i + b], vs) << (8 * b);
-          }
-        }
-        store_codes32(ck + 32 * half, w0);
-        store_codes32(ck + 64 + 32 * half, w1);
-        store_codes32(cv + 32 * half, w2);
-        store_codes32(cv + 64 + 32 * half, w3);
-        if (half == 0)
-          reinterpret_cast<padra_Q8KVScalePair *>(a.scales)[slot * a.hkv + h] = {ks, vs};
-      } else {
-        if constexpr (FMT == PADRA_KV_Q8_0) {
-          // K: 128-point transform, stages bit 0..4 in lane, bit 5 across the pair,
-          // bit 6 between the lane's two groups; V: two 64-point transforms (bits 0..5).
-          hadamard32(ka);
-          hadamard32(kb);
-          hadamard_cross(ka, half);
-          hadamard_cross(kb, half);
-#pragma unroll
-          for (int i = 0; i < 32; ++i) {
-            const float lower = ka[i], upper = kb[i];
-            ka[i] = (lower + upper) * .08838834764831845f;
-            kb[i] = (lower - upper) * .08838834764831845f;
-          }
-          hadamard32(va);
-          hadamard32(vb);
-          hadamard_cross(va, half);
-          hadamard_cross(vb, half);
-#pragma unroll
-          for (int i = 0; i < 32; ++i) {
-            va[i] = va[i] * .125f;
-            vb[i] = vb[i] * .125f;
-          }
-        }
-        // Blocks: this lane holds block `half` (ka, va) and block `half + 2` (kb, vb).
-        float kam = 0.f, kbm = 0.f, vam = 0.f, vbm = 0.f;
-#pragma unroll
-        for (int i = 0; i < 32; ++i) {
-          kam = fmaxf(kam, fabsf(ka[i]));
-          kbm = fmaxf(kbm, fabsf(kb[i]));
-          vam = fmaxf(vam, fabsf(va[i]));
-          vbm = fmaxf(vbm, fabsf(vb[i]));
-        }
-        const float kad = kam / 127.f, kbd = kbm / 127.f, vad = vam / 127.f, vbd = vbm / 127.f;
-        const __half kah = __float2half(kad), kbh = __float2half(kbd);
-        const __half vah = __float2half(vad), vbh = __float2half(vbd);
-        // A failing block stops the reference at that block (kv_q8_native.cuh:84-96):
-        // blocks before the first failing one are written, later ones are not.
-        const bool fa = !isfinite(kam) || !isfinite(vam) || !isfinite(__half2float(kah)) ||
-                        !isfinite(__half2float(vah));
-        const bool fb = !isfinite(kbm) || !isfinite(vbm) || !isfinite(__half2float(kbh)) ||
-                        !isfinite(__half2float(vbh));
-        const int mine = fa ? half : (fb ? half + 2 : 4);
-        const int stop = min(mine, __shfl_xor(mine, 1, 64)); // first failing block, 4 = none
-        if (stop < 4 && half == 0)
-          raise_bad(a.bad);
-        const int row_bytes = ((2 * (features / 32) + features) + 15) / 16 * 16;
-        uint8_t *rk = static_cast<uint8_t *>(a.kc) + slot * row_bytes;
-        uint8_t *rv = static_cast<uint8_t *>(a.vc) + slot * row_bytes;
-        int8_t *qk = reinterpret_cast<int8_t *>(rk + 2 * (features / 32) + h * D);
-        int8_t *qv = reinterpret_cast<int8_t *>(rv + 2 * (features / 32) + h * D);
-        uint16_t *dk = reinterpret_cast<uint16_t *>(rk) + h * 4;
-        uint16_t *dv = reinterpret_cast<uint16_t *>(rv) + h * 4;
-        const float kai = kad == 0.f ? 0.f : 1.f / kad, kbi = kbd == 0.f ? 0.f : 1.f / kbd;
-        const float vai = vad == 0.f ? 0.f : 1.f / vad, vbi = vbd == 0.f ? 0.f : 1.f / vbd;
-        uint32_t w0[8], w1[8], w2[8], w3[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          w0[i] = w1[i] = w2[i] = w3[i] = 0u;
-#pragma unroll
-          for (int b = 0; b < 4; ++b) {
-            w0[i] |= q8_0_code(ka[4 * i + b], kai) << (8 * b);
-            w1[i] |= q8_0_code(kb[4 * i + b], kbi) << (8 * b);
-            w2[i] |= q8_0_code(va[4 * i + b], vai) << (8 * b);
-            w3[i] |= q8_0_code(vb[4 * i + b], vbi) << (8 * b);
-          }
-        }
-        const uint16_t ka16 = __half_as_ushort(kah), kb16 = __half_as_ushort(kbh);
-        const uint16_t va16 = __half_as_ushort(vah), vb16 = __half_as_ushort(vbh);
-        if (stop == 4) {
-          // Gather the four block scales of the head into lane 0 of the pair: one 8-byte
-          // store per tensor.
-          const uint32_t kmine = (uint32_t)ka16 | ((uint32_t)kb16 << 16);
-          const uint32_t vmine = (uint32_t)va16 | ((uint32_t)vb16 << 16);
-          const uint32_t kother = __shfl_xor(kmine, 1, 64), vother = __shfl_xor(vmine, 1, 64);
-          if (half == 0) {
-            // d[0] = block 0 (lane 0, a), d[1] = block 1 (lane 1, a), d[2], d[3] the b's.
-            const uint2 kd = make_uint2((kmine & 0xffffu) | (kother << 16),
-                                        (kmine >> 16) | (kother & 0xffff0000u));
-            const uint2 vd = make_uint2((vmine & 0xffffu) | (vother << 16),
-                                        (vmine >> 16) | (vother & 0xffff0000u));
-            *reinterpret_cast<uint2 *>(dk) = kd;
-            *reinterpret_cast<uint2 *>(dv) = vd;
-          }
-          store_codes32(qk + 32 * half, w0);
-          store_codes32(qk + 64 + 32 * half, w1);
-          store_codes32(qv + 32 * half, w2);
-          store_codes32(qv + 64 + 32 * half, w3);
-        } else {
-          if (half < stop) {
-            dk[half] = ka16;
-            dv[half] = va16;
-            store_codes32(qk + 32 * half, w0);
-            store_codes32(qv + 32 * half, w2);
-          }
-          if (half + 2 < stop) {
-            dk[half + 2] = kb16;
-            dv[half + 2] = vb16;
-            store_codes32(qk + 64 + 32 * half, w1);
-            store_codes32(qv + 64 + 32 * half, w3);
-          }
-        }
-      }
+      encode_head_q<FMT, false>(a, ka, kb, slot, h, half);
     }
   }
 }

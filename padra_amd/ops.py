@@ -67,21 +67,28 @@ def positions_base(base: int = 0) -> abi.Positions:
 
 
 def positions_prefill(state: torch.Tensor, maximum=131072, binding_epoch=1) -> abi.Positions:
-    """state: device int32[8] holding a PrefillState."""
-    return abi.Positions(mode=abi.POS_PREFILL, base=0, prefill=state.data_ptr(), decode=None,
-                         maximum=int(maximum), vocab=98304, binding_epoch=int(binding_epoch))
+    """state: device int32[8] holding a PrefillState (kept alive by the returned object)."""
+    p = abi.Positions(mode=abi.POS_PREFILL, base=0, prefill=state.data_ptr(), decode=None,
+                      maximum=int(maximum), vocab=98304, binding_epoch=int(binding_epoch))
+    p._keep = state
+    return p
 
 
 def positions_decode(states: torch.Tensor, maximum=131072, vocab=98304) -> abi.Positions:
-    """states: device int32[n][8] holding one DecodeState per sequence."""
-    return abi.Positions(mode=abi.POS_DECODE, base=0, prefill=None, decode=states.data_ptr(),
-                         maximum=int(maximum), vocab=int(vocab), binding_epoch=1)
+    """states: device int32[n][8], one DecodeState per sequence (kept alive by the result)."""
+    p = abi.Positions(mode=abi.POS_DECODE, base=0, prefill=None, decode=states.data_ptr(),
+                      maximum=int(maximum), vocab=int(vocab), binding_epoch=1)
+    p._keep = states
+    return p
 
 
 def kv_cache(fmt, k, v, cap, scales=None, first=0, seq_stride=0) -> abi.KVCache:
-    return abi.KVCache(format=int(fmt), k=k.data_ptr(), v=v.data_ptr(),
-                       scales=None if scales is None else scales.data_ptr(), cap=int(cap),
-                       first=int(first), seq_stride=int(seq_stride))
+    """A cache binding; the returned object keeps k, v and scales alive."""
+    c = abi.KVCache(format=int(fmt), k=k.data_ptr(), v=v.data_ptr(),
+                    scales=None if scales is None else scales.data_ptr(), cap=int(cap),
+                    first=int(first), seq_stride=int(seq_stride))
+    c._keep = (k, v, scales)
+    return c
 
 
 def q8_0_row_bytes(features: int) -> int:

@@ -145,21 +145,21 @@ def test_qk_rope_no_store(oracle, tokens, base):
 def test_qk_rope_golden_order_heads(oracle):
     g = np.load(os.path.join(HERE, "golden", "reduction_order.npz"))
     heads = synth.bf16_bits(g["head128"])  # [2][128]
-    q = np.stack([heads] * 8, axis=1).reshape(2, 16, 128)[:, :16]
-    k = np.stack([heads] * 2, axis=1).reshape(2, 4, 128)
+    q = np.ascontiguousarray(np.repeat(heads[:, None, :], 16, axis=1))
+    k = np.ascontiguousarray(np.repeat(heads[:, None, :], 4, axis=1))
     ones = synth.bf16_bits(np.ones(128))
     tb = table_bits(oracle, 4)
-    wq, wk, _ = oracle.qk_norm_rope(q, k, ones, ones, tb, np.array([1, 3], np.int32))
+    wq, wk, _ = oracle.qk_norm_rope(q, k, ones, ones, tb, np.array([1, 2], np.int32))
     tq, tk = dev(q), dev(k)
     ops.QKNormRopeStore(tq, tk, dev(ones), dev(ones), dev(tb), ops.positions_base(1), flag())
     torch.cuda.synchronize()
     assert np.array_equal(host16(tq), wq) and np.array_equal(host16(tk), wk)
 
 
-def _prefill_state(base, tokens, capacity, **kw):
+def _prefill_state(base, tokens, capacity, overrides=None):
     s = dict(base=base, prompt_offset=base, tokens=tokens, capacity=capacity, committed=base,
              binding_epoch=1, request_epoch=1, valid=1)
-    s.update(kw)
+    s.update(overrides or {})
     return torch.tensor([s[k] for k in ("base", "prompt_offset", "tokens", "capacity",
                                         "committed", "binding_epoch", "request_epoch", "valid")],
                         dtype=torch.int32, device="cuda")
@@ -277,7 +277,7 @@ def test_invalid_prefill_state_writes_nothing(oracle):
     for field in ({"committed": 1}, {"valid": 0}, {"tokens": 7}, {"base": 60}):
         q, k = dev(d["q"]), dev(d["k"])
         kc, vc, _ = _alloc_cache(abi.KV_BF16, 64)
-        state = _prefill_state(0, 8, 64, **field)
+        state = _prefill_state(0, 8, 64, overrides=field)
         bad = flag()
         ops.QKNormRopeStore(q, k, dev(d["qn"]), dev(d["kn"]), dev(tb),
                             ops.positions_prefill(state, maximum=64), bad, v=dev(d["v"]),
