@@ -14,6 +14,13 @@
 
 using namespace padra;
 
+// Occupancy hint for the Q/K and chain kernels.  Forcing 4 waves per SIMD (<= 128 VGPRs)
+// makes the compiler spill the Q/K working set to scratch; measured on MI355X, the
+// unconstrained allocation (2-3 waves per SIMD) is 20% faster for a 2048-token chunk.
+#ifndef PADRA_WAVES_PER_EU
+#define PADRA_WAVES_PER_EU
+#endif
+
 namespace {
 
 template <int VT, int J, class T, bool RES>
@@ -28,14 +35,14 @@ __global__ __launch_bounds__(64) void k_norm_pipe(NormArgs<T> a) {
   norm_rows_pipelined<VT, J, T, RES>(a, blockIdx.x, gridDim.x);
 }
 
-template <class T, int FMT> __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4, 8))) void k_qk(QKArgs<T> a) {
+template <class T, int FMT> __global__ __launch_bounds__(64) PADRA_WAVES_PER_EU void k_qk(QKArgs<T> a) {
   qk_heads_wave<T, FMT>(a, blockIdx.x);
 }
 
 // Residual-norm waves and Q/K waves interleaved evenly over the grid, so every CU gets
 // the same mix of the (VALU-heavier) norm rows and the (store-heavier) head vectors.
 template <int VT, int J, int FMT>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4, 8))) void k_chain(NormArgs<uint16_t> n, QKArgs<uint16_t> q,
+__global__ __launch_bounds__(64) PADRA_WAVES_PER_EU void k_chain(NormArgs<uint16_t> n, QKArgs<uint16_t> q,
                                               long long norm_waves, long long waves) {
   const long long b = blockIdx.x;
   const long long n0 = b * norm_waves / waves, n1 = (b + 1) * norm_waves / waves;
