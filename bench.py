@@ -128,8 +128,12 @@ def time_eager(torch, sets, steps):
     return start.elapsed_time(end) / steps
 
 
-def copy_ceiling(torch, nbytes, reps=50):
-    """Device-to-device copy of `nbytes` (read + write), rotating over 8 buffer pairs."""
+COPY_BYTES = 2 * 32 * 1024 * 1024  # bytes moved (read + write) per copy-ceiling launch
+
+
+def copy_ceiling(torch, nbytes=COPY_BYTES, reps=50):
+    """Device-to-device copy (torch copy_) moving `nbytes` in total (read + write), rotating
+    over 8 buffer pairs; also the calibration kernel of the traffic counters."""
     n = nbytes // 2 // 2
     bufs = [(torch.empty(n, dtype=torch.int16, device="cuda").fill_(1),
              torch.empty(n, dtype=torch.int16, device="cuda")) for _ in range(8)]
@@ -178,6 +182,9 @@ def cpu_baseline(host, seconds):
 
 
 def main():
+    if len(sys.argv) > 2 and sys.argv[1] == "--summarize":
+        summarize(sys.argv[2], " ".join(sys.argv[3:]) or "(see profiles/README)")
+        return
     args = parse()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -205,7 +212,7 @@ def main():
         del sets
         torch.cuda.empty_cache()
     head = results[formats[0]]
-    ceiling = copy_ceiling(torch, head["bytes"])
+    ceiling = copy_ceiling(torch)
     achieved = head["gbs"]
     line = {
         "metric": "achieved HBM GB/s (% of peak) fused norm+RoPE+KV-store; tokens/s per layer",
@@ -239,6 +246,73 @@ def main():
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(host, args.cpu_seconds)
     print(json.dumps(line), flush=True)
+
+
+def summarize(outdir: str, command: str) -> None:
+    """Digests rocprofv3 CSV output of this script into profiles/ (text only):
+    <outdir>/trace/bench_kernel_stats.csv (--kernel-trace --stats) and
+    <outdir>/fetch|write/bench_counter_collection.csv (--pmc FETCH_SIZE / WRITE_SIZE).
+    HBM traffic per launch = counter KiB x calibration, the calibration being the known
+    bytes moved by the plain copy kernel of the same run over its counter reading."""
+    import csv
+    import statistics
+    prof = os.path.join(ROOT, "profiles")
+    os.makedirs(prof, exist_ok=True)
+    lines = ["# rocprofv3 summary: fused chain, config 1 (2048-token prefill chunk)", "",
+             "Command (from the repository root):", "", "```", command, "```", ""]
+    stats = os.path.join(outdir, "trace", "bench_kernel_stats.csv")
+    chain_ns = None
+    if os.path.exists(stats):
+        lines += ["## Kernel trace (--kernel-trace --stats)", "",
+                  "| kernel | calls | average us | min us | max us |", "|---|---:|---:|---:|---:|"]
+        for r in csv.DictReader(open(stats)):
+            name = r["Name"]
+            short = name.replace("void ", "").replace("(anonymous namespace)::", "").split("(")[0]
+            lines.append(f"| `{short[:70]}` | {r['Calls']} | {float(r['AverageNs'])/1e3:.2f} | "
+                         f"{float(r['MinNs'])/1e3:.2f} | {float(r['MaxNs'])/1e3:.2f} |")
+            if "k_chain" in name and chain_ns is None:
+                chain_ns = float(r["AverageNs"])
+        lines.append("")
+    traffic = {}
+    for counter, sub in (("FETCH_SIZE", "fetch"), ("WRITE_SIZE", "write")):
+        path = os.path.join(outdir, sub, "bench_counter_collection.csv")
+        if not os.path.exists(path):
+            continue
+        chain, copy = [], []
+        for r in csv.DictReader(open(path)):
+            if r["Counter_Name"] != counter:
+                continue
+            if "k_chain" in r["Kernel_Name"]:
+                chain.append(float(r["Counter_Value"]))
+            elif "copyBuffer" in r["Kernel_Name"] or "copy" in r["Kernel_Name"].lower():
+                copy.append(float(r["Counter_Value"]))
+        if chain and copy:
+            copy_bytes = COPY_BYTES // 2  # read (FETCH) or written (WRITE) per copy
+            factor = copy_bytes / (statistics.median(copy) * 1024)
+            traffic[counter] = {"chain_kib": statistics.median(chain), "copy_kib": statistics.median(copy),
+                                "calibration": factor,
+                                "chain_bytes": statistics.median(chain) * 1024 * factor}
+    if traffic:
+        lines += ["## HBM traffic per launch (--pmc, calibrated by the copy kernel)", "",
+                  "| counter | chain KiB | copy KiB (known %d B) | calibration | chain bytes |" % (COPY_BYTES // 2),
+                  "|---|---:|---:|---:|---:|"]
+        for c, t in traffic.items():
+            lines.append(f"| {c} | {t['chain_kib']:.0f} | {t['copy_kib']:.0f} | {t['calibration']:.3f} | "
+                         f"{t['chain_bytes']:.0f} |")
+        total = sum(t["chain_bytes"] for t in traffic.values())
+        alg = chain_bytes("bf16") * TOKENS
+        lines += ["", f"Total {total:.0f} B per launch against {alg} algorithmic bytes "
+                      f"({total / alg:.3f}x).", ""]
+        with open(os.path.join(prof, "chain_config1_traffic.json"), "w") as f:
+            json.dump({"bf16": {"bytes_per_launch": round(total), "counters": traffic,
+                                "algorithmic_bytes": alg}}, f, indent=1)
+    if chain_ns:
+        alg = chain_bytes("bf16") * TOKENS
+        lines += [f"Kernel-trace average {chain_ns/1e3:.2f} us per launch = "
+                  f"{alg / chain_ns:.1f} GB/s algorithmic.", ""]
+    with open(os.path.join(prof, "chain_config1_bf16.md"), "w") as f:
+        f.write("\n".join(lines))
+    print("\n".join(lines))
 
 
 def traffic_from_profiles(fmt):

@@ -152,6 +152,53 @@ int padra_ResidualNormQKRopeStore(void *stream, void *x, const void *residual,
                                   int kv_heads, int head_dim, float eps,
                                   const padra_KVCache *kv, int *bad);
 
+/* ---- KV store, commit, decode ---------------------------------------------------------
+ * padra_KVStore: the cache writers without the Q/K norm -- StorePrefillControlled /
+ * Store / StoreControlled (prefill_control.cuh:24-38, inference.cu:248-256,
+ * decode_control.cuh:213-224), kv_q8::Encode (kv_q8.cuh:28-74) and q8_native::EncodeKV
+ * (kv_q8_native.cuh:52-101).  k and v [T][Hkv][128] (k already normalized and rotated)
+ * go to slot position % kv->cap in kv->format; q8_0 applies its Hadamard rotation.  With
+ * kv->cap = T and positions 0.. this fills an encoded chunk buffer, as the reference's
+ * prefill encode does before attention. */
+int padra_KVStore(void *stream, const void *k, const void *v, const padra_Positions *pos,
+                  int tokens, int kv_heads, int head_dim, const padra_KVCache *kv, int *bad,
+                  int act);
+/* padra_KVCommit: kv_q8::Commit (kv_q8.cuh:75-98) and q8_native::Commit
+ * (kv_q8_native.cuh:440-463), and the BF16 chunk commit: rows r >= ring->first of the
+ * encoded chunk `chunk` (row r at index r, same format) are copied to ring slot
+ * position(r) % ring->cap.  pos: PADRA_POS_BASE or PADRA_POS_PREFILL. */
+int padra_KVCommit(void *stream, const padra_KVCache *chunk, const padra_KVCache *ring,
+                   const padra_Positions *pos, int tokens, int kv_heads, int *bad);
+/* padra_KvQ8_0Dequantize: q8_native::Dequantize (kv_q8_native.cuh:366-390): rows of q8_0
+ * K and V (544 B each for 4 heads) to [rows][Hkv*128] bf16(code * d); a -128 code or a
+ * negative / non-finite scale raises the flag. */
+int padra_KvQ8_0Dequantize(void *stream, const void *rows_k, const void *rows_v, void *out_k,
+                           void *out_v, long long rows, int kv_heads, int *bad, int act);
+/* padra_RotateRows: q8_native::RotateRows (kv_q8_native.cuh:391-412): rotates `rows`
+ * 128-wide rows in place with the K transform (value = 0) or the two 64-point V
+ * transforms (value = 1), output rounded to BF16. */
+int padra_RotateRows(void *stream, void *data, long long rows, int value, int *bad, int act);
+
+/* ---- SwiGLU ---------------------------------------------------------------------------
+ * padra_SiluTableBuild: exl3_silu_lut::Build (exl3_silu_lut.cuh:9-14): table[65536] of the
+ * BF16 bits of B(g / (1 + RN32(exp64(-g)))) per BF16 gate g.
+ * padra_SwiGLU: exl3_silu_lut::Activate (exl3_silu_lut.cuh:15-31) and Activate
+ * (inference.cu:575-579): out[i] = B(silu(gate[i]) * up[i]) over `count` elements
+ * (count % 8 == 0; out may alias gate, as in the reference).  A non-finite gate or up
+ * raises the flag and leaves the gate value in out. */
+int padra_SiluTableBuild(void *stream, uint16_t *table);
+int padra_SwiGLU(void *stream, const void *gate, const void *up, void *out, long long count,
+                 const uint16_t *table, int *bad, int act);
+
+/* ---- embedding gather ------------------------------------------------------------------
+ * Embed / EmbedPrefillControlled / EmbedControlled (inference.cu:181-187,
+ * prefill_control.cuh:3-22, decode_control.cuh:68-79): out[t][:] = table[token_t][:] for a
+ * BF16 table [vocab][hidden].  The token is ids[t] (src NULL or PADRA_POS_BASE), the prompt
+ * id ids[prompt_offset + t] (PADRA_POS_PREFILL), or decode[t].token (PADRA_POS_DECODE).  An
+ * invalid state or a token outside [0, vocab) raises the flag and writes nothing. */
+int padra_Embed(void *stream, const uint16_t *table, int vocab, int hidden, const int32_t *ids,
+                const padra_Positions *src, int tokens, void *out, int *bad, int act);
+
 /* ---- launch tuning ------------------------------------------------------------------
  * No counterpart in the reference (its launch shapes are fixed).  Process-wide launch
  * parameters for measurement sweeps; defaults need no call.

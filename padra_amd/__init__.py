@@ -35,12 +35,23 @@ from .abi import (  # noqa: F401
     library_path,
 )
 from .ops import (  # noqa: F401
+    Embed,
+    KVCommit,
+    KVStore,
+    KvQ8_0Dequantize,
+    ResidualNormQKRopeStore,
     ResidualPostNorm,
     QKNormRopeStore,
-    ResidualNormQKRopeStore,
     RopeTable,
-    q8_0_row_bytes,
+    RotateRows,
+    SiluTableBuild,
+    SwiGLU,
+    kv_cache,
     kv_cache_layout,
+    positions_base,
+    positions_decode,
+    positions_prefill,
+    q8_0_row_bytes,
 )
 
 __all__ = [name for name in dir() if not name.startswith("_")]

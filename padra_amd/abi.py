@@ -72,6 +72,15 @@ SIGNATURES = {
     "padra_ResidualNormQKRopeStore": [_P, _P, _P, _P, _P, _I, _I, _P, _P, _P, _P, _P, _P, _P, _I,
                                       ctypes.POINTER(Positions), _I, _I, _I, _I, _F,
                                       ctypes.POINTER(KVCache), _P],
+    "padra_KVStore": [_P, _P, _P, ctypes.POINTER(Positions), _I, _I, _I, ctypes.POINTER(KVCache),
+                      _P, _I],
+    "padra_KVCommit": [_P, ctypes.POINTER(KVCache), ctypes.POINTER(KVCache),
+                       ctypes.POINTER(Positions), _I, _I, _P],
+    "padra_KvQ8_0Dequantize": [_P, _P, _P, _P, _P, ctypes.c_longlong, _I, _P, _I],
+    "padra_RotateRows": [_P, _P, ctypes.c_longlong, _I, _P, _I],
+    "padra_SiluTableBuild": [_P, _P],
+    "padra_SwiGLU": [_P, _P, _P, _P, ctypes.c_longlong, _P, _P, _I],
+    "padra_Embed": [_P, _P, _I, _I, _P, ctypes.POINTER(Positions), _I, _P, _P, _I],
     "padra_Tune": [_I, _I],
     "padra_version": [],
 }

@@ -127,6 +127,12 @@ __device__ __forceinline__ void load8_bf16(const uint16_t *p, float (&v)[8]) {
   ActIO<uint16_t>::load8(p, v);
 }
 
+// True when x stays finite after rounding to BF16: 0x7f7f8000 is the midpoint between the
+// largest finite BF16 (0x7f7f, odd) and infinity, and it rounds to infinity.
+__device__ __forceinline__ bool bf16_finite(float x) {
+  return fabsf(x) < __uint_as_float(0x7f7f8000u);
+}
+
 // Sets the caller's sticky error flag (reference: atomicExch(bad, 1)).
 __device__ __forceinline__ void raise_bad(int *bad) {
   if (bad)

@@ -1,0 +1,400 @@
+// KV-cache writers that run apart from the Q/K norm: the store/encode of already rotated
+// K rows and V rows, the commit of an encoded chunk into the ring, the q8_0 decode back to
+// BF16, and the Hadamard row rotation used around q8_0 prefill attention.
+#include <stdio.h>
+
+#include <algorithm>
+#include <type_traits>
+
+#include "qk_heads.h"
+
+using namespace padra;
+
+namespace {
+
+int launched(const char *what) {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    fprintf(stderr, "padra: %s launch failed: %s\n", what, hipGetErrorString(e));
+    return PADRA_INTERNAL;
+  }
+  return PADRA_OK;
+}
+bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+PosSrc pos_src(const padra_Positions &p, int tokens) {
+  PosSrc s;
+  s.mode = p.mode;
+  s.base = p.base;
+  s.maximum = p.maximum;
+  s.vocab = p.vocab;
+  s.tokens = tokens;
+  s.epoch = p.binding_epoch;
+  s.prefill = p.prefill;
+  s.decode = p.decode;
+  return s;
+}
+
+int check_positions(const padra_Positions *pos, int tokens) {
+  if (!pos || tokens < 1)
+    return PADRA_INVALID_ARGUMENT;
+  switch (pos->mode) {
+  case PADRA_POS_BASE:
+    return pos->base < 0 || (long long)pos->base + tokens > 0x7fffffffLL ? PADRA_INVALID_ARGUMENT
+                                                                          : PADRA_OK;
+  case PADRA_POS_PREFILL:
+    return !pos->prefill || tokens > 2048 || pos->maximum < 1 || pos->maximum > 131072
+               ? PADRA_INVALID_ARGUMENT
+               : PADRA_OK;
+  case PADRA_POS_DECODE:
+    return !pos->decode || pos->maximum < 1 || pos->maximum > 131072 || pos->vocab < 1
+               ? PADRA_INVALID_ARGUMENT
+               : PADRA_OK;
+  }
+  return PADRA_INVALID_ARGUMENT;
+}
+
+// ---- store / encode of K and V rows ----------------------------------------------------
+//
+// Head vectors 0 .. T*Hkv-1 are K heads, T*Hkv .. 2*T*Hkv-1 V heads; 32 per wave, two
+// lanes each (the lane-pair layout of the quantizers).  BF16 rows are a plain copy.
+template <class T, int FMT>
+__global__ __launch_bounds__(64) void k_kv_store(QKArgs<T> a) {
+  constexpr int D = 128;
+  const int lane = threadIdx.x & 63, half = lane & 1;
+  const unsigned nk = (unsigned)a.tokens * (unsigned)a.hkv;
+  const unsigned hv = blockIdx.x * 32u + (unsigned)(lane >> 1);
+  if (hv >= 2 * nk)
+    return;
+  const bool isv = hv >= nk;
+  const unsigned idx = isv ? hv - nk : hv;
+  const int t = (int)(idx / (unsigned)a.hkv), h = (int)(idx % (unsigned)a.hkv);
+  const T *src = (isv ? a.v : a.k) + (size_t)idx * D;
+  Act32<T> xa, xb;
+  xa.load(src + 32 * half);
+  xb.load(src + 64 + 32 * half);
+  bool ok;
+  const int pos = resolve_position(a.pos, t, a.cap, a.first, FMT > PADRA_KV_BF16, ok);
+  if (!ok || pos < 0) {
+    if (half == 0)
+      raise_bad(a.bad);
+    return;
+  }
+  if (t < a.first)
+    return;
+  const long long seq = a.pos.mode == PADRA_POS_DECODE ? t : 0;
+  const long long slot = seq * a.seq_stride + pos % a.cap;
+  if constexpr (FMT == PADRA_KV_BF16) {
+    uint16_t *dst = static_cast<uint16_t *>(isv ? a.vc : a.kc) + slot * (a.hkv * D) + h * D;
+    uint32_t pa[16], pb[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      pa[i] = pack2(xa.get(2 * i), xa.get(2 * i + 1));
+      pb[i] = pack2(xb.get(2 * i), xb.get(2 * i + 1));
+    }
+    store32_bf16(dst + 32 * half, pa);
+    store32_bf16(dst + 64 + 32 * half, pb);
+  } else {
+    float fa[32], fb[32];
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+      fa[i] = xa.get(i);
+      fb[i] = xb.get(i);
+    }
+    if (isv)
+      encode_head_q<FMT, true>(a, fa, fb, slot, h, half);
+    else
+      encode_head_q<FMT, false>(a, fa, fb, slot, h, half);
+  }
+}
+
+// ---- commit: encoded chunk rows -> ring slots ----------------------------------------
+//
+// Row r of the chunk (r >= first) goes to slot (base + r) % cap; one wave per row, every
+// tensor of the format copied as 16-byte words (rows are 16-byte multiples except the q8
+// scale pairs, copied as 8-byte words).
+struct CommitArgs {
+  const uint8_t *src[3];
+  uint8_t *dst[3];
+  int row_bytes[3];
+  int tensors, tokens, cap, first, strict;
+  PosSrc pos;
+  int *bad;
+};
+
+__global__ __launch_bounds__(64) void k_kv_commit(CommitArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int r = a.first + (int)blockIdx.x;
+  if (r >= a.tokens)
+    return;
+  bool ok;
+  const int pos = resolve_position(a.pos, r, a.cap, a.first, a.strict != 0, ok);
+  if (!ok || pos < 0) {
+    if (lane == 0)
+      raise_bad(a.bad);
+    return;
+  }
+  const long long slot = pos % a.cap;
+  for (int tn = 0; tn < a.tensors; ++tn) {
+    const int rb = a.row_bytes[tn];
+    const uint8_t *s = a.src[tn] + (long long)r * rb;
+    uint8_t *d = a.dst[tn] + slot * rb;
+    if ((rb & 15) == 0) {
+      for (int w = lane; w < rb / 16; w += 64)
+        st_nt(reinterpret_cast<uint4 *>(d) + w, ld_nt(reinterpret_cast<const uint4 *>(s) + w));
+    } else {
+      for (int w = lane; w < rb / 8; w += 64)
+        st_nt(reinterpret_cast<uint2 *>(d) + w, ld_nt(reinterpret_cast<const uint2 *>(s) + w));
+    }
+  }
+}
+
+// ---- q8_0 rows -> BF16 ----------------------------------------------------------------
+//
+// q8_native::Dequantize (kv_q8_native.cuh:366-390): out = bf16(code * float(d)); a -128
+// code or a negative / non-finite scale raises the flag (the value is still written).
+template <class O>
+__global__ __launch_bounds__(256) void k_q8_0_dequant(const uint8_t *rk, const uint8_t *rv,
+                                                      O *ok_out, O *ov_out, long long rows,
+                                                      int features, int *bad) {
+  const int nd = features / 32, rb = ((2 * nd + features) + 15) / 16 * 16;
+  const long long groups = rows * (features / 8); // 8 codes per thread-step
+  for (long long g = blockIdx.x * (long long)blockDim.x + threadIdx.x; g < 2 * groups;
+       g += (long long)gridDim.x * blockDim.x) {
+    const bool isv = g >= groups;
+    const long long gg = isv ? g - groups : g;
+    const long long row = gg / (features / 8);
+    const int c0 = (int)(gg % (features / 8)) * 8;
+    const uint8_t *rowp = (isv ? rv : rk) + row * rb;
+    const uint16_t dbits = reinterpret_cast<const uint16_t *>(rowp)[c0 / 32];
+    const float d = __half2float(__ushort_as_half(dbits));
+    const uint2 codes = *reinterpret_cast<const uint2 *>(rowp + 2 * nd + c0);
+    bool flag = (c0 % 32 == 0) && (!isfinite(d) || d < 0.f);
+    uint32_t w[4];
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      const uint32_t src = p < 2 ? codes.x : codes.y;
+      const int8_t c0v = (int8_t)((src >> (16 * (p & 1))) & 0xff);
+      const int8_t c1v = (int8_t)((src >> (16 * (p & 1) + 8)) & 0xff);
+      flag |= c0v == -128 || c1v == -128;
+      w[p] = pack2((float)c0v * d, (float)c1v * d);
+    }
+    if (flag)
+      raise_bad(bad);
+    O *dst = (isv ? ov_out : ok_out) + row * features + c0;
+    ActIO<O>::store8(dst, w);
+  }
+}
+
+// ---- Hadamard row rotation -----------------------------------------------------------
+//
+// q8_native::RotateRows (kv_q8_native.cuh:391-412): each 128-wide row rotated with the K
+// transform (VALUE false) or the two 64-point V transforms (VALUE true), output B(x).
+template <class T, bool VALUE>
+__global__ __launch_bounds__(64) void k_rotate_rows(T *data, long long rows, int *bad) {
+  constexpr int D = 128;
+  const int lane = threadIdx.x & 63, half = lane & 1;
+  const long long r = blockIdx.x * 32ll + (lane >> 1);
+  if (r >= rows)
+    return;
+  T *p = data + r * D;
+  Act32<T> xa, xb;
+  xa.load(p + 32 * half);
+  xb.load(p + 64 + 32 * half);
+  float a[32], b[32];
+#pragma unroll
+  for (int i = 0; i < 32; ++i) {
+    a[i] = xa.get(i);
+    b[i] = xb.get(i);
+  }
+  hadamard32(a);
+  hadamard32(b);
+  hadamard_cross(a, half);
+  hadamard_cross(b, half);
+  if constexpr (!VALUE) {
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+      const float lower = a[i], upper = b[i];
+      a[i] = (lower + upper) * .08838834764831845f;
+      b[i] = (lower - upper) * .08838834764831845f;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+      a[i] = a[i] * .125f;
+      b[i] = b[i] * .125f;
+    }
+  }
+  bool fine = true;
+  uint32_t wa[16], wb[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    fine = fine && isfinite(a[2 * i]) && isfinite(a[2 * i + 1]) && isfinite(b[2 * i]) &&
+           isfinite(b[2 * i + 1]);
+    wa[i] = pack2(a[2 * i], a[2 * i + 1]);
+    wb[i] = pack2(b[2 * i], b[2 * i + 1]);
+  }
+  if (!fine)
+    raise_bad(bad);
+  store32<T>(p + 32 * half, wa);
+  store32<T>(p + 64 + 32 * half, wb);
+}
+
+template <class F> int with_kv_format(int fmt, F &&f) {
+  switch (fmt) {
+  case PADRA_KV_BF16:
+    return f(std::integral_constant<int, PADRA_KV_BF16>{});
+  case PADRA_KV_Q8:
+    return f(std::integral_constant<int, PADRA_KV_Q8>{});
+  case PADRA_KV_Q8_0:
+    return f(std::integral_constant<int, PADRA_KV_Q8_0>{});
+  case PADRA_KV_Q8_0_NOROT:
+    return f(std::integral_constant<int, PADRA_KV_Q8_0_NOROT>{});
+  }
+  return PADRA_INVALID_ARGUMENT;
+}
+
+int row_bytes_q8_0(int features) { return ((2 * (features / 32) + features) + 15) / 16 * 16; }
+
+} // namespace
+
+extern "C" int padra_KVStore(void *stream, const void *k, const void *v,
+                             const padra_Positions *pos, int tokens, int kv_heads, int head_dim,
+                             const padra_KVCache *kv, int *bad, int act) {
+  if (!k || !v || !kv || !bad || kv_heads < 1 || !aligned16(k) || !aligned16(v) ||
+      (act != PADRA_ACT_BF16 && act != PADRA_ACT_F32))
+    return PADRA_INVALID_ARGUMENT;
+  if (head_dim != 128)
+    return PADRA_UNSUPPORTED;
+  int st = check_positions(pos, tokens);
+  if (st)
+    return st;
+  if (!kv->k || !kv->v || kv->cap < 1 || kv->first < 0 || kv->first >= tokens ||
+      kv->seq_stride < 0 || kv->format < PADRA_KV_BF16 || kv->format > PADRA_KV_Q8_0_NOROT ||
+      (kv->format == PADRA_KV_Q8 && !kv->scales) ||
+      (pos->mode == PADRA_POS_DECODE && tokens > 1 && kv->seq_stride < kv->cap) ||
+      (pos->mode != PADRA_POS_DECODE && tokens - kv->first > kv->cap))
+    return PADRA_INVALID_ARGUMENT;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const long long grid = (2ll * tokens * kv_heads + 31) / 32;
+  auto launch = [&](auto tag) -> int {
+    using T = decltype(tag);
+    QKArgs<T> a{};
+    a.k = const_cast<T *>(static_cast<const T *>(k));
+    a.v = static_cast<const T *>(v);
+    a.tokens = tokens;
+    a.hq = 0;
+    a.hkv = kv_heads;
+    a.pos = pos_src(*pos, tokens);
+    a.kc = kv->k;
+    a.vc = kv->v;
+    a.scales = kv->scales;
+    a.cap = kv->cap;
+    a.first = kv->first;
+    a.seq_stride = kv->seq_stride;
+    a.bad = bad;
+    return with_kv_format(kv->format, [&](auto fmt) -> int {
+      hipLaunchKernelGGL((k_kv_store<T, fmt.value>), dim3((unsigned)grid), dim3(64), 0, s, a);
+      return launched("KVStore");
+    });
+  };
+  return act == PADRA_ACT_BF16 ? launch(uint16_t{}) : launch(float{});
+}
+
+extern "C" int padra_KVCommit(void *stream, const padra_KVCache *chunk, const padra_KVCache *ring,
+                              const padra_Positions *pos, int tokens, int kv_heads, int *bad) {
+  if (!chunk || !ring || !bad || kv_heads < 1 || chunk->format != ring->format ||
+      !chunk->k || !chunk->v || !ring->k || !ring->v || ring->cap < 1 || ring->first < 0 ||
+      ring->first >= tokens || tokens - ring->first > ring->cap)
+    return PADRA_INVALID_ARGUMENT;
+  if (pos && pos->mode == PADRA_POS_DECODE)
+    return PADRA_UNSUPPORTED; // commits are per prefill chunk
+  int st = check_positions(pos, tokens);
+  if (st)
+    return st;
+  const int features = kv_heads * 128;
+  CommitArgs a{};
+  a.tokens = tokens;
+  a.cap = ring->cap;
+  a.first = ring->first;
+  a.strict = ring->format > PADRA_KV_BF16;
+  a.pos = pos_src(*pos, tokens);
+  a.bad = bad;
+  a.src[0] = static_cast<const uint8_t *>(chunk->k);
+  a.src[1] = static_cast<const uint8_t *>(chunk->v);
+  a.dst[0] = static_cast<uint8_t *>(ring->k);
+  a.dst[1] = static_cast<uint8_t *>(ring->v);
+  a.tensors = 2;
+  switch (ring->format) {
+  case PADRA_KV_BF16:
+    a.row_bytes[0] = a.row_bytes[1] = 2 * features;
+    break;
+  case PADRA_KV_Q8:
+    if (!chunk->scales || !ring->scales)
+      return PADRA_INVALID_ARGUMENT;
+    a.row_bytes[0] = a.row_bytes[1] = features;
+    a.src[2] = static_cast<const uint8_t *>(chunk->scales);
+    a.dst[2] = static_cast<uint8_t *>(ring->scales);
+    a.row_bytes[2] = 8 * kv_heads;
+    a.tensors = 3;
+    break;
+  default:
+    a.row_bytes[0] = a.row_bytes[1] = row_bytes_q8_0(features);
+    break;
+  }
+  for (int t = 0; t < a.tensors; ++t)
+    if (!aligned16(a.src[t]) || !aligned16(a.dst[t]))
+      return PADRA_INVALID_ARGUMENT;
+  hipLaunchKernelGGL(k_kv_commit, dim3(tokens - ring->first), dim3(64), 0,
+                     static_cast<hipStream_t>(stream), a);
+  return launched("KVCommit");
+}
+
+extern "C" int padra_KvQ8_0Dequantize(void *stream, const void *rows_k, const void *rows_v,
+                                      void *out_k, void *out_v, long long rows, int kv_heads,
+                                      int *bad, int act) {
+  if (!rows_k || !rows_v || !out_k || !out_v || !bad || rows < 1 || kv_heads < 1 ||
+      !aligned16(rows_k) || !aligned16(rows_v) || !aligned16(out_k) || !aligned16(out_v) ||
+      (act != PADRA_ACT_BF16 && act != PADRA_ACT_F32))
+    return PADRA_INVALID_ARGUMENT;
+  const int features = kv_heads * 128;
+  const long long work = 2 * rows * (features / 8);
+  const unsigned grid = (unsigned)std::min<long long>((work + 255) / 256, 4096);
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  if (act == PADRA_ACT_BF16)
+    hipLaunchKernelGGL((k_q8_0_dequant<uint16_t>), dim3(grid), dim3(256), 0, s,
+                       static_cast<const uint8_t *>(rows_k), static_cast<const uint8_t *>(rows_v),
+                       static_cast<uint16_t *>(out_k), static_cast<uint16_t *>(out_v), rows,
+                       features, bad);
+  else
+    hipLaunchKernelGGL((k_q8_0_dequant<float>), dim3(grid), dim3(256), 0, s,
+                       static_cast<const uint8_t *>(rows_k), static_cast<const uint8_t *>(rows_v),
+                       static_cast<float *>(out_k), static_cast<float *>(out_v), rows, features,
+                       bad);
+  return launched("KvQ8_0Dequantize");
+}
+
+extern "C" int padra_RotateRows(void *stream, void *data, long long rows, int value, int *bad,
+                                int act) {
+  if (!data || !bad || rows < 1 || !aligned16(data) ||
+      (act != PADRA_ACT_BF16 && act != PADRA_ACT_F32))
+    return PADRA_INVALID_ARGUMENT;
+  const unsigned grid = (unsigned)((rows + 31) / 32);
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  if (act == PADRA_ACT_BF16) {
+    if (value)
+      hipLaunchKernelGGL((k_rotate_rows<uint16_t, true>), dim3(grid), dim3(64), 0, s,
+                         static_cast<uint16_t *>(data), rows, bad);
+    else
+      hipLaunchKernelGGL((k_rotate_rows<uint16_t, false>), dim3(grid), dim3(64), 0, s,
+                         static_cast<uint16_t *>(data), rows, bad);
+  } else {
+    if (value)
+      hipLaunchKernelGGL((k_rotate_rows<float, true>), dim3(grid), dim3(64), 0, s,
+                         static_cast<float *>(data), rows, bad);
+    else
+      hipLaunchKernelGGL((k_rotate_rows<float, false>), dim3(grid), dim3(64), 0, s,
+                         static_cast<float *>(data), rows, bad);
+  }
+  return launched("RotateRows");
+}

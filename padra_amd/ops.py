@@ -146,3 +146,54 @@ def ResidualNormQKRopeStore(x, residual, normalized, gamma, q, k, v, qn, kn, tab
              _p(gamma), x.shape[-1], int(tree), _p(statistics), _p(q), _p(k), _p(v), _p(qn),
              _p(kn), _p(table), table.shape[0], ctypes.byref(positions), tokens, q_heads,
              kv_heads, head_dim, float(eps), None if kv is None else ctypes.byref(kv), _p(bad))
+
+
+def KVStore(k, v, positions: abi.Positions, kv: abi.KVCache, bad):
+    """Store / encode K [T][Hkv][D] (already rotated) and V rows into the cache."""
+    _need_cuda(k, v, bad)
+    tokens, kv_heads, head_dim = k.shape
+    abi.call("padra_KVStore", _stream(k), _p(k), _p(v), ctypes.byref(positions), tokens,
+             kv_heads, head_dim, ctypes.byref(kv), _p(bad), _act(k))
+
+
+def KVCommit(chunk: abi.KVCache, ring: abi.KVCache, positions: abi.Positions, tokens, kv_heads,
+             bad):
+    """Copy encoded chunk rows r >= ring.first to ring slots position(r) % ring.cap."""
+    _need_cuda(bad)
+    abi.call("padra_KVCommit", _stream(bad), ctypes.byref(chunk), ctypes.byref(ring),
+             ctypes.byref(positions), int(tokens), int(kv_heads), _p(bad))
+
+
+def KvQ8_0Dequantize(rows_k, rows_v, out_k, out_v, bad, kv_heads=4):
+    _need_cuda(rows_k, rows_v, out_k, out_v, bad)
+    abi.call("padra_KvQ8_0Dequantize", _stream(out_k), _p(rows_k), _p(rows_v), _p(out_k),
+             _p(out_v), rows_k.shape[0], int(kv_heads), _p(bad), _act(out_k))
+
+
+def RotateRows(data, bad, value=False):
+    """In-place Hadamard rotation of 128-wide rows (K transform, or V with value=True)."""
+    _need_cuda(data, bad)
+    abi.call("padra_RotateRows", _stream(data), _p(data), data.numel() // 128, int(bool(value)),
+             _p(bad), _act(data))
+
+
+def SiluTableBuild(table):
+    """table: device int16/uint16 [65536]."""
+    _need_cuda(table)
+    abi.call("padra_SiluTableBuild", _stream(table), _p(table))
+
+
+def SwiGLU(gate, up, out, table, bad):
+    _need_cuda(gate, up, out, table, bad)
+    abi.call("padra_SwiGLU", _stream(gate), _p(gate), _p(up), _p(out), gate.numel(), _p(table),
+             _p(bad), _act(gate))
+
+
+def Embed(table, out, bad, ids=None, positions: abi.Positions | None = None, tokens=None):
+    """out[t] = table[token_t]; token from ids, a PrefillState prompt or DecodeStates."""
+    _need_cuda(table, out, bad, ids)
+    vocab, hidden = table.shape
+    tokens = out.shape[0] if tokens is None else tokens
+    abi.call("padra_Embed", _stream(out), _p(table), vocab, hidden, _p(ids),
+             None if positions is None else ctypes.byref(positions), int(tokens), _p(out),
+             _p(bad), _act(out))

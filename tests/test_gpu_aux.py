@@ -1,0 +1,266 @@
+"""GPU parity of the KV store/commit/decode, row rotation, SwiGLU and embedding gather
+kernels against the CPU oracle, through the C-ABI.  Exact equality throughout."""
+import numpy as np
+import pytest
+import torch
+
+from padra_amd import abi, ops, synth
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module", autouse=True)
+def gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    abi.lib()
+    yield
+    torch.cuda.synchronize()
+
+
+def dev(a):
+    a = np.ascontiguousarray(a)
+    if a.dtype == np.uint16:
+        return torch.from_numpy(a.view(np.int16)).cuda()
+    return torch.from_numpy(a).cuda()
+
+
+def host16(t):
+    return t.cpu().numpy().view(np.uint16)
+
+
+def flag():
+    return torch.zeros(1, dtype=torch.int32, device="cuda")
+
+
+def _cache(fmt, rows):
+    if fmt == abi.KV_BF16:
+        mk = lambda: torch.zeros((rows, 512), dtype=torch.int16, device="cuda")
+        return mk(), mk(), None
+    if fmt == abi.KV_Q8:
+        mk = lambda: torch.zeros((rows, 512), dtype=torch.int8, device="cuda")
+        return mk(), mk(), torch.zeros((rows, 4, 2), dtype=torch.float32, device="cuda")
+    mk = lambda: torch.zeros((rows, 544), dtype=torch.uint8, device="cuda")
+    return mk(), mk(), None
+
+
+def _expected(oracle, fmt, k, v, positions, cap, first):
+    if fmt == abi.KV_BF16:
+        kc = np.zeros((cap, 512), np.uint16)
+        vc = np.zeros((cap, 512), np.uint16)
+        oracle.kv_store_bf16(k, v, kc, vc, positions, cap, first)
+        return kc, vc, None
+    if fmt == abi.KV_Q8:
+        kc = np.zeros((cap, 512), np.int8)
+        vc = np.zeros((cap, 512), np.int8)
+        sc = np.zeros((cap, 4, 2), np.float32)
+        oracle.kv_q8_encode(k, v, kc, vc, sc, positions, cap, first)
+        return kc, vc, sc
+    kc = np.zeros((cap, 544), np.uint8)
+    vc = np.zeros((cap, 544), np.uint8)
+    oracle.kv_q8_0_encode(k, v, kc, vc, positions, cap, first, rotate=fmt == abi.KV_Q8_0)
+    return kc, vc, None
+
+
+def _np(t, fmt):
+    a = t.cpu().numpy()
+    return a.view(np.uint16) if fmt == abi.KV_BF16 else a
+
+
+FORMATS = [abi.KV_BF16, abi.KV_Q8, abi.KV_Q8_0, abi.KV_Q8_0_NOROT]
+
+
+@pytest.mark.parametrize("fmt", FORMATS)
+def test_kv_store_then_commit(oracle, fmt):
+    """Prefill encode into a chunk buffer (cap = T, positions 0..), then commit of the last
+    `cap` rows into a local ring at base 700 (the reference's local-layer sequence)."""
+    print(f"[case] kv store+commit fmt={fmt}", flush=True)
+    tokens, base, cap, capacity = 1500, 700, 1024, 4096
+    d = synth.chain_inputs(tokens, outliers=True, seed=50 + fmt)
+    first = max(0, tokens - cap)
+    ck, cv, cs = _cache(fmt, tokens)
+    bad = flag()
+    ops.KVStore(dev(d["k"]), dev(d["v"]), ops.positions_base(0),
+                ops.kv_cache(fmt, ck, cv, tokens, scales=cs), bad)
+    torch.cuda.synchronize()
+    assert bad.item() == 0
+    ek, ev, es = _expected(oracle, fmt, d["k"], d["v"], np.arange(tokens, dtype=np.int32),
+                           tokens, 0)
+    assert np.array_equal(_np(ck, fmt), ek) and np.array_equal(_np(cv, fmt), ev)
+    if es is not None:
+        assert np.array_equal(cs.cpu().numpy(), es)
+    rk, rv, rs = _cache(fmt, cap)
+    state = torch.tensor([base, base, tokens, capacity, base, 1, 1, 1], dtype=torch.int32,
+                         device="cuda")
+    ops.KVCommit(ops.kv_cache(fmt, ck, cv, tokens, scales=cs),
+                 ops.kv_cache(fmt, rk, rv, cap, scales=rs, first=first),
+                 ops.positions_prefill(state, maximum=capacity), tokens, 4, bad)
+    torch.cuda.synchronize()
+    assert bad.item() == 0
+    slots = (base + np.arange(first, tokens)) % cap
+    assert np.array_equal(_np(rk, fmt)[slots], ek[first:])
+    assert np.array_equal(_np(rv, fmt)[slots], ev[first:])
+    if es is not None:
+        assert np.array_equal(rs.cpu().numpy()[slots], es[first:])
+
+
+def test_kv_store_decode_states(oracle):
+    seqs, cap = 8, 128
+    rng = np.random.default_rng(3)
+    positions = rng.integers(0, cap, seqs).astype(np.int32)
+    states = np.zeros((seqs, 8), np.int32)
+    for s, p in enumerate(positions):
+        states[s] = [1, p, cap, 5, p, min(p, 1024), 0, 0]
+    d = synth.chain_inputs(seqs, seed=4)
+    kc, vc, _ = _cache(abi.KV_BF16, seqs * cap)
+    bad = flag()
+    ops.KVStore(dev(d["k"]), dev(d["v"]), ops.positions_decode(torch.from_numpy(states).cuda(),
+                                                               maximum=cap),
+                ops.kv_cache(abi.KV_BF16, kc, vc, cap, seq_stride=cap), bad)
+    torch.cuda.synchronize()
+    assert bad.item() == 0
+    k3, v3 = host16(kc).reshape(seqs, cap, 512), host16(vc).reshape(seqs, cap, 512)
+    for s in range(seqs):
+        assert np.array_equal(k3[s, positions[s]], d["k"][s].reshape(-1))
+        assert np.array_equal(v3[s, positions[s]], d["v"][s].reshape(-1))
+
+
+@pytest.mark.parametrize("act", ["bf16", "f32"])
+def test_q8_0_dequantize(oracle, act):
+    tokens = 300
+    d = synth.chain_inputs(tokens, outliers=True, seed=60)
+    rk = np.zeros((tokens, 544), np.uint8)
+    rv = np.zeros((tokens, 544), np.uint8)
+    oracle.kv_q8_0_encode(d["k"], d["v"], rk, rv, np.arange(tokens, dtype=np.int32), tokens)
+    wk, wv, _ = oracle.kv_q8_0_dequantize(rk, rv, tokens, 512)
+    if act == "bf16":
+        ok = torch.empty((tokens, 512), dtype=torch.int16, device="cuda")
+    else:
+        ok = torch.empty((tokens, 512), dtype=torch.float32, device="cuda")
+    ov = torch.empty_like(ok)
+    bad = flag()
+    ops.KvQ8_0Dequantize(dev(rk), dev(rv), ok, ov, bad)
+    torch.cuda.synchronize()
+    assert bad.item() == 0
+    gk = host16(ok) if act == "bf16" else synth.bf16_bits(ok.cpu().numpy())
+    gv = host16(ov) if act == "bf16" else synth.bf16_bits(ov.cpu().numpy())
+    assert np.array_equal(gk, wk) and np.array_equal(gv, wv)
+    bad_rows = rk.copy()
+    bad_rows[5, 32 + 7] = 0x80  # code -128
+    ops.KvQ8_0Dequantize(dev(bad_rows), dev(rv), ok, ov, bad)
+    torch.cuda.synchronize()
+    assert bad.item() == 1
+
+
+@pytest.mark.parametrize("value", [False, True])
+def test_rotate_rows(oracle, value):
+    rows = 96
+    rng = np.random.default_rng(7)
+    x = synth.bf16_bits(rng.standard_normal((rows, 128)))
+    want = []
+    for r in range(rows):
+        xf = synth.bf16_to_f32(x[r])
+        if value:
+            out = np.concatenate([oracle.hadamard(xf[:64], .125), oracle.hadamard(xf[64:], .125)])
+        else:
+            out = oracle.hadamard(xf, .08838834764831845)
+        want.append(synth.bf16_bits(out))
+    t = dev(x)
+    bad = flag()
+    ops.RotateRows(t, bad, value=value)
+    torch.cuda.synchronize()
+    assert np.array_equal(host16(t), np.stack(want))
+
+
+def test_silu_table_exhaustive(oracle):
+    table = torch.empty(65536, dtype=torch.int16, device="cuda")
+    ops.SiluTableBuild(table)
+    torch.cuda.synchronize()
+    got = host16(table)
+    want = oracle.silu_table()
+    g = synth.bf16_to_f32(np.arange(65536, dtype=np.uint16))
+    finite = np.isfinite(g)
+    assert np.array_equal(got[finite], want[finite])
+
+
+@pytest.mark.parametrize("act", ["bf16", "f32"])
+def test_swiglu_all_gates(oracle, act):
+    """Every BF16 gate value (finite ones), each with four up values, plus the config-3
+    distribution; the kernel's closed forms outside the staged table span included."""
+    table = torch.empty(65536, dtype=torch.int16, device="cuda")
+    ops.SiluTableBuild(table)
+    gates = np.arange(65536, dtype=np.uint16)
+    gates = gates[np.isfinite(synth.bf16_to_f32(gates))]
+    rng = np.random.default_rng(11)
+    gate = np.repeat(gates, 4)
+    up = synth.bf16_bits(rng.standard_normal(gate.size) * 4)
+    n = gate.size // 8 * 8
+    gate, up = gate[:n], up[:n]
+    want, wbad = oracle.swiglu(gate, up)
+    if act == "bf16":
+        tg, tu = dev(gate), dev(up)
+    else:
+        tg = torch.from_numpy(synth.bf16_to_f32(gate)).cuda()
+        tu = torch.from_numpy(synth.bf16_to_f32(up)).cuda()
+    out = torch.empty_like(tg)
+    bad = flag()
+    ops.SwiGLU(tg, tu, out, table, bad)
+    torch.cuda.synchronize()
+    got = host16(out) if act == "bf16" else synth.bf16_bits(out.cpu().numpy())
+    assert np.array_equal(got, want)
+    assert bool(bad.item()) == wbad
+
+
+def test_swiglu_config3_shape_in_place(oracle):
+    d = synth.swiglu_inputs(tokens=256, seed=0)  # 2048 rows x 1024, expert-permuted
+    want, _ = oracle.swiglu(d["gate"], d["up"])
+    table = torch.empty(65536, dtype=torch.int16, device="cuda")
+    ops.SiluTableBuild(table)
+    g = dev(d["gate"])
+    bad = flag()
+    ops.SwiGLU(g, dev(d["up"]), g, table, bad)  # in place over gate, as the reference
+    torch.cuda.synchronize()
+    assert np.array_equal(host16(g), want) and bad.item() == 0
+    gate = d["gate"].copy()
+    gate[3, 5] = 0x7FC0  # NaN gate: flag raised, element left as it was
+    g = dev(gate)
+    ops.SwiGLU(g, dev(d["up"]), g, table, bad)
+    torch.cuda.synchronize()
+    assert bad.item() == 1 and host16(g)[3, 5] == 0x7FC0
+
+
+def test_embed_sources(oracle):
+    rng = np.random.default_rng(12)
+    vocab, hidden = 5000, 2048
+    table_bits = synth.bf16_bits(rng.standard_normal((vocab, hidden)) * 0.02)
+    table = dev(table_bits)
+    ids = synth.zipf_ids(64, vocab, seed=1)
+    # ids
+    out = torch.empty((64, hidden), dtype=torch.int16, device="cuda")
+    bad = flag()
+    ops.Embed(table, out, bad, ids=torch.from_numpy(ids).cuda())
+    torch.cuda.synchronize()
+    want, _ = oracle.embed(table_bits, ids)
+    assert np.array_equal(host16(out), want) and bad.item() == 0
+    # prompt through a PrefillState (prompt_offset 10)
+    prompt = np.concatenate([np.zeros(10, np.int32), ids])
+    state = torch.tensor([10, 10, 64, 4096, 10, 1, 1, 1], dtype=torch.int32, device="cuda")
+    out.zero_()
+    ops.Embed(table, out, bad, ids=torch.from_numpy(prompt).cuda(),
+              positions=ops.positions_prefill(state, maximum=4096), tokens=64)
+    torch.cuda.synchronize()
+    assert np.array_equal(host16(out), want) and bad.item() == 0
+    # decode states, one token out of range: that row is left untouched, flag raised
+    states = np.zeros((64, 8), np.int32)
+    for s in range(64):
+        states[s] = [ids[s], 7, 64, 3, 7, 7, 0, 0]
+    states[9, 0] = vocab + 3
+    out32 = torch.full((64, hidden), 9.0, dtype=torch.float32, device="cuda")
+    ops.Embed(table, out32, bad, positions=ops.positions_decode(torch.from_numpy(states).cuda(),
+                                                                 maximum=64, vocab=vocab * 2))
+    torch.cuda.synchronize()
+    got = out32.cpu().numpy()
+    assert bad.item() == 1
+    assert np.all(got[9] == 9.0)
+    keep = [s for s in range(64) if s != 9]
+    assert np.array_equal(synth.bf16_bits(got[keep]), want[keep])
