@@ -50,6 +50,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--sets", type=int, default=8)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the config 0/3/4 measurements (headline only)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--formats", default="bf16,q8_0,q8_0_norot,q8",
                     help="KV formats measured (the first is the headline)")
@@ -181,6 +183,114 @@ def cpu_baseline(host, seconds):
     }
 
 
+
+def graph_time(torch, step, steps, warmup=3):
+    """Average ms per call of step(i), captured `steps` times in one HIP graph."""
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(graph, stream=stream):
+            for i in range(steps):
+                step(i)
+    torch.cuda.synchronize()
+    graph.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        start.record(stream)
+        graph.replay()
+        end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def bench_swiglu(torch, steps, sets=4):
+    """Config 3: SwiGLU over 2048 tokens x top-8 = 16384 expert-permuted rows of 1024."""
+    from padra_amd import ops, synth
+    d = synth.swiglu_inputs(tokens=2048, top_k=8, width=1024, experts=64, sigma=2.0, seed=0)
+    table = torch.empty(65536, dtype=torch.int16, device="cuda")
+    ops.SiluTableBuild(table)
+    bad = torch.zeros(1, dtype=torch.int32, device="cuda")
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).cuda()
+    bufs = [(dev(d["gate"]), dev(d["up"]), torch.empty(d["gate"].shape, dtype=torch.int16,
+                                                         device="cuda")) for _ in range(sets)]
+    ms = graph_time(torch, lambda i: ops.SwiGLU(bufs[i % sets][0], bufs[i % sets][1],
+                                                bufs[i % sets][2], table, bad), steps)
+    nbytes = 6 * d["gate"].size
+    if bad.item():
+        raise SystemExit("device error flag set in the SwiGLU benchmark")
+    return {"workload": "config3: SwiGLU 16384 rows x 1024, expert-permuted (64 experts)",
+            "us_per_launch": round(ms * 1e3, 3), "bytes_per_launch": nbytes,
+            "gbs": round(nbytes / (ms * 1e-3) / 1e9, 2),
+            "frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "rows_per_s": round(d["gate"].shape[0] / (ms * 1e-3), 1)}
+
+
+def bench_decode(torch, steps, seqs, vocab=131072, capacity=CAPACITY):
+    """Config 4 (seqs=64) and the GPU side of config 0 (seqs=1): embedding gather, then the
+    fused residual-norm (256-thread decode tree) + Q/K norm + RoPE + BF16 KV store at each
+    sequence's own position (DecodeState per sequence, per-sequence caches)."""
+    from padra_amd import abi, ops, synth
+    rng = np.random.default_rng(0)
+    gen = torch.Generator(device="cuda").manual_seed(0)
+    table = (torch.randn((vocab, HIDDEN), generator=gen, device="cuda") * 0.02).to(torch.bfloat16)
+    ids = synth.zipf_ids(seqs, vocab, s=1.1, seed=0)
+    positions = rng.integers(0, capacity, seqs).astype(np.int32) if seqs > 1 else \
+        np.array([4097], np.int32)
+    host = synth.chain_inputs(seqs, HIDDEN, HQ, HKV, D, outliers=False, seed=0)
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).cuda()
+    states = np.zeros((seqs, 8), np.int32)
+    for i, p in enumerate(positions):
+        states[i] = [ids[i], p, capacity, 1 << 20, p, min(int(p), 1024), 0, 0]
+    st = torch.from_numpy(states).cuda()
+    rope = torch.from_numpy(ops.RopeTable(capacity, D, 1e6).view(torch.int16).numpy()).cuda()
+    kc = torch.empty((seqs * capacity, HKV * D), dtype=torch.int16, device="cuda")
+    vc = torch.empty_like(kc)
+    x = torch.empty((seqs, HIDDEN), dtype=torch.int16, device="cuda")
+    r, y = dev(host["residual"]), torch.empty_like(x)
+    q, k, v = dev(host["q"]), dev(host["k"]), dev(host["v"])
+    g, qn, kn = dev(host["gamma"]), dev(host["qn"]), dev(host["kn"])
+    bad = torch.zeros(1, dtype=torch.int32, device="cuda")
+    pos = ops.positions_decode(st, maximum=capacity, vocab=vocab)
+    kv = ops.kv_cache(abi.KV_BF16, kc, vc, capacity, seq_stride=capacity)
+    tbl = table.view(torch.int16)
+
+    def step(i):
+        ops.Embed(tbl, x, bad, positions=pos)
+        ops.ResidualNormQKRopeStore(x, r, y, g, q, k, v, qn, kn, rope, pos, kv, bad, tree=256)
+    ms = graph_time(torch, step, steps)
+    if bad.item():
+        raise SystemExit("device error flag set in the decode benchmark")
+    nbytes = seqs * (2 * 2 * HIDDEN + chain_bytes("bf16"))
+    return {"workload": f"{'config4' if seqs > 1 else 'config0'}: decode step of {seqs} "
+                        "sequence(s): gather + fused chain (256-thread tree), ragged positions",
+            "us_per_step": round(ms * 1e3, 3), "tokens_per_s": round(seqs / (ms * 1e-3), 1),
+            "bytes_per_step": nbytes, "gbs": round(nbytes / (ms * 1e-3) / 1e9, 2)}
+
+
+def cpu_decode_token(seconds=2.0):
+    """Config 0 on the host: the oracle's single-token decode chain (256-thread tree,
+    position 4097, capacity 8192), repeated for `seconds`."""
+    from oracle import oracle
+    from padra_amd import synth
+    host = synth.chain_inputs(1, HIDDEN, HQ, HKV, D, outliers=False, seed=0)
+    table = synth.bf16_bits(oracle.rope_table(4098, D, 1e6))
+    pos = np.array([4097], np.int32)
+    kc = np.zeros((8192, HKV * D), np.uint16)
+    vc = np.zeros_like(kc)
+    reps, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        oracle.residual_rmsnorm(host["x"], host["residual"], host["gamma"], 1e-6, 256)
+        _, k, _ = oracle.qk_norm_rope(host["q"], host["k"], host["qn"], host["kn"], table, pos)
+        oracle.kv_store_bf16(k, host["v"], kc, vc, pos, 8192)
+        reps += 1
+    el = time.perf_counter() - t0
+    return {"us_per_token": round(el / reps * 1e6, 3), "tokens_per_s": round(reps / el, 1),
+            "cores": 1, "kind": "port"}
+
 def main():
     if len(sys.argv) > 2 and sys.argv[1] == "--summarize":
         summarize(sys.argv[2], " ".join(sys.argv[3:]) or "(see profiles/README)")
@@ -243,8 +353,15 @@ def main():
                         "bytes_per_launch": r["bytes"],
                         "frac": round(r["gbs"] / HBM_PEAK_GBS, 4)} for f, r in results.items()},
     }
+    if not args.no_configs:
+        torch.cuda.empty_cache()
+        line["configs"] = {"config3": bench_swiglu(torch, 50),
+                           "config4": bench_decode(torch, 100, 64),
+                           "config0_gpu": bench_decode(torch, 200, 1, capacity=8192)}
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(host, args.cpu_seconds)
+        if not args.no_configs:
+            line["configs"]["config0_cpu"] = cpu_decode_token()
     print(json.dumps(line), flush=True)
 
 

@@ -10,7 +10,7 @@
 #include <type_traits>
 
 #include "norm_rows.h"
-#include "qk_heads.h"
+#include "qk_quad.h"
 
 using namespace padra;
 
@@ -221,9 +221,9 @@ template <class F> int with_format(const padra_KVCache *kv, F &&f) {
   return PADRA_INVALID_ARGUMENT;
 }
 
-// Q/K waves (32 head vectors each) plus, with a cache binding, the V-row waves.
-long long qk_waves(int tokens, int q_heads, int kv_heads, bool store) {
-  return ((long long)tokens * (q_heads + kv_heads * (store ? 2 : 1)) + 31) / 32;
+// Q/K waves plus, with a cache binding, the V-row waves (`per` head vectors per wave).
+long long qk_waves(int tokens, int q_heads, int kv_heads, bool store, int per) {
+  return ((long long)tokens * (q_heads + kv_heads * (store ? 2 : 1)) + per - 1) / per;
 }
 
 } // namespace
@@ -279,12 +279,13 @@ extern "C" int padra_QKNormRopeStore(void *stream, void *q, void *k, const void 
   if (st)
     return st;
   const hipStream_t s = static_cast<hipStream_t>(stream);
-  const long long grid = qk_waves(tokens, q_heads, kv_heads, kv != nullptr);
   auto launch = [&](auto tag) -> int {
     using T = decltype(tag);
     const QKArgs<T> a =
         make_qk<T>(q, k, v, qn, kn, table, table_rows, pos, tokens, q_heads, kv_heads, eps, kv, bad);
     return with_format(kv, [&](auto fmt) -> int {
+      const long long grid = qk_waves(tokens, q_heads, kv_heads, kv != nullptr,
+                                      qk_heads_per_wave<T, fmt.value>());
       hipLaunchKernelGGL((k_qk<T, fmt.value>), dim3((unsigned)grid), dim3(64), 0, s, a);
       return launched();
     });
@@ -320,11 +321,12 @@ extern "C" int padra_ResidualNormQKRopeStore(
   const QKArgs<uint16_t> a = make_qk<uint16_t>(q, k, v, qn, kn, table, table_rows, pos, tokens,
                                                q_heads, kv_heads, eps, kv, bad);
   const long long norm_waves = (tokens + rows_per_wave(tree) - 1) / rows_per_wave(tree);
-  const long long waves = norm_waves + qk_waves(tokens, q_heads, kv_heads, kv != nullptr);
   const int j = hidden / tree;
   if (!((tree == 128 && (j == 16 || j == 18)) || (tree == 256 && (j == 8 || j == 9))))
     return PADRA_UNSUPPORTED;
   return with_format(kv, [&](auto fmt) -> int {
+    const long long waves = norm_waves + qk_waves(tokens, q_heads, kv_heads, kv != nullptr,
+                                                  qk_heads_per_wave<uint16_t, fmt.value>());
     if (tree == 128 && j == 16)
       hipLaunchKernelGGL((k_chain<128, 16, fmt.value>), dim3((unsigned)waves), dim3(64), 0, s, n, a,
                          norm_waves, waves);

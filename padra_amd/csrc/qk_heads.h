@@ -694,12 +694,5 @@ __device__ __forceinline__ void qk_heads_wave_staged(const QKArgs<uint16_t> &a, 
   }
 }
 
-template <class T, int FMT>
-__device__ __forceinline__ void qk_heads_wave(const QKArgs<T> &a, long long wave) {
-  if constexpr (std::is_same<T, uint16_t>::value)
-    qk_heads_wave_staged<FMT>(a, wave);
-  else
-    qk_heads_wave_direct<T, FMT>(a, wave);
-}
 
 } // namespace padra
