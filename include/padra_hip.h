@@ -174,6 +174,13 @@ int padra_KVCommit(void *stream, const padra_KVCache *chunk, const padra_KVCache
  * negative / non-finite scale raises the flag. */
 int padra_KvQ8_0Dequantize(void *stream, const void *rows_k, const void *rows_v, void *out_k,
                            void *out_v, long long rows, int kv_heads, int *bad, int act);
+/* padra_KvQ8_0DequantizePrefix: q8_native::DequantizePrefix (kv_q8_native.cuh:391-413):
+ * decodes the ring's first min(prefill->base, cap) rows to BF16, the row count read on
+ * the device after ValidPrefillState (tokens = chunk rows) and the ring check (cap is the
+ * capacity or min(1024, capacity)).  out_k / out_v hold cap rows. */
+int padra_KvQ8_0DequantizePrefix(void *stream, const void *rows_k, const void *rows_v,
+                                 void *out_k, void *out_v, const padra_Positions *prefill,
+                                 int tokens, int cap, int kv_heads, int *bad);
 /* padra_RotateRows: q8_native::RotateRows (kv_q8_native.cuh:391-412): rotates `rows`
  * 128-wide rows in place with the K transform (value = 0) or the two 64-point V
  * transforms (value = 1), output rounded to BF16. */

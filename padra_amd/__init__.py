@@ -39,6 +39,7 @@ from .ops import (  # noqa: F401
     KVCommit,
     KVStore,
     KvQ8_0Dequantize,
+    KvQ8_0DequantizePrefix,
     ResidualNormQKRopeStore,
     ResidualPostNorm,
     QKNormRopeStore,

@@ -139,23 +139,38 @@ __device__ __forceinline__ void raise_bad(int *bad) {
     atomicExch(bad, 1);
 }
 
+// A 32-byte control record read as eight words issued together: the checks below then
+// work on registers, instead of one dependent load per field under short-circuit tests.
+template <class S> __device__ __forceinline__ S load_state(const S *p) {
+  static_assert(sizeof(S) == 32, "control records are 32 bytes");
+  const uint32_t *w = reinterpret_cast<const uint32_t *>(p);
+  uint32_t r[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    r[i] = w[i];
+  S s;
+  __builtin_memcpy(&s, r, sizeof(S));
+  return s;
+}
+
 // DecodeReadyAtLimit (context_admission.cuh:5-11) with the vocabulary bound a parameter.
-__device__ __forceinline__ bool decode_ready(const padra_DecodeState *s, int maximum, int vocab) {
-  return maximum > 0 && maximum <= 131072 && s && !s->stopped && !s->eos && s->remaining > 0 &&
-         s->token >= 0 && s->token < vocab && s->capacity > 0 && s->capacity <= maximum &&
-         s->position >= 0 && s->position < s->capacity && s->global_valid == s->position &&
-         s->local_valid == min(s->position, 1024);
+// Bitwise '&' keeps the test branch-free.
+__device__ __forceinline__ bool decode_ready(const padra_DecodeState &s, int maximum, int vocab) {
+  return (maximum > 0) & (maximum <= 131072) & !s.stopped & !s.eos & (s.remaining > 0) &
+         (s.token >= 0) & (s.token < vocab) & (s.capacity > 0) & (s.capacity <= maximum) &
+         (s.position >= 0) & (s.position < s.capacity) & (s.global_valid == s.position) &
+         (s.local_valid == min(s.position, 1024));
 }
 // ValidPrefillState (src/runtime/prefill_state.h:16-24).
 __device__ __forceinline__ bool prefill_valid(const padra_PrefillState &s, int active_tokens,
                                               int capacity, uint32_t binding_epoch,
                                               int maximum) {
-  return s.valid == 1 && s.binding_epoch == binding_epoch && s.request_epoch != 0 &&
-         maximum > 0 && maximum <= 131072 && s.capacity == capacity && capacity > 0 &&
-         capacity <= maximum && s.tokens == active_tokens && active_tokens > 0 &&
-         active_tokens <= 2048 && s.base >= 0 && s.base <= capacity - active_tokens &&
-         s.committed == s.base && s.prompt_offset >= 0 &&
-         s.prompt_offset <= capacity - active_tokens;
+  return (s.valid == 1) & (s.binding_epoch == binding_epoch) & (s.request_epoch != 0) &
+         (maximum > 0) & (maximum <= 131072) & (s.capacity == capacity) & (capacity > 0) &
+         (capacity <= maximum) & (s.tokens == active_tokens) & (active_tokens > 0) &
+         (active_tokens <= 2048) & (s.base >= 0) & (s.base <= capacity - active_tokens) &
+         (s.committed == s.base) & (s.prompt_offset >= 0) &
+         (s.prompt_offset <= capacity - active_tokens);
 }
 
 // Position source passed by value to kernels.
@@ -166,36 +181,58 @@ struct PosSrc {
   const padra_DecodeState *decode;
 };
 
+// The control record token t's position depends on (PADRA_POS_PREFILL: the chunk's
+// PrefillState; PADRA_POS_DECODE: sequence t's DecodeState).  Fetched apart from
+// resolve_position so that a kernel can put the load in flight before its data loads.
+union PosState {
+  padra_PrefillState prefill;
+  padra_DecodeState decode;
+};
+__device__ __forceinline__ PosState fetch_state(const PosSrc &p, int t) {
+  PosState s;
+  if (p.mode == PADRA_POS_PREFILL)
+    s.prefill = load_state(p.prefill);
+  else if (p.mode == PADRA_POS_DECODE)
+    s.decode = load_state(p.decode + t);
+  else
+    s.prefill = padra_PrefillState{};
+  return s;
+}
+
 // Resolves token t's absolute position; `ok` false means the unit must write nothing
 // and the caller raises the flag.  With a cache binding (cap > 0) the state must admit
 // the ring: cap <= capacity (StorePrefillControlled prefill_control.cuh:27-29,
 // QKNormRopeStoreControlled qk_rope_store_exact.cuh:8), and for the quantized formats
 // (`ring_exact`) cap is the capacity or the 1024-row local ring and `first` is the
 // chunk rows that do not fit (kv_q8.cuh:36-38, 80-82; kv_q8_native.cuh:447-450).
-__device__ __forceinline__ int resolve_position(const PosSrc &p, int t, int cap, int first,
-                                                bool ring_exact, bool &ok) {
+__device__ __forceinline__ int resolve_position(const PosSrc &p, const PosState &st, int t,
+                                                int cap, int first, bool ring_exact, bool &ok) {
   ok = true;
   if (p.mode == PADRA_POS_BASE)
     return p.base + t;
   if (p.mode == PADRA_POS_PREFILL) {
-    const padra_PrefillState s = *p.prefill;
+    const padra_PrefillState &s = st.prefill;
     ok = prefill_valid(s, p.tokens, s.capacity, p.epoch, p.maximum);
     if (cap > 0) {
-      ok = ok && cap <= s.capacity;
+      ok = ok & (cap <= s.capacity);
       if (ring_exact)
         ok = ok && (cap == s.capacity || cap == min(1024, s.capacity)) &&
              first == (cap == s.capacity ? 0 : max(0, p.tokens - cap));
     }
     return s.base + t;
   }
-  const padra_DecodeState *s = p.decode + t;
+  const padra_DecodeState &s = st.decode;
   ok = decode_ready(s, p.maximum, p.vocab);
-  if (ok && cap > 0) {
-    ok = cap <= s->capacity;
+  if (cap > 0) {
+    ok = ok & (cap <= s.capacity);
     if (ring_exact)
-      ok = ok && (cap == s->capacity || cap == min(1024, s->capacity));
+      ok = ok & ((cap == s.capacity) | (cap == min(1024, s.capacity)));
   }
-  return ok ? s->position : 0;
+  return ok ? s.position : 0;
+}
+__device__ __forceinline__ int resolve_position(const PosSrc &p, int t, int cap, int first,
+                                                bool ring_exact, bool &ok) {
+  return resolve_position(p, fetch_state(p, t), t, cap, first, ring_exact, ok);
 }
 
 } // namespace padra

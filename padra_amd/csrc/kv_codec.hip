@@ -70,11 +70,12 @@ __global__ __launch_bounds__(64) void k_kv_store(QKArgs<T> a) {
   const unsigned idx = isv ? hv - nk : hv;
   const int t = (int)(idx / (unsigned)a.hkv), h = (int)(idx % (unsigned)a.hkv);
   const T *src = (isv ? a.v : a.k) + (size_t)idx * D;
+  const PosState ps = fetch_state(a.pos, t);
   Act32<T> xa, xb;
   xa.load(src + 32 * half);
   xb.load(src + 64 + 32 * half);
   bool ok;
-  const int pos = resolve_position(a.pos, t, a.cap, a.first, FMT > PADRA_KV_BF16, ok);
+  const int pos = resolve_position(a.pos, ps, t, a.cap, a.first, FMT > PADRA_KV_BF16, ok);
   if (!ok || pos < 0) {
     if (half == 0)
       raise_bad(a.bad);
@@ -156,8 +157,21 @@ __global__ __launch_bounds__(64) void k_kv_commit(CommitArgs a) {
 template <class O>
 __global__ __launch_bounds__(256) void k_q8_0_dequant(const uint8_t *rk, const uint8_t *rv,
                                                       O *ok_out, O *ov_out, long long rows,
-                                                      int features, int *bad) {
+                                                      int features, int *bad,
+                                                      PosSrc prefix, int cap) {
   const int nd = features / 32, rb = ((2 * nd + features) + 15) / 16 * 16;
+  if (prefix.prefill) {
+    // q8_native::DequantizePrefix (kv_q8_native.cuh:391-413): the ring's valid rows,
+    // min(base, cap), after ValidPrefillState and the ring-capacity check.
+    const padra_PrefillState st = load_state(prefix.prefill);
+    if (!prefill_valid(st, prefix.tokens, st.capacity, prefix.epoch, prefix.maximum) ||
+        (cap != st.capacity && cap != min(1024, st.capacity))) {
+      if (blockIdx.x == 0 && threadIdx.x == 0)
+        raise_bad(bad);
+      return;
+    }
+    rows = min(st.base, cap);
+  }
   const long long groups = rows * (features / 8); // 8 codes per thread-step
   for (long long g = blockIdx.x * (long long)blockDim.x + threadIdx.x; g < 2 * groups;
        g += (long long)gridDim.x * blockDim.x) {
@@ -361,17 +375,38 @@ extern "C" int padra_KvQ8_0Dequantize(void *stream, const void *rows_k, const vo
   const long long work = 2 * rows * (features / 8);
   const unsigned grid = (unsigned)std::min<long long>((work + 255) / 256, 4096);
   const hipStream_t s = static_cast<hipStream_t>(stream);
+  const PosSrc none{};
   if (act == PADRA_ACT_BF16)
     hipLaunchKernelGGL((k_q8_0_dequant<uint16_t>), dim3(grid), dim3(256), 0, s,
                        static_cast<const uint8_t *>(rows_k), static_cast<const uint8_t *>(rows_v),
                        static_cast<uint16_t *>(out_k), static_cast<uint16_t *>(out_v), rows,
-                       features, bad);
+                       features, bad, none, 0);
   else
     hipLaunchKernelGGL((k_q8_0_dequant<float>), dim3(grid), dim3(256), 0, s,
                        static_cast<const uint8_t *>(rows_k), static_cast<const uint8_t *>(rows_v),
                        static_cast<float *>(out_k), static_cast<float *>(out_v), rows, features,
-                       bad);
+                       bad, none, 0);
   return launched("KvQ8_0Dequantize");
+}
+
+extern "C" int padra_KvQ8_0DequantizePrefix(void *stream, const void *rows_k, const void *rows_v,
+                                            void *out_k, void *out_v,
+                                            const padra_Positions *prefill, int tokens, int cap,
+                                            int kv_heads, int *bad) {
+  if (!rows_k || !rows_v || !out_k || !out_v || !bad || !prefill ||
+      prefill->mode != PADRA_POS_PREFILL || !prefill->prefill || tokens < 1 || tokens > 2048 ||
+      cap < 1 || cap > 131072 || kv_heads < 1 || !aligned16(rows_k) || !aligned16(rows_v) ||
+      !aligned16(out_k) || !aligned16(out_v))
+    return PADRA_INVALID_ARGUMENT;
+  const int features = kv_heads * 128;
+  const long long work = 2ll * cap * (features / 8);
+  const unsigned grid = (unsigned)std::min<long long>((work + 255) / 256, 4096);
+  hipLaunchKernelGGL((k_q8_0_dequant<uint16_t>), dim3(grid), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const uint8_t *>(rows_k),
+                     static_cast<const uint8_t *>(rows_v), static_cast<uint16_t *>(out_k),
+                     static_cast<uint16_t *>(out_v), (long long)cap, features, bad,
+                     pos_src(*prefill, tokens), cap);
+  return launched("KvQ8_0DequantizePrefix");
 }
 
 extern "C" int padra_RotateRows(void *stream, void *data, long long rows, int value, int *bad,

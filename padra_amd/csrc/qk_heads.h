@@ -481,9 +481,11 @@ __device__ __forceinline__ void v_rows_copy(const A &a, unsigned block0, unsigne
   const int features = a.hkv * D;
   // Loads first (clamped, unconditional), so that all eight are in flight together.
   uint4 d[8];
+  PosState ps[8];
 #pragma unroll
   for (int m = 0; m < 8; ++m) {
     const unsigned idx = min(block0 + (unsigned)((64 * m + lane) >> 4) - nq - nk, nk - 1u);
+    ps[m] = fetch_state(a.pos, (int)(idx / (unsigned)a.hkv));
     d[m] = ld_nt(reinterpret_cast<const uint4 *>(a.v + (size_t)idx * D) + ((64 * m + lane) & 15));
   }
 #pragma unroll
@@ -494,7 +496,7 @@ __device__ __forceinline__ void v_rows_copy(const A &a, unsigned block0, unsigne
       continue;
     const int t = (int)(idx / (unsigned)a.hkv), h = (int)(idx % (unsigned)a.hkv), ci = c & 15;
     bool ok;
-    const int pos = resolve_position(a.pos, t, a.cap, a.first, false, ok);
+    const int pos = resolve_position(a.pos, ps[m], t, a.cap, a.first, false, ok);
     if (!ok || pos < 0 || pos >= a.table_rows) {
       if (ci == 0)
         raise_bad(a.bad);
@@ -525,6 +527,15 @@ __device__ __forceinline__ void qk_heads_wave_staged(const QKArgs<uint16_t> &a, 
     }
   }
 
+  // This lane pair's head vector; its control record is requested first.
+  const unsigned hv = block0 + (unsigned)(lane >> 1);
+  const bool live = hv < total;
+  const int role = hv < nq ? 0 : (hv < nq + nk ? 1 : 2); // 0 q, 1 k, 2 v
+  const unsigned idx = role == 0 ? hv : (role == 1 ? hv - nq : hv - nq - nk);
+  const unsigned heads = role == 0 ? (unsigned)a.hq : (unsigned)a.hkv;
+  const int t = live ? (int)(idx / heads) : 0, h = (int)(idx % heads);
+  const PosState ps = fetch_state(a.pos, t);
+
   // 1. The block's chunks, eight coalesced loads per lane, into the LDS image.  The loads
   // are unconditional (chunks past the end re-read the last head) so that all eight are in
   // flight before the first is waited for.
@@ -541,18 +552,10 @@ __device__ __forceinline__ void qk_heads_wave_staged(const QKArgs<uint16_t> &a, 
     stage[chunk_slot(c >> 4, c & 15)] = in[m];
   }
 
-  // 2. This lane pair's head vector.
-  const unsigned hv = block0 + (unsigned)(lane >> 1);
-  const bool live = hv < total;
-  const int role = hv < nq ? 0 : (hv < nq + nk ? 1 : 2); // 0 q, 1 k, 2 v
-  const unsigned idx = role == 0 ? hv : (role == 1 ? hv - nq : hv - nq - nk);
-  const unsigned heads = role == 0 ? (unsigned)a.hq : (unsigned)a.hkv;
-  const int t = (int)(idx / heads), h = (int)(idx % heads);
+  // 2. The head's position.
   bool ok = false;
-  int pos = 0;
-  if (live)
-    pos = resolve_position(a.pos, t, FMT >= 0 ? a.cap : 0, a.first, FMT > PADRA_KV_BF16, ok);
-  ok = ok && pos >= 0 && pos < a.table_rows;
+  int pos = resolve_position(a.pos, ps, t, FMT >= 0 ? a.cap : 0, a.first, FMT > PADRA_KV_BF16, ok);
+  ok = ok && live && pos >= 0 && pos < a.table_rows;
   if (live && !ok && half == 0)
     raise_bad(a.bad);
   // The head's norm weights and table row come in four pieces of eight pairs; piece 0 is

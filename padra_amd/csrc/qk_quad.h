@@ -42,9 +42,11 @@ __device__ __forceinline__ void v_rows_copy16(const A &a, unsigned block0, unsig
   constexpr int D = 128;
   const int lane = threadIdx.x & 63, features = a.hkv * D;
   uint4 d[4];
+  PosState ps[4];
 #pragma unroll
   for (int m = 0; m < 4; ++m) {
     const unsigned idx = min(block0 + (unsigned)((64 * m + lane) >> 4) - nq - nk, nk - 1u);
+    ps[m] = fetch_state(a.pos, (int)(idx / (unsigned)a.hkv));
     d[m] = ld_nt(reinterpret_cast<const uint4 *>(a.v + (size_t)idx * D) + ((64 * m + lane) & 15));
   }
 #pragma unroll
@@ -55,7 +57,7 @@ __device__ __forceinline__ void v_rows_copy16(const A &a, unsigned block0, unsig
       continue;
     const int t = (int)(idx / (unsigned)a.hkv), h = (int)(idx % (unsigned)a.hkv), ci = c & 15;
     bool ok;
-    const int pos = resolve_position(a.pos, t, a.cap, a.first, false, ok);
+    const int pos = resolve_position(a.pos, ps[m], t, a.cap, a.first, false, ok);
     if (!ok || pos < 0 || pos >= a.table_rows) {
       if (ci == 0)
         raise_bad(a.bad);
@@ -87,6 +89,15 @@ __device__ __forceinline__ void qk_heads_wave_quad(const QKArgs<uint16_t> &a, lo
     }
   }
 
+  // This lane's head and warp group; its control record is requested first.
+  const unsigned hv = block0 + (unsigned)(lane >> 2);
+  const bool live = hv < total;
+  const int role = hv < nq ? 0 : (hv < nq + nk ? 1 : 2); // 0 q, 1 k, 2 v
+  const unsigned idx = role == 0 ? hv : (role == 1 ? hv - nq : hv - nq - nk);
+  const unsigned heads = role == 0 ? (unsigned)a.hq : (unsigned)a.hkv;
+  const int t = live ? (int)(idx / heads) : 0;
+  const PosState ps = fetch_state(a.pos, t);
+
   // 1. Four coalesced loads per lane (clamped, unconditional), into the LDS image.
   uint4 in[4];
 #pragma unroll
@@ -101,18 +112,10 @@ __device__ __forceinline__ void qk_heads_wave_quad(const QKArgs<uint16_t> &a, lo
     stage[quad_slot(4 * (c >> 4) + ((c & 15) >> 2), c & 3)] = in[m];
   }
 
-  // 2. This lane's head and warp group.
-  const unsigned hv = block0 + (unsigned)(lane >> 2);
-  const bool live = hv < total;
-  const int role = hv < nq ? 0 : (hv < nq + nk ? 1 : 2); // 0 q, 1 k, 2 v
-  const unsigned idx = role == 0 ? hv : (role == 1 ? hv - nq : hv - nq - nk);
-  const unsigned heads = role == 0 ? (unsigned)a.hq : (unsigned)a.hkv;
-  const int t = (int)(idx / heads);
+  // 2. The head's position.
   bool ok = false;
-  int pos = 0;
-  if (live)
-    pos = resolve_position(a.pos, t, FMT >= 0 ? a.cap : 0, a.first, false, ok);
-  ok = ok && pos >= 0 && pos < a.table_rows;
+  int pos = resolve_position(a.pos, ps, t, FMT >= 0 ? a.cap : 0, a.first, false, ok);
+  ok = ok && live && pos >= 0 && pos < a.table_rows;
   if (live && !ok && g == 0)
     raise_bad(a.bad);
   // Norm weights of the group and the table entries of its pair index (f mod 64).

@@ -110,13 +110,13 @@ __global__ __launch_bounds__(64) void k_embed(const uint16_t *table, const int32
   if (src.mode == PADRA_POS_BASE) {
     token = ids[t];
   } else if (src.mode == PADRA_POS_PREFILL) {
-    const padra_PrefillState s = *src.prefill;
+    const padra_PrefillState s = load_state(src.prefill);
     ok = prefill_valid(s, src.tokens, s.capacity, src.epoch, src.maximum);
     token = ok ? ids[s.prompt_offset + t] : -1;
   } else {
-    const padra_DecodeState *s = src.decode + t;
+    const padra_DecodeState s = load_state(src.decode + t);
     ok = decode_ready(s, src.maximum, src.vocab);
-    token = ok ? s->token : -1;
+    token = ok ? s.token : -1;
   }
   if (!ok || token < 0 || token >= vocab) {
     if (lane == 0)

@@ -170,6 +170,15 @@ def KvQ8_0Dequantize(rows_k, rows_v, out_k, out_v, bad, kv_heads=4):
              _p(out_v), rows_k.shape[0], int(kv_heads), _p(bad), _act(out_k))
 
 
+def KvQ8_0DequantizePrefix(rows_k, rows_v, out_k, out_v, positions: abi.Positions, tokens, bad,
+                           kv_heads=4):
+    """Decode the ring's first min(base, cap) rows (cap = rows_k.shape[0]) to BF16."""
+    _need_cuda(rows_k, rows_v, out_k, out_v, bad)
+    abi.call("padra_KvQ8_0DequantizePrefix", _stream(out_k), _p(rows_k), _p(rows_v), _p(out_k),
+             _p(out_v), ctypes.byref(positions), int(tokens), rows_k.shape[0], int(kv_heads),
+             _p(bad))
+
+
 def RotateRows(data, bad, value=False):
     """In-place Hadamard rotation of 128-wide rows (K transform, or V with value=True)."""
     _need_cuda(data, bad)

@@ -152,6 +152,34 @@ def test_q8_0_dequantize(oracle, act):
     assert bad.item() == 1
 
 
+def test_q8_0_dequantize_prefix(oracle):
+    """Ring of 64 rows, PrefillState base 40: rows 0..39 decoded, the rest untouched; an
+    invalid state writes nothing."""
+    cap, base = 64, 40
+    d = synth.chain_inputs(cap, seed=61)
+    rk = np.zeros((cap, 544), np.uint8)
+    rv = np.zeros((cap, 544), np.uint8)
+    oracle.kv_q8_0_encode(d["k"], d["v"], rk, rv, np.arange(cap, dtype=np.int32), cap)
+    wk, wv, _ = oracle.kv_q8_0_dequantize(rk, rv, cap, 512)
+    ok = torch.full((cap, 512), 7, dtype=torch.int16, device="cuda")
+    ov = torch.full((cap, 512), 7, dtype=torch.int16, device="cuda")
+    state = torch.tensor([base, base, 8, cap, base, 1, 1, 1], dtype=torch.int32, device="cuda")
+    bad = flag()
+    ops.KvQ8_0DequantizePrefix(dev(rk), dev(rv), ok, ov, ops.positions_prefill(state, maximum=cap),
+                               8, bad)
+    torch.cuda.synchronize()
+    assert bad.item() == 0
+    assert np.array_equal(host16(ok)[:base], wk[:base]) and np.array_equal(host16(ov)[:base], wv[:base])
+    assert np.all(host16(ok)[base:] == 7)
+    bad_state = torch.tensor([base, base, 8, cap, base + 1, 1, 1, 1], dtype=torch.int32,
+                             device="cuda")
+    ok.fill_(7)
+    ops.KvQ8_0DequantizePrefix(dev(rk), dev(rv), ok, ov,
+                               ops.positions_prefill(bad_state, maximum=cap), 8, bad)
+    torch.cuda.synchronize()
+    assert bad.item() == 1 and np.all(host16(ok) == 7)
+
+
 @pytest.mark.parametrize("value", [False, True])
 def test_rotate_rows(oracle, value):
     rows = 96

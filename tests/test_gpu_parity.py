@@ -346,3 +346,37 @@ def test_config1_full_chunk(oracle):
     assert np.array_equal(host16(kc[:tokens]), wk.reshape(tokens, -1))
     assert np.array_equal(host16(vc[:tokens]), d["v"].reshape(tokens, -1))
     assert not kc[tokens:].any().item()
+
+
+@pytest.mark.parametrize("fmt", FORMATS)
+@pytest.mark.parametrize("tree", [128, 256])
+def test_reference_geometry_chain(oracle, fmt, tree):
+    """The reference model's own shapes: hidden 2304, 32 Q heads, 4 KV heads
+    (inference.cu:184-186, qk_rope_store_exact.cuh:23-26), ragged token count."""
+    print(f"[case] reference geometry fmt={fmt} tree={tree}", flush=True)
+    tokens, capacity, hidden, hq = 97, 2048, 2304, 32
+    d = synth.chain_inputs(tokens, hidden=hidden, q_heads=hq, outliers=True, seed=70 + fmt)
+    tb = table_bits(oracle, capacity, theta=5e5)
+    positions = np.arange(tokens, dtype=np.int32) + 1000
+    wx, wy, wst, _ = oracle.residual_rmsnorm(d["x"], d["residual"], d["gamma"], threads=tree)
+    wq, wk, _ = _qk_oracle(oracle, d, tb, positions)
+    ek, ev, es = _expected_cache(oracle, fmt, wk, d["v"], positions, capacity, 0)
+    x, r, g = dev(d["x"]), dev(d["residual"]), dev(d["gamma"])
+    y = torch.empty_like(x)
+    st = torch.empty((tokens, 2), dtype=torch.float32, device="cuda")
+    q, k = dev(d["q"]), dev(d["k"])
+    kc, vc, sc = _alloc_cache(fmt, capacity)
+    state = _prefill_state(1000, tokens, capacity)
+    bad = flag()
+    ops.ResidualNormQKRopeStore(x, r, y, g, q, k, dev(d["v"]), dev(d["qn"]), dev(d["kn"]),
+                                dev(tb), ops.positions_prefill(state, maximum=capacity),
+                                ops.kv_cache(fmt, kc, vc, capacity, scales=sc), bad, tree=tree,
+                                statistics=st)
+    torch.cuda.synchronize()
+    assert not bad.item()
+    assert np.array_equal(host16(x), wx) and np.array_equal(host16(y), wy)
+    assert np.array_equal(st.cpu().numpy(), wst)
+    assert np.array_equal(host16(q), wq) and np.array_equal(host16(k), wk)
+    assert np.array_equal(_np(kc, fmt), ek) and np.array_equal(_np(vc, fmt), ev)
+    if es is not None:
+        assert np.array_equal(sc.cpu().numpy(), es)
