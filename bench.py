@@ -365,6 +365,9 @@ def main():
     print(json.dumps(line), flush=True)
 
 
+CHAIN_KERNEL = "k_chain<128, 16, 0>"  # the config-1 instantiation (tree 128, H 2048, BF16 KV)
+
+
 def summarize(outdir: str, command: str) -> None:
     """Digests rocprofv3 CSV output of this script into profiles/ (text only):
     <outdir>/trace/bench_kernel_stats.csv (--kernel-trace --stats) and
@@ -387,7 +390,7 @@ def summarize(outdir: str, command: str) -> None:
             short = name.replace("void ", "").replace("(anonymous namespace)::", "").split("(")[0]
             lines.append(f"| `{short[:70]}` | {r['Calls']} | {float(r['AverageNs'])/1e3:.2f} | "
                          f"{float(r['MinNs'])/1e3:.2f} | {float(r['MaxNs'])/1e3:.2f} |")
-            if "k_chain" in name and chain_ns is None:
+            if CHAIN_KERNEL in name and chain_ns is None:
                 chain_ns = float(r["AverageNs"])
         lines.append("")
     traffic = {}
@@ -399,9 +402,9 @@ def summarize(outdir: str, command: str) -> None:
         for r in csv.DictReader(open(path)):
             if r["Counter_Name"] != counter:
                 continue
-            if "k_chain" in r["Kernel_Name"]:
+            if CHAIN_KERNEL in r["Kernel_Name"]:
                 chain.append(float(r["Counter_Value"]))
-            elif "copyBuffer" in r["Kernel_Name"] or "copy" in r["Kernel_Name"].lower():
+            elif "copyBuffer" in r["Kernel_Name"]:
                 copy.append(float(r["Counter_Value"]))
         if chain and copy:
             copy_bytes = COPY_BYTES // 2  # read (FETCH) or written (WRITE) per copy

@@ -2,9 +2,10 @@
 // residual-norm, Q/K-norm + RoPE + KV-store and fused chain paths.
 //
 // Launch geometry: one 64-lane wavefront per workgroup.  A residual-norm wave covers one
-// row; a Q/K wave covers 32 head vectors (two lanes per head).  Every wave streams its inputs with 16-byte loads issued
-// before any arithmetic, and there is no inter-wave communication, so the grid is a
-// flat list of independent waves (thousands for a 2048-token chunk: >> 256 CUs).
+// row; a Q/K wave covers 16 head vectors (BF16, four lanes each) or 32 (fp32 activations
+// and the quantized caches, two lanes each).  Every wave issues its loads before any
+// arithmetic, and there is no inter-wave communication, so the grid is a flat list of
+// independent waves (thousands for a 2048-token chunk: >> 256 CUs).
 #include <stdio.h>
 
 #include <type_traits>
@@ -39,17 +40,18 @@ template <class T, int FMT> __global__ __launch_bounds__(64) PADRA_WAVES_PER_EU 
   qk_heads_wave<T, FMT>(a, blockIdx.x);
 }
 
-// Residual-norm waves and Q/K waves interleaved evenly over the grid, so every CU gets
-// the same mix of the (VALU-heavier) norm rows and the (store-heavier) head vectors.
+// Residual-norm waves first, then the Q/K waves.  Measured on MI355X for a 2048-token
+// chunk, this order is 10% faster than spreading the norm rows evenly over the grid
+// (Bresenham interleave) or over its first half: the early grid streams the four norm
+// tensors alone, and the VALU-heavier Q/K waves follow as norm waves retire.
 template <int VT, int J, int FMT>
 __global__ __launch_bounds__(64) PADRA_WAVES_PER_EU void k_chain(NormArgs<uint16_t> n, QKArgs<uint16_t> q,
                                               long long norm_waves, long long waves) {
   const long long b = blockIdx.x;
-  const long long n0 = b * norm_waves / waves, n1 = (b + 1) * norm_waves / waves;
-  if (n1 > n0)
-    norm_row_wave<VT, J, uint16_t, true>(n, (int)n0);
-  else
-    qk_heads_wave<uint16_t, FMT>(q, b - n1);
+  if (b < norm_waves)
+    norm_row_wave<VT, J, uint16_t, true>(n, (int)b);
+  else if (b < waves)
+    qk_heads_wave<uint16_t, FMT>(q, b - norm_waves);
 }
 
 // Launch tuning (padra_Tune): waves per CU for the pipelined row kernel, 0 = one wave

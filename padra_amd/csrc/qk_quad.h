@@ -18,14 +18,15 @@ namespace padra {
 
 // DPP quad permutations: the value of lane (lane ^ 2), of lane (lane ^ 1), and of lane
 // (lane & ~3) (the first lane of the quad).
+// Every lane of a quad permutation has a source, so no old value is needed (bound_ctrl).
 __device__ __forceinline__ uint32_t quad_xor2(uint32_t v) {
-  return __builtin_amdgcn_update_dpp(0, (int)v, 0x4e /* quad_perm [2,3,0,1] */, 0xf, 0xf, false);
+  return __builtin_amdgcn_mov_dpp((int)v, 0x4e /* quad_perm [2,3,0,1] */, 0xf, 0xf, true);
 }
 __device__ __forceinline__ uint32_t quad_xor1(uint32_t v) {
-  return __builtin_amdgcn_update_dpp(0, (int)v, 0xb1 /* quad_perm [1,0,3,2] */, 0xf, 0xf, false);
+  return __builtin_amdgcn_mov_dpp((int)v, 0xb1 /* quad_perm [1,0,3,2] */, 0xf, 0xf, true);
 }
 __device__ __forceinline__ uint32_t quad_first(uint32_t v) {
-  return __builtin_amdgcn_update_dpp(0, (int)v, 0x00 /* quad_perm [0,0,0,0] */, 0xf, 0xf, false);
+  return __builtin_amdgcn_mov_dpp((int)v, 0x00 /* quad_perm [0,0,0,0] */, 0xf, 0xf, true);
 }
 __device__ __forceinline__ float fquad_xor2(float v) { return __uint_as_float(quad_xor2(__float_as_uint(v))); }
 __device__ __forceinline__ float fquad_xor1(float v) { return __uint_as_float(quad_xor1(__float_as_uint(v))); }
@@ -157,16 +158,17 @@ __device__ __forceinline__ void qk_heads_wave_quad(const QKArgs<uint16_t> &a, lo
     }
     // Partner group (features f +- 64): lower lanes rotate lo = A c - P s, upper lanes
     // hi = A c + P s (c, s of the pair index).
-    const float sgn = g < 2 ? -1.f : 1.f;
+    // B(-P s) = -B(P s): the lower lanes flip the partner's sign bits.
+    const uint32_t sgn = g < 2 ? 0x80008000u : 0u;
     bool fine = isfinite(sum);
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      const uint32_t pw = quad_xor2(an[i]);
+      const uint32_t pw = quad_xor2(an[i]) ^ sgn;
       const int k0 = 2 * i, k1 = 2 * i + 1;
       const float c0 = c8[k0 / 8].get(k0 & 7), c1 = c8[k1 / 8].get(k1 & 7);
       const float s0 = s8[k0 / 8].get(k0 & 7), s1 = s8[k1 / 8].get(k1 & 7);
       const uint32_t p3 = pack2(lo16(an[i]) * c0, hi16(an[i]) * c1);
-      const uint32_t p4 = pack2((sgn * lo16(pw)) * s0, (sgn * hi16(pw)) * s1);
+      const uint32_t p4 = pack2(lo16(pw) * s0, hi16(pw) * s1);
       const float r0 = lo16(p3) + lo16(p4), r1 = hi16(p3) + hi16(p4);
       fine = fine && bf16_finite_after_round(r0) && bf16_finite_after_round(r1);
       out[i] = pack2(r0, r1);
