@@ -114,6 +114,18 @@ int padra_ResidualPostNorm(void *stream, void *x, const void *residual, void *no
                            const uint16_t *gamma, int rows, int hidden, float eps, int tree,
                            float *statistics, int *bad, int act);
 
+/* padra_NormFP8: NormFP8Exact (norm_fp8_exact.cuh:6-62) and NormFP8WideExact
+ * (norm_fp8_wide_exact.cuh:7-67), which give the same bytes: the 128-thread RMSNorm of each
+ * row of x [rows][hidden] into normalized, plus its E4M3 encoding packed [rows][hidden]
+ * (u8) with scales[row] = max|y|/448 (1 for an all-zero row), codes through
+ * fp8_exact_reciprocal::Encode (fp8_exact_reciprocal.cuh:12-21).  statistics (2 floats,
+ * may be NULL) receives {variance, inv} of row 0 only, as the reference writes it.  A
+ * non-finite normalized value raises *bad; the row is still written.  hidden is a multiple
+ * of 128 in {1024, 1152, 2048, 2304, 4096, 4608}; x, normalized, gamma and packed are
+ * 16-byte aligned.  act: PADRA_ACT_BF16 or PADRA_ACT_F32 for x and normalized. */
+int padra_NormFP8(void *stream, const void *x, void *normalized, const uint16_t *gamma,
+                  uint8_t *packed, float *scales, int rows, int hidden, float eps,
+                  float *statistics, int *bad, int act);
 /* ---- RoPE table (host) --------------------------------------------------------------
  * Replaces RopeTable (inference.cu:764-785): fills the HOST buffer table[positions][D]
  * with BF16 bit patterns of cos (first D/2) and sin (last D/2), theta a parameter;

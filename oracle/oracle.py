@@ -36,6 +36,10 @@ def lib() -> ctypes.CDLL:
             "po_sumsq_tree": ([P, I, I], F),
             "po_residual_rmsnorm": ([P, P, P, P, I, I, F, I, P, P], None),
             "po_rmsnorm": ([P, P, P, I, I, F, I, P, P], None),
+            "po_e4m3": ([F], ctypes.c_uint8),
+            "po_fp8_needs_division": ([ctypes.c_uint32], I),
+            "po_fp8_encode": ([F, F, F], ctypes.c_uint8),
+            "po_norm_fp8": ([P, P, P, P, P, I, I, F, P, P], None),
             "po_rope_table": ([P, I, I, F, I, F, I], None),
             "po_qk_norm_rope": ([P, P, P, P, P, P, I, I, I, I, F, P], None),
             "po_kv_store_bf16": ([P, P, P, P, P, I, I, I, I], None),
@@ -99,6 +103,25 @@ def rmsnorm(x, gamma, eps=1e-6, threads=128):
     lib().po_rmsnorm(_p(x), _p(y), _p(np.ascontiguousarray(gamma, np.uint16)), rows, hidden,
                      eps, threads, _p(stats), bad.ptr)
     return y, stats, bool(bad)
+
+
+def norm_fp8(x, gamma, eps=1e-6):
+    """Returns (normalized, packed u8, scales [rows], stats [2] of row 0, bad)."""
+    x = np.ascontiguousarray(x, np.uint16)
+    rows, hidden = x.shape
+    y = np.empty_like(x)
+    packed = np.empty((rows, hidden), np.uint8)
+    scales = np.empty(rows, np.float32)
+    stats = np.empty(2, np.float32)
+    bad = Bad()
+    lib().po_norm_fp8(_p(x), _p(y), _p(np.ascontiguousarray(gamma, np.uint16)), _p(packed),
+                      _p(scales), rows, hidden, eps, _p(stats), bad.ptr)
+    return y, packed, scales, stats, bool(bad)
+
+
+def e4m3(values) -> np.ndarray:
+    f = lib().po_e4m3
+    return np.array([f(float(v)) for v in np.asarray(values, np.float32)], np.uint8)
 
 
 def rope_table(positions, head_dim=128, theta=1e6, yarn=False, factor=16.0,

@@ -199,6 +199,85 @@ void po_rmsnorm(const uint16_t *x, uint16_t *y, const uint16_t *gamma, int rows,
   }
 }
 
+/* ---- A3 FP8 E4M3 row encoding ---------------------------------------------------- */
+
+/* E4M3 per the OCP 8-bit floating point specification: normals 2^-6 .. 448 with three
+ * mantissa bits, subnormals k * 2^-9.  Written from the format definition. */
+uint8_t po_e4m3(float x) {
+  uint32_t bits;
+  memcpy(&bits, &x, 4);
+  const uint8_t sign = (uint8_t)((bits >> 24) & 0x80u);
+  const uint32_t mag = bits & 0x7fffffffu;
+  if (mag > 0x7f800000u)
+    return 0x7f; /* one NaN code whatever the input NaN's sign and payload */
+  float a;
+  memcpy(&a, &mag, 4);
+  if (a >= 448.f)
+    return (uint8_t)(sign | 0x7e);
+  if (a < 0.015625f) /* 2^-6: subnormal codes k = RNE(a * 2^9), k = 8 is the least normal */
+    return (uint8_t)(sign | (uint8_t)rintf(a * 512.f));
+  /* normal: keep 3 of 23 mantissa bits, ties to even; a carry moves into the exponent */
+  const uint32_t rounded = mag + 0x7ffffu + ((mag >> 20) & 1u);
+  const uint32_t code = (rounded >> 20) - ((127u - 7u) << 3);
+  return (uint8_t)(sign | (code > 0x7eu ? 0x7eu : code));
+}
+
+/* fp8_exact_reciprocal.cuh:5-11 */
+int po_fp8_needs_division(uint32_t b) {
+  if (b < 0x3a800000u)
+    return b >= 0x3a800000u - 4u;
+  const uint32_t e = b >> 23, shift = e < 121u ? 140u - e : 19u;
+  const uint32_t residue = b & ((1u << (shift + 1)) - 1u), midpoint = 1u << shift;
+  return residue >= midpoint - 4u && residue <= midpoint + 4u;
+}
+
+/* fp8_exact_reciprocal.cuh:12-21 */
+uint8_t po_fp8_encode(float value, float scale, float inverse) {
+  uint32_t ib;
+  memcpy(&ib, &inverse, 4);
+  ib &= 0x7fffffffu;
+  if ((ib & 0x7f800000u) == 0 || (ib & 0x7f800000u) == 0x7f800000u)
+    return po_e4m3(value / scale);
+  float q = value * inverse;
+  uint32_t b;
+  memcpy(&b, &q, 4);
+  if (po_fp8_needs_division(b & 0x7fffffffu))
+    q = value / scale;
+  return po_e4m3(q);
+}
+
+/* norm_fp8_exact.cuh:19-61 (MaxReduce inference.cu:257-268: fmaxf drops NaN operands). */
+void po_norm_fp8(const uint16_t *x, uint16_t *normalized, const uint16_t *gamma,
+                 uint8_t *packed, float *scales, int rows, int hidden, float eps, float *stats,
+                 int *bad) {
+  float v[8192], y[8192];
+  for (int r = 0; r < rows; ++r) {
+    const uint16_t *xr = x + (long long)r * hidden;
+    for (int i = 0; i < hidden; ++i)
+      v[i] = po_bf16_to_f32(xr[i]);
+    const float s = po_sumsq_tree(v, hidden, 128);
+    float var, inv;
+    po_rms_inv(s, hidden, eps, &var, &inv);
+    if (stats && r == 0) {
+      stats[0] = var;
+      stats[1] = inv;
+    }
+    float maximum = 0.f;
+    for (int i = 0; i < hidden; ++i) {
+      y[i] = po_bf16_round(po_bf16_round(v[i] * inv) * po_bf16_to_f32(gamma[i]));
+      normalized[(long long)r * hidden + i] = po_f32_to_bf16(y[i]);
+      if (!finite_f(y[i]))
+        set_bad(bad);
+      maximum = fmaxf(maximum, fabsf(y[i]));
+    }
+    const float scale = maximum == 0.f ? 1.f : maximum / 448.f;
+    const float inverse = 1.f / scale;
+    scales[r] = scale;
+    for (int i = 0; i < hidden; ++i)
+      packed[(long long)r * hidden + i] = po_fp8_encode(y[i], scale, inverse);
+  }
+}
+
 /* ---- A5 -------------------------------------------------------------------------- */
 
 /* RopeTable (inference.cu:764-785), with theta, head_dim and the YaRN constants as

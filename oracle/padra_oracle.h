@@ -45,6 +45,23 @@ void po_residual_rmsnorm(uint16_t *x, const uint16_t *residual, uint16_t *y,
 void po_rmsnorm(const uint16_t *x, uint16_t *y, const uint16_t *gamma, int rows, int hidden,
                 float eps, int threads, float *stats, int *bad);
 
+/* ---- A3 FP8 E4M3 row encoding (NormFP8Exact / NormFP8WideExact) ------------- */
+/* OCP E4M3 (bias 7, max 448, no infinities, NaN S.1111.111) of x: round to nearest even,
+ * finite overflow and infinities saturate to +-448, every NaN -> 0x7f. */
+uint8_t po_e4m3(float x);
+/* True when q's magnitude bits sit within 4 ulp of an E4M3 rounding midpoint
+ * (fp8_exact_reciprocal.cuh:5-11). */
+int po_fp8_needs_division(uint32_t magnitude_bits);
+/* fp8_exact_reciprocal::Encode (fp8_exact_reciprocal.cuh:12-21): the code of value/scale
+ * through the cached reciprocal, with a correctly rounded division near midpoints. */
+uint8_t po_fp8_encode(float value, float scale, float inverse);
+/* NormFP8Exact (norm_fp8_exact.cuh:6-62; the 256-thread NormFP8WideExact computes the
+ * same bytes): per row the 128-thread norm, normalized = y, scales[row] = max|y|/448 (1 for
+ * an all-zero row) and packed[row][i] = code of y_i.  stats (2 floats) from row 0 only. */
+void po_norm_fp8(const uint16_t *x, uint16_t *normalized, const uint16_t *gamma,
+                 uint8_t *packed, float *scales, int rows, int hidden, float eps, float *stats,
+                 int *bad);
+
 /* ---- A5 RoPE table --------------------------------------------------------- */
 /* table[p][i] = B(cos(p*f_i)*scale), table[p][D/2+i] = B(sin(p*f_i)*scale), fp32 values.
  * yarn=0: plain NeoX f_i = 1/theta^(2i/D).  yarn=1: the reference's global-layer ramp

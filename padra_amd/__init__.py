@@ -40,6 +40,7 @@ from .ops import (  # noqa: F401
     KVStore,
     KvQ8_0Dequantize,
     KvQ8_0DequantizePrefix,
+    NormFP8,
     ResidualNormQKRopeStore,
     ResidualPostNorm,
     QKNormRopeStore,

@@ -10,6 +10,7 @@
 
 #include <type_traits>
 
+#include "norm_fp8.h"
 #include "norm_rows.h"
 #include "qk_quad.h"
 
@@ -38,6 +39,10 @@ __global__ __launch_bounds__(64) void k_norm_pipe(NormArgs<T> a) {
 
 template <class T, int FMT> __global__ __launch_bounds__(64) PADRA_WAVES_PER_EU void k_qk(QKArgs<T> a) {
   qk_heads_wave<T, FMT>(a, blockIdx.x);
+}
+
+template <int J, class T> __global__ __launch_bounds__(64) void k_norm_fp8(NormFP8Args<T> a) {
+  norm_fp8_row_wave<J, T>(a, blockIdx.x);
 }
 
 // Residual-norm waves first, then the Q/K waves.  Measured on MI355X for a 2048-token
@@ -264,6 +269,35 @@ extern "C" int padra_ResidualPostNorm(void *stream, void *x, const void *residua
       } else {
         hipLaunchKernelGGL((k_norm<vt.value, j.value, T, false>), dim3(grid), dim3(64), 0, s, a);
       }
+      return launched();
+    });
+  };
+  return act == PADRA_ACT_BF16 ? launch(uint16_t{}) : launch(float{});
+}
+
+extern "C" int padra_NormFP8(void *stream, const void *x, void *normalized,
+                             const uint16_t *gamma, uint8_t *packed, float *scales, int rows,
+                             int hidden, float eps, float *statistics, int *bad, int act) {
+  int st = check_norm(x, normalized, gamma, rows, hidden, eps, 128, bad, act);
+  if (st)
+    return st;
+  if (!packed || !scales || !aligned16(packed))
+    return PADRA_INVALID_ARGUMENT;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  auto launch = [&](auto tag) -> int {
+    using T = decltype(tag);
+    NormFP8Args<T> a;
+    a.x = static_cast<const T *>(x);
+    a.y = static_cast<T *>(normalized);
+    a.gamma = gamma;
+    a.packed = packed;
+    a.scales = scales;
+    a.stats = statistics;
+    a.bad = bad;
+    a.rows = rows;
+    a.eps = eps;
+    return norm_shape(128, hidden / 128, [&](auto, auto j) -> int {
+      hipLaunchKernelGGL((k_norm_fp8<j.value, T>), dim3(rows), dim3(64), 0, s, a);
       return launched();
     });
   };

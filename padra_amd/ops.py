@@ -52,6 +52,15 @@ def ResidualPostNorm(x, residual, normalized, gamma, bad, eps=1e-6, tree=abi.TRE
              _p(gamma), rows, hidden, float(eps), int(tree), _p(statistics), _p(bad), _act(x))
 
 
+def NormFP8(x, normalized, gamma, packed, scales, bad, eps=1e-6, statistics=None):
+    """normalized <- 128-thread RMSNorm of x; packed <- E4M3 codes of normalized/scale,
+    scales[row] = max|normalized|/448 (NormFP8Exact, norm_fp8_exact.cuh:6-62)."""
+    _need_cuda(x, normalized, gamma, packed, scales, bad, statistics)
+    rows, hidden = x.shape[0], x.shape[-1]
+    abi.call("padra_NormFP8", _stream(x), _p(x), _p(normalized), _p(gamma), _p(packed),
+             _p(scales), rows, hidden, float(eps), _p(statistics), _p(bad), _act(x))
+
+
 def RopeTable(positions, head_dim=128, theta=1e6, yarn=False, factor=16.0,
               original_context=8192) -> torch.Tensor:
     """Host BF16 cos|sin table [positions][head_dim] (RopeTable, inference.cu:764-785)."""

@@ -122,6 +122,70 @@ def test_residual_norm_nonfinite_sets_bad():
     assert bad.item() == 1
 
 
+# ---- RMSNorm + FP8 E4M3 row encoding ---------------------------------------------------------
+
+@pytest.mark.parametrize("hidden", [2048, 2304])
+@pytest.mark.parametrize("rows", [1, 37, 512])
+@pytest.mark.parametrize("act", ["bf16", "f32"])
+def test_norm_fp8(oracle, hidden, rows, act):
+    print(f"[case] norm fp8 hidden={hidden} rows={rows} act={act}", flush=True)
+    d = synth.chain_inputs(rows, hidden=hidden, outliers=True, seed=rows + hidden)
+    xb = d["x"].copy()
+    if rows > 1:
+        xb[rows // 2] = 0  # all-zero row: scale 1
+    want_y, want_p, want_s, want_st, want_bad = oracle.norm_fp8(xb, d["gamma"])
+    if act == "bf16":
+        x = dev(xb)
+    else:
+        x = torch.from_numpy(synth.bf16_to_f32(xb)).cuda()
+    y = torch.empty_like(x)
+    packed = torch.empty((rows, hidden), dtype=torch.uint8, device="cuda")
+    scales = torch.empty(rows, dtype=torch.float32, device="cuda")
+    st = torch.full((2,), -1.0, dtype=torch.float32, device="cuda")
+    bad = flag()
+    ops.NormFP8(x, y, dev(d["gamma"]), packed, scales, bad, statistics=st)
+    torch.cuda.synchronize()
+    got_y = host16(y) if act == "bf16" else synth.bf16_bits(y.cpu().numpy())
+    assert np.array_equal(got_y, want_y)
+    assert np.array_equal(scales.cpu().numpy(), want_s)
+    assert np.array_equal(packed.cpu().numpy(), want_p)
+    assert np.array_equal(st.cpu().numpy(), want_st)
+    assert bool(bad.item()) == want_bad
+
+
+def test_norm_fp8_nonfinite_and_extremes(oracle):
+    """A NaN and an infinite input row (flag raised; bytes as the reference writes them), a
+    row of tiny values (scale near the fp32 minimum) and a row whose sum of squares
+    overflows (inv = 0, so y = 0 and scale 1)."""
+    print("[case] norm fp8 extremes", flush=True)
+    hidden, rows = 2304, 6
+    d = synth.chain_inputs(rows, hidden=hidden, outliers=True, seed=91)
+    xb = d["x"].copy()
+    xb[1, 5] = 0x7FC0  # NaN
+    xb[2, 9] = 0x7F80  # +inf
+    xb[3] = synth.bf16_bits(synth.bf16_to_f32(xb[3]) * np.float32(2.0**-120))
+    xb[4] = synth.bf16_bits(synth.bf16_to_f32(xb[4]) * np.float32(2.0**100))
+    want_y, want_p, want_s, _, want_bad = oracle.norm_fp8(xb, d["gamma"])
+    assert want_bad
+    x = dev(xb)
+    y = torch.empty_like(x)
+    packed = torch.empty((rows, hidden), dtype=torch.uint8, device="cuda")
+    scales = torch.empty(rows, dtype=torch.float32, device="cuda")
+    bad = flag()
+    ops.NormFP8(x, y, dev(d["gamma"]), packed, scales, bad)
+    torch.cuda.synchronize()
+    assert bad.item() == 1
+    # NaN signs and payloads are platform-defined (x86 and gfx950 make different default
+    # NaNs): NaN outputs match as NaN, every other bit exactly.
+    got_y = host16(y)
+    nan_w = (want_y & 0x7FFF) > 0x7F80
+    nan_g = (got_y & 0x7FFF) > 0x7F80
+    assert np.array_equal(nan_g, nan_w) and nan_w.any()
+    assert np.array_equal(got_y[~nan_w], want_y[~nan_w])
+    assert np.array_equal(scales.cpu().numpy(), want_s)
+    assert np.array_equal(packed.cpu().numpy(), want_p)
+
+
 # ---- Q/K norm + RoPE + KV store -------------------------------------------------------------
 
 def _qk_oracle(oracle, d, tb, positions):

@@ -22,6 +22,13 @@ Per oracle function, what checks it:
   po_kv_q8_0_dequantize           bf16(code * fp16 d) via torch
   po_silu_table                   all 65536 gates against a long-double evaluation
   po_embed / state predicates     numpy indexing; reference truth tables
+  po_e4m3                         torch float8_e4m3fn (RNE) on every finite BF16 value and
+                                  random float32 below 464; saturation and NaN by the OCP
+                                  format definition
+  po_fp8_encode                   equals the code of a correctly rounded division (numpy
+                                  float32 + torch) on values aimed at every E4M3 midpoint
+  po_norm_fp8                     y = po_rmsnorm's, scale = max|y|/448, codes = torch
+                                  float8 of y/scale, zero row, non-finite row
 """
 import numpy as np
 import pytest
@@ -179,6 +186,78 @@ def test_residual_norm_nonfinite_sets_bad(oracle):
     x = d["x"].copy()
     x[1, 7] = 0x7F80  # +inf
     _, _, _, bad = oracle.residual_rmsnorm(x, d["residual"], d["gamma"])
+    assert bad
+
+
+# ---- A3 FP8 ----------------------------------------------------------------------------
+
+def torch_e4m3(values):
+    return torch.from_numpy(np.ascontiguousarray(values, np.float32)).to(
+        torch.float8_e4m3fn).view(torch.uint8).numpy()
+
+
+def test_e4m3_matches_torch(oracle):
+    bf = np.arange(65536, dtype=np.uint32)
+    vals = (bf << 16).view(np.float32)
+    vals = vals[np.isfinite(vals) & (np.abs(vals) < 464)]
+    rng = np.random.default_rng(11)
+    rand = rng.integers(0, 2**32, 60000, dtype=np.uint64).astype(np.uint32).view(np.float32)
+    rand = rand[np.isfinite(rand) & (np.abs(rand) < 464)]
+    for v in (vals, rand):
+        assert np.array_equal(oracle.e4m3(v), torch_e4m3(v))
+
+
+def test_e4m3_saturation_and_nan(oracle):
+    big = np.array([464, 480, 1e6, 3e38, np.inf], np.float32)
+    assert np.all(oracle.e4m3(big) == 0x7E) and np.all(oracle.e4m3(-big) == 0xFE)
+    assert oracle.e4m3([np.nan])[0] == 0x7F and oracle.e4m3([-np.nan])[0] == 0x7F
+    # the 127 finite positive codes decode to k * 2^-9 (subnormal) or 2^(e-7) (1 + m/8)
+    for code in range(0x7F):
+        e, m = code >> 3, code & 7
+        value = m * 2.0**-9 if e == 0 else 2.0**(e - 7) * (1 + m / 8)
+        assert oracle.e4m3([value])[0] == code
+
+
+def test_fp8_encode_equals_division(oracle):
+    """The cached-reciprocal path with its midpoint fallback gives the code of the correctly
+    rounded quotient, on BF16 values aimed at E4M3 rounding midpoints."""
+    rng = np.random.default_rng(12)
+    amax = synth.bf16_to_f32(synth.bf16_bits(np.exp2(rng.uniform(-30, 30, 120)).astype(F32)))
+    codes = np.arange(0x7E, dtype=np.float64)
+    grid = np.where(codes < 8, codes * 2.0**-9, 2.0**((codes // 8) - 7) * (1 + (codes % 8) / 8))
+    mids = (grid[:-1] + grid[1:]) / 2
+    enc = oracle.lib().po_fp8_encode
+    checked = 0
+    for a in amax:
+        scale = F32(a / F32(448))
+        inverse = F32(F32(1) / scale)
+        target = synth.bf16_bits((mids * np.float64(scale)).astype(F32)).astype(np.int64)
+        vals = np.concatenate([target + d for d in (-2, -1, 0, 1, 2)])
+        vals = synth.bf16_to_f32(np.clip(vals, 0, 0x7F7F).astype(np.uint16))
+        vals = vals[np.abs(vals) <= a]
+        vals = np.concatenate([vals, -vals])
+        want = torch_e4m3(vals / scale)
+        got = np.array([enc(float(v), float(scale), float(inverse)) for v in vals], np.uint8)
+        assert np.array_equal(got, want), a
+        checked += len(vals)
+    assert checked > 100000
+
+
+def test_norm_fp8(oracle):
+    d = synth.chain_inputs(12, hidden=2304, outliers=True, seed=13)
+    x = d["x"].copy()
+    x[3] = 0  # all-zero row: scale 1, codes 0
+    y, packed, scales, stats, bad = oracle.norm_fp8(x, d["gamma"])
+    assert not bad
+    y_ref, st_ref, _ = oracle.rmsnorm(x, d["gamma"], threads=128)
+    assert np.array_equal(y, y_ref) and np.array_equal(stats, st_ref[0])
+    yf = synth.bf16_to_f32(y)
+    amax = np.abs(yf).max(axis=1)
+    want_scale = np.where(amax == 0, F32(1), (amax / F32(448)).astype(F32))
+    assert np.array_equal(scales, want_scale) and scales[3] == 1
+    assert np.array_equal(packed, torch_e4m3(yf / scales[:, None]))
+    x[5, 9] = 0x7FC0  # NaN input
+    *_, bad = oracle.norm_fp8(x, d["gamma"])
     assert bad
 
 
