@@ -52,7 +52,7 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-configs", action="store_true",
                     help="skip the config 0/3/4 measurements (headline only)")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--formats", default="bf16,q8_0,q8_0_norot,q8",
                     help="KV formats measured (the first is the headline)")
     return ap.parse_args()
@@ -153,35 +153,58 @@ def copy_ceiling(torch, nbytes=COPY_BYTES, reps=50):
     return 2 * n * 2 / (ms * 1e-3) / 1e9
 
 
-def cpu_baseline(host, seconds):
-    """The C oracle on the host: residual-norm (128-thread tree), Q/K norm + RoPE and the
-    BF16 store over the full 2048-token chunk, repeated until `seconds` have elapsed."""
+def cpu_chain_rate(host, seconds, threads):
+    """Seconds per 2048-token config-1 chunk of the C oracle on the host: residual-norm
+    (128-thread tree), Q/K norm + RoPE and the BF16 store, with the chunk's tokens split
+    into `threads` contiguous slices run concurrently (ctypes releases the GIL during each
+    oracle call).  Repeats whole chunks until `seconds` have elapsed; returns (s, chunks)."""
+    from concurrent.futures import ThreadPoolExecutor
+
     from oracle import oracle
-    table = __import__("padra_amd").synth.bf16_bits(oracle.rope_table(TOKENS, D, 1e6))
-    pos = np.arange(TOKENS, dtype=np.int32)
+    from padra_amd import synth
+    table = synth.bf16_bits(oracle.rope_table(TOKENS, D, 1e6))
     kc = np.zeros((TOKENS, HKV * D), np.uint16)
     vc = np.zeros_like(kc)
-    reps, t0 = 0, time.perf_counter()
-    while True:
-        xn, y, _, _ = oracle.residual_rmsnorm(host["x"], host["residual"], host["gamma"], 1e-6,
-                                              128)
-        q, k, _ = oracle.qk_norm_rope(host["q"], host["k"], host["qn"], host["kn"], table, pos)
-        oracle.kv_store_bf16(k, host["v"], kc, vc, pos, TOKENS)
-        reps += 1
-        el = time.perf_counter() - t0
-        if el >= seconds:
-            break
-    per_chunk = el / reps
-    return {
-        "value": round(chain_bytes("bf16") * TOKENS / per_chunk / 1e9, 3),
-        "unit": "GB/s",
-        "cores": 1,
-        "kind": "port",
-        "sample": f"{reps} full 2048-token config-1 chunks (BF16 KV) in {el:.1f} s, one thread",
-        "tokens_per_s": round(TOKENS / per_chunk, 1),
-        "us_per_token": round(per_chunk / TOKENS * 1e6, 3),
-    }
+    bounds = np.linspace(0, TOKENS, threads + 1).astype(int)
 
+    def piece(i):
+        lo, hi = bounds[i], bounds[i + 1]
+        pos = np.arange(lo, hi, dtype=np.int32)
+        oracle.residual_rmsnorm(host["x"][lo:hi], host["residual"][lo:hi], host["gamma"], 1e-6,
+                                128)
+        _, k, _ = oracle.qk_norm_rope(host["q"][lo:hi], host["k"][lo:hi], host["qn"],
+                                      host["kn"], table, pos)
+        oracle.kv_store_bf16(k, host["v"][lo:hi], kc, vc, pos, TOKENS)
+
+    oracle.lib()
+    reps, t0 = 0, time.perf_counter()
+    with ThreadPoolExecutor(threads) as pool:
+        while True:
+            list(pool.map(piece, range(threads)))
+            reps += 1
+            el = time.perf_counter() - t0
+            if el >= seconds:
+                break
+    return el / reps, reps
+
+
+def cpu_baseline(host, seconds, threads):
+    """The oracle (kind "port") on the GPU box's host cores, single-threaded and on
+    `threads` threads; the threaded figure is the reported value."""
+    one, reps1 = cpu_chain_rate(host, seconds / 2, 1)
+    many, reps = cpu_chain_rate(host, seconds / 2, threads)
+    rate = lambda per_chunk: round(chain_bytes("bf16") * TOKENS / per_chunk / 1e9, 3)
+    return {
+        "value": rate(many),
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{reps} full 2048-token config-1 chunks (BF16 KV) on {threads} threads and "
+                  f"{reps1} on one thread, about {seconds / 2:.0f} s each",
+        "tokens_per_s": round(TOKENS / many, 1),
+        "us_per_token": round(many / TOKENS * 1e6, 3),
+        "single_thread": {"value": rate(one), "tokens_per_s": round(TOKENS / one, 1)},
+    }
 
 
 def graph_time(torch, step, steps, warmup=3):
@@ -229,6 +252,32 @@ def bench_swiglu(torch, steps, sets=4):
             "rows_per_s": round(d["gate"].shape[0] / (ms * 1e-3), 1)}
 
 
+def bench_norm_fp8(torch, steps, sets=8):
+    """The input RMSNorm with its FP8 E4M3 row encoding (the QKV GEMM's input) over the
+    config-1 chunk: 2048 rows of 2048; reads x, writes normalized (BF16) and codes."""
+    from padra_amd import ops, synth
+    host = synth.chain_inputs(TOKENS, HIDDEN, HQ, HKV, D, outliers=True, seed=0)
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).cuda()
+    g = dev(host["gamma"])
+    bad = torch.zeros(1, dtype=torch.int32, device="cuda")
+    bufs = []
+    for _ in range(sets):
+        x = dev(host["x"])
+        bufs.append((x, torch.empty_like(x),
+                     torch.empty((TOKENS, HIDDEN), dtype=torch.uint8, device="cuda"),
+                     torch.empty(TOKENS, dtype=torch.float32, device="cuda")))
+    ms = graph_time(torch, lambda i: ops.NormFP8(bufs[i % sets][0], bufs[i % sets][1], g,
+                                                 bufs[i % sets][2], bufs[i % sets][3], bad),
+                    steps)
+    if bad.item():
+        raise SystemExit("device error flag set in the FP8 norm benchmark")
+    nbytes = TOKENS * (HIDDEN * (2 + 2 + 1) + 4)
+    return {"workload": "RMSNorm + FP8 E4M3 row encoding, 2048 rows x 2048 (BF16 in/out)",
+            "us_per_launch": round(ms * 1e3, 3), "bytes_per_launch": nbytes,
+            "gbs": round(nbytes / (ms * 1e-3) / 1e9, 2),
+            "frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+
+
 def bench_decode(torch, steps, seqs, vocab=131072, capacity=CAPACITY):
     """Config 4 (seqs=64) and the GPU side of config 0 (seqs=1): embedding gather, then the
     fused residual-norm (256-thread decode tree) + Q/K norm + RoPE + BF16 KV store at each
@@ -269,6 +318,16 @@ def bench_decode(torch, steps, seqs, vocab=131072, capacity=CAPACITY):
                         "sequence(s): gather + fused chain (256-thread tree), ragged positions",
             "us_per_step": round(ms * 1e3, 3), "tokens_per_s": round(seqs / (ms * 1e-3), 1),
             "bytes_per_step": nbytes, "gbs": round(nbytes / (ms * 1e-3) / 1e9, 2)}
+
+
+def cpu_threads() -> int:
+    """Host threads for the CPU baseline: the box's CPU share for one GPU (16), or fewer
+    where fewer cores exist."""
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except AttributeError:
+        avail = os.cpu_count() or 1
+    return max(1, min(16, avail))
 
 
 def cpu_decode_token(seconds=2.0):
@@ -357,9 +416,10 @@ def main():
         torch.cuda.empty_cache()
         line["configs"] = {"config3": bench_swiglu(torch, 50),
                            "config4": bench_decode(torch, 100, 64),
-                           "config0_gpu": bench_decode(torch, 200, 1, capacity=8192)}
+                           "config0_gpu": bench_decode(torch, 200, 1, capacity=8192),
+                           "norm_fp8": bench_norm_fp8(torch, 200)}
     if not args.no_cpu:
-        line["cpu_baseline"] = cpu_baseline(host, args.cpu_seconds)
+        line["cpu_baseline"] = cpu_baseline(host, args.cpu_seconds, cpu_threads())
         if not args.no_configs:
             line["configs"]["config0_cpu"] = cpu_decode_token()
     print(json.dumps(line), flush=True)

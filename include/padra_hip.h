@@ -218,6 +218,12 @@ int padra_SwiGLU(void *stream, const void *gate, const void *up, void *out, long
 int padra_Embed(void *stream, const uint16_t *table, int vocab, int hidden, const int32_t *ids,
                 const padra_Positions *src, int tokens, void *out, int *bad, int act);
 
+/* padra_CheckFP8Paths: no counterpart in the reference.  Checks, over their whole domains,
+ * the two identities padra_NormFP8's fast path relies on (the hardware E4M3 conversion, and
+ * the reciprocal-plus-correction quotient) and writes the mismatch counts to counts[0..1]
+ * (device memory, 2 x u64; both 0 when the fast path is exact).  About 4.4e9 evaluations,
+ * a few milliseconds. */
+int padra_CheckFP8Paths(void *stream, unsigned long long *counts);
 /* ---- launch tuning ------------------------------------------------------------------
  * No counterpart in the reference (its launch shapes are fixed).  Process-wide launch
  * parameters for measurement sweeps; defaults need no call.

@@ -41,6 +41,11 @@ template <class T, int FMT> __global__ __launch_bounds__(64) PADRA_WAVES_PER_EU 
   qk_heads_wave<T, FMT>(a, blockIdx.x);
 }
 
+__global__ void k_zero_u64(unsigned long long *p, int n) {
+  if ((int)threadIdx.x < n)
+    p[threadIdx.x] = 0;
+}
+
 template <int J, class T> __global__ __launch_bounds__(64) void k_norm_fp8(NormFP8Args<T> a) {
   norm_fp8_row_wave<J, T>(a, blockIdx.x);
 }
@@ -302,6 +307,16 @@ extern "C" int padra_NormFP8(void *stream, const void *x, void *normalized,
     });
   };
   return act == PADRA_ACT_BF16 ? launch(uint16_t{}) : launch(float{});
+}
+
+extern "C" int padra_CheckFP8Paths(void *stream, unsigned long long *counts) {
+  if (!counts)
+    return PADRA_INVALID_ARGUMENT;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(k_zero_u64, dim3(1), dim3(64), 0, s, counts, 2);
+  hipLaunchKernelGGL(k_check_fp8_hw, dim3(8192), dim3(256), 0, s, 2ull * 0x43f00000ull, counts);
+  hipLaunchKernelGGL(k_check_fp8_quotient, dim3(0x7f7f), dim3(256), 0, s, counts);
+  return launched();
 }
 
 extern "C" int padra_QKNormRopeStore(void *stream, void *q, void *k, const void *v,

@@ -5,8 +5,10 @@
 // norm_rows.h.  Then, per row:
 //   y_i      = B(B(x_i * inv) * gamma_i)          (normalized, BF16-exact; flag if not finite)
 //   scale    = max|y| == 0 ? 1 : max|y| / 448     (fmaxf drops NaN, as MaxReduce does)
-//   packed_i = E4M3 code of y_i / scale, through the cached reciprocal with a correctly
-//              rounded division near rounding midpoints (fp8_exact_reciprocal.cuh:5-21)
+//   packed_i = E4M3 code of the correctly rounded y_i / scale, which is what the
+//              reference's reciprocal-with-midpoint-division computes
+//              (fp8_exact_reciprocal.cuh:5-21); see fp8_encode_pairs for how
+//              it is computed here
 // The maximum is order-independent, so the wave reduces it with any exchange pattern.
 #pragma once
 #include "norm_rows.h"
@@ -32,28 +34,58 @@ __device__ __forceinline__ uint32_t e4m3_code(float x) {
   const uint32_t bits = __float_as_uint(x), sign = (bits >> 24) & 0x80u, mag = bits & 0x7fffffffu;
   const float a = __uint_as_float(mag);
   const uint32_t sub = (uint32_t)rintf(a * 512.f); // k * 2^-9, k = 8 is the least normal
-  const uint32_t normal = ((mag + 0x7ffffu + ((mag >> 20) & 1u)) >> 20) - (120u << 3);
-  uint32_t code = a < 0.015625f ? sub : min(normal, 0x7eu);
-  code = a >= 448.f ? 0x7eu : code;
-  return mag > 0x7f800000u ? 0x7fu : (sign | code);
+  const uint32_t normal = min(((mag + 0x7ffffu + ((mag >> 20) & 1u)) >> 20) - (120u << 3), 0x7eu);
+  // Branch-free selects (the compiler would otherwise branch per element).
+  const uint32_t small = 0u - (uint32_t)(mag < 0x3c800000u); // a < 2^-6
+  const uint32_t big = 0u - (uint32_t)(mag >= 0x43e00000u);  // a >= 448 (infinities too)
+  const uint32_t nan = 0u - (uint32_t)(mag > 0x7f800000u);
+  uint32_t code = (sub & small) | (normal & ~small);
+  code = (0x7eu & big) | (code & ~big);
+  return (0x7fu & nan) | ((sign | code) & ~nan);
 }
 
-// fp8_exact_reciprocal::NeedsDivision: q's magnitude within 4 ulp of an E4M3 midpoint.
-__device__ __forceinline__ bool fp8_needs_division(uint32_t b) {
-  if (b < 0x3a800000u)
-    return b >= 0x3a800000u - 4u;
-  const uint32_t e = b >> 23, shift = e < 121u ? 140u - e : 19u;
-  const uint32_t residue = b & ((2u << shift) - 1u), midpoint = 1u << shift;
-  return residue - (midpoint - 4u) <= 8u;
+// E4M3 code of a finite quotient q with |q| <= 480 through gfx950's v_cvt_pk_fp8_f32 (OCP
+// E4M3, round to nearest even), after clamping to +-448; equal to e4m3_code there
+// (padra_CheckFP8Paths compares the two on every such float).
+__device__ __forceinline__ uint32_t e4m3_pair_hw(float q0, float q1) {
+  return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(__builtin_amdgcn_fmed3f(q0, -448.f, 448.f),
+                                                   __builtin_amdgcn_fmed3f(q1, -448.f, 448.f), 0,
+                                                   false) & 0xffffu;
 }
 
-// fp8_exact_reciprocal::Encode.
-__device__ __forceinline__ uint32_t fp8_encode(float value, float scale, float inverse) {
+// The quotient v / scale from the cached reciprocal plus one exact-remainder correction:
+// q = v * inverse, r = v - q * scale (one fused multiply-add), q + r * inverse, with v's
+// sign restored (a zero v would otherwise come back +0).  For BF16 v and a scale derived
+// from a BF16 maximum of at least 2^-100 (inverse normal), its E4M3 code equals the code of
+// the correctly rounded quotient for every such pair, as padra_CheckFP8Paths verifies.
+__device__ __forceinline__ float fp8_quotient(float v, float scale, float inverse) {
+  const float q = v * inverse;
+  const float r = __builtin_fmaf(-q, scale, v);
+  return __builtin_copysignf(__builtin_fmaf(r, inverse, q), v);
+}
+
+// Whether a row may take the fast path: finite values, maximum >= 2^-100, normal inverse.
+__device__ __forceinline__ bool fp8_fast_ok(float amax, float inverse) {
   const uint32_t ie = __float_as_uint(inverse) & 0x7f800000u;
-  float q = value * inverse;
-  if (ie == 0 || ie == 0x7f800000u || fp8_needs_division(__float_as_uint(q) & 0x7fffffffu))
-    q = value / scale;
-  return e4m3_code(q);
+  return amax >= 0x1p-100f && ie != 0 && ie != 0x7f800000u;
+}
+
+// The codes of J pairs of values (BF16 pairs in words w) with one scale: the reference's
+// fp8_exact_reciprocal::Encode, whose code is the code of the correctly rounded quotient
+// (its midpoint test only chooses when to divide; the CPU tests check this on values aimed
+// at every E4M3 midpoint).  FAST: fp8_quotient and the hardware conversion; otherwise a
+// correctly rounded division and e4m3_code (rows with a NaN or an infinity, tiny maxima).
+template <int J, bool FAST>
+__device__ __forceinline__ void fp8_encode_pairs(const uint32_t (&w)[J], float scale,
+                                                 float inverse, uint32_t (&codes)[J]) {
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    if constexpr (FAST)
+      codes[j] = e4m3_pair_hw(fp8_quotient(lo16(w[j]), scale, inverse),
+                              fp8_quotient(hi16(w[j]), scale, inverse));
+    else
+      codes[j] = e4m3_code(lo16(w[j]) / scale) | (e4m3_code(hi16(w[j]) / scale) << 8);
+  }
 }
 
 template <int J, class T>
@@ -91,37 +123,92 @@ __device__ __forceinline__ void norm_fp8_row_wave(const NormFP8Args<T> &a, int r
     a.stats[1] = inv;
   }
 
-  // y, its maximum magnitude, the normalized row.
+  // y, the normalized row, and the largest |y| as BF16 magnitude bits: two 16-bit lanes of
+  // an unsigned max per word (the integer order of magnitude bits is the order of |y|, with
+  // infinities above every finite value and NaNs above infinities).
+  typedef uint16_t u16x2_t __attribute__((ext_vector_type(2)));
   uint32_t yw[J];
-  float amax = 0.f;
-  bool fine = true;
+  u16x2_t mag2 = {0, 0};
 #pragma unroll
   for (int j = 0; j < J; ++j) {
     const uint32_t p = pack2(lo16(vp[j]) * inv, hi16(vp[j]) * inv);
     yw[j] = pack2(lo16(p) * gr[j].get(0), hi16(p) * gr[j].get(1));
-    const float y0 = lo16(yw[j]), y1 = hi16(yw[j]);
-    fine = fine && isfinite(y0) && isfinite(y1);
-    amax = fmaxf(amax, fmaxf(fabsf(y0), fabsf(y1)));
+    mag2 = __builtin_elementwise_max(mag2, __builtin_bit_cast(u16x2_t, yw[j] & 0x7fff7fffu));
     Lanes<T, K>::store(a.y + off + VT * j, &yw[j]);
   }
-  if (__ballot(!fine) != 0 && lane == 0)
-    raise_bad(a.bad);
+  uint32_t mag = max((uint32_t)mag2.x, (uint32_t)mag2.y);
 #pragma unroll
   for (int d = 32; d >= 1; d /= 2)
-    amax = fmaxf(amax, __shfl_xor(amax, d, 64));
+    mag = max(mag, (uint32_t)__shfl_xor((int)mag, d, 64));
+  // Every y finite <=> the largest magnitude is below the BF16 infinity (wave-uniform).
+  const bool row_fine = mag < 0x7f80u;
+  if (!row_fine && lane == 0)
+    raise_bad(a.bad);
+  if (!row_fine) {
+    // MaxReduce's fmaxf drops NaN operands: the maximum over the non-NaN magnitudes.
+    mag = 0;
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      const uint32_t lo = yw[j] & 0x7fffu, hi = (yw[j] >> 16) & 0x7fffu;
+      mag = max(mag, lo > 0x7f80u ? 0u : lo);
+      mag = max(mag, hi > 0x7f80u ? 0u : hi);
+    }
+#pragma unroll
+    for (int d = 32; d >= 1; d /= 2)
+      mag = max(mag, (uint32_t)__shfl_xor((int)mag, d, 64));
+  }
+  const float amax = __uint_as_float(mag << 16);
   const float scale = amax == 0.f ? 1.f : amax / 448.f;
   const float inverse = 1.f / scale;
   if (lane == 0)
     a.scales[row] = scale;
 
   // Codes: two per j, one 2-byte store each (128 contiguous bytes per instruction).
+  uint32_t codes[J];
+  if (row_fine && fp8_fast_ok(amax, inverse)) // wave-uniform
+    fp8_encode_pairs<J, true>(yw, scale, inverse, codes);
+  else
+    fp8_encode_pairs<J, false>(yw, scale, inverse, codes);
   uint8_t *const out = a.packed + off;
 #pragma unroll
-  for (int j = 0; j < J; ++j) {
-    const uint32_t c0 = fp8_encode(lo16(yw[j]), scale, inverse);
-    const uint32_t c1 = fp8_encode(hi16(yw[j]), scale, inverse);
-    *reinterpret_cast<uint16_t *>(out + VT * j) = (uint16_t)(c0 | (c1 << 8));
+  for (int j = 0; j < J; ++j)
+    *reinterpret_cast<uint16_t *>(out + VT * j) = (uint16_t)codes[j];
+}
+
+// Self-check of the two fast-path identities, over their whole domains:
+//   A. e4m3_pair_hw(x) == e4m3_code(x) for every float with |x| <= 480 (2.28e9 inputs);
+//   B. for every BF16 maximum m >= 2^-100 (scale = m/448, inverse normal) and every BF16
+//      v with |v| <= m, both signs: code of fp8_quotient == code of the correctly rounded
+//      division (2.1e9 pairs).
+// Mismatches are added to counts[0] (A) and counts[1] (B).
+__global__ __launch_bounds__(256) void k_check_fp8_hw(unsigned long long n,
+                                                      unsigned long long *counts) {
+  unsigned long long bad = 0;
+  const unsigned long long stride = (unsigned long long)gridDim.x * blockDim.x;
+  for (unsigned long long i = blockIdx.x * (unsigned long long)blockDim.x + threadIdx.x; i < n;
+       i += stride) {
+    const float x = __uint_as_float((uint32_t)(i >> 1) | ((uint32_t)(i & 1) << 31));
+    bad += (e4m3_pair_hw(x, 0.f) & 0xffu) != e4m3_code(x);
   }
+  if (bad)
+    atomicAdd(&counts[0], bad);
+}
+__global__ __launch_bounds__(256) void k_check_fp8_quotient(unsigned long long *counts) {
+  const uint32_t mb = blockIdx.x + 1; // BF16 bits of the maximum, 0x0001 .. 0x7f7f
+  const float amax = __uint_as_float(mb << 16);
+  const float scale = amax / 448.f, inverse = 1.f / scale;
+  if (!fp8_fast_ok(amax, inverse))
+    return; // block-uniform
+  unsigned long long bad = 0;
+  for (uint32_t vb = threadIdx.x; vb <= mb; vb += blockDim.x) {
+#pragma unroll
+    for (int sg = 0; sg < 2; ++sg) {
+      const float v = __uint_as_float((vb << 16) | (sg ? 0x80000000u : 0u));
+      bad += (e4m3_pair_hw(fp8_quotient(v, scale, inverse), 0.f) & 0xffu) != e4m3_code(v / scale);
+    }
+  }
+  if (bad)
+    atomicAdd(&counts[1], bad);
 }
 
 } // namespace padra

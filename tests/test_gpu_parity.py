@@ -153,6 +153,18 @@ def test_norm_fp8(oracle, hidden, rows, act):
     assert bool(bad.item()) == want_bad
 
 
+def test_fp8_fast_path_identities_exhaustive():
+    """The two identities the FP8 fast path rests on, over their whole domains: the hardware
+    E4M3 conversion equals the format-defined encoder on every float up to 480, and the
+    reciprocal-plus-correction quotient gives the correctly rounded quotient's code for
+    every BF16 (maximum, value) pair the fast path admits."""
+    print("[case] fp8 fast-path identities", flush=True)
+    counts = torch.full((2,), -1, dtype=torch.int64, device="cuda")
+    abi.call("padra_CheckFP8Paths", None, counts.data_ptr())
+    torch.cuda.synchronize()
+    assert counts.tolist() == [0, 0]
+
+
 def test_norm_fp8_nonfinite_and_extremes(oracle):
     """A NaN and an infinite input row (flag raised; bytes as the reference writes them), a
     row of tiny values (scale near the fp32 minimum) and a row whose sum of squares
