@@ -218,6 +218,24 @@ int padra_SwiGLU(void *stream, const void *gate, const void *up, void *out, long
 int padra_Embed(void *stream, const uint16_t *table, int vocab, int hidden, const int32_t *ids,
                 const padra_Positions *src, int tokens, void *out, int *bad, int act);
 
+/* padra_Combine: Combine (inference.cu:580-590) and exl3_packed_activations::Combine
+ * (expert_exl3_prefill_packed_activations.cuh:86-102).  For each row t and column i of
+ * x [rows][hidden]: c = 0; for e = 0..experts-1: c = B(c + B(down[t][e][i] * weights[t][e]));
+ * x = residual ? B(x + c) : c.  down is [rows][experts][hidden] in the activation type,
+ * weights [rows][experts] fp32 routing weights.  A non-finite result raises *bad and is
+ * still written.  experts must be 8; hidden a multiple of 8; x, down 16-byte aligned. */
+int padra_Combine(void *stream, void *x, const void *down, const float *weights, int rows,
+                  int hidden, int experts, int residual, int *bad, int act);
+/* padra_CombineNorm: combine_norm_exact::CombineNorm (combine_norm_exact.cuh:7-72), one row
+ * per row of x: the residual combine above, then the 128-thread RMSNorm of the new x into
+ * normalized and, when packed != NULL, its E4M3 encoding as padra_NormFP8 writes it
+ * (packed [rows][hidden], scales [rows]).  statistics (2 floats, may be NULL) receives
+ * {variance, inv} of row 0.  Non-finite combined or normalized values raise *bad.  hidden
+ * in {1024, 1152, 2048, 2304, 4096, 4608}; experts must be 8. */
+int padra_CombineNorm(void *stream, void *x, const void *down, const float *weights,
+                      void *normalized, const uint16_t *gamma, uint8_t *packed, float *scales,
+                      int rows, int hidden, int experts, float eps, float *statistics, int *bad,
+                      int act);
 /* padra_CheckFP8Paths: no counterpart in the reference.  Checks, over their whole domains,
  * the two identities padra_NormFP8's fast path relies on (the hardware E4M3 conversion, and
  * the reciprocal-plus-correction quotient) and writes the mismatch counts to counts[0..1]

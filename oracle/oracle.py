@@ -40,6 +40,8 @@ def lib() -> ctypes.CDLL:
             "po_fp8_needs_division": ([ctypes.c_uint32], I),
             "po_fp8_encode": ([F, F, F], ctypes.c_uint8),
             "po_norm_fp8": ([P, P, P, P, P, I, I, F, P, P], None),
+            "po_combine": ([P, P, P, I, I, I, I, P], None),
+            "po_combine_norm": ([P, P, P, P, P, P, P, I, I, I, F, P, P], None),
             "po_rope_table": ([P, I, I, F, I, F, I], None),
             "po_qk_norm_rope": ([P, P, P, P, P, P, I, I, I, I, F, P], None),
             "po_kv_store_bf16": ([P, P, P, P, P, I, I, I, I], None),
@@ -117,6 +119,36 @@ def norm_fp8(x, gamma, eps=1e-6):
     lib().po_norm_fp8(_p(x), _p(y), _p(np.ascontiguousarray(gamma, np.uint16)), _p(packed),
                       _p(scales), rows, hidden, eps, _p(stats), bad.ptr)
     return y, packed, scales, stats, bool(bad)
+
+
+def combine(x, down, weights, residual=True):
+    """x [rows][H] BF16 bits, down [rows][E][H] BF16 bits, weights [rows][E] f32.
+    Returns (x_new, bad)."""
+    x = np.array(x, dtype=np.uint16, copy=True, order="C")
+    rows, hidden = x.shape
+    experts = down.shape[1]
+    bad = Bad()
+    lib().po_combine(_p(x), _p(np.ascontiguousarray(down, np.uint16)),
+                     _p(np.ascontiguousarray(weights, np.float32)), rows, hidden, experts,
+                     int(bool(residual)), bad.ptr)
+    return x, bool(bad)
+
+
+def combine_norm(x, down, weights, gamma, fp8=True, eps=1e-6):
+    """Returns (x_new, normalized, packed or None, scales or None, stats [2], bad)."""
+    x = np.array(x, dtype=np.uint16, copy=True, order="C")
+    rows, hidden = x.shape
+    experts = down.shape[1]
+    y = np.empty_like(x)
+    packed = np.empty((rows, hidden), np.uint8) if fp8 else None
+    scales = np.empty(rows, np.float32) if fp8 else None
+    stats = np.empty(2, np.float32)
+    bad = Bad()
+    lib().po_combine_norm(_p(x), _p(np.ascontiguousarray(down, np.uint16)),
+                          _p(np.ascontiguousarray(weights, np.float32)), _p(y),
+                          _p(np.ascontiguousarray(gamma, np.uint16)), _p(packed), _p(scales),
+                          rows, hidden, experts, eps, _p(stats), bad.ptr)
+    return x, y, packed, scales, stats, bool(bad)
 
 
 def e4m3(values) -> np.ndarray:

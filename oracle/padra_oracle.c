@@ -278,6 +278,63 @@ void po_norm_fp8(const uint16_t *x, uint16_t *normalized, const uint16_t *gamma,
   }
 }
 
+/* ---- Expert combine -------------------------------------------------------------- */
+
+/* inference.cu:580-590; expert_exl3_prefill_packed_activations.cuh:86-102 */
+void po_combine(uint16_t *x, const uint16_t *down, const float *weights, int rows, int hidden,
+                int experts, int residual, int *bad) {
+  for (int t = 0; t < rows; ++t)
+    for (int i = 0; i < hidden; ++i) {
+      float c = 0.f;
+      for (int e = 0; e < experts; ++e) {
+        const float d = po_bf16_to_f32(down[((long long)t * experts + e) * hidden + i]);
+        c = po_bf16_round(c + po_bf16_round(d * weights[t * experts + e]));
+      }
+      uint16_t *xi = x + (long long)t * hidden + i;
+      const float value = residual ? po_bf16_round(po_bf16_to_f32(*xi) + c) : c;
+      if (!finite_f(value))
+        set_bad(bad);
+      *xi = po_f32_to_bf16(value);
+    }
+}
+
+/* combine_norm_exact.cuh:22-71 */
+void po_combine_norm(uint16_t *x, const uint16_t *down, const float *weights,
+                     uint16_t *normalized, const uint16_t *gamma, uint8_t *packed,
+                     float *scales, int rows, int hidden, int experts, float eps, float *stats,
+                     int *bad) {
+  float v[8192], y[8192];
+  for (int t = 0; t < rows; ++t) {
+    uint16_t *xr = x + (long long)t * hidden;
+    po_combine(xr, down + (long long)t * experts * hidden, weights + (long long)t * experts, 1,
+               hidden, experts, 1, bad);
+    for (int i = 0; i < hidden; ++i)
+      v[i] = po_bf16_to_f32(xr[i]);
+    const float s = po_sumsq_tree(v, hidden, 128);
+    float var, inv;
+    po_rms_inv(s, hidden, eps, &var, &inv);
+    if (stats && t == 0) {
+      stats[0] = var;
+      stats[1] = inv;
+    }
+    float maximum = 0.f;
+    for (int i = 0; i < hidden; ++i) {
+      y[i] = po_bf16_round(po_bf16_round(v[i] * inv) * po_bf16_to_f32(gamma[i]));
+      normalized[(long long)t * hidden + i] = po_f32_to_bf16(y[i]);
+      if (!finite_f(y[i]))
+        set_bad(bad);
+      maximum = fmaxf(maximum, fabsf(y[i]));
+    }
+    if (packed) {
+      const float scale = maximum != 0.f ? maximum / 448.f : 1.f;
+      const float inverse = 1.f / scale;
+      scales[t] = scale;
+      for (int i = 0; i < hidden; ++i)
+        packed[(long long)t * hidden + i] = po_fp8_encode(y[i], scale, inverse);
+    }
+  }
+}
+
 /* ---- A5 -------------------------------------------------------------------------- */
 
 /* RopeTable (inference.cu:764-785), with theta, head_dim and the YaRN constants as

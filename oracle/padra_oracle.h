@@ -62,6 +62,23 @@ void po_norm_fp8(const uint16_t *x, uint16_t *normalized, const uint16_t *gamma,
                  uint8_t *packed, float *scales, int rows, int hidden, float eps, float *stats,
                  int *bad);
 
+/* ---- Expert combine (+ residual) and combine + RMSNorm (+ FP8) ---------------- */
+/* Combine (inference.cu:580-590) and exl3_packed_activations::Combine
+ * (expert_exl3_prefill_packed_activations.cuh:86-102): per row t and column i,
+ * c = 0; for e in 0..experts-1: c = B(c + B(down[t][e][i] * weights[t][e])); then
+ * x[t][i] = residual ? B(x + c) : c, a non-finite result raising *bad (still written).
+ * weights are fp32 routing weights [rows][experts]. */
+void po_combine(uint16_t *x, const uint16_t *down, const float *weights, int rows, int hidden,
+                int experts, int residual, int *bad);
+/* combine_norm_exact::CombineNorm (combine_norm_exact.cuh:7-72), one row per row of x:
+ * the residual combine above, then the 128-thread RMSNorm of the new x into normalized
+ * (non-finite v or y raise *bad), and with packed != NULL the FP8 E4M3 encoding
+ * (scales[row]).  stats (2 floats) from row 0. */
+void po_combine_norm(uint16_t *x, const uint16_t *down, const float *weights,
+                     uint16_t *normalized, const uint16_t *gamma, uint8_t *packed,
+                     float *scales, int rows, int hidden, int experts, float eps, float *stats,
+                     int *bad);
+
 /* ---- A5 RoPE table --------------------------------------------------------- */
 /* table[p][i] = B(cos(p*f_i)*scale), table[p][D/2+i] = B(sin(p*f_i)*scale), fp32 values.
  * yarn=0: plain NeoX f_i = 1/theta^(2i/D).  yarn=1: the reference's global-layer ramp

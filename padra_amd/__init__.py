@@ -35,6 +35,8 @@ from .abi import (  # noqa: F401
     library_path,
 )
 from .ops import (  # noqa: F401
+    Combine,
+    CombineNorm,
     Embed,
     KVCommit,
     KVStore,

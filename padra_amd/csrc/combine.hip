@@ -1,0 +1,215 @@
+// Expert combine (+ residual) and the fused combine + RMSNorm (+ FP8 E4M3) that follows the
+// MoE down projection.
+//
+// Combine (inference.cu:580-590), exl3_packed_activations::Combine
+// (expert_exl3_prefill_packed_activations.cuh:86-102): for row t and column i,
+//   c = 0;  for e = 0..7: c = B(c + B(down[t][e][i] * w[t][e]));  x = residual ? B(x + c) : c
+// with the experts in their routing order.  combine_norm_exact::CombineNorm
+// (combine_norm_exact.cuh:7-72) continues with the 128-thread RMSNorm of the new row and,
+// optionally, its E4M3 encoding.
+#include <stdio.h>
+
+#include <algorithm>
+
+#include "norm_fp8.h"
+
+using namespace padra;
+
+namespace {
+
+constexpr int kExperts = 8; // the reference's top-8 routing
+
+int launched(const char *what) {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    fprintf(stderr, "padra: %s launch failed: %s\n", what, hipGetErrorString(e));
+    return PADRA_INTERNAL;
+  }
+  return PADRA_OK;
+}
+bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// The combine of 8 consecutive columns: every load (the row's 8 weights, the 8 expert rows,
+// x) is issued before the arithmetic.  Returns the packed BF16 results; `fine` is false
+// when one of them is not finite.
+template <class T, bool RES>
+__device__ __forceinline__ void combine8(const T *x, const T *down, size_t expert_stride,
+                                         const float *w, uint32_t (&out)[4], bool &fine) {
+  float d[kExperts][8], xv[8];
+  float wt[kExperts];
+#pragma unroll
+  for (int e = 0; e < kExperts; ++e)
+    wt[e] = w[e];
+#pragma unroll
+  for (int e = 0; e < kExperts; ++e)
+    ActIO<T>::load8(down + e * expert_stride, d[e]);
+  if constexpr (RES)
+    ActIO<T>::load8(x, xv);
+  float c[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k)
+    c[k] = 0.f;
+#pragma unroll
+  for (int e = 0; e < kExperts; ++e) {
+#pragma unroll
+    for (int k = 0; k < 8; k += 2) {
+      const uint32_t p = pack2(d[e][k] * wt[e], d[e][k + 1] * wt[e]);
+      const uint32_t q = pack2(c[k] + lo16(p), c[k + 1] + hi16(p));
+      c[k] = lo16(q);
+      c[k + 1] = hi16(q);
+    }
+  }
+  uint32_t bad_bits = 0;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    out[k] = RES ? pack2(xv[2 * k] + c[2 * k], xv[2 * k + 1] + c[2 * k + 1])
+                 : pack2(c[2 * k], c[2 * k + 1]);
+    // a half is not finite iff its exponent bits are all ones
+    bad_bits |= ((out[k] & 0x7f80u) == 0x7f80u) | ((out[k] & 0x7f800000u) == 0x7f800000u);
+  }
+  fine = bad_bits == 0;
+}
+
+// Plain combine: one thread per 8 consecutive columns, grid-stride over the rows.
+template <class T, bool RES>
+__global__ __launch_bounds__(256) void k_combine(T *x, const T *down, const float *weights,
+                                                 int hidden, long long groups, int *bad) {
+  const int per_row = hidden / 8;
+  bool all_fine = true;
+  for (long long g = blockIdx.x * 256ll + threadIdx.x; g < groups; g += (long long)gridDim.x * 256) {
+    const long long t = g / per_row;
+    const int col = (int)(g - t * per_row) * 8;
+    T *xr = x + t * hidden + col;
+    uint32_t out[4];
+    bool fine;
+    combine8<T, RES>(xr, down + (t * kExperts) * hidden + col, (size_t)hidden,
+                     weights + t * kExperts, out, fine);
+    ActIO<T>::store8(xr, out);
+    all_fine = all_fine && fine;
+  }
+  if (!all_fine)
+    raise_bad(bad);
+}
+
+// Combine + RMSNorm (+ FP8): one wave per row.  The combine runs in the natural layout
+// (lane l takes columns 8l..8l+7 of each 512-column chunk, 16-byte accesses), its BF16
+// results go through LDS, and the norm reads them back in the 128-thread ownership layout
+// (lane l: columns 2l, 2l+1 of each 128).
+template <int J, class T, bool FP8>
+__global__ __launch_bounds__(64) void k_combine_norm(T *x, const T *down, const float *weights,
+                                                     NormFP8Args<T> a) {
+  constexpr int H = 128 * J, CHUNKS = (H + 511) / 512;
+  __shared__ uint32_t v_lds[H / 2];
+  const int row = blockIdx.x, lane = threadIdx.x & 63;
+  if (row >= a.rows)
+    return;
+  Lanes<uint16_t, 2> gr[J];
+  norm_load_gamma<128, J>(a.gamma, gr);
+  bool fine = true;
+#pragma unroll
+  for (int ch = 0; ch < CHUNKS; ++ch) {
+    const int col = ch * 512 + 8 * lane;
+    if (col < H) {
+      T *xr = x + (size_t)row * H + col;
+      uint32_t out[4];
+      bool f;
+      combine8<T, true>(xr, down + (size_t)row * kExperts * H + col, (size_t)H,
+                        weights + (size_t)row * kExperts, out, f);
+      ActIO<T>::store8(xr, out);
+      fine = fine && f;
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        v_lds[col / 2 + k] = out[k];
+    }
+  }
+  if (__ballot(!fine) != 0 && lane == 0)
+    raise_bad(a.bad);
+  __syncthreads();
+  uint32_t vp[J];
+#pragma unroll
+  for (int j = 0; j < J; ++j)
+    vp[j] = v_lds[64 * j + lane];
+  norm_fp8_finish<J, T, FP8>(a, row, vp, gr);
+}
+
+#define PADRA_COMBINE_J(JV)                                                                  \
+  case JV:                                                                                   \
+    return f(std::integral_constant<int, JV>{});
+template <class F> int combine_shape(int hidden, F &&f) {
+  if (hidden % 128)
+    return PADRA_UNSUPPORTED;
+  switch (hidden / 128) {
+    PADRA_COMBINE_J(8)
+    PADRA_COMBINE_J(9)
+    PADRA_COMBINE_J(16)
+    PADRA_COMBINE_J(18)
+    PADRA_COMBINE_J(32)
+    PADRA_COMBINE_J(36)
+  }
+  return PADRA_UNSUPPORTED;
+}
+#undef PADRA_COMBINE_J
+
+} // namespace
+
+extern "C" int padra_Combine(void *stream, void *x, const void *down, const float *weights,
+                             int rows, int hidden, int experts, int residual, int *bad,
+                             int act) {
+  if (!x || !down || !weights || !bad || rows < 1 || hidden < 8 || hidden % 8 ||
+      (act != PADRA_ACT_BF16 && act != PADRA_ACT_F32) || !aligned16(x) || !aligned16(down))
+    return PADRA_INVALID_ARGUMENT;
+  if (experts != kExperts)
+    return PADRA_UNSUPPORTED;
+  const long long groups = (long long)rows * (hidden / 8);
+  const unsigned grid = (unsigned)std::min<long long>((groups + 255) / 256, 8192);
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  auto launch = [&](auto tag) -> int {
+    using T = decltype(tag);
+    if (residual)
+      hipLaunchKernelGGL((k_combine<T, true>), dim3(grid), dim3(256), 0, s, static_cast<T *>(x),
+                         static_cast<const T *>(down), weights, hidden, groups, bad);
+    else
+      hipLaunchKernelGGL((k_combine<T, false>), dim3(grid), dim3(256), 0, s,
+                         static_cast<T *>(x), static_cast<const T *>(down), weights, hidden,
+                         groups, bad);
+    return launched("Combine");
+  };
+  return act == PADRA_ACT_BF16 ? launch(uint16_t{}) : launch(float{});
+}
+
+extern "C" int padra_CombineNorm(void *stream, void *x, const void *down, const float *weights,
+                                 void *normalized, const uint16_t *gamma, uint8_t *packed,
+                                 float *scales, int rows, int hidden, int experts, float eps,
+                                 float *statistics, int *bad, int act) {
+  if (!x || !down || !weights || !normalized || !gamma || !bad || x == normalized || rows < 1 ||
+      !(eps >= 0.f) || (act != PADRA_ACT_BF16 && act != PADRA_ACT_F32) || !aligned16(x) ||
+      !aligned16(down) || !aligned16(normalized) || !aligned16(gamma) ||
+      (packed && (!scales || !aligned16(packed))))
+    return PADRA_INVALID_ARGUMENT;
+  if (experts != kExperts)
+    return PADRA_UNSUPPORTED;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  auto launch = [&](auto tag) -> int {
+    using T = decltype(tag);
+    NormFP8Args<T> a;
+    a.x = static_cast<const T *>(x);
+    a.y = static_cast<T *>(normalized);
+    a.gamma = gamma;
+    a.packed = packed;
+    a.scales = scales;
+    a.stats = statistics;
+    a.bad = bad;
+    a.rows = rows;
+    a.eps = eps;
+    return combine_shape(hidden, [&](auto j) -> int {
+      if (packed)
+        hipLaunchKernelGGL((k_combine_norm<j.value, T, true>), dim3(rows), dim3(64), 0, s,
+                           static_cast<T *>(x), static_cast<const T *>(down), weights, a);
+      else
+        hipLaunchKernelGGL((k_combine_norm<j.value, T, false>), dim3(rows), dim3(64), 0, s,
+                           static_cast<T *>(x), static_cast<const T *>(down), weights, a);
+      return launched("CombineNorm");
+    });
+  };
+  return act == PADRA_ACT_BF16 ? launch(uint16_t{}) : launch(float{});
+}

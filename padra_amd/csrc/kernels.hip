@@ -41,6 +41,42 @@ template <class T, int FMT> __global__ __launch_bounds__(64) PADRA_WAVES_PER_EU 
   qk_heads_wave<T, FMT>(a, blockIdx.x);
 }
 
+// Self-check of the two fast-path identities, over their whole domains:
+//   A. e4m3_pair_hw(x) == e4m3_code(x) for every float with |x| <= 480 (2.28e9 inputs);
+//   B. for every BF16 maximum m >= 2^-100 (scale = m/448, inverse normal) and every BF16
+//      v with |v| <= m, both signs: code of fp8_quotient == code of the correctly rounded
+//      division (2.1e9 pairs).
+// Mismatches are added to counts[0] (A) and counts[1] (B).
+__global__ __launch_bounds__(256) void k_check_fp8_hw(unsigned long long n,
+                                                      unsigned long long *counts) {
+  unsigned long long bad = 0;
+  const unsigned long long stride = (unsigned long long)gridDim.x * blockDim.x;
+  for (unsigned long long i = blockIdx.x * (unsigned long long)blockDim.x + threadIdx.x; i < n;
+       i += stride) {
+    const float x = __uint_as_float((uint32_t)(i >> 1) | ((uint32_t)(i & 1) << 31));
+    bad += (e4m3_pair_hw(x, 0.f) & 0xffu) != e4m3_code(x);
+  }
+  if (bad)
+    atomicAdd(&counts[0], bad);
+}
+__global__ __launch_bounds__(256) void k_check_fp8_quotient(unsigned long long *counts) {
+  const uint32_t mb = blockIdx.x + 1; // BF16 bits of the maximum, 0x0001 .. 0x7f7f
+  const float amax = __uint_as_float(mb << 16);
+  const float scale = amax / 448.f, inverse = 1.f / scale;
+  if (!fp8_fast_ok(amax, inverse))
+    return; // block-uniform
+  unsigned long long bad = 0;
+  for (uint32_t vb = threadIdx.x; vb <= mb; vb += blockDim.x) {
+#pragma unroll
+    for (int sg = 0; sg < 2; ++sg) {
+      const float v = __uint_as_float((vb << 16) | (sg ? 0x80000000u : 0u));
+      bad += (e4m3_pair_hw(fp8_quotient(v, scale, inverse), 0.f) & 0xffu) != e4m3_code(v / scale);
+    }
+  }
+  if (bad)
+    atomicAdd(&counts[1], bad);
+}
+
 __global__ void k_zero_u64(unsigned long long *p, int n) {
   if ((int)threadIdx.x < n)
     p[threadIdx.x] = 0;

@@ -88,26 +88,19 @@ __device__ __forceinline__ void fp8_encode_pairs(const uint32_t (&w)[J], float s
   }
 }
 
-template <int J, class T>
-__device__ __forceinline__ void norm_fp8_row_wave(const NormFP8Args<T> &a, int row) {
+// Everything after the row's values are in registers: lane l holds v_{2l+k+128j} (k = 0, 1)
+// in vp[j] (BF16 pair) and the matching gamma pairs.  The 128-thread tree, the normalized
+// row, and with FP8 the scale and codes.
+template <int J, class T, bool FP8>
+__device__ __forceinline__ void norm_fp8_finish(const NormFP8Args<T> &a, int row,
+                                                const uint32_t (&vp)[J],
+                                                const Lanes<uint16_t, 2> (&gr)[J]) {
   constexpr int VT = 128, K = 2, H = VT * J;
-  if (row >= a.rows)
-    return; // wave-uniform
   const int lane = threadIdx.x & 63;
   const size_t off = (size_t)row * H + K * lane;
-  Lanes<T, K> x[J];
-  Lanes<uint16_t, K> gr[J];
-#pragma unroll
-  for (int j = 0; j < J; ++j)
-    x[j].load(a.x + off + VT * j);
-  norm_load_gamma<VT, J>(a.gamma, gr);
-
-  // Sum of squares: thread 2l+k owns elements 2l + k + 128 j, summed in j order.
-  uint32_t vp[J];
   float s[K] = {0.f, 0.f}, e[K] = {0.f, 0.f};
 #pragma unroll
   for (int j = 0; j < J; ++j) {
-    vp[j] = pack2(x[j].get(0), x[j].get(1));
     const float v0 = lo16(vp[j]), v1 = hi16(vp[j]);
     acc_pos(v0 * v0, s[0], e[0]);
     acc_pos(v1 * v1, s[1], e[1]);
@@ -144,71 +137,57 @@ __device__ __forceinline__ void norm_fp8_row_wave(const NormFP8Args<T> &a, int r
   const bool row_fine = mag < 0x7f80u;
   if (!row_fine && lane == 0)
     raise_bad(a.bad);
-  if (!row_fine) {
-    // MaxReduce's fmaxf drops NaN operands: the maximum over the non-NaN magnitudes.
-    mag = 0;
+  if constexpr (FP8) {
+    if (!row_fine) {
+      // MaxReduce's fmaxf drops NaN operands: the maximum over the non-NaN magnitudes.
+      mag = 0;
 #pragma unroll
-    for (int j = 0; j < J; ++j) {
-      const uint32_t lo = yw[j] & 0x7fffu, hi = (yw[j] >> 16) & 0x7fffu;
-      mag = max(mag, lo > 0x7f80u ? 0u : lo);
-      mag = max(mag, hi > 0x7f80u ? 0u : hi);
+      for (int j = 0; j < J; ++j) {
+        const uint32_t lo = yw[j] & 0x7fffu, hi = (yw[j] >> 16) & 0x7fffu;
+        mag = max(mag, lo > 0x7f80u ? 0u : lo);
+        mag = max(mag, hi > 0x7f80u ? 0u : hi);
+      }
+#pragma unroll
+      for (int d = 32; d >= 1; d /= 2)
+        mag = max(mag, (uint32_t)__shfl_xor((int)mag, d, 64));
     }
-#pragma unroll
-    for (int d = 32; d >= 1; d /= 2)
-      mag = max(mag, (uint32_t)__shfl_xor((int)mag, d, 64));
-  }
-  const float amax = __uint_as_float(mag << 16);
-  const float scale = amax == 0.f ? 1.f : amax / 448.f;
-  const float inverse = 1.f / scale;
-  if (lane == 0)
-    a.scales[row] = scale;
+    const float amax = __uint_as_float(mag << 16);
+    const float scale = amax == 0.f ? 1.f : amax / 448.f;
+    const float inverse = 1.f / scale;
+    if (lane == 0)
+      a.scales[row] = scale;
 
-  // Codes: two per j, one 2-byte store each (128 contiguous bytes per instruction).
-  uint32_t codes[J];
-  if (row_fine && fp8_fast_ok(amax, inverse)) // wave-uniform
-    fp8_encode_pairs<J, true>(yw, scale, inverse, codes);
-  else
-    fp8_encode_pairs<J, false>(yw, scale, inverse, codes);
-  uint8_t *const out = a.packed + off;
+    // Codes: two per j, one 2-byte store each (128 contiguous bytes per instruction).
+    uint32_t codes[J];
+    if (row_fine && fp8_fast_ok(amax, inverse)) // wave-uniform
+      fp8_encode_pairs<J, true>(yw, scale, inverse, codes);
+    else
+      fp8_encode_pairs<J, false>(yw, scale, inverse, codes);
+    uint8_t *const out = a.packed + off;
+#pragma unroll
+    for (int j = 0; j < J; ++j)
+      *reinterpret_cast<uint16_t *>(out + VT * j) = (uint16_t)codes[j];
+  }
+}
+
+template <int J, class T>
+__device__ __forceinline__ void norm_fp8_row_wave(const NormFP8Args<T> &a, int row) {
+  constexpr int VT = 128, K = 2, H = VT * J;
+  if (row >= a.rows)
+    return; // wave-uniform
+  const size_t off = (size_t)row * H + K * (threadIdx.x & 63);
+  Lanes<T, K> x[J];
+  Lanes<uint16_t, K> gr[J];
 #pragma unroll
   for (int j = 0; j < J; ++j)
-    *reinterpret_cast<uint16_t *>(out + VT * j) = (uint16_t)codes[j];
-}
-
-// Self-check of the two fast-path identities, over their whole domains:
-//   A. e4m3_pair_hw(x) == e4m3_code(x) for every float with |x| <= 480 (2.28e9 inputs);
-//   B. for every BF16 maximum m >= 2^-100 (scale = m/448, inverse normal) and every BF16
-//      v with |v| <= m, both signs: code of fp8_quotient == code of the correctly rounded
-//      division (2.1e9 pairs).
-// Mismatches are added to counts[0] (A) and counts[1] (B).
-__global__ __launch_bounds__(256) void k_check_fp8_hw(unsigned long long n,
-                                                      unsigned long long *counts) {
-  unsigned long long bad = 0;
-  const unsigned long long stride = (unsigned long long)gridDim.x * blockDim.x;
-  for (unsigned long long i = blockIdx.x * (unsigned long long)blockDim.x + threadIdx.x; i < n;
-       i += stride) {
-    const float x = __uint_as_float((uint32_t)(i >> 1) | ((uint32_t)(i & 1) << 31));
-    bad += (e4m3_pair_hw(x, 0.f) & 0xffu) != e4m3_code(x);
-  }
-  if (bad)
-    atomicAdd(&counts[0], bad);
-}
-__global__ __launch_bounds__(256) void k_check_fp8_quotient(unsigned long long *counts) {
-  const uint32_t mb = blockIdx.x + 1; // BF16 bits of the maximum, 0x0001 .. 0x7f7f
-  const float amax = __uint_as_float(mb << 16);
-  const float scale = amax / 448.f, inverse = 1.f / scale;
-  if (!fp8_fast_ok(amax, inverse))
-    return; // block-uniform
-  unsigned long long bad = 0;
-  for (uint32_t vb = threadIdx.x; vb <= mb; vb += blockDim.x) {
+    x[j].load(a.x + off + VT * j);
+  norm_load_gamma<VT, J>(a.gamma, gr);
+  // Thread 2l+k owns elements 2l + k + 128 j, summed in j order.
+  uint32_t vp[J];
 #pragma unroll
-    for (int sg = 0; sg < 2; ++sg) {
-      const float v = __uint_as_float((vb << 16) | (sg ? 0x80000000u : 0u));
-      bad += (e4m3_pair_hw(fp8_quotient(v, scale, inverse), 0.f) & 0xffu) != e4m3_code(v / scale);
-    }
-  }
-  if (bad)
-    atomicAdd(&counts[1], bad);
+  for (int j = 0; j < J; ++j)
+    vp[j] = pack2(x[j].get(0), x[j].get(1));
+  norm_fp8_finish<J, T, true>(a, row, vp, gr);
 }
 
 } // namespace padra

@@ -61,6 +61,26 @@ def NormFP8(x, normalized, gamma, packed, scales, bad, eps=1e-6, statistics=None
              _p(scales), rows, hidden, float(eps), _p(statistics), _p(bad), _act(x))
 
 
+def Combine(x, down, weights, bad, residual=True):
+    """x <- [B(x + c) | c], c the ordered BF16 combine of the 8 expert rows
+    (Combine, inference.cu:580-590).  down [rows][8][hidden], weights [rows][8] fp32."""
+    _need_cuda(x, down, weights, bad)
+    rows, hidden = x.shape[0], x.shape[-1]
+    abi.call("padra_Combine", _stream(x), _p(x), _p(down), _p(weights), rows, hidden,
+             down.shape[1], int(bool(residual)), _p(bad), _act(x))
+
+
+def CombineNorm(x, down, weights, normalized, gamma, bad, packed=None, scales=None, eps=1e-6,
+                statistics=None):
+    """Residual combine, then RMSNorm (+ FP8 when packed is given)
+    (combine_norm_exact::CombineNorm, combine_norm_exact.cuh:7-72)."""
+    _need_cuda(x, down, weights, normalized, gamma, bad, packed, scales, statistics)
+    rows, hidden = x.shape[0], x.shape[-1]
+    abi.call("padra_CombineNorm", _stream(x), _p(x), _p(down), _p(weights), _p(normalized),
+             _p(gamma), _p(packed), _p(scales), rows, hidden, down.shape[1], float(eps),
+             _p(statistics), _p(bad), _act(x))
+
+
 def RopeTable(positions, head_dim=128, theta=1e6, yarn=False, factor=16.0,
               original_context=8192) -> torch.Tensor:
     """Host BF16 cos|sin table [positions][head_dim] (RopeTable, inference.cu:764-785)."""

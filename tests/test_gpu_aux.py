@@ -292,3 +292,77 @@ def test_embed_sources(oracle):
     assert np.all(got[9] == 9.0)
     keep = [s for s in range(64) if s != 9]
     assert np.array_equal(synth.bf16_bits(got[keep]), want[keep])
+
+
+# ---- expert combine ----------------------------------------------------------------------
+
+def _combine_inputs(rows, hidden, seed):
+    rng = np.random.default_rng(seed)
+    d = synth.chain_inputs(rows, hidden=hidden, outliers=True, seed=seed)
+    down = synth.bf16_bits((rng.standard_normal((rows, 8, hidden)) * 0.5).astype(np.float32))
+    w = rng.dirichlet(np.ones(8), rows).astype(np.float32)
+    return d, down, w
+
+
+@pytest.mark.parametrize("residual", [True, False])
+@pytest.mark.parametrize("act", ["bf16", "f32"])
+def test_combine(oracle, residual, act):
+    print(f"[case] combine residual={residual} act={act}", flush=True)
+    rows, hidden = 300, 2304
+    d, down, w = _combine_inputs(rows, hidden, 31)
+    want, want_bad = oracle.combine(d["x"], down, w, residual=residual)
+    if act == "bf16":
+        x, dn = dev(d["x"]), dev(down)
+    else:
+        x = torch.from_numpy(synth.bf16_to_f32(d["x"])).cuda()
+        dn = torch.from_numpy(synth.bf16_to_f32(down)).cuda()
+    bad = flag()
+    ops.Combine(x, dn, torch.from_numpy(w).cuda(), bad, residual=residual)
+    torch.cuda.synchronize()
+    got = host16(x) if act == "bf16" else synth.bf16_bits(x.cpu().numpy())
+    assert np.array_equal(got, want)
+    assert bool(bad.item()) == want_bad
+
+
+@pytest.mark.parametrize("hidden", [2048, 2304])
+@pytest.mark.parametrize("fp8", [True, False])
+def test_combine_norm(oracle, hidden, fp8):
+    print(f"[case] combine norm hidden={hidden} fp8={fp8}", flush=True)
+    rows = 67
+    d, down, w = _combine_inputs(rows, hidden, 32 + hidden)
+    want_x, want_y, want_p, want_s, want_st, want_bad = oracle.combine_norm(
+        d["x"], down, w, d["gamma"], fp8=fp8)
+    x = dev(d["x"])
+    y = torch.empty_like(x)
+    packed = torch.empty((rows, hidden), dtype=torch.uint8, device="cuda") if fp8 else None
+    scales = torch.empty(rows, dtype=torch.float32, device="cuda") if fp8 else None
+    st = torch.empty(2, dtype=torch.float32, device="cuda")
+    bad = flag()
+    ops.CombineNorm(x, dev(down), torch.from_numpy(w).cuda(), y, dev(d["gamma"]), bad,
+                    packed=packed, scales=scales, statistics=st)
+    torch.cuda.synchronize()
+    assert np.array_equal(host16(x), want_x) and np.array_equal(host16(y), want_y)
+    assert np.array_equal(st.cpu().numpy(), want_st)
+    if fp8:
+        assert np.array_equal(packed.cpu().numpy(), want_p)
+        assert np.array_equal(scales.cpu().numpy(), want_s)
+    assert bool(bad.item()) == want_bad
+
+
+def test_combine_nonfinite_sets_bad(oracle):
+    rows, hidden = 4, 2304
+    d, down, w = _combine_inputs(rows, hidden, 33)
+    down = down.copy()
+    down[2, 3, 17] = 0x7F80
+    want_x, want_bad = oracle.combine(d["x"], down, w)
+    assert want_bad
+    x = dev(d["x"])
+    bad = flag()
+    ops.Combine(x, dev(down), torch.from_numpy(w).cuda(), bad)
+    torch.cuda.synchronize()
+    assert bad.item() == 1 and np.array_equal(host16(x), want_x)
+    y = torch.empty_like(x)
+    bad2 = flag()
+    ops.CombineNorm(dev(d["x"]), dev(down), torch.from_numpy(w).cuda(), y, dev(d["gamma"]), bad2)
+    torch.cuda.synchronize()
+    assert bad2.item() == 1

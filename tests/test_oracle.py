@@ -29,6 +29,10 @@ Per oracle function, what checks it:
                                   float32 + torch) on values aimed at every E4M3 midpoint
   po_norm_fp8                     y = po_rmsnorm's, scale = max|y|/448, codes = torch
                                   float8 of y/scale, zero row, non-finite row
+  po_combine                      one-hot weights give B(x + down_e); power-of-two weights
+                                  on small integers are exact; float64 weighted sum within
+                                  the rounding bound; the expert order of the accumulation
+  po_combine_norm                 = po_combine, then po_norm_fp8 / po_rmsnorm of the new x
 """
 import numpy as np
 import pytest
@@ -259,6 +263,67 @@ def test_norm_fp8(oracle):
     x[5, 9] = 0x7FC0  # NaN input
     *_, bad = oracle.norm_fp8(x, d["gamma"])
     assert bad
+
+
+# ---- Expert combine ---------------------------------------------------------------------
+
+def test_combine_closed_forms(oracle):
+    rng = np.random.default_rng(21)
+    rows, experts, hidden = 3, 8, 256
+    x = synth.bf16_bits(rng.standard_normal((rows, hidden)).astype(F32))
+    down = synth.bf16_bits(rng.standard_normal((rows, experts, hidden)).astype(F32))
+    onehot = np.zeros((rows, experts), F32)
+    onehot[np.arange(rows), [0, 5, 7]] = 1
+    got, bad = oracle.combine(x, down, onehot)
+    pick = down[np.arange(rows), [0, 5, 7]]
+    want = synth.bf16_bits(synth.bf16_to_f32(x) + synth.bf16_to_f32(pick))
+    assert not bad and np.array_equal(got, want)
+    got, _ = oracle.combine(x, down, onehot, residual=False)
+    assert np.array_equal(got, pick)
+    # small integers times powers of two: every step exact
+    ints = rng.integers(-8, 9, (rows, experts, hidden)).astype(F32)
+    w = np.exp2(-rng.integers(0, 4, (rows, experts))).astype(F32)
+    got, _ = oracle.combine(np.zeros((rows, hidden), np.uint16), synth.bf16_bits(ints), w,
+                            residual=False)
+    assert np.array_equal(synth.bf16_to_f32(got), (ints * w[:, :, None]).sum(axis=1))
+
+
+def test_combine_rounding_bound_and_order(oracle):
+    rng = np.random.default_rng(22)
+    rows, experts, hidden = 4, 8, 512
+    down = synth.bf16_bits(rng.standard_normal((rows, experts, hidden)).astype(F32))
+    w = rng.dirichlet(np.ones(experts), rows).astype(F32)
+    got, _ = oracle.combine(np.zeros((rows, hidden), np.uint16), down, w, residual=False)
+    exact = (synth.bf16_to_f32(down).astype(np.float64) * w[:, :, None]).sum(axis=1)
+    # 16 BF16 roundings of partial sums bounded by sum |d w|
+    bound = 16 * 2.0**-8 * (np.abs(synth.bf16_to_f32(down)) * w[:, :, None]).sum(axis=1)
+    assert np.all(np.abs(synth.bf16_to_f32(got) - exact) <= bound + 1e-30)
+    # the accumulation runs e = 0..7: reversing the experts changes some results
+    rev, _ = oracle.combine(np.zeros((rows, hidden), np.uint16), down[:, ::-1].copy(),
+                            w[:, ::-1].copy(), residual=False)
+    assert not np.array_equal(rev, got)
+    seq = np.zeros((rows, hidden), F32)
+    for e in range(experts):
+        prod = synth.bf16_to_f32(synth.bf16_bits(synth.bf16_to_f32(down[:, e]) * w[:, e:e + 1]))
+        seq = synth.bf16_to_f32(synth.bf16_bits(seq + prod))
+    assert np.array_equal(synth.bf16_to_f32(got), seq)
+
+
+def test_combine_norm_composition(oracle):
+    rng = np.random.default_rng(23)
+    rows, experts, hidden = 5, 8, 2304
+    d = synth.chain_inputs(rows, hidden=hidden, outliers=True, seed=24)
+    down = synth.bf16_bits(rng.standard_normal((rows, experts, hidden)).astype(F32))
+    w = rng.dirichlet(np.ones(experts), rows).astype(F32)
+    xn, y, packed, scales, stats, bad = oracle.combine_norm(d["x"], down, w, d["gamma"])
+    assert not bad
+    want_x, _ = oracle.combine(d["x"], down, w)
+    assert np.array_equal(xn, want_x)
+    y2, p2, s2, st2, _ = oracle.norm_fp8(want_x, d["gamma"])
+    assert np.array_equal(y, y2) and np.array_equal(packed, p2) and np.array_equal(scales, s2)
+    assert np.array_equal(stats, st2)
+    _, y3, none_p, none_s, _, _ = oracle.combine_norm(d["x"], down, w, d["gamma"], fp8=False)
+    assert none_p is None and np.array_equal(y3, y)
 
 
 # ---- A5 --------------------------------------------------------------------------------
