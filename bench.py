@@ -278,6 +278,39 @@ def bench_norm_fp8(torch, steps, sets=8):
             "frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
 
 
+def bench_combine_norm(torch, steps, sets=8):
+    """The step after the expert down projection over the config-1 chunk: the ordered BF16
+    combine of 8 expert rows into the residual, the RMSNorm and its FP8 encoding; 2048 rows
+    of 2048.  Reads down (8 rows) and x, writes x, normalized and codes."""
+    from padra_amd import ops, synth
+    rng = np.random.default_rng(0)
+    host = synth.chain_inputs(TOKENS, HIDDEN, HQ, HKV, D, outliers=True, seed=0)
+    down_h = synth.bf16_bits((rng.standard_normal((TOKENS, 8, HIDDEN)) * 0.5).astype(np.float32))
+    w = torch.from_numpy(rng.dirichlet(np.ones(8), TOKENS).astype(np.float32)).cuda()
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).cuda()
+    g = dev(host["gamma"])
+    bad = torch.zeros(1, dtype=torch.int32, device="cuda")
+    bufs = []
+    for _ in range(sets):
+        x = dev(host["x"])
+        bufs.append((x, dev(down_h), torch.empty_like(x),
+                     torch.empty((TOKENS, HIDDEN), dtype=torch.uint8, device="cuda"),
+                     torch.empty(TOKENS, dtype=torch.float32, device="cuda")))
+
+    def step(i):
+        x, down, y, packed, scales = bufs[i % sets]
+        ops.CombineNorm(x, down, w, y, g, bad, packed=packed, scales=scales)
+
+    ms = graph_time(torch, step, steps)
+    if bad.item():
+        raise SystemExit("device error flag set in the combine + norm benchmark")
+    nbytes = TOKENS * (HIDDEN * (8 * 2 + 2 + 2 + 2 + 1) + 8 * 4 + 4)
+    return {"workload": "expert combine (8 rows) + residual + RMSNorm + FP8, 2048 rows x 2048",
+            "us_per_launch": round(ms * 1e3, 3), "bytes_per_launch": nbytes,
+            "gbs": round(nbytes / (ms * 1e-3) / 1e9, 2),
+            "frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+
+
 def bench_decode(torch, steps, seqs, vocab=131072, capacity=CAPACITY):
     """Config 4 (seqs=64) and the GPU side of config 0 (seqs=1): embedding gather, then the
     fused residual-norm (256-thread decode tree) + Q/K norm + RoPE + BF16 KV store at each
@@ -417,7 +450,8 @@ def main():
         line["configs"] = {"config3": bench_swiglu(torch, 50),
                            "config4": bench_decode(torch, 100, 64),
                            "config0_gpu": bench_decode(torch, 200, 1, capacity=8192),
-                           "norm_fp8": bench_norm_fp8(torch, 200)}
+                           "norm_fp8": bench_norm_fp8(torch, 200),
+                           "combine_norm": bench_combine_norm(torch, 100)}
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(host, args.cpu_seconds, cpu_threads())
         if not args.no_configs:

@@ -1,6 +1,8 @@
 // Per-head Q/K RMSNorm + NeoX RoPE, and the KV-cache store of the rotated K row and
-// the V row in BF16, q8 or q8_0 form.  Two lanes per 128-wide head vector, 32 head
-// vectors per wavefront.
+// the V row in BF16, q8 or q8_0 form, with two lanes per 128-wide head vector and 32 head
+// vectors per wavefront: the fp32-activation path, and the lane-pair encoders the
+// store-only kernel (padra_KVStore) uses.  BF16 activations take the four-lane layout of
+// qk_quad.h, which builds on the helpers here.
 //
 // Reference: QKNormRopeStoreControlled (qk_rope_store_exact.cuh:4-49), QKNormRope
 // (qknorm_rope.cuh:4-50), QKNormRopePair64 (qknorm_rope_pair64.cuh:3-83).  The reference
@@ -446,25 +448,7 @@ __device__ __forceinline__ void qk_heads_wave_direct(const QKArgs<T> &a, long lo
   }
 }
 
-
-// ---- BF16 path: wave blocks staged through LDS ------------------------------------------
-//
-// A wave's 32 head vectors are one contiguous 8 KB block per role (the boundary waves
-// between roles aside).  Global memory is read and written as eight 1 KB instructions,
-// each lane moving one 16-byte chunk (8 features), which the memory system serves as
-// whole cache lines; the chunks are transposed through LDS into the lane-pair layout of
-// the arithmetic (lane 2j + half: features 32*half + i and 64 + 32*half + i of head j).
-// Slot (pair lane pl, piece mp) of the LDS image sits at mp * 64 + (pl + 2*mp) mod 64:
-// reads are one contiguous 1 KB row per piece, and the 16 chunks of one head written by
-// 16 neighbouring lanes land in 16 different bank groups.
-
-__device__ __forceinline__ int stage_slot(int pl, int mp) { return mp * 64 + ((pl + 2 * mp) & 63); }
-// Chunk ci (features 8ci..8ci+7) of head j of the block.
-__device__ __forceinline__ int chunk_slot(int j, int ci) {
-  const int half = (ci >> 2) & 1, mp = (ci & 3) + 4 * (ci >> 3);
-  return stage_slot(2 * j + half, mp);
-}
-
+// The source row of head vector hv of the flat index space (q heads, k heads, v heads).
 template <class A>
 __device__ __forceinline__ const uint16_t *head_src(const A &a, unsigned hv, unsigned nq,
                                                     unsigned nk) {
@@ -472,230 +456,5 @@ __device__ __forceinline__ const uint16_t *head_src(const A &a, unsigned hv, uns
   return hv < nq ? a.q + (size_t)hv * D
                  : (hv < nq + nk ? a.k + (size_t)(hv - nq) * D : a.v + (size_t)(hv - nq - nk) * D);
 }
-
-// An all-V block with a BF16 cache: a coalesced copy of each token's V row into its slot.
-template <class A>
-__device__ __forceinline__ void v_rows_copy(const A &a, unsigned block0, unsigned nq, unsigned nk) {
-  constexpr int D = 128;
-  const int lane = threadIdx.x & 63;
-  const int features = a.hkv * D;
-  // Loads first (clamped, unconditional), so that all eight are in flight together.
-  uint4 d[8];
-  PosState ps[8];
-#pragma unroll
-  for (int m = 0; m < 8; ++m) {
-    const unsigned idx = min(block0 + (unsigned)((64 * m + lane) >> 4) - nq - nk, nk - 1u);
-    ps[m] = fetch_state(a.pos, (int)(idx / (unsigned)a.hkv));
-    d[m] = ld_nt(reinterpret_cast<const uint4 *>(a.v + (size_t)idx * D) + ((64 * m + lane) & 15));
-  }
-#pragma unroll
-  for (int m = 0; m < 8; ++m) {
-    const int c = 64 * m + lane;
-    const unsigned idx = block0 + (unsigned)(c >> 4) - nq - nk;
-    if (idx >= nk)
-      continue;
-    const int t = (int)(idx / (unsigned)a.hkv), h = (int)(idx % (unsigned)a.hkv), ci = c & 15;
-    bool ok;
-    const int pos = resolve_position(a.pos, ps[m], t, a.cap, a.first, false, ok);
-    if (!ok || pos < 0 || pos >= a.table_rows) {
-      if (ci == 0)
-        raise_bad(a.bad);
-      continue;
-    }
-    if (t < a.first)
-      continue;
-    const long long seq = a.pos.mode == PADRA_POS_DECODE ? t : 0;
-    const long long slot = seq * a.seq_stride + pos % a.cap;
-    st_nt(reinterpret_cast<uint4 *>(static_cast<uint16_t *>(a.vc) + slot * features + h * D) + ci, d[m]);
-  }
-}
-
-template <int FMT>
-__device__ __forceinline__ void qk_heads_wave_staged(const QKArgs<uint16_t> &a, long long wave) {
-  constexpr int D = 128;
-  __shared__ uint4 stage[512];
-  __shared__ int head_pos[32]; // per head of the block: cache position, -1 = write nothing
-  const int lane = threadIdx.x & 63, half = lane & 1;
-  const unsigned block0 = (unsigned)wave * 32u;
-  const unsigned nq = (unsigned)a.tokens * (unsigned)a.hq;
-  const unsigned nk = (unsigned)a.tokens * (unsigned)a.hkv;
-  const unsigned total = nq + nk + (FMT >= 0 ? nk : 0u);
-  if constexpr (FMT == PADRA_KV_BF16) {
-    if (block0 >= nq + nk) { // wave-uniform
-      v_rows_copy(a, block0, nq, nk);
-      return;
-    }
-  }
-
-  // This lane pair's head vector; its control record is requested first.
-  const unsigned hv = block0 + (unsigned)(lane >> 1);
-  const bool live = hv < total;
-  const int role = hv < nq ? 0 : (hv < nq + nk ? 1 : 2); // 0 q, 1 k, 2 v
-  const unsigned idx = role == 0 ? hv : (role == 1 ? hv - nq : hv - nq - nk);
-  const unsigned heads = role == 0 ? (unsigned)a.hq : (unsigned)a.hkv;
-  const int t = live ? (int)(idx / heads) : 0, h = (int)(idx % heads);
-  const PosState ps = fetch_state(a.pos, t);
-
-  // 1. The block's chunks, eight coalesced loads per lane, into the LDS image.  The loads
-  // are unconditional (chunks past the end re-read the last head) so that all eight are in
-  // flight before the first is waited for.
-  uint4 in[8];
-#pragma unroll
-  for (int m = 0; m < 8; ++m) {
-    const int c = 64 * m + lane;
-    const unsigned hc = min(block0 + (unsigned)(c >> 4), total - 1u);
-    in[m] = ld_nt(reinterpret_cast<const uint4 *>(head_src(a, hc, nq, nk)) + (c & 15));
-  }
-#pragma unroll
-  for (int m = 0; m < 8; ++m) {
-    const int c = 64 * m + lane;
-    stage[chunk_slot(c >> 4, c & 15)] = in[m];
-  }
-
-  // 2. The head's position.
-  bool ok = false;
-  int pos = resolve_position(a.pos, ps, t, FMT >= 0 ? a.cap : 0, a.first, FMT > PADRA_KV_BF16, ok);
-  ok = ok && live && pos >= 0 && pos < a.table_rows;
-  if (live && !ok && half == 0)
-    raise_bad(a.bad);
-  // The head's norm weights and table row come in four pieces of eight pairs; piece 0 is
-  // requested now, while the block's chunks are in flight, and each later piece one step
-  // ahead of its use (clamped addresses: every load is unconditional).
-  const uint16_t *wsrc = role == 1 ? a.kn : a.qn;
-  const uint16_t *row = a.table + (size_t)(ok ? pos : 0) * D;
-  Bf8 wa[2], wb[2], c8[2], s8[2];
-  wa[0].load(wsrc + 32 * half);
-  wb[0].load(wsrc + 64 + 32 * half);
-  c8[0].load(row + 32 * half);
-  s8[0].load(row + 64 + 32 * half);
-  __syncthreads();
-  Act32<uint16_t> xa, xb;
-#pragma unroll
-  for (int mp = 0; mp < 4; ++mp) {
-    xa.w[mp] = stage[stage_slot(lane, mp)];
-    xb.w[mp] = stage[stage_slot(lane, mp + 4)];
-  }
-  const long long seq = a.pos.mode == PADRA_POS_DECODE ? t : 0;
-  const long long slot = seq * a.seq_stride + (ok ? pos % max(a.cap, 1) : 0);
-
-  uint32_t lo[16], hi[16];
-  const bool qk = live && ok && role < 2;
-  if (qk) {
-    float S, E, S2, E2;
-    group_sumsq(xa, S, E);
-    group_sumsq(xb, S2, E2);
-    fold(S2, E2, S, E); // w_half + w_{half+2}
-    const float So = shfl_xor(S, 1), Eo = shfl_xor(E, 1);
-    float bs = half ? So : S, be = half ? Eo : E;
-    fold(half ? S : So, half ? E : Eo, bs, be); // (w0 + w2) + (w1 + w3)
-    const float sum = bs + be;
-    const float inv = 1.f / sqrtf(sum / (float)D + a.eps);
-    bool fine = isfinite(sum);
-#pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      const int cur = m & 1, nxt = cur ^ 1;
-      if (m < 3) {
-        wa[nxt].load(wsrc + 32 * half + 8 * (m + 1));
-        wb[nxt].load(wsrc + 64 + 32 * half + 8 * (m + 1));
-        c8[nxt].load(row + 32 * half + 8 * (m + 1));
-        s8[nxt].load(row + 64 + 32 * half + 8 * (m + 1));
-      }
-#pragma unroll
-      for (int q = 0; q < 8; q += 2) {
-        float l2[2], h2[2];
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          const int i = 8 * m + q + u;
-          const uint32_t p1 = pack2(xa.get(i) * inv, xb.get(i) * inv);
-          const uint32_t p2 = pack2(lo16(p1) * wa[cur].get(q + u), hi16(p1) * wb[cur].get(q + u));
-          const float A = lo16(p2), Bv = hi16(p2), c = c8[cur].get(q + u), sn = s8[cur].get(q + u);
-          const uint32_t p3 = pack2(A * c, Bv * c);
-          const uint32_t p4 = pack2((-Bv) * sn, A * sn);
-          l2[u] = lo16(p3) + lo16(p4);
-          h2[u] = hi16(p3) + hi16(p4);
-          fine = fine && bf16_finite_after_round(l2[u]) && bf16_finite_after_round(h2[u]);
-        }
-        lo[(8 * m + q) / 2] = pack2(l2[0], l2[1]);
-        hi[(8 * m + q) / 2] = pack2(h2[0], h2[1]);
-      }
-    }
-    if (!fine)
-      raise_bad(a.bad);
-  }
-  __syncthreads(); // every lane has read its input pieces: the image can be overwritten
-
-  // 3. Outputs back into the image, then coalesced stores (in place, and K rows to a
-  // BF16 cache).
-  if (qk) {
-#pragma unroll
-    for (int mp = 0; mp < 4; ++mp) {
-      stage[stage_slot(lane, mp)] = make_uint4(lo[4 * mp], lo[4 * mp + 1], lo[4 * mp + 2], lo[4 * mp + 3]);
-      stage[stage_slot(lane, mp + 4)] = make_uint4(hi[4 * mp], hi[4 * mp + 1], hi[4 * mp + 2], hi[4 * mp + 3]);
-    }
-  }
-  // V heads of a block that straddles the K/V boundary keep their input chunks in the
-  // image and are copied to a BF16 cache by the same coalesced stores.
-  const bool vcopy = FMT == PADRA_KV_BF16 && live && ok && role == 2 && t >= a.first;
-  if (half == 0)
-    head_pos[lane >> 1] = (qk || vcopy) ? pos : -1;
-  __syncthreads();
-  const int features = a.hkv * D;
-#pragma unroll
-  for (int m = 0; m < 8; ++m) {
-    const int c = 64 * m + lane, j = c >> 4, ci = c & 15;
-    const unsigned hc = block0 + (unsigned)j;
-    const int hp = head_pos[j];
-    if (hp < 0)
-      continue; // past the end, a V head, or a head that writes nothing
-    const uint4 d = stage[chunk_slot(j, ci)];
-    if constexpr (FMT == PADRA_KV_BF16) {
-      if (hc >= nq + nk) { // V head: cache only
-        const unsigned vi = hc - nq - nk;
-        const int tc = (int)(vi / (unsigned)a.hkv), hh = (int)(vi % (unsigned)a.hkv);
-        const long long sq = a.pos.mode == PADRA_POS_DECODE ? tc : 0;
-        const long long sl = sq * a.seq_stride + hp % a.cap;
-        st_nt(reinterpret_cast<uint4 *>(static_cast<uint16_t *>(a.vc) + sl * features + hh * D) + ci, d);
-        continue;
-      }
-    }
-    st_nt(reinterpret_cast<uint4 *>(const_cast<uint16_t *>(head_src(a, hc, nq, nk))) + ci, d);
-    if constexpr (FMT == PADRA_KV_BF16) {
-      if (hc >= nq) {
-        const unsigned kvi = hc - nq;
-        const int tc = (int)(kvi / (unsigned)a.hkv), hh = (int)(kvi % (unsigned)a.hkv);
-        if (tc >= a.first) {
-          const long long sq = a.pos.mode == PADRA_POS_DECODE ? tc : 0;
-          const long long sl = sq * a.seq_stride + hp % a.cap;
-          st_nt(reinterpret_cast<uint4 *>(static_cast<uint16_t *>(a.kc) + sl * features + hh * D) + ci, d);
-        }
-      }
-    }
-  }
-
-  // 4. Quantized formats: K rows (from the rotated values) and V rows, lane-pair layout.
-  if constexpr (FMT > PADRA_KV_BF16) {
-    if (!live || !ok || role == 0 || t < a.first)
-      return;
-    float fa[32], fb[32];
-    if (role == 1) {
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        fa[2 * i] = lo16(lo[i]);
-        fa[2 * i + 1] = hi16(lo[i]);
-        fb[2 * i] = lo16(hi[i]);
-        fb[2 * i + 1] = hi16(hi[i]);
-      }
-      encode_head_q<FMT, false>(a, fa, fb, slot, h, half);
-    } else {
-#pragma unroll
-      for (int i = 0; i < 32; ++i) {
-        fa[i] = xa.get(i);
-        fb[i] = xb.get(i);
-      }
-      encode_head_q<FMT, true>(a, fa, fb, slot, h, half);
-    }
-  }
-}
-
 
 } // namespace padra

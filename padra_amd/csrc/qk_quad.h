@@ -72,7 +72,125 @@ __device__ __forceinline__ void v_rows_copy16(const A &a, unsigned block0, unsig
   }
 }
 
-// FMT: -1 (no cache) or PADRA_KV_BF16.
+// Hadamard stage across lanes of the quad: this lane's features pair with lane (lane ^ D)'s
+// (D = 1: feature bit 5, D = 2: bit 6); the lower lane keeps lower + upper, the upper lane
+// lower - upper.
+template <int D> __device__ __forceinline__ void hadamard_quad(float (&x)[32], int g) {
+#pragma unroll
+  for (int f = 0; f < 32; ++f) {
+    const uint32_t o = D == 1 ? quad_xor1(__float_as_uint(x[f])) : quad_xor2(__float_as_uint(x[f]));
+    const float other = __uint_as_float(o);
+    x[f] = (g & D) ? other - x[f] : x[f] + other;
+  }
+}
+
+// Encodes one K or V head vector held by a quad (lane g: features 32g .. 32g+31, BF16
+// pairs in w) into a quantized cache row.  `active` is quad-uniform; every lane runs the
+// quad exchanges.
+//  - q8 (kv_q8::Encode, kv_q8.cuh:41-73): a head with a non-finite value raises the flag
+//    and writes nothing; scale = amax/127 (1 for a zero head), codes RNE(x / scale)
+//    clamped to +-127, scale into the (k, v) pair of the row's head.
+//  - q8_0 (q8_native::EncodeKV, kv_q8_native.cuh:52-101): the rotation (K 128-point,
+//    V two 64-point; stages on feature bits 0-4 inside the lane, bits 5 and 6 across the
+//    quad), then block g = this lane's 32 features: d = half(amax/127), codes
+//    roundf(x * (1/d_fp32)) clamped.  Blocks from the first failing one (non-finite amax
+//    or d) on are not written, and the flag is raised.
+template <int FMT, bool ISV>
+__device__ __forceinline__ void encode_quad(const QKArgs<uint16_t> &a, const uint32_t (&w)[16],
+                                            long long slot, int h, int g, bool active) {
+  constexpr int D = 128;
+  const int features = a.hkv * D;
+  float x[32];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    x[2 * i] = lo16(w[i]);
+    x[2 * i + 1] = hi16(w[i]);
+  }
+  uint32_t cw[8];
+  if constexpr (FMT == PADRA_KV_Q8) {
+    bool finite = true;
+    float m = 0.f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+      finite = finite && isfinite(x[i]);
+      m = fmaxf(m, fabsf(x[i]));
+    }
+    uint32_t fin = finite ? 1u : 0u;
+    fin &= quad_xor1(fin);
+    fin &= quad_xor2(fin);
+    m = fmaxf(m, __uint_as_float(quad_xor1(__float_as_uint(m))));
+    m = fmaxf(m, __uint_as_float(quad_xor2(__float_as_uint(m))));
+    if (!active)
+      return;
+    if (!fin) {
+      if (g == 0)
+        raise_bad(a.bad);
+      return;
+    }
+    const float scale = m == 0.f ? 1.f : m / 127.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      cw[i] = 0u;
+#pragma unroll
+      for (int b = 0; b < 4; ++b)
+        cw[i] |= q8_code(x[4 * i + b], scale) << (8 * b);
+    }
+    int8_t *codes = static_cast<int8_t *>(ISV ? a.vc : a.kc) + slot * features + h * D + 32 * g;
+    st_nt(reinterpret_cast<uint4 *>(codes), make_uint4(cw[0], cw[1], cw[2], cw[3]));
+    st_nt(reinterpret_cast<uint4 *>(codes) + 1, make_uint4(cw[4], cw[5], cw[6], cw[7]));
+    if (g == 0)
+      reinterpret_cast<float *>(a.scales)[(slot * a.hkv + h) * 2 + (ISV ? 1 : 0)] = scale;
+  } else {
+    if constexpr (FMT == PADRA_KV_Q8_0) {
+      hadamard32(x);
+      hadamard_quad<1>(x, g);
+      if constexpr (!ISV) {
+        // the last K stage (bit 6) with the 1/sqrt(128) scale
+#pragma unroll
+        for (int f = 0; f < 32; ++f) {
+          const float other = __uint_as_float(quad_xor2(__float_as_uint(x[f])));
+          x[f] = ((g & 2) ? other - x[f] : x[f] + other) * .08838834764831845f;
+        }
+      } else {
+#pragma unroll
+        for (int f = 0; f < 32; ++f)
+          x[f] = x[f] * .125f;
+      }
+    }
+    float am = 0.f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i)
+      am = fmaxf(am, fabsf(x[i]));
+    const float ad = am / 127.f;
+    const __half dh = __float2half(ad);
+    const bool fail = !isfinite(am) || !isfinite(__half2float(dh));
+    uint32_t stop = fail ? (uint32_t)g : 4u; // first failing block of the head, 4 = none
+    stop = min(stop, quad_xor1(stop));
+    stop = min(stop, quad_xor2(stop));
+    if (!active)
+      return;
+    if (stop < 4u && g == 0)
+      raise_bad(a.bad);
+    if ((uint32_t)g >= stop)
+      return;
+    const float inverse = ad == 0.f ? 0.f : 1.f / ad;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      cw[i] = 0u;
+#pragma unroll
+      for (int b = 0; b < 4; ++b)
+        cw[i] |= q8_0_code(x[4 * i + b], inverse) << (8 * b);
+    }
+    const int row_bytes = ((2 * (features / 32) + features) + 15) / 16 * 16;
+    uint8_t *row = static_cast<uint8_t *>(ISV ? a.vc : a.kc) + slot * row_bytes;
+    int8_t *qs = reinterpret_cast<int8_t *>(row + 2 * (features / 32) + h * D + 32 * g);
+    st_nt(reinterpret_cast<uint4 *>(qs), make_uint4(cw[0], cw[1], cw[2], cw[3]));
+    st_nt(reinterpret_cast<uint4 *>(qs) + 1, make_uint4(cw[4], cw[5], cw[6], cw[7]));
+    reinterpret_cast<uint16_t *>(row)[h * 4 + g] = __half_as_ushort(dh);
+  }
+}
+
+// FMT: -1 (no cache), PADRA_KV_BF16, or a quantized cache format.
 template <int FMT>
 __device__ __forceinline__ void qk_heads_wave_quad(const QKArgs<uint16_t> &a, long long wave) {
   constexpr int D = 128;
@@ -97,6 +215,7 @@ __device__ __forceinline__ void qk_heads_wave_quad(const QKArgs<uint16_t> &a, lo
   const unsigned idx = role == 0 ? hv : (role == 1 ? hv - nq : hv - nq - nk);
   const unsigned heads = role == 0 ? (unsigned)a.hq : (unsigned)a.hkv;
   const int t = live ? (int)(idx / heads) : 0;
+  const int hh = live ? (int)(idx - (unsigned)t * heads) : 0;
   const PosState ps = fetch_state(a.pos, t);
 
   // 1. Four coalesced loads per lane (clamped, unconditional), into the LDS image.
@@ -115,7 +234,8 @@ __device__ __forceinline__ void qk_heads_wave_quad(const QKArgs<uint16_t> &a, lo
 
   // 2. The head's position.
   bool ok = false;
-  int pos = resolve_position(a.pos, ps, t, FMT >= 0 ? a.cap : 0, a.first, false, ok);
+  int pos = resolve_position(a.pos, ps, t, FMT >= 0 ? a.cap : 0, a.first, FMT > PADRA_KV_BF16,
+                             ok);
   ok = ok && live && pos >= 0 && pos < a.table_rows;
   if (live && !ok && g == 0)
     raise_bad(a.bad);
@@ -176,6 +296,20 @@ __device__ __forceinline__ void qk_heads_wave_quad(const QKArgs<uint16_t> &a, lo
     if (!fine)
       raise_bad(a.bad);
   }
+  if constexpr (FMT > PADRA_KV_BF16) {
+    // K heads encode their rotated values, V heads their inputs (quad-uniform roles).
+    const bool enc = live && ok && role >= 1 && t >= a.first;
+    const long long seq = a.pos.mode == PADRA_POS_DECODE ? t : 0;
+    const long long slot = seq * a.seq_stride + (ok ? pos % max(a.cap, 1) : 0);
+    uint32_t w16[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      w16[i] = role == 1 ? out[i] : x.word(i);
+    if (role == 2)
+      encode_quad<FMT, true>(a, w16, slot, hh, g, enc);
+    else
+      encode_quad<FMT, false>(a, w16, slot, hh, g, enc && role == 1);
+  }
   __syncthreads(); // every lane has read its input pieces: the image can be overwritten
 
   // 3. Outputs back into the image, then four coalesced stores per lane.
@@ -224,18 +358,14 @@ __device__ __forceinline__ void qk_heads_wave_quad(const QKArgs<uint16_t> &a, lo
 
 // Head vectors per wave of each Q/K kernel variant.
 template <class T, int FMT> constexpr int qk_heads_per_wave() {
-  return std::is_same<T, uint16_t>::value && FMT <= PADRA_KV_BF16 ? 16 : 32;
+  return std::is_same<T, uint16_t>::value ? 16 : 32;
 }
 
-// BF16 without a cache or with a BF16 cache: four lanes per head; quantized caches and
-// fp32 activations: two lanes per head.
+// BF16 activations: four lanes per head; fp32 activations: two lanes per head.
 template <class T, int FMT>
 __device__ __forceinline__ void qk_heads_wave(const QKArgs<T> &a, long long wave) {
   if constexpr (std::is_same<T, uint16_t>::value) {
-    if constexpr (FMT <= PADRA_KV_BF16)
-      qk_heads_wave_quad<FMT>(a, wave);
-    else
-      qk_heads_wave_staged<FMT>(a, wave);
+    qk_heads_wave_quad<FMT>(a, wave);
   } else {
     qk_heads_wave_direct<T, FMT>(a, wave);
   }
