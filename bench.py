@@ -107,8 +107,7 @@ def time_graph(torch, sets, steps, warmup):
             for i in range(steps):
                 sets[i % len(sets)].launch()
     torch.cuda.synchronize()
-    graph.replay()  # warm replay
-    torch.cuda.synchronize()
+    warm_graph(torch, graph)
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     with torch.cuda.stream(stream):
         torch.cuda.synchronize()
@@ -117,6 +116,19 @@ def time_graph(torch, sets, steps, warmup):
         end.record(stream)
     torch.cuda.synchronize()
     return start.elapsed_time(end) / steps
+
+
+def warm_graph(torch, graph, seconds=0.03, most=50):
+    """Untimed replays of the captured graph for about `seconds` (at most `most` replays)
+    before the timed one: on a fresh process the GPU clocks are still ramping during the
+    first milliseconds of work (measured: the first 32-launch replay runs 4% slower than
+    later ones), so the timed replay starts from the steady state a busy server runs in."""
+    t0 = time.perf_counter()
+    for _ in range(most):
+        graph.replay()
+        torch.cuda.synchronize()
+        if time.perf_counter() - t0 >= seconds:
+            break
 
 
 def time_eager(torch, sets, steps):
@@ -219,8 +231,7 @@ def graph_time(torch, step, steps, warmup=3):
             for i in range(steps):
                 step(i)
     torch.cuda.synchronize()
-    graph.replay()
-    torch.cuda.synchronize()
+    warm_graph(torch, graph)
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     with torch.cuda.stream(stream):
         start.record(stream)
