@@ -456,3 +456,66 @@ def test_reference_geometry_chain(oracle, fmt, tree):
     assert np.array_equal(_np(kc, fmt), ek) and np.array_equal(_np(vc, fmt), ev)
     if es is not None:
         assert np.array_equal(sc.cpu().numpy(), es)
+
+
+# ---- graph capture ----------------------------------------------------------------------------
+
+def test_decode_chain_graph_replays(oracle):
+    """The decode step (residual norm, 256-thread tree, + Q/K norm/RoPE + BF16 store at each
+    sequence's DecodeState position) captured once into a graph and replayed at new
+    positions: positions are read on the device, so each replay must match the oracle at
+    the positions the state held when it ran.  Eager work and synchronizations run between
+    the replays (state updates, input resets)."""
+    print("[case] decode chain graph replays", flush=True)
+    seqs, capacity = 8, 512
+    d = synth.chain_inputs(seqs, outliers=True, seed=81)
+    tb = table_bits(oracle, capacity)
+    x0, q0, k0 = dev(d["x"]), dev(d["q"]), dev(d["k"])
+    x, q, k = x0.clone(), q0.clone(), k0.clone()
+    r, g, v = dev(d["residual"]), dev(d["gamma"]), dev(d["v"])
+    qn, kn, table = dev(d["qn"]), dev(d["kn"]), dev(tb)
+    y = torch.empty_like(x)
+    kc = torch.zeros((seqs * capacity, 512), dtype=torch.int16, device="cuda")
+    vc = torch.zeros_like(kc)
+    states = torch.zeros((seqs, 8), dtype=torch.int32, device="cuda")
+    bad = flag()
+    pos = ops.positions_decode(states, maximum=capacity)
+    kv = ops.kv_cache(abi.KV_BF16, kc, vc, capacity, seq_stride=capacity)
+
+    def set_positions(p):
+        host = np.zeros((seqs, 8), np.int32)
+        for s, ps in enumerate(p):
+            host[s] = [5, ps, capacity, 10, ps, min(int(ps), 1024), 0, 0]
+        states.copy_(torch.from_numpy(host))
+
+    rng = np.random.default_rng(82)
+    set_positions(rng.integers(0, capacity, seqs))
+    stream = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        ops.ResidualNormQKRopeStore(x, r, y, g, q, k, v, qn, kn, table, pos, kv, bad, tree=256)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=stream):
+            ops.ResidualNormQKRopeStore(x, r, y, g, q, k, v, qn, kn, table, pos, kv, bad,
+                                        tree=256)
+    torch.cuda.synchronize()
+    wx, wy, _, _ = oracle.residual_rmsnorm(d["x"], d["residual"], d["gamma"], threads=256)
+    for replay in range(4):
+        p = rng.integers(0, capacity, seqs).astype(np.int32)
+        set_positions(p)
+        x.copy_(x0), q.copy_(q0), k.copy_(k0)
+        kc.zero_(), vc.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert not bad.item(), replay
+        wq, wk, _ = _qk_oracle(oracle, d, tb, p)
+        assert np.array_equal(host16(x), wx) and np.array_equal(host16(y), wy), replay
+        assert np.array_equal(host16(q), wq) and np.array_equal(host16(k), wk), replay
+        kca = host16(kc).reshape(seqs, capacity, 512)
+        vca = host16(vc).reshape(seqs, capacity, 512)
+        for s in range(seqs):
+            assert np.array_equal(kca[s, p[s]], wk[s].reshape(-1)), (replay, s)
+            assert np.array_equal(vca[s, p[s]], d["v"][s].reshape(-1)), (replay, s)
+            assert np.count_nonzero(kca[s].any(axis=1)) == 1, (replay, s)
