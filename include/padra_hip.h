@@ -114,6 +114,22 @@ int padra_ResidualPostNorm(void *stream, void *x, const void *residual, void *no
                            const uint16_t *gamma, int rows, int hidden, float eps, int tree,
                            float *statistics, int *bad, int act);
 
+/* padra_KVCheckpointCapture: kv_checkpoint::CaptureLocal / CaptureEncoded
+ * (kv_checkpoint.cuh:27-89).  Before a chunk's suffix commit into a 1024-row local ring,
+ * copies the ring as it will read at `anchor` into the snapshot `saved` (1024 rows per
+ * plane, the ring's byte layout; encoded bits are copied, never decoded): slot s holds
+ * position p = anchor-1 - ((anchor-1 - s + 1024) % 1024), taken from the chunk's row
+ * p - base (chunk rows [tokens]) when p >= base, from the old ring's slot s when
+ * 0 <= p < base, and zero before position 0.  Planes: K and V, plus the scale pairs for q8
+ * (the reference's single CaptureEncoded buffer is saved->k, then saved->v at +1024 rows,
+ * then saved->scales).  The capture runs only for a valid PrefillState (tokens rows,
+ * prefill->binding_epoch; the reference passes 1) with capacity >= 1024 and
+ * base < anchor <= base + tokens; otherwise *bad is raised.  If *bad is already set
+ * nothing is copied.  ring, chunk and saved share one format; saved aliases no source. */
+int padra_KVCheckpointCapture(void *stream, const padra_KVCache *ring,
+                              const padra_KVCache *chunk, const padra_KVCache *saved,
+                              const padra_Positions *prefill, int tokens, int anchor,
+                              int kv_heads, int *bad);
 /* padra_NormFP8: NormFP8Exact (norm_fp8_exact.cuh:6-62) and NormFP8WideExact
  * (norm_fp8_wide_exact.cuh:7-67), which give the same bytes: the 128-thread RMSNorm of each
  * row of x [rows][hidden] into normalized, plus its E4M3 encoding packed [rows][hidden]

@@ -41,6 +41,8 @@ def lib() -> ctypes.CDLL:
             "po_fp8_encode": ([F, F, F], ctypes.c_uint8),
             "po_norm_fp8": ([P, P, P, P, P, I, I, F, P, P], None),
             "po_combine": ([P, P, P, I, I, I, I, P], None),
+            "po_kv_checkpoint_plane": ([P, P, P, I, I, I], None),
+            "po_kv_checkpoint_admitted": ([P, I, I, ctypes.c_uint32, I], I),
             "po_combine_norm": ([P, P, P, P, P, P, P, I, I, I, F, P, P], None),
             "po_rope_table": ([P, I, I, F, I, F, I], None),
             "po_qk_norm_rope": ([P, P, P, P, P, P, I, I, I, I, F, P], None),
@@ -149,6 +151,25 @@ def combine_norm(x, down, weights, gamma, fp8=True, eps=1e-6):
                           _p(np.ascontiguousarray(gamma, np.uint16)), _p(packed), _p(scales),
                           rows, hidden, experts, eps, _p(stats), bad.ptr)
     return x, y, packed, scales, stats, bool(bad)
+
+
+def kv_checkpoint(old_planes, current_planes, state, tokens, anchor, epoch=1, maximum=131072):
+    """Snapshot of a 1024-row local ring.  old_planes / current_planes: lists of 2-D byte
+    arrays (rows x row_bytes; old: 1024 rows, current: `tokens` rows), one per plane (K, V
+    and, for q8, the scale pairs).  state: int32[8] PrefillState.  Returns the saved planes,
+    or None when the capture is not admitted."""
+    st = np.ascontiguousarray(state, np.int32)
+    if not lib().po_kv_checkpoint_admitted(_p(st), tokens, anchor, epoch, maximum):
+        return None
+    out = []
+    for old, cur in zip(old_planes, current_planes):
+        old = np.ascontiguousarray(old).view(np.uint8).reshape(1024, -1)
+        cur = np.ascontiguousarray(cur).view(np.uint8).reshape(cur.shape[0], -1)
+        saved = np.empty_like(old)
+        lib().po_kv_checkpoint_plane(_p(old), _p(cur), _p(saved), old.shape[1], int(st[0]),
+                                     anchor)
+        out.append(saved)
+    return out
 
 
 def e4m3(values) -> np.ndarray:

@@ -657,3 +657,27 @@ int po_valid_prefill_state(const po_PrefillState *s, int active_tokens, int capa
          s->committed == s->base && s->prompt_offset >= 0 &&
          s->prompt_offset <= capacity - active_tokens;
 }
+
+/* ---- Local-ring checkpoint capture ------------------------------------------------ */
+
+/* kv_checkpoint.cuh:12-25 */
+void po_kv_checkpoint_plane(const uint8_t *old_rows, const uint8_t *current_rows,
+                            uint8_t *saved_rows, int row_bytes, int base, int anchor) {
+  for (int slot = 0; slot < 1024; ++slot) {
+    const int position = anchor - 1 - ((anchor - 1 - slot + 1024) % 1024);
+    uint8_t *dst = saved_rows + (long long)slot * row_bytes;
+    if (position >= base)
+      memcpy(dst, current_rows + (long long)(position - base) * row_bytes, (size_t)row_bytes);
+    else if (position >= 0)
+      memcpy(dst, old_rows + (long long)slot * row_bytes, (size_t)row_bytes);
+    else
+      memset(dst, 0, (size_t)row_bytes);
+  }
+}
+
+/* kv_checkpoint.cuh:33-38 */
+int po_kv_checkpoint_admitted(const po_PrefillState *s, int tokens, int anchor,
+                              uint32_t binding_epoch, int maximum) {
+  return po_valid_prefill_state(s, tokens, s->capacity, binding_epoch, maximum) &&
+         s->capacity >= 1024 && anchor > s->base && anchor <= s->base + tokens;
+}

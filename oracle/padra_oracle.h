@@ -147,6 +147,18 @@ int po_decode_ready(const po_DecodeState *s, int maximum, int vocab); /* context
 int po_valid_prefill_state(const po_PrefillState *s, int active_tokens, int capacity,
                            uint32_t binding_epoch, int maximum); /* prefill_state.h:16-24 */
 
+/* ---- Local-ring checkpoint capture (kv_checkpoint.cuh) --------------------------- */
+/* CopyEncodedPlane / CaptureLocal's copy (kv_checkpoint.cuh:12-25, 70-88): slot s of the
+ * 1024-row snapshot holds position p = anchor-1 - ((anchor-1 - s + 1024) % 1024): the
+ * chunk's row p - base when p >= base, the old ring's slot s when 0 <= p < base, zeros
+ * before position 0.  Rows of row_bytes bytes. */
+void po_kv_checkpoint_plane(const uint8_t *old_rows, const uint8_t *current_rows,
+                            uint8_t *saved_rows, int row_bytes, int base, int anchor);
+/* The capture's admission (kv_checkpoint.cuh:33-38, 62-67): a valid PrefillState for
+ * `tokens` rows, capacity >= 1024, base < anchor <= base + tokens. */
+int po_kv_checkpoint_admitted(const po_PrefillState *s, int tokens, int anchor,
+                              uint32_t binding_epoch, int maximum);
+
 #ifdef __cplusplus
 }
 #endif

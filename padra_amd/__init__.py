@@ -38,6 +38,7 @@ from .ops import (  # noqa: F401
     Combine,
     CombineNorm,
     Embed,
+    KVCheckpointCapture,
     KVCommit,
     KVStore,
     KvQ8_0Dequantize,

@@ -80,6 +80,9 @@ SIGNATURES = {
     "padra_KvQ8_0DequantizePrefix": [_P, _P, _P, _P, _P, ctypes.POINTER(Positions), _I, _I, _I,
                                      _P],
     "padra_CheckFP8Paths": [_P, _P],
+    "padra_KVCheckpointCapture": [_P, ctypes.POINTER(KVCache), ctypes.POINTER(KVCache),
+                                  ctypes.POINTER(KVCache), ctypes.POINTER(Positions), _I, _I, _I,
+                                  _P],
     "padra_Combine": [_P, _P, _P, _P, _I, _I, _I, _I, _P, _I],
     "padra_CombineNorm": [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, ctypes.c_float, _P, _P,
                           _I],

@@ -270,6 +270,57 @@ template <class F> int with_kv_format(int fmt, F &&f) {
 
 int row_bytes_q8_0(int features) { return ((2 * (features / 32) + features) + 15) / 16 * 16; }
 
+// ---- local-ring checkpoint capture -------------------------------------------------
+//
+// kv_checkpoint::CaptureEncoded / CaptureLocal (kv_checkpoint.cuh:27-89): a 1024-row snapshot
+// of a local ring taken before the chunk's suffix commit, copying encoded bits only.  Slot
+// s holds position p = anchor-1 - ((anchor-1 - s + 1024) % 1024): the chunk's row p - base
+// when p >= base, the old ring's slot s when 0 <= p < base, zeros before position 0.  Up to
+// three planes (K, V, and the q8 scale pairs); every row is a multiple of 16 bytes, so each
+// thread moves one 16-byte word.
+struct CheckpointArgs {
+  const uint8_t *old_rows[3], *current_rows[3];
+  uint8_t *saved[3];
+  int row_bytes[3];
+  int planes, tokens, anchor;
+  PosSrc pos;
+  int *bad;
+};
+
+__global__ __launch_bounds__(256) void k_kv_checkpoint(CheckpointArgs a) {
+  __shared__ int admitted;
+  if (threadIdx.x == 0) {
+    const padra_PrefillState st = load_state(a.pos.prefill);
+    const bool ok = prefill_valid(st, a.tokens, st.capacity, a.pos.epoch, a.pos.maximum) &&
+                    st.capacity >= 1024 && a.anchor > st.base && a.anchor <= st.base + a.tokens;
+    // A flag already raised by earlier work stops the capture (kv_checkpoint.cuh:43-44).
+    const bool pending = __atomic_load_n(a.bad, __ATOMIC_RELAXED) != 0;
+    if (!ok && blockIdx.x == 0)
+      raise_bad(a.bad);
+    admitted = ok && !pending ? st.base + 1 : 0;
+  }
+  __syncthreads();
+  if (!admitted)
+    return; // block-uniform
+  const int base = admitted - 1;
+  for (int pl = 0; pl < a.planes; ++pl) {
+    const int words = a.row_bytes[pl] / 16, n = 1024 * words;
+    const uint4 *old = reinterpret_cast<const uint4 *>(a.old_rows[pl]);
+    const uint4 *cur = reinterpret_cast<const uint4 *>(a.current_rows[pl]);
+    uint4 *saved = reinterpret_cast<uint4 *>(a.saved[pl]);
+    for (int i = blockIdx.x * 256 + threadIdx.x; i < n; i += gridDim.x * 256) {
+      const int slot = i / words, word = i - slot * words;
+      const int position = a.anchor - 1 - ((a.anchor - 1 - slot + 1024) % 1024);
+      uint4 v = make_uint4(0, 0, 0, 0);
+      if (position >= base)
+        v = ld_nt(cur + (size_t)(position - base) * words + word);
+      else if (position >= 0)
+        v = ld_nt(old + i);
+      st_nt(saved + i, v);
+    }
+  }
+}
+
 } // namespace
 
 extern "C" int padra_KVStore(void *stream, const void *k, const void *v,
@@ -432,4 +483,59 @@ extern "C" int padra_RotateRows(void *stream, void *data, long long rows, int va
                          static_cast<float *>(data), rows, bad);
   }
   return launched("RotateRows");
+}
+
+extern "C" int padra_KVCheckpointCapture(void *stream, const padra_KVCache *ring,
+                                         const padra_KVCache *chunk, const padra_KVCache *saved,
+                                         const padra_Positions *prefill, int tokens, int anchor,
+                                         int kv_heads, int *bad) {
+  if (!ring || !chunk || !saved || !prefill || !bad || kv_heads < 1 ||
+      prefill->mode != PADRA_POS_PREFILL || !prefill->prefill || tokens < 1 || tokens > 2048 ||
+      prefill->maximum < 1 || prefill->maximum > 131072 || ring->format != chunk->format ||
+      saved->format != ring->format || ring->format < PADRA_KV_BF16 ||
+      ring->format > PADRA_KV_Q8_0_NOROT || !ring->k || !ring->v || !chunk->k || !chunk->v ||
+      !saved->k || !saved->v)
+    return PADRA_INVALID_ARGUMENT;
+  const int features = kv_heads * 128;
+  CheckpointArgs a{};
+  a.tokens = tokens;
+  a.anchor = anchor;
+  a.pos = pos_src(*prefill, tokens);
+  a.bad = bad;
+  const void *olds[3] = {ring->k, ring->v, ring->scales};
+  const void *curs[3] = {chunk->k, chunk->v, chunk->scales};
+  void *outs[3] = {saved->k, saved->v, saved->scales};
+  int rb;
+  switch (ring->format) {
+  case PADRA_KV_BF16:
+    rb = 2 * features;
+    a.planes = 2;
+    break;
+  case PADRA_KV_Q8:
+    rb = features;
+    a.planes = 3;
+    if (!ring->scales || !chunk->scales || !saved->scales)
+      return PADRA_INVALID_ARGUMENT;
+    break;
+  default:
+    rb = row_bytes_q8_0(features);
+    a.planes = 2;
+    break;
+  }
+  for (int pl = 0; pl < a.planes; ++pl) {
+    a.old_rows[pl] = static_cast<const uint8_t *>(olds[pl]);
+    a.current_rows[pl] = static_cast<const uint8_t *>(curs[pl]);
+    a.saved[pl] = static_cast<uint8_t *>(outs[pl]);
+    a.row_bytes[pl] = pl == 2 ? 8 * kv_heads : rb;
+    if (a.row_bytes[pl] % 16 || !aligned16(olds[pl]) || !aligned16(curs[pl]) ||
+        !aligned16(outs[pl]))
+      return PADRA_INVALID_ARGUMENT;
+    // the snapshot may not alias any source plane (kv_checkpoint.cuh:37-38)
+    for (int q = 0; q < 3; ++q)
+      if (outs[pl] && (outs[pl] == olds[q] || outs[pl] == curs[q]))
+        return PADRA_INVALID_ARGUMENT;
+  }
+  hipLaunchKernelGGL(k_kv_checkpoint, dim3(128), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     a);
+  return launched("KVCheckpointCapture");
 }

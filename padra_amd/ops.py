@@ -208,6 +208,15 @@ def KvQ8_0DequantizePrefix(rows_k, rows_v, out_k, out_v, positions: abi.Position
              _p(bad))
 
 
+def KVCheckpointCapture(ring: abi.KVCache, chunk: abi.KVCache, saved: abi.KVCache,
+                        positions: abi.Positions, tokens, anchor, bad, kv_heads=4):
+    """Snapshot of a 1024-row local ring at `anchor` (kv_checkpoint.cuh:27-89)."""
+    _need_cuda(bad)
+    abi.call("padra_KVCheckpointCapture", _stream(bad), ctypes.byref(ring), ctypes.byref(chunk),
+             ctypes.byref(saved), ctypes.byref(positions), int(tokens), int(anchor),
+             int(kv_heads), _p(bad))
+
+
 def RotateRows(data, bad, value=False):
     """In-place Hadamard rotation of 128-wide rows (K transform, or V with value=True)."""
     _need_cuda(data, bad)

@@ -366,3 +366,51 @@ def test_combine_nonfinite_sets_bad(oracle):
     ops.CombineNorm(dev(d["x"]), dev(down), torch.from_numpy(w).cuda(), y, dev(d["gamma"]), bad2)
     torch.cuda.synchronize()
     assert bad2.item() == 1
+
+
+# ---- local-ring checkpoint capture ----------------------------------------------------------
+
+@pytest.mark.parametrize("fmt", FORMATS)
+def test_kv_checkpoint_capture(oracle, fmt):
+    """Snapshot of a 1024-row ring before a 600-row chunk at base 700, anchor 1250: slots
+    from the chunk, from the old ring and (positions < 0 never occur here) bit copies."""
+    print(f"[case] checkpoint fmt={fmt}", flush=True)
+    base, tokens, anchor, capacity = 700, 600, 1250, 4096
+    rng = np.random.default_rng(70 + fmt)
+    def planes(rows):
+        if fmt == abi.KV_BF16:
+            return [rng.integers(0, 65536, (rows, 512), dtype=np.uint16) for _ in range(2)]
+        if fmt == abi.KV_Q8:
+            return [rng.integers(-127, 128, (rows, 512), dtype=np.int8) for _ in range(2)] + \
+                [rng.standard_normal((rows, 4, 2)).astype(np.float32)]
+        return [rng.integers(0, 256, (rows, 544), dtype=np.uint8) for _ in range(2)]
+    old, cur = planes(1024), planes(tokens)
+    state = np.array([base, base, tokens, capacity, base, 1, 1, 1], np.int32)
+    want = oracle.kv_checkpoint(old, cur, state, tokens, anchor)
+    todev = lambda a: torch.from_numpy(np.ascontiguousarray(a).view(np.uint8)).cuda()
+    o, c = [todev(a) for a in old], [todev(a) for a in cur]
+    sv = [torch.full_like(t, 0xAB) for t in o]
+    sc = lambda lst: lst[2] if len(lst) > 2 else None
+    ring = ops.kv_cache(fmt, o[0], o[1], 1024, scales=sc(o))
+    chunk = ops.kv_cache(fmt, c[0], c[1], tokens, scales=sc(c))
+    saved = ops.kv_cache(fmt, sv[0], sv[1], 1024, scales=sc(sv))
+    st = torch.from_numpy(state).cuda()
+    bad = flag()
+    ops.KVCheckpointCapture(ring, chunk, saved, ops.positions_prefill(st, maximum=capacity),
+                            tokens, anchor, bad)
+    torch.cuda.synchronize()
+    assert bad.item() == 0
+    for got, w in zip(sv, want):
+        assert np.array_equal(got.cpu().numpy().reshape(w.shape), w)
+    # a capture whose anchor lies outside the chunk writes nothing and raises the flag
+    for t in sv:
+        t.fill_(0xAB)
+    ops.KVCheckpointCapture(ring, chunk, saved, ops.positions_prefill(st, maximum=capacity),
+                            tokens, base, bad)
+    torch.cuda.synchronize()
+    assert bad.item() == 1 and all(bool((t == 0xAB).all()) for t in sv)
+    # with the flag already raised, a valid capture copies nothing
+    ops.KVCheckpointCapture(ring, chunk, saved, ops.positions_prefill(st, maximum=capacity),
+                            tokens, anchor, bad)
+    torch.cuda.synchronize()
+    assert all(bool((t == 0xAB).all()) for t in sv)

@@ -33,6 +33,8 @@ Per oracle function, what checks it:
                                   on small integers are exact; float64 weighted sum within
                                   the rounding bound; the expert order of the accumulation
   po_combine_norm                 = po_combine, then po_norm_fp8 / po_rmsnorm of the new x
+  po_kv_checkpoint_*              slot contents by search over positions (the newest p <
+                                  anchor with p = slot mod 1024), admission truth table
 """
 import numpy as np
 import pytest
@@ -596,3 +598,41 @@ def test_state_predicates(oracle):
         bad = PrefillState.from_buffer_copy(p)
         setattr(bad, field, value)
         assert not lib.po_valid_prefill_state(ctypes.byref(bad), 2048, 131072, 1, 131072), field
+
+
+# ---- local-ring checkpoint capture ---------------------------------------------------------
+
+@pytest.mark.parametrize("base,tokens,anchor", [(0, 300, 200), (700, 600, 1300),
+                                                (3000, 2048, 5048), (1500, 100, 1501)])
+def test_kv_checkpoint_plane(oracle, base, tokens, anchor):
+    rng = np.random.default_rng(base + anchor)
+    old = rng.integers(0, 256, (1024, 48), dtype=np.uint8)
+    cur = rng.integers(0, 256, (tokens, 48), dtype=np.uint8)
+    state = np.array([base, base, tokens, 8192, base, 1, 1, 1], np.int32)
+    (saved,) = oracle.kv_checkpoint([old], [cur], state, tokens, anchor)
+    for slot in range(1024):
+        p = max(q for q in range(anchor - 1024, anchor) if q % 1024 == slot)
+        if p >= base:
+            want = cur[p - base]
+        elif p >= 0:
+            want = old[slot]
+        else:
+            want = np.zeros(48, np.uint8)
+        assert np.array_equal(saved[slot], want), slot
+
+
+def test_kv_checkpoint_admission(oracle):
+    old = np.zeros((1024, 16), np.uint8)
+    cur = np.zeros((10, 16), np.uint8)
+    good = np.array([100, 100, 10, 2048, 100, 1, 1, 1], np.int32)
+    assert oracle.kv_checkpoint([old], [cur], good, 10, 105) is not None
+    assert oracle.kv_checkpoint([old], [cur], good, 10, 110) is not None
+    assert oracle.kv_checkpoint([old], [cur], good, 10, 100) is None   # anchor <= base
+    assert oracle.kv_checkpoint([old], [cur], good, 10, 111) is None   # past the chunk
+    small = good.copy()
+    small[3] = 512                                                     # capacity < 1024
+    assert oracle.kv_checkpoint([old], [cur], small, 10, 105) is None
+    stale = good.copy()
+    stale[4] = 99                                                      # committed != base
+    assert oracle.kv_checkpoint([old], [cur], stale, 10, 105) is None
+    assert oracle.kv_checkpoint([old], [cur], good, 10, 105, epoch=2) is None
