@@ -322,6 +322,44 @@ def bench_combine_norm(torch, steps, sets=8):
             "frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
 
 
+def bench_attention(torch, steps, seqs=64, capacity=CAPACITY, fill_seed=0):
+    """Decode attention over BF16 caches (the consumer of the stored rows), one step of
+    `seqs` sequences at ragged positions U[0, capacity) with per-sequence caches of
+    `capacity` rows: the split-K pass and the per-head merge.  Bytes: every key and value
+    row of the window (4 KV heads x 256 B each) plus q and the output."""
+    from padra_amd import abi, ops, synth
+    rng = np.random.default_rng(fill_seed)
+    positions = rng.integers(0, capacity, seqs).astype(np.int32)
+    states = np.zeros((seqs, 8), np.int32)
+    for i, p in enumerate(positions):
+        states[i] = [1, p, capacity, 1 << 20, p, min(int(p), 1024), 0, 0]
+    st = torch.from_numpy(states).cuda()
+    gen = torch.Generator(device="cuda").manual_seed(fill_seed)
+    kc = (torch.randn((seqs * capacity, HKV * D), generator=gen, device="cuda")).to(
+        torch.bfloat16).view(torch.int16)
+    vc = (torch.randn((seqs * capacity, HKV * D), generator=gen, device="cuda")).to(
+        torch.bfloat16).view(torch.int16)
+    q = (torch.randn((seqs, HQ, D), generator=gen, device="cuda") * 0.1).to(
+        torch.bfloat16).view(torch.int16)
+    out = torch.empty_like(q)
+    bad = torch.zeros(1, dtype=torch.int32, device="cuda")
+    kv = ops.kv_cache(abi.KV_BF16, kc, vc, capacity, seq_stride=capacity)
+    pos = ops.positions_decode(st, maximum=capacity)
+    scratch = ops.DecodeAttention(q, kv, out, pos, bad)
+    ms = graph_time(torch, lambda i: ops.DecodeAttention(q, kv, out, pos, bad, scratch=scratch),
+                    steps)
+    if bad.item():
+        raise SystemExit("device error flag set in the decode attention benchmark")
+    nbytes = int((positions.astype(np.int64) + 1).sum()) * HKV * D * 2 * 2 + 2 * q.numel() * 2
+    del kc, vc
+    torch.cuda.empty_cache()
+    return {"workload": f"decode attention, {seqs} sequences at ragged positions < {capacity}, "
+                        "BF16 caches (split-K + merge)",
+            "us_per_step": round(ms * 1e3, 3), "bytes_per_step": nbytes,
+            "gbs": round(nbytes / (ms * 1e-3) / 1e9, 2),
+            "frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+
+
 def bench_decode(torch, steps, seqs, vocab=131072, capacity=CAPACITY):
     """Config 4 (seqs=64) and the GPU side of config 0 (seqs=1): embedding gather, then the
     fused residual-norm (256-thread decode tree) + Q/K norm + RoPE + BF16 KV store at each
@@ -462,7 +500,8 @@ def main():
                            "config4": bench_decode(torch, 100, 64),
                            "config0_gpu": bench_decode(torch, 200, 1, capacity=8192),
                            "norm_fp8": bench_norm_fp8(torch, 200),
-                           "combine_norm": bench_combine_norm(torch, 100)}
+                           "combine_norm": bench_combine_norm(torch, 100),
+                           "attention": bench_attention(torch, 10)}
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(host, args.cpu_seconds, cpu_threads())
         if not args.no_configs:

@@ -41,6 +41,7 @@ def lib() -> ctypes.CDLL:
             "po_fp8_encode": ([F, F, F], ctypes.c_uint8),
             "po_norm_fp8": ([P, P, P, P, P, I, I, F, P, P], None),
             "po_combine": ([P, P, P, I, I, I, I, P], None),
+            "po_decode_attention": ([P, P, P, I, I, I, I, I, I, P, P], I),
             "po_kv_checkpoint_plane": ([P, P, P, I, I, I], None),
             "po_kv_checkpoint_admitted": ([P, I, I, ctypes.c_uint32, I], I),
             "po_combine_norm": ([P, P, P, P, P, P, P, I, I, I, F, P, P], None),
@@ -170,6 +171,21 @@ def kv_checkpoint(old_planes, current_planes, state, tokens, anchor, epoch=1, ma
                                      anchor)
         out.append(saved)
     return out
+
+
+def decode_attention(q, kc, vc, position, local=False, splits=0):
+    """q [hq][128] BF16 bits, kc / vc [cap][hkv*128] BF16 bits.  Returns (out [hq][128]
+    BF16 bits, splits used, bad)."""
+    q = np.ascontiguousarray(q, np.uint16)
+    kc = np.ascontiguousarray(kc, np.uint16)
+    vc = np.ascontiguousarray(vc, np.uint16)
+    hq = q.shape[0]
+    cap, features = kc.shape
+    out = np.empty((hq, 128), np.uint16)
+    bad = Bad()
+    used = lib().po_decode_attention(_p(q), _p(kc), _p(vc), cap, int(position), int(bool(local)),
+                                     hq, features // 128, int(splits), _p(out), bad.ptr)
+    return out, used, bool(bad)
 
 
 def e4m3(values) -> np.ndarray:

@@ -8,6 +8,7 @@
  */
 #include "padra_oracle.h"
 #include <math.h>
+#include <stdlib.h>
 #include <string.h>
 
 static uint32_t bits_of(float x) {
@@ -680,4 +681,118 @@ int po_kv_checkpoint_admitted(const po_PrefillState *s, int tokens, int anchor,
                               uint32_t binding_epoch, int maximum) {
   return po_valid_prefill_state(s, tokens, s->capacity, binding_epoch, maximum) &&
          s->capacity >= 1024 && anchor > s->base && anchor <= s->base + tokens;
+}
+
+/* ---- Decode attention -------------------------------------------------------------- */
+
+/* __shfl_xor butterfly sum over 32 lanes (levels 16, 8, 4, 2, 1): every lane ends with
+ * the same value; this is lane 0's. */
+static float butterfly_sum32(const float *x) {
+  float v[32], w[32];
+  memcpy(v, x, sizeof v);
+  for (int d = 16; d; d /= 2) {
+    for (int l = 0; l < 32; ++l)
+      w[l] = v[l] + v[l ^ d];
+    memcpy(v, w, sizeof v);
+  }
+  return v[0];
+}
+
+int po_decode_attention(const uint16_t *q, const uint16_t *kc, const uint16_t *vc, int cap,
+                        int position, int local, int hq, int hkv, int splits, uint16_t *out,
+                        int *bad) {
+  const int D = 128, G = hq / hkv, features = hkv * D;
+  const float scale = .08838834764831845f;
+  const int n = local ? (position + 1 < 1024 ? position + 1 : 1024) : position + 1;
+  const int first = position + 1 - n, tiles = (n + 31) / 32;
+  if (splits <= 0) {
+    splits = (cap + 31) / 32;
+    if (splits > (local ? 16 : 32))
+      splits = local ? 16 : 32;
+  }
+  const int active = splits < tiles ? splits : tiles;
+  float *partial = (float *)calloc((size_t)active * hq * D, sizeof(float));
+  float *lse = (float *)calloc((size_t)active * hq, sizeof(float));
+  for (int sp = 0; sp < active; ++sp) {
+    const int begin = tiles * sp / active, end = tiles * (sp + 1) / active;
+    for (int head = 0; head < hq; ++head) {
+      const int kv = head / G;
+      float qf[128], accum[128], maximum = -INFINITY, denominator = 0.f;
+      for (int d = 0; d < D; ++d) {
+        qf[d] = po_bf16_to_f32(q[head * D + d]);
+        accum[d] = 0.f;
+      }
+      for (int tile = begin; tile < end; ++tile) {
+        float s[32], prob[32], p[32], mx = -INFINITY;
+        int row[32];
+        for (int j = 0; j < 32; ++j) {
+          const int offset = tile * 32 + j;
+          row[j] = offset < n ? (first + offset) % cap : -1;
+          if (row[j] < 0) {
+            s[j] = -INFINITY;
+            continue;
+          }
+          float dot = 0.f;
+          for (int d = 0; d < D; ++d)
+            dot += qf[d] * po_bf16_to_f32(kc[(long long)row[j] * features + kv * D + d]);
+          s[j] = dot * scale;
+          if (!finite_f(s[j]))
+            set_bad(bad);
+          mx = fmaxf(mx, s[j]);
+        }
+        const float next = fmaxf(maximum, mx);
+        const float a = finite_f(maximum) ? expf(maximum - next) : 0.f;
+        for (int j = 0; j < 32; ++j) {
+          prob[j] = finite_f(s[j]) ? expf(s[j] - next) : 0.f;
+          p[j] = po_bf16_round(prob[j]);
+        }
+        const float total = butterfly_sum32(prob);
+        maximum = next;
+        denominator = fmaf(denominator, a, total);
+        for (int d = 0; d < D; ++d) {
+          float acc = accum[d] * a;
+          for (int j = 0; j < 32; ++j)
+            if (row[j] >= 0)
+              acc += p[j] * po_bf16_to_f32(vc[(long long)row[j] * features + kv * D + d]);
+          accum[d] = acc;
+        }
+      }
+      for (int d = 0; d < D; ++d) {
+        const float value = accum[d] / denominator;
+        partial[((long long)sp * hq + head) * D + d] = value;
+        if (!finite_f(value))
+          set_bad(bad);
+      }
+      lse[sp * hq + head] = maximum + logf(denominator);
+      if (!finite_f(lse[sp * hq + head]))
+        set_bad(bad);
+    }
+  }
+  for (int head = 0; head < hq; ++head) {
+    float v[32], w[32], weights[32], mx = -INFINITY;
+    for (int l = 0; l < 32; ++l) {
+      v[l] = l < active ? lse[l * hq + head] : -INFINITY;
+      mx = fmaxf(mx, v[l]);
+    }
+    for (int l = 0; l < 32; ++l)
+      w[l] = l < active ? expf(v[l] - mx) : 0.f;
+    const float den = butterfly_sum32(w);
+    for (int l = 0; l < active; ++l) {
+      weights[l] = w[l] / den;
+      if (!finite_f(weights[l]))
+        set_bad(bad);
+    }
+    for (int d = 0; d < D; ++d) {
+      float sum = 0.f;
+      for (int sp = 0; sp < active; ++sp)
+        sum = fmaf(weights[sp], partial[((long long)sp * hq + head) * D + d], sum);
+      const float value = po_bf16_round(sum);
+      out[head * D + d] = po_f32_to_bf16(value);
+      if (!finite_f(value))
+        set_bad(bad);
+    }
+  }
+  free(partial);
+  free(lse);
+  return active;
 }

@@ -159,6 +159,23 @@ void po_kv_checkpoint_plane(const uint8_t *old_rows, const uint8_t *current_rows
 int po_kv_checkpoint_admitted(const po_PrefillState *s, int tokens, int anchor,
                               uint32_t binding_epoch, int maximum);
 
+/* ---- Decode attention over a BF16 cache (split-K + per-head merge) ---------------- */
+/* One sequence at `position`: gqa8_fragment_validation::SplitBF16
+ * (attention_gqa8_fragment_validation.cuh:79-214) and attention_perhead_exact::Merge
+ * (attention_perhead_exact.cuh:7-38), generalised to hq / hkv query heads per KV head.
+ * Keys are positions first .. position (n = position + 1, or min(that, 1024) for a local
+ * ring), cache row (first + offset) % cap of kc / vc [cap][hkv*128].  Splits of 32-key
+ * tiles; per tile the online softmax with the score scale 1/sqrt(128) applied after the
+ * dot product, BF16 probabilities in the PV product and fp32 ones in the denominator;
+ * partial = accum / denominator, lse = max + log(denominator); then the merge:
+ * weights exp(lse - max) / sum, out = B(sum_s w_s * partial_s) (fmaf, split order).
+ * splits = 0 takes the reference's count, min(ceil(cap/32), local ? 16 : 32).  The dot
+ * products and PV sums run sequentially in fp32 (the reference's tensor-core order is not
+ * specified); expf/logf are the host libm's.  Returns the split count used. */
+int po_decode_attention(const uint16_t *q, const uint16_t *kc, const uint16_t *vc, int cap,
+                        int position, int local, int hq, int hkv, int splits, uint16_t *out,
+                        int *bad);
+
 #ifdef __cplusplus
 }
 #endif

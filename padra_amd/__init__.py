@@ -37,6 +37,7 @@ from .abi import (  # noqa: F401
 from .ops import (  # noqa: F401
     Combine,
     CombineNorm,
+    DecodeAttention,
     Embed,
     KVCheckpointCapture,
     KVCommit,

@@ -80,6 +80,9 @@ SIGNATURES = {
     "padra_KvQ8_0DequantizePrefix": [_P, _P, _P, _P, _P, ctypes.POINTER(Positions), _I, _I, _I,
                                      _P],
     "padra_CheckFP8Paths": [_P, _P],
+    "padra_DecodeAttentionScratch": [_I, _I, _I],
+    "padra_DecodeAttention": [_P, _P, ctypes.POINTER(KVCache), _P, ctypes.POINTER(Positions), _I,
+                              _I, _I, _I, _I, _P, ctypes.c_longlong, _P, _I],
     "padra_KVCheckpointCapture": [_P, ctypes.POINTER(KVCache), ctypes.POINTER(KVCache),
                                   ctypes.POINTER(KVCache), ctypes.POINTER(Positions), _I, _I, _I,
                                   _P],
@@ -94,7 +97,7 @@ SIGNATURES = {
     "padra_Tune": [_I, _I],
     "padra_version": [],
 }
-RESTYPES = {"padra_version": ctypes.c_char_p}
+RESTYPES = {"padra_version": ctypes.c_char_p, "padra_DecodeAttentionScratch": ctypes.c_longlong}
 
 _lib = None
 

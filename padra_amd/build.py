@@ -13,7 +13,7 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 SOURCES = ["csrc/kernels.hip", "csrc/kv_codec.hip", "csrc/swiglu_embed.hip", "csrc/combine.hip",
-           "csrc/rope_table.cpp"]
+           "csrc/attention.hip", "csrc/rope_table.cpp"]
 OUT = os.path.join(HERE, "libpadra_hip.so")
 
 

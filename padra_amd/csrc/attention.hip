@@ -1,0 +1,329 @@
+// Decode attention over a BF16 KV cache: split-K partial softmax, then a per-head merge.
+//
+// Reference: gqa8_fragment_validation::SplitBF16 (attention_gqa8_fragment_validation.cuh:
+// 79-214) with attention_perhead_exact::Merge (attention_perhead_exact.cuh:7-38), for any
+// number of query heads per KV head (the reference fixes 8).  One token per sequence, at
+// its DecodeState position; keys are the last n positions (n = position + 1, or at most
+// 1024 for a local ring), read from cache row (first + offset) % cap.
+//
+// Split kernel: one wave per (sequence, KV head, split), over that split's 32-key tiles.
+//  - Scores: lane l takes key l % 32 and half l / 32 of the 128 dimensions, against the
+//    G query rows held in LDS; the halves meet in one lane exchange.  scale 1/sqrt(128)
+//    after the dot product, as the reference applies it.
+//  - Online softmax per row with the reference's arithmetic: the tile maximum and the sum
+//    of probabilities are xor-butterflies over the 32 key lanes (the reference's warp
+//    order), probabilities in fp32 for the denominator (fmaf(den, alpha, total)) and
+//    rounded to BF16 for the PV product.
+//  - PV: lane l owns dimensions 2l, 2l+1 of every row; the V tile is staged in LDS.
+// Merge kernel: one wave per (sequence, query head): weights exp(lse_s - max) / sum, then
+// out = B(sum_s w_s * partial_s) in split order.
+//
+// Not bit-identical to the reference: its QK and PV products run on tensor-core MMA with an
+// unspecified accumulation order, and its expf/logf are CUDA's.  Products of two BF16
+// values are exact in fp32, so only the order of the fp32 sums and the exp/log ulps differ.
+#include <stdio.h>
+
+#include <algorithm>
+
+#include "common.h"
+
+using namespace padra;
+
+namespace {
+
+constexpr int kD = 128, kKeys = 32;
+constexpr float kScoreScale = .08838834764831845f;
+
+int launched(const char *what) {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    fprintf(stderr, "padra: %s launch failed: %s\n", what, hipGetErrorString(e));
+    return PADRA_INTERNAL;
+  }
+  return PADRA_OK;
+}
+bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+struct AttnArgs {
+  const void *q; // [seqs][hq][128], activation type
+  const uint16_t *kc, *vc;
+  void *out; // [seqs][hq][128]
+  float *partial, *lse;
+  const padra_DecodeState *decode;
+  int seqs, hq, hkv, cap, local, splits, maximum, vocab;
+  long long seq_stride; // cache rows between sequences
+  int *bad;
+};
+
+// The sequence's admission and key window (Admitted, attention_gqa8_fragment_validation.cuh:
+// 49-55, with the split count a parameter): n keys from position `first`.
+__device__ __forceinline__ bool attn_window(const AttnArgs &a, int seq, int &n, int &first) {
+  const padra_DecodeState st = load_state(a.decode + seq);
+  const bool ok = decode_ready(st, a.maximum, a.vocab) && a.cap <= st.capacity &&
+                  (a.local ? a.cap == min(1024, st.capacity) : a.cap == st.capacity);
+  n = a.local ? min(st.position + 1, 1024) : st.position + 1;
+  first = st.position + 1 - n;
+  return ok;
+}
+
+__device__ __forceinline__ float xor_max32(float v) {
+#pragma unroll
+  for (int d = 16; d >= 1; d /= 2)
+    v = fmaxf(v, __shfl_xor(v, d, 64));
+  return v;
+}
+__device__ __forceinline__ float xor_sum32(float v) {
+#pragma unroll
+  for (int d = 16; d >= 1; d /= 2)
+    v = v + __shfl_xor(v, d, 64);
+  return v;
+}
+
+template <class T> __device__ __forceinline__ float act_value(const void *p, size_t i) {
+  if constexpr (std::is_same<T, uint16_t>::value)
+    return __uint_as_float((uint32_t) static_cast<const uint16_t *>(p)[i] << 16);
+  else
+    return static_cast<const float *>(p)[i];
+}
+
+template <int G, class T>
+__global__ __launch_bounds__(64) void k_attn_split(AttnArgs a) {
+  __shared__ float qs[G][kD];
+  __shared__ uint32_t vs[kKeys][kD / 2]; // V tile, BF16 pairs
+  __shared__ float ps[kKeys][G];         // BF16-rounded probabilities
+  const int split = blockIdx.x, kv = blockIdx.y, seq = blockIdx.z, lane = threadIdx.x;
+  int n, first;
+  const bool ok = attn_window(a, seq, n, first);
+  if (!ok) {
+    if (split == 0 && kv == 0 && lane == 0)
+      raise_bad(a.bad);
+    return;
+  }
+  const int tiles = (n + kKeys - 1) / kKeys, active = min(a.splits, tiles);
+  if (split >= active)
+    return; // block-uniform
+  const int begin = tiles * split / active, end = tiles * (split + 1) / active;
+  const int features = a.hkv * kD;
+  const uint16_t *kc = a.kc + (size_t)seq * a.seq_stride * features + kv * kD;
+  const uint16_t *vc = a.vc + (size_t)seq * a.seq_stride * features + kv * kD;
+
+  // Query rows: finite and BF16-exact, as the reference requires of its fp32 input.
+  bool qfine = true;
+  for (int i = lane; i < G * kD; i += 64) {
+    const float x = act_value<T>(a.q, ((size_t)seq * a.hq + kv * G) * kD + i);
+    qfine = qfine && isfinite(x) && (__float_as_uint(x) & 0xffffu) == 0;
+    qs[i / kD][i % kD] = x;
+  }
+  if (__ballot(!qfine) != 0 && lane == 0)
+    raise_bad(a.bad);
+
+  const int key = lane & 31, half = lane >> 5;
+  float maximum[G], den[G], acc[G][2];
+#pragma unroll
+  for (int r = 0; r < G; ++r) {
+    maximum[r] = -INFINITY;
+    den[r] = 0.f;
+    acc[r][0] = acc[r][1] = 0.f;
+  }
+  bool fine = true;
+  __syncthreads();
+  for (int tile = begin; tile < end; ++tile) {
+    // Loads: this lane's half key row (8 x 16 B) and eight 16-byte chunks of the V tile.
+    const int offset = tile * kKeys + key;
+    const bool valid = offset < n;
+    const int row = (first + (valid ? offset : 0)) % a.cap;
+    uint4 kw[8], vw[8];
+#pragma unroll
+    for (int m = 0; m < 8; ++m)
+      kw[m] = ld_nt(reinterpret_cast<const uint4 *>(kc + (size_t)row * features + half * 64) + m);
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+      const int c = lane + 64 * m, vk = c >> 4, part = c & 15, vo = tile * kKeys + vk;
+      const int vrow = (first + (vo < n ? vo : 0)) % a.cap;
+      vw[m] = ld_nt(reinterpret_cast<const uint4 *>(vc + (size_t)vrow * features) + part);
+      if (vo >= n)
+        vw[m] = make_uint4(0, 0, 0, 0); // the reference zero-fills rows past the window
+    }
+    // Scores of this lane's key for every row.
+    float s[G];
+#pragma unroll
+    for (int r = 0; r < G; ++r) {
+      float dot = 0.f;
+#pragma unroll
+      for (int m = 0; m < 8; ++m) {
+        const uint32_t w[4] = {kw[m].x, kw[m].y, kw[m].z, kw[m].w};
+        const float4 q0 = *reinterpret_cast<const float4 *>(&qs[r][half * 64 + 8 * m]);
+        const float4 q1 = *reinterpret_cast<const float4 *>(&qs[r][half * 64 + 8 * m + 4]);
+        const float qv[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          dot = __builtin_fmaf(qv[2 * i], lo16(w[i]), dot);
+          dot = __builtin_fmaf(qv[2 * i + 1], hi16(w[i]), dot);
+        }
+      }
+      s[r] = (dot + __shfl_xor(dot, 32, 64)) * kScoreScale;
+      if (valid)
+        fine = fine && isfinite(s[r]);
+      else
+        s[r] = -INFINITY;
+    }
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+      const int c = lane + 64 * m;
+      *reinterpret_cast<uint4 *>(&vs[c >> 4][(c & 15) * 4]) = vw[m];
+    }
+    // Online softmax per row (every lane holds every row's running state).
+    float alpha[G];
+#pragma unroll
+    for (int r = 0; r < G; ++r) {
+      const float next = fmaxf(maximum[r], xor_max32(s[r]));
+      alpha[r] = isfinite(maximum[r]) ? expf(maximum[r] - next) : 0.f;
+      const float prob = isfinite(s[r]) ? expf(s[r] - next) : 0.f;
+      const float total = xor_sum32(prob);
+      if (half == 0)
+        ps[key][r] = B(prob);
+      den[r] = __builtin_fmaf(den[r], alpha[r], total);
+      maximum[r] = next;
+    }
+    __syncthreads();
+    // PV: dimensions 2*lane, 2*lane + 1.
+#pragma unroll
+    for (int r = 0; r < G; ++r) {
+      acc[r][0] *= alpha[r];
+      acc[r][1] *= alpha[r];
+    }
+    for (int j = 0; j < kKeys; ++j) {
+      const uint32_t v2 = vs[j][lane];
+      const float v0 = lo16(v2), v1 = hi16(v2);
+      fine = fine && ((v2 & 0x7f80u) != 0x7f80u) && ((v2 & 0x7f800000u) != 0x7f800000u);
+#pragma unroll
+      for (int r = 0; r < G; ++r) {
+        const float p = ps[j][r];
+        acc[r][0] = __builtin_fmaf(p, v0, acc[r][0]);
+        acc[r][1] = __builtin_fmaf(p, v1, acc[r][1]);
+      }
+    }
+    __syncthreads();
+  }
+  const int head0 = kv * G;
+#pragma unroll
+  for (int r = 0; r < G; ++r) {
+    float *dst = a.partial + (((size_t)seq * a.splits + split) * a.hq + head0 + r) * kD;
+    const float v0 = acc[r][0] / den[r], v1 = acc[r][1] / den[r];
+    fine = fine && isfinite(v0) && isfinite(v1);
+    *reinterpret_cast<float2 *>(dst + 2 * lane) = make_float2(v0, v1);
+    if (lane == 0) {
+      const float l = maximum[r] + logf(den[r]);
+      fine = fine && isfinite(l);
+      a.lse[((size_t)seq * a.splits + split) * a.hq + head0 + r] = l;
+    }
+  }
+  if (__ballot(!fine) != 0 && lane == 0)
+    raise_bad(a.bad);
+}
+
+template <class T> __global__ __launch_bounds__(64) void k_attn_merge(AttnArgs a) {
+  __shared__ float weights[32];
+  const int head = blockIdx.x, seq = blockIdx.y, lane = threadIdx.x;
+  int n, first;
+  if (!attn_window(a, seq, n, first))
+    return; // the split kernel raised the flag
+  const int active = min(a.splits, (n + kKeys - 1) / kKeys);
+  const float v = lane < active ? a.lse[((size_t)seq * a.splits + lane) * a.hq + head] : -INFINITY;
+  const float mx = xor_max32(v);
+  const float w = lane < active ? expf(v - mx) : 0.f;
+  const float total = xor_sum32(w);
+  bool fine = true;
+  if (lane < active) {
+    weights[lane] = w / total;
+    fine = isfinite(weights[lane]);
+  }
+  __syncthreads();
+  float s0 = 0.f, s1 = 0.f;
+  for (int sp = 0; sp < active; ++sp) {
+    const float2 p = *reinterpret_cast<const float2 *>(
+        a.partial + (((size_t)seq * a.splits + sp) * a.hq + head) * kD + 2 * lane);
+    s0 = __builtin_fmaf(weights[sp], p.x, s0);
+    s1 = __builtin_fmaf(weights[sp], p.y, s1);
+  }
+  const uint32_t word = pack2(s0, s1);
+  fine = fine && ((word & 0x7f80u) != 0x7f80u) && ((word & 0x7f800000u) != 0x7f800000u);
+  const size_t o = ((size_t)seq * a.hq + head) * kD + 2 * lane;
+  if constexpr (std::is_same<T, uint16_t>::value)
+    static_cast<uint32_t *>(a.out)[o / 2] = word;
+  else
+    *reinterpret_cast<float2 *>(static_cast<float *>(a.out) + o) =
+        make_float2(lo16(word), hi16(word));
+  if (__ballot(!fine) != 0 && lane == 0)
+    raise_bad(a.bad);
+}
+
+} // namespace
+
+extern "C" long long padra_DecodeAttentionScratch(int seqs, int q_heads, int splits) {
+  if (seqs < 1 || q_heads < 1 || splits < 1 || splits > 32)
+    return -1;
+  return (long long)seqs * splits * q_heads * (kD + 1);
+}
+
+extern "C" int padra_DecodeAttention(void *stream, const void *q, const padra_KVCache *kv,
+                                     void *out, const padra_Positions *pos, int seqs,
+                                     int q_heads, int kv_heads, int local, int splits,
+                                     float *scratch, long long scratch_floats, int *bad,
+                                     int act) {
+  if (!q || !kv || !out || !pos || !bad || !scratch || seqs < 1 || q_heads < 1 ||
+      kv_heads < 1 || q_heads % kv_heads || kv->format != PADRA_KV_BF16 || !kv->k || !kv->v ||
+      kv->cap < 1 || kv->cap > 131072 || pos->mode != PADRA_POS_DECODE || !pos->decode ||
+      pos->maximum < 1 || pos->maximum > 131072 || pos->vocab < 1 ||
+      (seqs > 1 && kv->seq_stride < kv->cap) || (act != PADRA_ACT_BF16 && act != PADRA_ACT_F32) ||
+      !aligned16(kv->k) || !aligned16(kv->v) || !aligned16(scratch) || splits < 0 || splits > 32)
+    return PADRA_INVALID_ARGUMENT;
+  if (splits == 0) // the reference's count (MaxSplits)
+    splits = std::min((kv->cap + kKeys - 1) / kKeys, local ? 16 : 32);
+  const long long need = padra_DecodeAttentionScratch(seqs, q_heads, splits);
+  if (scratch_floats < need)
+    return PADRA_INVALID_ARGUMENT;
+  AttnArgs a{};
+  a.q = q;
+  a.kc = static_cast<const uint16_t *>(kv->k);
+  a.vc = static_cast<const uint16_t *>(kv->v);
+  a.out = out;
+  a.partial = scratch;
+  a.lse = scratch + (long long)seqs * splits * q_heads * kD;
+  a.decode = pos->decode;
+  a.seqs = seqs;
+  a.hq = q_heads;
+  a.hkv = kv_heads;
+  a.cap = kv->cap;
+  a.local = local ? 1 : 0;
+  a.splits = splits;
+  a.maximum = pos->maximum;
+  a.vocab = pos->vocab;
+  a.seq_stride = seqs > 1 ? kv->seq_stride : 0;
+  a.bad = bad;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 split_grid(splits, kv_heads, seqs), merge_grid(q_heads, seqs);
+  const int group = q_heads / kv_heads;
+  auto launch = [&](auto tag) -> int {
+    using T = decltype(tag);
+    switch (group) {
+    case 1:
+      hipLaunchKernelGGL((k_attn_split<1, T>), split_grid, dim3(64), 0, s, a);
+      break;
+    case 2:
+      hipLaunchKernelGGL((k_attn_split<2, T>), split_grid, dim3(64), 0, s, a);
+      break;
+    case 4:
+      hipLaunchKernelGGL((k_attn_split<4, T>), split_grid, dim3(64), 0, s, a);
+      break;
+    case 8:
+      hipLaunchKernelGGL((k_attn_split<8, T>), split_grid, dim3(64), 0, s, a);
+      break;
+    default:
+      return PADRA_UNSUPPORTED;
+    }
+    hipLaunchKernelGGL((k_attn_merge<T>), merge_grid, dim3(64), 0, s, a);
+    return launched("DecodeAttention");
+  };
+  return act == PADRA_ACT_BF16 ? launch(uint16_t{}) : launch(float{});
+}

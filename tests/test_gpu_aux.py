@@ -414,3 +414,95 @@ def test_kv_checkpoint_capture(oracle, fmt):
                             tokens, anchor, bad)
     torch.cuda.synchronize()
     assert all(bool((t == 0xAB).all()) for t in sv)
+
+
+# ---- decode attention --------------------------------------------------------------------
+
+def _attn_close(got_bits, want_bits):
+    """Per element: within 1 BF16 ulp of the oracle, or within 2^-12 of the head's largest
+    |output|.  The second bound covers near-cancelling sums, where a BF16 probability that
+    rounds the other way (the score's fp32 sum order differs) moves the output by a
+    fraction of one term, not of the small result."""
+    d = _ulp_diff(got_bits, want_bits)
+    g, w = synth.bf16_to_f32(got_bits), synth.bf16_to_f32(want_bits)
+    head_max = np.abs(w).max(axis=-1, keepdims=True)
+    return (d <= 1) | (np.abs(g - w) <= 2.0**-12 * head_max), d
+
+
+def _ulp_diff(got_bits, want_bits):
+    """Distance in BF16 ulps (ordered bit patterns, both signs)."""
+    def ordered(b):
+        b = b.astype(np.int32)
+        return np.where(b & 0x8000, 0x8000 - (b & 0x7FFF), 0x8000 + b)
+    return np.abs(ordered(got_bits) - ordered(want_bits))
+
+
+@pytest.mark.parametrize("hq,local,splits", [(16, False, 0), (32, False, 0), (16, True, 0),
+                                             (16, False, 5)])
+def test_decode_attention(oracle, hq, local, splits):
+    """Ragged decode batch against the oracle's attention at each sequence's position,
+    within the _attn_close tolerance (the reference's tensor-core order and CUDA expf/logf
+    differ from any other implementation by fp32 ulps before the BF16 roundings)."""
+    print(f"[case] decode attention hq={hq} local={local} splits={splits}", flush=True)
+    seqs, hkv, capacity = 6, 4, 4096
+    cap = 1024 if local else capacity
+    rng = np.random.default_rng(90 + hq + local + splits)
+    positions = rng.integers(0, capacity, seqs).astype(np.int32)
+    positions[0], positions[1] = 0, 33
+    q = synth.bf16_bits((rng.standard_normal((seqs, hq, 128)) * 2).astype(np.float32))
+    kc = synth.bf16_bits(rng.standard_normal((seqs, cap, hkv * 128)).astype(np.float32))
+    vc = synth.bf16_bits(rng.standard_normal((seqs, cap, hkv * 128)).astype(np.float32))
+    states = np.zeros((seqs, 8), np.int32)
+    for s, p in enumerate(positions):
+        states[s] = [5, p, capacity, 10, p, min(p, 1024), 0, 0]
+    out = torch.empty((seqs, hq, 128), dtype=torch.int16, device="cuda")
+    bad = flag()
+    kv = ops.kv_cache(abi.KV_BF16, dev(kc.reshape(seqs * cap, -1)), dev(vc.reshape(seqs * cap, -1)),
+                      cap, seq_stride=cap)
+    st = torch.from_numpy(states).cuda()
+    ops.DecodeAttention(dev(q), kv, out, ops.positions_decode(st, maximum=capacity), bad,
+                        kv_heads=hkv, local=local, splits=splits)
+    torch.cuda.synchronize()
+    assert bad.item() == 0
+    got = host16(out)
+    worst = 0
+    for s in range(seqs):
+        want, _, wbad = oracle.decode_attention(q[s], kc[s], vc[s], positions[s], local=local,
+                                                splits=splits)
+        assert not wbad
+        close, d = _attn_close(got[s], want)
+        assert close.all(), s
+        worst = max(worst, int(d.max()))
+        if d.max() > 1:
+            i = np.unravel_index(np.argmax(d), d.shape)
+            gv, wv = synth.bf16_to_f32(got[s])[i], synth.bf16_to_f32(want)[i]
+            hm = np.abs(synth.bf16_to_f32(want)[i[0]]).max()
+            print(f"  seq {s} pos {positions[s]} at {i}: got {gv} want {wv} head max {hm} "
+                  f"count>1: {(d > 1).sum()}", flush=True)
+    print(f"  max BF16 ulp difference {worst}", flush=True)
+
+
+def test_decode_attention_f32_and_invalid(oracle):
+    seqs, hq, hkv, cap = 3, 16, 4, 512
+    rng = np.random.default_rng(97)
+    positions = np.array([100, 511, 7], np.int32)
+    q = synth.bf16_bits(rng.standard_normal((seqs, hq, 128)).astype(np.float32))
+    kc = synth.bf16_bits(rng.standard_normal((seqs, cap, hkv * 128)).astype(np.float32))
+    vc = synth.bf16_bits(rng.standard_normal((seqs, cap, hkv * 128)).astype(np.float32))
+    states = np.zeros((seqs, 8), np.int32)
+    for s, p in enumerate(positions):
+        states[s] = [5, p, cap, 10, p, min(p, 1024), 0, 0]
+    states[2, 6] = 1  # eos: not admitted, nothing written, flag raised
+    out = torch.full((seqs, hq, 128), 7.0, dtype=torch.float32, device="cuda")
+    bad = flag()
+    kv = ops.kv_cache(abi.KV_BF16, dev(kc.reshape(seqs * cap, -1)), dev(vc.reshape(seqs * cap, -1)),
+                      cap, seq_stride=cap)
+    ops.DecodeAttention(torch.from_numpy(synth.bf16_to_f32(q)).cuda(), kv, out,
+                        ops.positions_decode(torch.from_numpy(states).cuda(), maximum=cap), bad)
+    torch.cuda.synchronize()
+    assert bad.item() == 1
+    got = out.cpu().numpy()
+    assert np.all(got[2] == 7.0)
+    for s in range(2):
+        want, _, _ = oracle.decode_attention(q[s], kc[s], vc[s], positions[s])
+        assert _attn_close(synth.bf16_bits(got[s]), want)[0].all()

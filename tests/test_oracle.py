@@ -35,6 +35,9 @@ Per oracle function, what checks it:
   po_combine_norm                 = po_combine, then po_norm_fp8 / po_rmsnorm of the new x
   po_kv_checkpoint_*              slot contents by search over positions (the newest p <
                                   anchor with p = slot mod 1024), admission truth table
+  po_decode_attention             float64 softmax attention over the same keys (global and
+                                  local ring) within the BF16-probability error bound; the
+                                  split count changes results only within that bound
 """
 import numpy as np
 import pytest
@@ -636,3 +639,48 @@ def test_kv_checkpoint_admission(oracle):
     stale[4] = 99                                                      # committed != base
     assert oracle.kv_checkpoint([old], [cur], stale, 10, 105) is None
     assert oracle.kv_checkpoint([old], [cur], good, 10, 105, epoch=2) is None
+
+
+# ---- decode attention -------------------------------------------------------------------------
+
+def _attn_inputs(cap, hq, hkv, seed):
+    rng = np.random.default_rng(seed)
+    q = synth.bf16_bits((rng.standard_normal((hq, 128)) * 2).astype(F32))
+    kc = synth.bf16_bits(rng.standard_normal((cap, hkv * 128)).astype(F32))
+    vc = synth.bf16_bits(rng.standard_normal((cap, hkv * 128)).astype(F32))
+    return q, kc, vc
+
+
+def _attn_float64(q, kc, vc, rows, hkv):
+    hq = q.shape[0]
+    g = hq // hkv
+    qf = synth.bf16_to_f32(q).astype(np.float64)
+    out = np.empty((hq, 128))
+    for h in range(hq):
+        kv = h // g
+        k = synth.bf16_to_f32(kc[rows, kv * 128:(kv + 1) * 128]).astype(np.float64)
+        v = synth.bf16_to_f32(vc[rows, kv * 128:(kv + 1) * 128]).astype(np.float64)
+        s = k @ qf[h] / np.sqrt(128.0)
+        w = np.exp(s - s.max())
+        out[h] = (w / w.sum()) @ v
+    return out
+
+
+@pytest.mark.parametrize("position,local,cap", [(0, False, 256), (77, False, 256),
+                                                (4000, False, 4096), (3000, True, 1024)])
+def test_decode_attention_float64(oracle, position, local, cap):
+    hq, hkv = 16, 4
+    q, kc, vc = _attn_inputs(cap, hq, hkv, position)
+    out, used, bad = oracle.decode_attention(q, kc, vc, position, local=local)
+    assert not bad
+    n = min(position + 1, 1024) if local else position + 1
+    rows = np.arange(position + 1 - n, position + 1) % cap
+    ref = _attn_float64(q, kc, vc, rows, hkv)
+    got = synth.bf16_to_f32(out).astype(np.float64)
+    # BF16 probabilities (relative 2^-9 each) and the final BF16 rounding
+    vmax = np.abs(synth.bf16_to_f32(vc)).max()
+    assert np.all(np.abs(got - ref) <= 2.0**-8 * np.abs(ref) + 2.0**-8 * vmax)
+    if not local and cap == 4096:
+        other, used2, _ = oracle.decode_attention(q, kc, vc, position, splits=7)
+        assert used2 == 7 and used == 32
+        assert np.all(np.abs(synth.bf16_to_f32(other) - got) <= 2.0**-7 * vmax)
