@@ -67,3 +67,75 @@ def test_rope_table_host_matches_oracle(oracle, theta, yarn):
     got = ops.RopeTable(3000, 128, theta, yarn=yarn).view(__import__("torch").int16).numpy()
     want = synth.bf16_bits(oracle.rope_table(3000, 128, theta, yarn=yarn))
     assert np.array_equal(got.view(np.uint16), want)
+
+
+def _p(v):
+    return ctypes.c_void_p(v)
+
+
+def test_host_validation_newer_entry_points():
+    """Argument checks of the FP8 norm, combine, checkpoint, q8_0 prefix decode and decode
+    attention entry points: each returns its status and launches nothing."""
+    lib = abi.lib()
+    bad = _p(16)
+    # FP8 norm: packed must be given and 16-byte aligned; hidden from the supported set
+    assert lib.padra_NormFP8(None, _p(16), _p(32), _p(48), None, _p(64), 4, 2048, 1e-6, None, bad,
+                             0) == abi.INVALID_ARGUMENT
+    assert lib.padra_NormFP8(None, _p(16), _p(32), _p(48), _p(72), _p(64), 4, 2048, 1e-6, None,
+                             bad, 0) == abi.INVALID_ARGUMENT
+    assert lib.padra_NormFP8(None, _p(16), _p(32), _p(48), _p(64), _p(64), 4, 1536, 1e-6, None,
+                             bad, 0) == abi.UNSUPPORTED
+    # combine: the reference's top-8 only
+    assert lib.padra_Combine(None, _p(16), _p(32), _p(48), 4, 2048, 6, 1, bad, 0) == \
+        abi.UNSUPPORTED
+    assert lib.padra_Combine(None, _p(16), _p(32), _p(48), 4, 2044, 8, 1, bad, 0) == \
+        abi.INVALID_ARGUMENT
+    # combine + norm: normalized may not alias x; scales required with packed
+    assert lib.padra_CombineNorm(None, _p(16), _p(32), _p(48), _p(16), _p(64), None, None, 1,
+                                 2304, 8, 1e-6, None, bad, 0) == abi.INVALID_ARGUMENT
+    assert lib.padra_CombineNorm(None, _p(16), _p(32), _p(48), _p(80), _p(64), _p(96), None, 1,
+                                 2304, 8, 1e-6, None, bad, 0) == abi.INVALID_ARGUMENT
+    # checkpoint: formats must agree, the snapshot may not alias a source
+    ring = abi.KVCache(format=abi.KV_BF16, k=16, v=32, scales=None, cap=1024, first=0,
+                       seq_stride=0)
+    chunk = abi.KVCache(format=abi.KV_BF16, k=48, v=64, scales=None, cap=16, first=0,
+                        seq_stride=0)
+    other = abi.KVCache(format=abi.KV_Q8_0, k=80, v=96, scales=None, cap=1024, first=0,
+                        seq_stride=0)
+    alias = abi.KVCache(format=abi.KV_BF16, k=48, v=96, scales=None, cap=1024, first=0,
+                        seq_stride=0)
+    good = abi.KVCache(format=abi.KV_BF16, k=80, v=96, scales=None, cap=1024, first=0,
+                       seq_stride=0)
+    state = np.zeros(8, np.int32)
+    pre = abi.Positions(mode=abi.POS_PREFILL, base=0, prefill=state.ctypes.data, decode=None,
+                        maximum=4096, vocab=1, binding_epoch=1)
+    for saved, want in ((other, abi.INVALID_ARGUMENT), (alias, abi.INVALID_ARGUMENT)):
+        assert lib.padra_KVCheckpointCapture(None, ctypes.byref(ring), ctypes.byref(chunk),
+                                             ctypes.byref(saved), ctypes.byref(pre), 16, 8, 4,
+                                             bad) == want
+    base = abi.Positions(mode=abi.POS_BASE, base=0, prefill=None, decode=None, maximum=4096,
+                         vocab=1, binding_epoch=1)
+    assert lib.padra_KVCheckpointCapture(None, ctypes.byref(ring), ctypes.byref(chunk),
+                                         ctypes.byref(good), ctypes.byref(base), 16, 8, 4,
+                                         bad) == abi.INVALID_ARGUMENT
+    # q8_0 prefix decode needs a PrefillState
+    assert lib.padra_KvQ8_0DequantizePrefix(None, _p(16), _p(32), _p(48), _p(64),
+                                            ctypes.byref(base), 8, 64, 4, bad) == \
+        abi.INVALID_ARGUMENT
+    # decode attention: a BF16 cache, decode states, enough scratch, supported head groups
+    dec = abi.Positions(mode=abi.POS_DECODE, base=0, prefill=None, decode=state.ctypes.data,
+                        maximum=4096, vocab=98304, binding_epoch=1)
+    kv = abi.KVCache(format=abi.KV_BF16, k=16, v=32, scales=None, cap=4096, first=0,
+                     seq_stride=4096)
+    need = lib.padra_DecodeAttentionScratch(2, 16, 32)
+    assert need == 2 * 32 * 16 * 129
+    assert lib.padra_DecodeAttentionScratch(2, 16, 33) == -1
+    assert lib.padra_DecodeAttention(None, _p(16), ctypes.byref(kv), _p(32), ctypes.byref(dec), 2,
+                                     16, 4, 0, 0, _p(64), need - 1, bad, 0) == abi.INVALID_ARGUMENT
+    assert lib.padra_DecodeAttention(None, _p(16), ctypes.byref(kv), _p(32), ctypes.byref(dec), 2,
+                                     24, 4, 0, 0, _p(64), need * 2, bad, 0) == abi.UNSUPPORTED
+    q8 = abi.KVCache(format=abi.KV_Q8, k=16, v=32, scales=48, cap=4096, first=0, seq_stride=4096)
+    assert lib.padra_DecodeAttention(None, _p(16), ctypes.byref(q8), _p(32), ctypes.byref(dec), 2,
+                                     16, 4, 0, 0, _p(64), need, bad, 0) == abi.INVALID_ARGUMENT
+    assert lib.padra_DecodeAttention(None, _p(16), ctypes.byref(kv), _p(32), ctypes.byref(base),
+                                     2, 16, 4, 0, 0, _p(64), need, bad, 0) == abi.INVALID_ARGUMENT
