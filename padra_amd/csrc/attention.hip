@@ -79,6 +79,12 @@ __device__ __forceinline__ float xor_sum32(float v) {
   return v;
 }
 
+// a.lo * b.lo + a.hi * b.hi + c for BF16 pairs (v_dot2_f32_bf16).
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
+                                        __builtin_bit_cast(bf16x2_t, b), c, false);
+}
+
 template <class T> __device__ __forceinline__ float act_value(const void *p, size_t i) {
   if constexpr (std::is_same<T, uint16_t>::value)
     return __uint_as_float((uint32_t) static_cast<const uint16_t *>(p)[i] << 16);
@@ -88,9 +94,9 @@ template <class T> __device__ __forceinline__ float act_value(const void *p, siz
 
 template <int G, class T>
 __global__ __launch_bounds__(64) void k_attn_split(AttnArgs a) {
-  __shared__ float qs[G][kD];
-  __shared__ uint32_t vs[kKeys][kD / 2]; // V tile, BF16 pairs
-  __shared__ float ps[kKeys][G];         // BF16-rounded probabilities
+  __shared__ uint32_t qs[G][kD / 2];         // query rows, BF16 pairs
+  __shared__ uint32_t vs[kKeys][kD / 2];     // V tile, BF16 pairs
+  __shared__ uint16_t ps[kKeys / 2][G][2];   // BF16 probabilities, key pairs per row
   const int split = blockIdx.x, kv = blockIdx.y, seq = blockIdx.z, lane = threadIdx.x;
   int n, first;
   const bool ok = attn_window(a, seq, n, first);
@@ -109,10 +115,12 @@ __global__ __launch_bounds__(64) void k_attn_split(AttnArgs a) {
 
   // Query rows: finite and BF16-exact, as the reference requires of its fp32 input.
   bool qfine = true;
-  for (int i = lane; i < G * kD; i += 64) {
-    const float x = act_value<T>(a.q, ((size_t)seq * a.hq + kv * G) * kD + i);
-    qfine = qfine && isfinite(x) && (__float_as_uint(x) & 0xffffu) == 0;
-    qs[i / kD][i % kD] = x;
+  for (int i = lane; i < G * kD / 2; i += 64) {
+    const size_t o = ((size_t)seq * a.hq + kv * G) * kD + 2 * i;
+    const float x0 = act_value<T>(a.q, o), x1 = act_value<T>(a.q, o + 1);
+    qfine = qfine && isfinite(x0) && isfinite(x1) && (__float_as_uint(x0) & 0xffffu) == 0 &&
+            (__float_as_uint(x1) & 0xffffu) == 0;
+    qs[i / (kD / 2)][i % (kD / 2)] = (__float_as_uint(x0) >> 16) | (__float_as_uint(x1) & 0xffff0000u);
   }
   if (__ballot(!qfine) != 0 && lane == 0)
     raise_bad(a.bad);
@@ -144,22 +152,19 @@ __global__ __launch_bounds__(64) void k_attn_split(AttnArgs a) {
       if (vo >= n)
         vw[m] = make_uint4(0, 0, 0, 0); // the reference zero-fills rows past the window
     }
-    // Scores of this lane's key for every row.
+    // Scores of this lane's key for every row: dot products of BF16 pairs (each product of
+    // two BF16 values is exact in fp32).
     float s[G];
 #pragma unroll
     for (int r = 0; r < G; ++r) {
       float dot = 0.f;
 #pragma unroll
       for (int m = 0; m < 8; ++m) {
-        const uint32_t w[4] = {kw[m].x, kw[m].y, kw[m].z, kw[m].w};
-        const float4 q0 = *reinterpret_cast<const float4 *>(&qs[r][half * 64 + 8 * m]);
-        const float4 q1 = *reinterpret_cast<const float4 *>(&qs[r][half * 64 + 8 * m + 4]);
-        const float qv[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          dot = __builtin_fmaf(qv[2 * i], lo16(w[i]), dot);
-          dot = __builtin_fmaf(qv[2 * i + 1], hi16(w[i]), dot);
-        }
+        const uint4 qw = *reinterpret_cast<const uint4 *>(&qs[r][half * 32 + 4 * m]);
+        dot = dot2(qw.x, kw[m].x, dot);
+        dot = dot2(qw.y, kw[m].y, dot);
+        dot = dot2(qw.z, kw[m].z, dot);
+        dot = dot2(qw.w, kw[m].w, dot);
       }
       s[r] = (dot + __shfl_xor(dot, 32, 64)) * kScoreScale;
       if (valid)
@@ -181,7 +186,7 @@ __global__ __launch_bounds__(64) void k_attn_split(AttnArgs a) {
       const float prob = isfinite(s[r]) ? expf(s[r] - next) : 0.f;
       const float total = xor_sum32(prob);
       if (half == 0)
-        ps[key][r] = B(prob);
+        ps[key / 2][r][key & 1] = (uint16_t)(pack2(prob, 0.f) & 0xffffu);
       den[r] = __builtin_fmaf(den[r], alpha[r], total);
       maximum[r] = next;
     }
@@ -192,15 +197,18 @@ __global__ __launch_bounds__(64) void k_attn_split(AttnArgs a) {
       acc[r][0] *= alpha[r];
       acc[r][1] *= alpha[r];
     }
-    for (int j = 0; j < kKeys; ++j) {
-      const uint32_t v2 = vs[j][lane];
-      const float v0 = lo16(v2), v1 = hi16(v2);
-      fine = fine && ((v2 & 0x7f80u) != 0x7f80u) && ((v2 & 0x7f800000u) != 0x7f800000u);
+    // Key pairs: (V[2jp][d], V[2jp+1][d]) against the row's probability pair.  A
+    // non-finite V value reaches the outputs (inf or NaN) and is flagged there.
+#pragma unroll 4
+    for (int jp = 0; jp < kKeys / 2; ++jp) {
+      const uint32_t va = vs[2 * jp][lane], vb = vs[2 * jp + 1][lane];
+      const uint32_t x0 = __builtin_amdgcn_perm(vb, va, 0x05040100u); // (va.lo, vb.lo)
+      const uint32_t x1 = __builtin_amdgcn_perm(vb, va, 0x07060302u); // (va.hi, vb.hi)
 #pragma unroll
       for (int r = 0; r < G; ++r) {
-        const float p = ps[j][r];
-        acc[r][0] = __builtin_fmaf(p, v0, acc[r][0]);
-        acc[r][1] = __builtin_fmaf(p, v1, acc[r][1]);
+        const uint32_t pw = *reinterpret_cast<const uint32_t *>(ps[jp][r]);
+        acc[r][0] = dot2(pw, x0, acc[r][0]);
+        acc[r][1] = dot2(pw, x1, acc[r][1]);
       }
     }
     __syncthreads();
