@@ -95,7 +95,10 @@ template <class T> __device__ __forceinline__ float act_value(const void *p, siz
 template <int G, class T>
 __global__ __launch_bounds__(64) void k_attn_split(AttnArgs a) {
   __shared__ uint32_t qs[G][kD / 2];         // query rows, BF16 pairs
-  __shared__ uint32_t vs[kKeys][kD / 2];     // V tile, BF16 pairs
+  // K and V tiles, BF16 pairs; K rows padded to 68 words so that the 32 key lanes' 16-byte
+  // reads spread over the banks.
+  __shared__ uint32_t ks[kKeys][kD / 2 + 4];
+  __shared__ uint32_t vs[kKeys][kD / 2];
   __shared__ uint16_t ps[kKeys / 2][G][2];   // BF16 probabilities, key pairs per row
   const int split = blockIdx.x, kv = blockIdx.y, seq = blockIdx.z, lane = threadIdx.x;
   int n, first;
@@ -135,23 +138,34 @@ __global__ __launch_bounds__(64) void k_attn_split(AttnArgs a) {
   }
   bool fine = true;
   __syncthreads();
-  for (int tile = begin; tile < end; ++tile) {
-    // Loads: this lane's half key row (8 x 16 B) and eight 16-byte chunks of the V tile.
-    const int offset = tile * kKeys + key;
-    const bool valid = offset < n;
-    const int row = (first + (valid ? offset : 0)) % a.cap;
-    uint4 kw[8], vw[8];
-#pragma unroll
-    for (int m = 0; m < 8; ++m)
-      kw[m] = ld_nt(reinterpret_cast<const uint4 *>(kc + (size_t)row * features + half * 64) + m);
+  // Tile loads: 16-byte chunk c = lane + 64 m of the tile's 32 key rows (key c / 16,
+  // dimensions 8 (c % 16) ..), contiguous 1 KB per instruction.  Rows past the window load
+  // a valid row and are zeroed (the reference zero-fills them).
+  auto load_tile = [&](int tile, uint4 (&kw)[8], uint4 (&vw)[8]) {
 #pragma unroll
     for (int m = 0; m < 8; ++m) {
-      const int c = lane + 64 * m, vk = c >> 4, part = c & 15, vo = tile * kKeys + vk;
-      const int vrow = (first + (vo < n ? vo : 0)) % a.cap;
-      vw[m] = ld_nt(reinterpret_cast<const uint4 *>(vc + (size_t)vrow * features) + part);
-      if (vo >= n)
-        vw[m] = make_uint4(0, 0, 0, 0); // the reference zero-fills rows past the window
+      const int c = lane + 64 * m, o = tile * kKeys + (c >> 4);
+      const size_t r = (size_t)((first + (o < n ? o : 0)) % a.cap) * features;
+      kw[m] = ld_nt(reinterpret_cast<const uint4 *>(kc + r) + (c & 15));
+      vw[m] = ld_nt(reinterpret_cast<const uint4 *>(vc + r) + (c & 15));
     }
+  };
+  uint4 kw[8], vw[8];
+  load_tile(begin, kw, vw);
+  for (int tile = begin; tile < end; ++tile) {
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+      const int c = lane + 64 * m;
+      if (tile * kKeys + (c >> 4) >= n)
+        kw[m] = vw[m] = make_uint4(0, 0, 0, 0);
+      *reinterpret_cast<uint4 *>(&ks[c >> 4][(c & 15) * 4]) = kw[m];
+      *reinterpret_cast<uint4 *>(&vs[c >> 4][(c & 15) * 4]) = vw[m];
+    }
+    __syncthreads();
+    // The next tile's loads are in flight during this tile's arithmetic (the last tile
+    // reloads itself, keeping the loads unconditional).
+    load_tile(min(tile + 1, end - 1), kw, vw);
+    const bool valid = tile * kKeys + key < n;
     // Scores of this lane's key for every row: dot products of BF16 pairs (each product of
     // two BF16 values is exact in fp32).
     float s[G];
@@ -161,21 +175,17 @@ __global__ __launch_bounds__(64) void k_attn_split(AttnArgs a) {
 #pragma unroll
       for (int m = 0; m < 8; ++m) {
         const uint4 qw = *reinterpret_cast<const uint4 *>(&qs[r][half * 32 + 4 * m]);
-        dot = dot2(qw.x, kw[m].x, dot);
-        dot = dot2(qw.y, kw[m].y, dot);
-        dot = dot2(qw.z, kw[m].z, dot);
-        dot = dot2(qw.w, kw[m].w, dot);
+        const uint4 kq = *reinterpret_cast<const uint4 *>(&ks[key][half * 32 + 4 * m]);
+        dot = dot2(qw.x, kq.x, dot);
+        dot = dot2(qw.y, kq.y, dot);
+        dot = dot2(qw.z, kq.z, dot);
+        dot = dot2(qw.w, kq.w, dot);
       }
       s[r] = (dot + __shfl_xor(dot, 32, 64)) * kScoreScale;
       if (valid)
         fine = fine && isfinite(s[r]);
       else
         s[r] = -INFINITY;
-    }
-#pragma unroll
-    for (int m = 0; m < 8; ++m) {
-      const int c = lane + 64 * m;
-      *reinterpret_cast<uint4 *>(&vs[c >> 4][(c & 15) * 4]) = vw[m];
     }
     // Online softmax per row (every lane holds every row's running state).
     float alpha[G];
