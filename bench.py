@@ -345,7 +345,7 @@ def bench_attention(torch, steps, seqs=64, capacity=CAPACITY, fill_seed=0):
     bad = torch.zeros(1, dtype=torch.int32, device="cuda")
     kv = ops.kv_cache(abi.KV_BF16, kc, vc, capacity, seq_stride=capacity)
     pos = ops.positions_decode(st, maximum=capacity)
-    scratch = ops.DecodeAttention(q, kv, out, pos, bad)
+    scratch = ops.DecodeAttention(q, kv, out, pos, bad)  # allocates the scratch once
     ms = graph_time(torch, lambda i: ops.DecodeAttention(q, kv, out, pos, bad, scratch=scratch),
                     steps)
     if bad.item():

@@ -252,25 +252,28 @@ int padra_CombineNorm(void *stream, void *x, const void *down, const float *weig
                       void *normalized, const uint16_t *gamma, uint8_t *packed, float *scales,
                       int rows, int hidden, int experts, float eps, float *statistics, int *bad,
                       int act);
-/* padra_DecodeAttention: decode attention over a BF16 cache, one token per sequence:
- * gqa8_fragment_validation::SplitBF16 (attention_gqa8_fragment_validation.cuh:79-214) and
- * attention_perhead_exact::Merge (attention_perhead_exact.cuh:7-38), for q_heads/kv_heads
- * in {1, 2, 4, 8} query heads per KV head.  q [seqs][q_heads][128] (BF16-exact), out
- * likewise; kv: a BF16 cache binding (cap rows per sequence, seq_stride rows apart);
- * pos: PADRA_POS_DECODE states.  local != 0: a 1024-row local ring (cap must be
- * min(1024, capacity)), else cap must equal capacity.  splits: 1..32 split-K partitions,
- * 0 for the reference's count min(ceil(cap/32), local ? 16 : 32).  scratch: device fp32
- * workspace of padra_DecodeAttentionScratch(seqs, q_heads, splits) floats (partials and
- * log-sum-exps).  A sequence whose state is not admitted raises *bad and writes nothing;
- * non-finite scores, values or outputs raise *bad.  Results match the reference within
- * the tolerance its tensor-core accumulation order and CUDA expf/logf leave (the
- * products of BF16 values are exact in fp32; the sums run in another order). */
+/* padra_DecodeAttention: decode attention, one token per sequence, for q_heads/kv_heads in
+ * {1, 2, 4, 8} query heads per KV head.
+ *  - BF16 cache: gqa8_fragment_validation::SplitBF16 (attention_gqa8_fragment_validation.cuh:
+ *    79-214) and attention_perhead_exact::Merge (attention_perhead_exact.cuh:7-38).
+ *  - q8_0 cache (rotated v2, 4 KV heads): q8_native::EncodeQuery, Split and Merge
+ *    (kv_q8_native.cuh:103-148, 198-363); a local ring must have cap 1024.
+ * q [seqs][q_heads][128] (BF16-exact), out likewise; kv: the cache binding (cap rows per
+ * sequence, seq_stride rows apart); pos: PADRA_POS_DECODE states.  local != 0: a local
+ * ring (BF16: cap = min(1024, capacity)), else cap must equal capacity.  splits: 1..32
+ * split-K partitions, 0 for the reference's count (BF16: min(ceil(cap/32), local ? 16 : 32);
+ * q8_0: local ? 16 : 32).  scratch: device fp32 workspace of
+ * padra_DecodeAttentionScratch(kv->format, seqs, q_heads, splits) floats.  A sequence whose
+ * state is not admitted raises *bad and writes nothing; non-finite queries, scores or
+ * outputs raise *bad.  Results match the reference within the tolerance its tensor-core
+ * accumulation order (BF16) and CUDA expf/logf leave. */
 int padra_DecodeAttention(void *stream, const void *q, const padra_KVCache *kv, void *out,
                           const padra_Positions *pos, int seqs, int q_heads, int kv_heads,
                           int local, int splits, float *scratch, long long scratch_floats,
                           int *bad, int act);
-/* Floats of scratch padra_DecodeAttention needs (splits as passed, 1..32); -1 if invalid. */
-long long padra_DecodeAttentionScratch(int seqs, int q_heads, int splits);
+/* Floats of scratch padra_DecodeAttention needs for a cache format (splits as passed,
+ * 1..32); -1 if invalid. */
+long long padra_DecodeAttentionScratch(int format, int seqs, int q_heads, int splits);
 /* padra_CheckFP8Paths: no counterpart in the reference.  Checks, over their whole domains,
  * the two identities padra_NormFP8's fast path relies on (the hardware E4M3 conversion, and
  * the reciprocal-plus-correction quotient) and writes the mismatch counts to counts[0..1]

@@ -42,6 +42,7 @@ def lib() -> ctypes.CDLL:
             "po_norm_fp8": ([P, P, P, P, P, I, I, F, P, P], None),
             "po_combine": ([P, P, P, I, I, I, I, P], None),
             "po_decode_attention": ([P, P, P, I, I, I, I, I, I, P, P], I),
+            "po_decode_attention_q8_0": ([P, P, P, I, I, I, I, I, I, P, P], I),
             "po_kv_checkpoint_plane": ([P, P, P, I, I, I], None),
             "po_kv_checkpoint_admitted": ([P, I, I, ctypes.c_uint32, I], I),
             "po_combine_norm": ([P, P, P, P, P, P, P, I, I, I, F, P, P], None),
@@ -185,6 +186,21 @@ def decode_attention(q, kc, vc, position, local=False, splits=0):
     bad = Bad()
     used = lib().po_decode_attention(_p(q), _p(kc), _p(vc), cap, int(position), int(bool(local)),
                                      hq, features // 128, int(splits), _p(out), bad.ptr)
+    return out, used, bool(bad)
+
+
+def decode_attention_q8_0(q, rows_k, rows_v, position, local=False, splits=0, hkv=4):
+    """q [hq][128] BF16 bits, rows_k / rows_v [cap][544] q8_0 rows.  Returns (out [hq][128]
+    BF16 bits, splits used, bad)."""
+    q = np.ascontiguousarray(q, np.uint16)
+    rows_k = np.ascontiguousarray(rows_k, np.uint8)
+    rows_v = np.ascontiguousarray(rows_v, np.uint8)
+    hq = q.shape[0]
+    out = np.zeros((hq, 128), np.uint16)
+    bad = Bad()
+    used = lib().po_decode_attention_q8_0(_p(q), _p(rows_k), _p(rows_v), rows_k.shape[0],
+                                          int(position), int(bool(local)), hq, hkv, int(splits),
+                                          _p(out), bad.ptr)
     return out, used, bool(bad)
 
 

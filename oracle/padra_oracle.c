@@ -796,3 +796,177 @@ int po_decode_attention(const uint16_t *q, const uint16_t *kc, const uint16_t *v
   free(lse);
   return active;
 }
+
+/* ---- Decode attention over a q8_0 cache ----------------------------------------------- */
+
+static float half_bits_to_f32(const uint8_t *p) {
+  uint16_t h;
+  memcpy(&h, p, 2);
+  return po_f16_to_f32(h);
+}
+
+/* kv_q8_native.cuh:103-148, 198-363 */
+int po_decode_attention_q8_0(const uint16_t *q, const uint8_t *kc, const uint8_t *vc, int cap,
+                             int position, int local, int hq, int hkv, int splits, uint16_t *out,
+                             int *bad) {
+  const int D = 128, G = hq / hkv, features = hkv * D, rb = po_q8_0_row_bytes(features);
+  const int dbytes = 2 * (features / 32);
+  const float scale = .08838834764831845f;
+  if (local ? cap != 1024 : position >= cap) { /* the ring the reference admits */
+    set_bad(bad);
+    return -1;
+  }
+  /* EncodeQuery */
+  int8_t qcode[64][128];
+  float qd[64][4];
+  for (int h = 0; h < hq; ++h) {
+    float x[128];
+    for (int d = 0; d < D; ++d) {
+      x[d] = po_bf16_to_f32(q[h * D + d]);
+      if (!finite_f(x[d])) {
+        set_bad(bad);
+        return -1;
+      }
+    }
+    po_hadamard(x, 128, .08838834764831845f);
+    for (int b = 0; b < 4; ++b) {
+      float m = 0.f;
+      for (int i = 0; i < 32; ++i)
+        m = fmaxf(m, fabsf(x[32 * b + i]));
+      const float d = m / 127.f;
+      if (!finite_f(d)) {
+        set_bad(bad);
+        return -1;
+      }
+      qd[h][b] = d;
+      for (int i = 0; i < 32; ++i)
+        qcode[h][32 * b + i] = q8_0_code(x[32 * b + i], d == 0.f ? 0.f : 1.f / d);
+    }
+  }
+  const int n = local ? (position + 1 < 1024 ? position + 1 : 1024) : position + 1;
+  const int first = position + 1 - n, tiles = (n + 127) / 128;
+  if (splits <= 0)
+    splits = local ? 16 : 32;
+  const int active = splits < tiles ? splits : tiles;
+  float *partial = (float *)calloc((size_t)active * hq * D, sizeof(float));
+  float *lse = (float *)calloc((size_t)active * hq, sizeof(float));
+  for (int sp = 0; sp < active; ++sp) {
+    const int begin = tiles * sp / active, end = tiles * (sp + 1) / active;
+    for (int head = 0; head < hq; ++head) {
+      const int kv = head / G;
+      float mx[4], den[4][32], accum[4][128];
+      for (int s = 0; s < 4; ++s) {
+        mx[s] = -INFINITY;
+        for (int l = 0; l < 32; ++l)
+          den[s][l] = 0.f;
+        for (int d = 0; d < D; ++d)
+          accum[s][d] = 0.f;
+      }
+      for (int tile = begin; tile < end; ++tile)
+        for (int s = 0; s < 4; ++s) {
+          float own[32], p[32], ks[32][4], vs[32][4];
+          const int8_t *kq[32], *vq[32];
+          static const int8_t zeros[128];
+          float top = -INFINITY;
+          for (int k = 0; k < 32; ++k) {
+            const int offset = tile * 128 + s * 32 + k;
+            if (offset < n) {
+              const int row = local ? (first + offset) & 1023 : first + offset;
+              const uint8_t *kr = kc + (long long)row * rb, *vr = vc + (long long)row * rb;
+              for (int b = 0; b < 4; ++b) {
+                ks[k][b] = half_bits_to_f32(kr + 2 * (kv * 4 + b));
+                vs[k][b] = half_bits_to_f32(vr + 2 * (kv * 4 + b));
+              }
+              kq[k] = (const int8_t *)(kr + dbytes + kv * D);
+              vq[k] = (const int8_t *)(vr + dbytes + kv * D);
+            } else {
+              for (int b = 0; b < 4; ++b)
+                ks[k][b] = vs[k][b] = 0.f;
+              kq[k] = vq[k] = zeros;
+            }
+            float part[4];
+            for (int sub = 0; sub < 4; ++sub) {
+              float dot = 0.f;
+              for (int b = 0; b < 4; ++b) {
+                int sum = 0;
+                for (int half = 0; half < 2; ++half) {
+                  const int word = b * 8 + sub + 4 * half; /* 4-code group of block b */
+                  for (int i = 0; i < 4; ++i)
+                    sum += kq[k][4 * word + i] * qcode[head][4 * word + i];
+                }
+                dot = fmaf((float)sum, ks[k][b] * qd[head][b], dot);
+              }
+              part[sub] = dot;
+            }
+            const float dot = (part[0] + part[1]) + (part[2] + part[3]);
+            own[k] = offset < n ? dot * scale : -INFINITY;
+            top = fmaxf(top, own[k]);
+          }
+          const float next = fmaxf(mx[s], top);
+          const float alpha = finite_f(mx[s]) ? expf(mx[s] - next) : 0.f;
+          for (int k = 0; k < 32; ++k) {
+            p[k] = finite_f(own[k]) ? expf(own[k] - next) : 0.f;
+            den[s][k] = fmaf(den[s][k], alpha, p[k]);
+          }
+          mx[s] = next;
+          for (int d = 0; d < D; ++d) {
+            float acc = accum[s][d] * alpha;
+            for (int k = 0; k < 32; ++k)
+              acc = fmaf(p[k] * vs[k][d / 32], (float)vq[k][d], acc);
+            accum[s][d] = acc;
+          }
+        }
+      float total = 0.f, sum[128], top = -INFINITY;
+      for (int s = 0; s < 4; ++s) {
+        const float d = butterfly_sum32(den[s]);
+        mx[s] = d > 0 ? mx[s] + logf(d) : -INFINITY;
+        for (int i = 0; i < D; ++i)
+          accum[s][i] = d > 0 ? accum[s][i] / d : 0.f;
+      }
+      top = fmaxf(fmaxf(mx[0], mx[1]), fmaxf(mx[2], mx[3]));
+      for (int i = 0; i < D; ++i)
+        sum[i] = 0.f;
+      for (int s = 0; s < 4; ++s) {
+        const float w = finite_f(mx[s]) ? expf(mx[s] - top) : 0.f;
+        total += w;
+        for (int i = 0; i < D; ++i)
+          sum[i] = fmaf(w, accum[s][i], sum[i]);
+      }
+      if (!(total > 0.f) || !finite_f(total)) {
+        set_bad(bad);
+        continue;
+      }
+      for (int i = 0; i < D; ++i)
+        partial[((long long)sp * hq + head) * D + i] = sum[i] / total;
+      lse[sp * hq + head] = top + logf(total);
+    }
+  }
+  for (int head = 0; head < hq; ++head) {
+    float v[32], w[32], weights[32], mx = -INFINITY, x[128];
+    for (int l = 0; l < 32; ++l) {
+      v[l] = l < active ? lse[l * hq + head] : -INFINITY;
+      mx = fmaxf(mx, v[l]);
+    }
+    for (int l = 0; l < 32; ++l)
+      w[l] = l < active ? expf(v[l] - mx) : 0.f;
+    const float den = butterfly_sum32(w);
+    for (int l = 0; l < active; ++l)
+      weights[l] = w[l] / den;
+    for (int d = 0; d < D; ++d) {
+      float acc = 0.f;
+      for (int sp = 0; sp < active; ++sp)
+        acc = fmaf(weights[sp], partial[((long long)sp * hq + head) * D + d], acc);
+      x[d] = acc;
+    }
+    po_hadamard(x, 64, .125f);
+    po_hadamard(x + 64, 64, .125f);
+    for (int d = 0; d < D; ++d) {
+      if (!finite_f(x[d]))
+        set_bad(bad);
+      out[head * D + d] = po_f32_to_bf16(x[d]);
+    }
+  }
+  free(partial);
+  free(lse);
+  return active;
+}

@@ -176,6 +176,20 @@ int po_decode_attention(const uint16_t *q, const uint16_t *kc, const uint16_t *v
                         int position, int local, int hq, int hkv, int splits, uint16_t *out,
                         int *bad);
 
+/* Decode attention over a q8_0 cache, one sequence: q8_native::EncodeQuery, Split and
+ * Merge (kv_q8_native.cuh:103-148, 198-363) for hq / hkv query heads per KV head.  The
+ * query is rotated (128-point) and coded per 32-block with an fp32 scale; scores are
+ * integer code dot products scaled per block (fmaf order of the reference: four partial
+ * sums, then ((p0 + p1) + (p2 + p3))); 128-key tiles run as four interleaved 32-key online
+ * softmax streams (per-key denominators, fp32 probabilities in PV against V codes times
+ * their block scale), joined per split; the merge rotates the result back (two 64-point
+ * transforms) and rounds to BF16.  Rows are the 544-byte q8_0 cache rows [cap]; a local
+ * ring has cap 1024.  splits = 0: the reference's 16 (local) or 32.  Returns the splits
+ * used, or -1 (flag raised) for a non-finite query. */
+int po_decode_attention_q8_0(const uint16_t *q, const uint8_t *kc, const uint8_t *vc, int cap,
+                             int position, int local, int hq, int hkv, int splits, uint16_t *out,
+                             int *bad);
+
 #ifdef __cplusplus
 }
 #endif

@@ -53,6 +53,10 @@ struct AttnArgs {
   int seqs, hq, hkv, cap, local, splits, maximum, vocab;
   long long seq_stride; // cache rows between sequences
   int *bad;
+  // q8_0 caches: the coded query (int8 [seqs][hq][128]) and its block scales
+  // (fp32 [seqs][hq][4]), both in the scratch.
+  int8_t *qcodes;
+  float *qscale;
 };
 
 // The sequence's admission and key window (Admitted, attention_gqa8_fragment_validation.cuh:
@@ -276,12 +280,281 @@ template <class T> __global__ __launch_bounds__(64) void k_attn_merge(AttnArgs a
     raise_bad(a.bad);
 }
 
+
+// ---- q8_0 caches ------------------------------------------------------------------------
+//
+// q8_native::EncodeQuery, Split, Merge (kv_q8_native.cuh:103-148, 198-363).  The query is
+// rotated like the K rows (128-point Hadamard, bit 0 first) and coded per 32-block with an
+// fp32 scale; a score is the integer dot product of codes, block by block, scaled by
+// RN(k_scale * q_scale):  four partial sums P_sub over the 4-code groups sub and sub + 4 of
+// each block (fmaf in block order), then ((P0 + P1) + (P2 + P3)), times 1/sqrt(128).  Each
+// 128-key tile runs as four 32-key online-softmax streams (slice s: keys 32 s .. 32 s + 31),
+// each key lane keeping its own denominator; PV multiplies V codes by p * v_scale.  The four
+// streams join per split; the merge rotates the result back (two 64-point transforms).
+// Here one half-wave (32 lanes) serves one query head: lane = key for the scores, lane =
+// four dimensions for PV; the tile of 128 K and V rows is staged in LDS once for the G heads.
+
+constexpr int kQ8Tile = 128, kRowBytes = 544;
+
+template <class T> __global__ __launch_bounds__(64) void k_q8_0_query(AttnArgs a) {
+  const int head = blockIdx.x, seq = blockIdx.y, lane = threadIdx.x;
+  const size_t base = ((size_t)seq * a.hq + head) * kD;
+  float x0 = act_value<T>(a.q, base + lane), x1 = act_value<T>(a.q, base + 64 + lane);
+  if (__ballot(!isfinite(x0) || !isfinite(x1)) != 0) {
+    if (lane == 0)
+      raise_bad(a.bad);
+    return;
+  }
+  // features lane and lane + 64: stages on bits 0..5 across lanes, bit 6 in the lane
+#pragma unroll
+  for (int bit = 1; bit < 64; bit *= 2) {
+    const float o0 = __shfl_xor(x0, bit, 64), o1 = __shfl_xor(x1, bit, 64);
+    x0 = (lane & bit) ? o0 - x0 : x0 + o0;
+    x1 = (lane & bit) ? o1 - x1 : x1 + o1;
+  }
+  const float y0 = (x0 + x1) * .08838834764831845f, y1 = (x0 - x1) * .08838834764831845f;
+  // blocks lane / 32 (feature lane) and 2 + lane / 32 (feature lane + 64)
+  float m0 = fabsf(y0), m1 = fabsf(y1);
+#pragma unroll
+  for (int d = 16; d >= 1; d /= 2) {
+    m0 = fmaxf(m0, __shfl_xor(m0, d, 64));
+    m1 = fmaxf(m1, __shfl_xor(m1, d, 64));
+  }
+  const float d0 = m0 / 127.f, d1 = m1 / 127.f;
+  if (__ballot(!isfinite(d0) || !isfinite(d1)) != 0) {
+    if (lane == 0)
+      raise_bad(a.bad);
+    return;
+  }
+  a.qcodes[base + lane] = (int8_t)q8_0_code(y0, d0 == 0.f ? 0.f : 1.f / d0);
+  a.qcodes[base + 64 + lane] = (int8_t)q8_0_code(y1, d1 == 0.f ? 0.f : 1.f / d1);
+  if ((lane & 31) == 0) {
+    a.qscale[((size_t)seq * a.hq + head) * 4 + lane / 32] = d0;
+    a.qscale[((size_t)seq * a.hq + head) * 4 + 2 + lane / 32] = d1;
+  }
+}
+
+__device__ __forceinline__ float f16_bits(uint32_t h) {
+  return __half2float(__ushort_as_half((unsigned short)h));
+}
+
+template <int G> __global__ __launch_bounds__(32 * G < 64 ? 64 : 32 * G) void k_q8_0_split(AttnArgs a) {
+  constexpr int NT = 32 * G < 64 ? 64 : 32 * G;
+  __shared__ uint32_t kq[kQ8Tile][36]; // K codes, rows padded to 36 words
+  __shared__ uint32_t vq[kQ8Tile][32]; // V codes
+  __shared__ float ksc[kQ8Tile][4], vsc[kQ8Tile][4];
+  const int split = blockIdx.x, kv = blockIdx.y, seq = blockIdx.z, tid = threadIdx.x;
+  const int hg = tid >> 5, lane = tid & 31, head = kv * G + (hg < G ? hg : G - 1);
+  int n, first;
+  if (!attn_window(a, seq, n, first) || (a.local && a.cap != 1024)) {
+    if (split == 0 && kv == 0 && tid == 0)
+      raise_bad(a.bad);
+    return;
+  }
+  const int tiles = (n + kQ8Tile - 1) / kQ8Tile, active = min(a.splits, tiles);
+  if (split >= active)
+    return; // block-uniform
+  const int begin = tiles * split / active, end = tiles * (split + 1) / active;
+  const int features = a.hkv * kD, dbytes = 2 * (features / 32);
+  const uint8_t *krows = static_cast<const uint8_t *>(static_cast<const void *>(a.kc)) +
+                         (size_t)seq * a.seq_stride * kRowBytes;
+  const uint8_t *vrows = static_cast<const uint8_t *>(static_cast<const void *>(a.vc)) +
+                         (size_t)seq * a.seq_stride * kRowBytes;
+  // this head's coded query
+  int qi[32];
+  float qd[4];
+  {
+    const int *src = reinterpret_cast<const int *>(a.qcodes + ((size_t)seq * a.hq + head) * kD);
+#pragma unroll
+    for (int i = 0; i < 32; ++i)
+      qi[i] = src[i];
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+      qd[b] = a.qscale[((size_t)seq * a.hq + head) * 4 + b];
+  }
+  float mx[4], den[4], acc[4][4];
+#pragma unroll
+  for (int sl = 0; sl < 4; ++sl) {
+    mx[sl] = -INFINITY;
+    den[sl] = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      acc[sl][i] = 0.f;
+  }
+  for (int tile = begin; tile < end; ++tile) {
+    // Stage the tile: codes as 16-byte chunks (8 per row and tensor), scales 8 bytes per row.
+    for (int c = tid; c < kQ8Tile * 8; c += NT) {
+      const int key = c >> 3, part = c & 7, o = tile * kQ8Tile + key;
+      uint4 kw = make_uint4(0, 0, 0, 0), vw = make_uint4(0, 0, 0, 0);
+      if (o < n) {
+        const size_t row = (size_t)(a.local ? (first + o) & 1023 : first + o) * kRowBytes;
+        kw = ld_nt(reinterpret_cast<const uint4 *>(krows + row + dbytes + kv * kD) + part);
+        vw = ld_nt(reinterpret_cast<const uint4 *>(vrows + row + dbytes + kv * kD) + part);
+      }
+      *reinterpret_cast<uint4 *>(&kq[key][4 * part]) = kw;
+      *reinterpret_cast<uint4 *>(&vq[key][4 * part]) = vw;
+    }
+    for (int key = tid; key < kQ8Tile; key += NT) {
+      const int o = tile * kQ8Tile + key;
+      uint2 kd = make_uint2(0, 0), vd = make_uint2(0, 0);
+      if (o < n) {
+        const size_t row = (size_t)(a.local ? (first + o) & 1023 : first + o) * kRowBytes;
+        kd = *reinterpret_cast<const uint2 *>(krows + row + 8 * kv);
+        vd = *reinterpret_cast<const uint2 *>(vrows + row + 8 * kv);
+      }
+      ksc[key][0] = f16_bits(kd.x & 0xffffu);
+      ksc[key][1] = f16_bits(kd.x >> 16);
+      ksc[key][2] = f16_bits(kd.y & 0xffffu);
+      ksc[key][3] = f16_bits(kd.y >> 16);
+      vsc[key][0] = f16_bits(vd.x & 0xffffu);
+      vsc[key][1] = f16_bits(vd.x >> 16);
+      vsc[key][2] = f16_bits(vd.y & 0xffffu);
+      vsc[key][3] = f16_bits(vd.y >> 16);
+    }
+    __syncthreads();
+    if (hg < G) {
+#pragma unroll
+      for (int sl = 0; sl < 4; ++sl) {
+        const int key = sl * 32 + lane, o = tile * kQ8Tile + key;
+        int kw[32];
+#pragma unroll
+        for (int m = 0; m < 8; ++m) {
+          const uint4 w = *reinterpret_cast<const uint4 *>(&kq[key][4 * m]);
+          kw[4 * m] = (int)w.x;
+          kw[4 * m + 1] = (int)w.y;
+          kw[4 * m + 2] = (int)w.z;
+          kw[4 * m + 3] = (int)w.w;
+        }
+        float part[4];
+#pragma unroll
+        for (int sub = 0; sub < 4; ++sub) {
+          float dot = 0.f;
+#pragma unroll
+          for (int b = 0; b < 4; ++b) {
+            int sum = __builtin_amdgcn_sdot4(kw[b * 8 + sub], qi[b * 8 + sub], 0, false);
+            sum = __builtin_amdgcn_sdot4(kw[b * 8 + sub + 4], qi[b * 8 + sub + 4], sum, false);
+            dot = __builtin_fmaf((float)sum, ksc[key][b] * qd[b], dot);
+          }
+          part[sub] = dot;
+        }
+        const float dot = (part[0] + part[1]) + (part[2] + part[3]);
+        const float own = o < n ? dot * kScoreScale : -INFINITY;
+        float top = own;
+#pragma unroll
+        for (int d = 16; d >= 1; d /= 2)
+          top = fmaxf(top, __shfl_xor(top, d, 32));
+        const float next = fmaxf(mx[sl], top);
+        const float alpha = isfinite(mx[sl]) ? expf(mx[sl] - next) : 0.f;
+        const float p = isfinite(own) ? expf(own - next) : 0.f;
+        mx[sl] = next;
+        den[sl] = __builtin_fmaf(den[sl], alpha, p);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          acc[sl][i] *= alpha;
+        for (int k = 0; k < 32; ++k) {
+          const float factor = __shfl(p, k, 32) * vsc[sl * 32 + k][lane >> 3];
+          const uint32_t codes = vq[sl * 32 + k][lane];
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            acc[sl][i] = __builtin_fmaf(factor, (float)(int8_t)(codes >> (8 * i)), acc[sl][i]);
+        }
+      }
+    }
+    __syncthreads();
+  }
+  if (hg >= G)
+    return;
+  float top = -INFINITY;
+#pragma unroll
+  for (int sl = 0; sl < 4; ++sl) {
+    float d = den[sl];
+#pragma unroll
+    for (int o = 16; o >= 1; o /= 2)
+      d = d + __shfl_xor(d, o, 32);
+    mx[sl] = d > 0.f ? mx[sl] + logf(d) : -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      acc[sl][i] = d > 0.f ? acc[sl][i] / d : 0.f;
+    top = fmaxf(top, mx[sl]);
+  }
+  top = fmaxf(fmaxf(mx[0], mx[1]), fmaxf(mx[2], mx[3]));
+  float total = 0.f, sum[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int sl = 0; sl < 4; ++sl) {
+    const float w = isfinite(mx[sl]) ? expf(mx[sl] - top) : 0.f;
+    total += w;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      sum[i] = __builtin_fmaf(w, acc[sl][i], sum[i]);
+  }
+  if (!(total > 0.f) || !isfinite(total)) {
+    if (lane == 0)
+      raise_bad(a.bad);
+    return;
+  }
+  float *dst = a.partial + (((size_t)seq * a.splits + split) * a.hq + head) * kD + 4 * lane;
+  *reinterpret_cast<float4 *>(dst) =
+      make_float4(sum[0] / total, sum[1] / total, sum[2] / total, sum[3] / total);
+  if (lane == 0)
+    a.lse[((size_t)seq * a.splits + split) * a.hq + head] = top + logf(total);
+}
+
+template <class T> __global__ __launch_bounds__(64) void k_q8_0_merge(AttnArgs a) {
+  const int head = blockIdx.x, seq = blockIdx.y, lane = threadIdx.x;
+  int n, first;
+  if (!attn_window(a, seq, n, first) || (a.local && a.cap != 1024))
+    return; // the split kernel raised the flag
+  const int active = min(a.splits, (n + kQ8Tile - 1) / kQ8Tile), l32 = lane & 31;
+  const float v = l32 < active ? a.lse[((size_t)seq * a.splits + l32) * a.hq + head] : -INFINITY;
+  float mxv = v;
+#pragma unroll
+  for (int d = 16; d >= 1; d /= 2)
+    mxv = fmaxf(mxv, __shfl_xor(mxv, d, 32));
+  const float p = l32 < active ? expf(v - mxv) : 0.f;
+  float den = p;
+#pragma unroll
+  for (int d = 16; d >= 1; d /= 2)
+    den = den + __shfl_xor(den, d, 32);
+  const float weight = p / den;
+  float x0 = 0.f, x1 = 0.f;
+  for (int sp = 0; sp < active; ++sp) {
+    const float w = __shfl(weight, sp, 64);
+    const float *src = a.partial + (((size_t)seq * a.splits + sp) * a.hq + head) * kD;
+    x0 = __builtin_fmaf(w, src[lane], x0);
+    x1 = __builtin_fmaf(w, src[64 + lane], x1);
+  }
+  // back from the V rotation: two 64-point transforms (features lane and lane + 64)
+#pragma unroll
+  for (int bit = 1; bit < 64; bit *= 2) {
+    const float o0 = __shfl_xor(x0, bit, 64), o1 = __shfl_xor(x1, bit, 64);
+    x0 = (lane & bit) ? o0 - x0 : x0 + o0;
+    x1 = (lane & bit) ? o1 - x1 : x1 + o1;
+  }
+  x0 *= .125f;
+  x1 *= .125f;
+  const uint32_t word = pack2(x0, x1); // lo: feature lane, hi: feature lane + 64
+  if (__ballot(!isfinite(x0) || !isfinite(x1)) != 0 && lane == 0)
+    raise_bad(a.bad);
+  const size_t o = ((size_t)seq * a.hq + head) * kD;
+  if constexpr (std::is_same<T, uint16_t>::value) {
+    static_cast<uint16_t *>(a.out)[o + lane] = (uint16_t)(word & 0xffffu);
+    static_cast<uint16_t *>(a.out)[o + 64 + lane] = (uint16_t)(word >> 16);
+  } else {
+    static_cast<float *>(a.out)[o + lane] = lo16(word);
+    static_cast<float *>(a.out)[o + 64 + lane] = hi16(word);
+  }
+}
+
 } // namespace
 
-extern "C" long long padra_DecodeAttentionScratch(int seqs, int q_heads, int splits) {
-  if (seqs < 1 || q_heads < 1 || splits < 1 || splits > 32)
+extern "C" long long padra_DecodeAttentionScratch(int format, int seqs, int q_heads,
+                                                  int splits) {
+  if (seqs < 1 || q_heads < 1 || splits < 1 || splits > 32 ||
+      (format != PADRA_KV_BF16 && format != PADRA_KV_Q8_0))
     return -1;
-  return (long long)seqs * splits * q_heads * (kD + 1);
+  const long long base = (long long)seqs * splits * q_heads * (kD + 1);
+  // q8_0: the coded query (128 bytes) and its 4 block scales per head
+  return format == PADRA_KV_Q8_0 ? base + (long long)seqs * q_heads * (kD / 4 + 4) : base;
 }
 
 extern "C" int padra_DecodeAttention(void *stream, const void *q, const padra_KVCache *kv,
@@ -290,15 +563,20 @@ extern "C" int padra_DecodeAttention(void *stream, const void *q, const padra_KV
                                      float *scratch, long long scratch_floats, int *bad,
                                      int act) {
   if (!q || !kv || !out || !pos || !bad || !scratch || seqs < 1 || q_heads < 1 ||
-      kv_heads < 1 || q_heads % kv_heads || kv->format != PADRA_KV_BF16 || !kv->k || !kv->v ||
-      kv->cap < 1 || kv->cap > 131072 || pos->mode != PADRA_POS_DECODE || !pos->decode ||
-      pos->maximum < 1 || pos->maximum > 131072 || pos->vocab < 1 ||
-      (seqs > 1 && kv->seq_stride < kv->cap) || (act != PADRA_ACT_BF16 && act != PADRA_ACT_F32) ||
-      !aligned16(kv->k) || !aligned16(kv->v) || !aligned16(scratch) || splits < 0 || splits > 32)
+      kv_heads < 1 || q_heads % kv_heads || !kv->k || !kv->v || kv->cap < 1 ||
+      kv->cap > 131072 || pos->mode != PADRA_POS_DECODE || !pos->decode || pos->maximum < 1 ||
+      pos->maximum > 131072 || pos->vocab < 1 || (seqs > 1 && kv->seq_stride < kv->cap) ||
+      (act != PADRA_ACT_BF16 && act != PADRA_ACT_F32) || !aligned16(kv->k) ||
+      !aligned16(kv->v) || !aligned16(scratch) || splits < 0 || splits > 32)
     return PADRA_INVALID_ARGUMENT;
-  if (splits == 0) // the reference's count (MaxSplits)
-    splits = std::min((kv->cap + kKeys - 1) / kKeys, local ? 16 : 32);
-  const long long need = padra_DecodeAttentionScratch(seqs, q_heads, splits);
+  if (kv->format != PADRA_KV_BF16 && kv->format != PADRA_KV_Q8_0)
+    return PADRA_UNSUPPORTED;
+  const bool q8 = kv->format == PADRA_KV_Q8_0;
+  if (q8 && kv_heads * kD != 512)
+    return PADRA_UNSUPPORTED; // the 544-byte q8_0 row of 4 KV heads
+  if (splits == 0) // the reference's counts
+    splits = q8 ? (local ? 16 : 32) : std::min((kv->cap + kKeys - 1) / kKeys, local ? 16 : 32);
+  const long long need = padra_DecodeAttentionScratch(kv->format, seqs, q_heads, splits);
   if (scratch_floats < need)
     return PADRA_INVALID_ARGUMENT;
   AttnArgs a{};
@@ -308,6 +586,8 @@ extern "C" int padra_DecodeAttention(void *stream, const void *q, const padra_KV
   a.out = out;
   a.partial = scratch;
   a.lse = scratch + (long long)seqs * splits * q_heads * kD;
+  a.qscale = a.lse + (long long)seqs * splits * q_heads;
+  a.qcodes = reinterpret_cast<int8_t *>(a.qscale + (long long)seqs * q_heads * 4);
   a.decode = pos->decode;
   a.seqs = seqs;
   a.hq = q_heads;
@@ -322,8 +602,29 @@ extern "C" int padra_DecodeAttention(void *stream, const void *q, const padra_KV
   const hipStream_t s = static_cast<hipStream_t>(stream);
   const dim3 split_grid(splits, kv_heads, seqs), merge_grid(q_heads, seqs);
   const int group = q_heads / kv_heads;
+  if (group != 1 && group != 2 && group != 4 && group != 8)
+    return PADRA_UNSUPPORTED;
   auto launch = [&](auto tag) -> int {
     using T = decltype(tag);
+    if (q8) {
+      hipLaunchKernelGGL((k_q8_0_query<T>), merge_grid, dim3(64), 0, s, a);
+      switch (group) {
+      case 1:
+        hipLaunchKernelGGL((k_q8_0_split<1>), split_grid, dim3(64), 0, s, a);
+        break;
+      case 2:
+        hipLaunchKernelGGL((k_q8_0_split<2>), split_grid, dim3(64), 0, s, a);
+        break;
+      case 4:
+        hipLaunchKernelGGL((k_q8_0_split<4>), split_grid, dim3(128), 0, s, a);
+        break;
+      default:
+        hipLaunchKernelGGL((k_q8_0_split<8>), split_grid, dim3(256), 0, s, a);
+        break;
+      }
+      hipLaunchKernelGGL((k_q8_0_merge<T>), merge_grid, dim3(64), 0, s, a);
+      return launched("DecodeAttention");
+    }
     switch (group) {
     case 1:
       hipLaunchKernelGGL((k_attn_split<1, T>), split_grid, dim3(64), 0, s, a);
@@ -334,11 +635,9 @@ extern "C" int padra_DecodeAttention(void *stream, const void *q, const padra_KV
     case 4:
       hipLaunchKernelGGL((k_attn_split<4, T>), split_grid, dim3(64), 0, s, a);
       break;
-    case 8:
+    default:
       hipLaunchKernelGGL((k_attn_split<8, T>), split_grid, dim3(64), 0, s, a);
       break;
-    default:
-      return PADRA_UNSUPPORTED;
     }
     hipLaunchKernelGGL((k_attn_merge<T>), merge_grid, dim3(64), 0, s, a);
     return launched("DecodeAttention");

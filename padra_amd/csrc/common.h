@@ -139,6 +139,16 @@ __device__ __forceinline__ void raise_bad(int *bad) {
     atomicExch(bad, 1);
 }
 
+// q8 code (kv_q8.cuh:12-14): RNE of the correctly rounded quotient, clamped to +-127.
+__device__ __forceinline__ uint32_t q8_code(float value, float scale) {
+  const int c = max(-127, min(127, (int)rintf(value / scale)));
+  return (uint32_t)(c & 0xff);
+}
+// q8_0 code (kv_q8_native.cuh:46-48): roundf (half away from zero) of v * inverse.
+__device__ __forceinline__ uint32_t q8_0_code(float value, float inverse) {
+  const int c = max(-127, min(127, (int)roundf(value * inverse)));
+  return (uint32_t)(c & 0xff);
+}
 // A 32-byte control record read as eight words issued together: the checks below then
 // work on registers, instead of one dependent load per field under short-circuit tests.
 template <class S> __device__ __forceinline__ S load_state(const S *p) {

@@ -106,16 +106,6 @@ __device__ __forceinline__ void hadamard_cross(float (&x)[32], int half) {
   }
 }
 
-// q8 code (kv_q8.cuh:12-14): RNE of the correctly rounded quotient, clamped to +-127.
-__device__ __forceinline__ uint32_t q8_code(float value, float scale) {
-  const int c = max(-127, min(127, (int)rintf(value / scale)));
-  return (uint32_t)(c & 0xff);
-}
-// q8_0 code (kv_q8_native.cuh:46-48): roundf (half away from zero) of v * inverse.
-__device__ __forceinline__ uint32_t q8_0_code(float value, float inverse) {
-  const int c = max(-127, min(127, (int)roundf(value * inverse)));
-  return (uint32_t)(c & 0xff);
-}
 __device__ __forceinline__ void store_codes32(int8_t *p, const uint32_t (&w)[8]) {
   st_nt(reinterpret_cast<uint4 *>(p), make_uint4(w[0], w[1], w[2], w[3]));
   st_nt(reinterpret_cast<uint4 *>(p) + 1, make_uint4(w[4], w[5], w[6], w[7]));

@@ -219,13 +219,17 @@ def KVCheckpointCapture(ring: abi.KVCache, chunk: abi.KVCache, saved: abi.KVCach
 
 def DecodeAttention(q, kv: abi.KVCache, out, positions: abi.Positions, bad, kv_heads=4,
                     local=False, splits=0, scratch=None):
-    """Decode attention over a BF16 cache for q [seqs][q_heads][128]
+    """Decode attention over a BF16 or q8_0 cache for q [seqs][q_heads][128]
     (SplitBF16 + per-head Merge, attention_gqa8_fragment_validation.cuh:79-214,
-    attention_perhead_exact.cuh:7-38).  Allocates the fp32 scratch when none is given."""
+    attention_perhead_exact.cuh:7-38; q8_native EncodeQuery/Split/Merge,
+    kv_q8_native.cuh:103-363).  Allocates the fp32 scratch when none is given."""
     _need_cuda(q, out, bad, scratch)
     seqs, q_heads = q.shape[0], q.shape[1]
-    used = splits or min((kv.cap + 31) // 32, 16 if local else 32)
-    need = abi.lib().padra_DecodeAttentionScratch(seqs, q_heads, used)
+    if kv.format == abi.KV_Q8_0:
+        used = splits or (16 if local else 32)
+    else:
+        used = splits or min((kv.cap + 31) // 32, 16 if local else 32)
+    need = abi.lib().padra_DecodeAttentionScratch(kv.format, seqs, q_heads, used)
     if scratch is None:
         scratch = torch.empty(need, dtype=torch.float32, device=q.device)
     abi.call("padra_DecodeAttention", _stream(q), _p(q), ctypes.byref(kv), _p(out),

@@ -506,3 +506,42 @@ def test_decode_attention_f32_and_invalid(oracle):
     for s in range(2):
         want, _, _ = oracle.decode_attention(q[s], kc[s], vc[s], positions[s])
         assert _attn_close(synth.bf16_bits(got[s]), want)[0].all()
+
+
+@pytest.mark.parametrize("hq,local", [(16, False), (32, False), (16, True)])
+def test_decode_attention_q8_0(oracle, hq, local):
+    """q8_0 caches (rotated v2) against the oracle's EncodeQuery/Split/Merge, within the
+    _attn_close tolerance (CUDA expf/logf against any other implementation)."""
+    print(f"[case] decode attention q8_0 hq={hq} local={local}", flush=True)
+    seqs, hkv, capacity = 5, 4, 4096
+    cap = 1024 if local else capacity
+    rng = np.random.default_rng(110 + hq + local)
+    positions = rng.integers(0, capacity, seqs).astype(np.int32)
+    positions[0], positions[1] = 0, 200
+    q = synth.bf16_bits((rng.standard_normal((seqs, hq, 128)) * 2).astype(np.float32))
+    rk = np.zeros((seqs, cap, 544), np.uint8)
+    rv = np.zeros((seqs, cap, 544), np.uint8)
+    for s in range(seqs):
+        d = synth.chain_inputs(cap, outliers=True, seed=200 + s)
+        oracle.kv_q8_0_encode(d["k"], d["v"], rk[s], rv[s], np.arange(cap, dtype=np.int32), cap)
+    states = np.zeros((seqs, 8), np.int32)
+    for s, p in enumerate(positions):
+        states[s] = [5, p, capacity, 10, p, min(p, 1024), 0, 0]
+    out = torch.empty((seqs, hq, 128), dtype=torch.int16, device="cuda")
+    bad = flag()
+    kv = ops.kv_cache(abi.KV_Q8_0, dev(rk.reshape(seqs * cap, 544)), dev(rv.reshape(seqs * cap, 544)),
+                      cap, seq_stride=cap)
+    ops.DecodeAttention(dev(q), kv, out, ops.positions_decode(torch.from_numpy(states).cuda(),
+                                                              maximum=capacity),
+                        bad, kv_heads=hkv, local=local)
+    torch.cuda.synchronize()
+    assert bad.item() == 0
+    got = host16(out)
+    worst = 0
+    for s in range(seqs):
+        want, _, wbad = oracle.decode_attention_q8_0(q[s], rk[s], rv[s], positions[s], local=local)
+        assert not wbad
+        close, d = _attn_close(got[s], want)
+        worst = max(worst, int(d.max()))
+        assert close.all(), (s, int(d.max()))
+    print(f"  max BF16 ulp difference {worst}", flush=True)

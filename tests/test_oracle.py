@@ -684,3 +684,39 @@ def test_decode_attention_float64(oracle, position, local, cap):
         other, used2, _ = oracle.decode_attention(q, kc, vc, position, splits=7)
         assert used2 == 7 and used == 32
         assert np.all(np.abs(synth.bf16_to_f32(other) - got) <= 2.0**-7 * vmax)
+
+
+@pytest.mark.parametrize("position,local", [(5, False), (700, False), (3000, True)])
+def test_decode_attention_q8_0_float64(oracle, position, local):
+    """Against float64 attention of the original query over the cache's decoded rows (codes
+    times scale, rotated back): the query's own int8 coding (relative 1/254 per block)
+    bounds the difference."""
+    hq, hkv = 16, 4
+    cap = 1024 if local else 4096
+    rng = np.random.default_rng(position)
+    q = synth.bf16_bits(rng.standard_normal((hq, 128)).astype(F32))
+    k = synth.bf16_bits(rng.standard_normal((cap, hkv, 128)).astype(F32))
+    v = synth.bf16_bits(rng.standard_normal((cap, hkv, 128)).astype(F32))
+    rk = np.zeros((cap, 544), np.uint8)
+    rv = np.zeros((cap, 544), np.uint8)
+    oracle.kv_q8_0_encode(k, v, rk, rv, np.arange(cap, dtype=np.int32), cap)
+    out, used, bad = oracle.decode_attention_q8_0(q, rk, rv, position, local=local)
+    assert not bad and used == min(16 if local else 32, (min(position + 1, 1024 if local else 10**9) + 127) // 128)
+    # decoded rows in the original basis
+    dk, dv, _ = oracle.kv_q8_0_dequantize(rk, rv, cap, 512)
+    kf = synth.bf16_to_f32(dk).reshape(cap, hkv, 128).astype(np.float64)
+    vf = synth.bf16_to_f32(dv).reshape(cap, hkv, 128).astype(np.float64)
+    h128 = __import__("scipy").linalg.hadamard(128) / np.sqrt(128)
+    h64 = __import__("scipy").linalg.hadamard(64) / 8.0
+    kf = kf @ h128.T  # inverse rotation (symmetric, orthonormal)
+    vf = np.concatenate([vf[..., :64] @ h64.T, vf[..., 64:] @ h64.T], axis=-1)
+    n = min(position + 1, 1024) if local else position + 1
+    rows = np.arange(position + 1 - n, position + 1) % cap
+    g = hq // hkv
+    qf = synth.bf16_to_f32(q).astype(np.float64)
+    got = synth.bf16_to_f32(out).astype(np.float64)
+    for h in range(hq):
+        s = kf[rows, h // g] @ qf[h] / np.sqrt(128)
+        w = np.exp(s - s.max())
+        ref = (w / w.sum()) @ vf[rows, h // g]
+        assert np.max(np.abs(got[h] - ref)) <= 0.02 * np.abs(vf).max(), h
