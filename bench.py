@@ -322,7 +322,7 @@ def bench_combine_norm(torch, steps, sets=8):
             "frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
 
 
-def bench_attention(torch, steps, seqs=64, capacity=CAPACITY, fill_seed=0):
+def bench_attention(torch, steps, seqs=64, capacity=CAPACITY, fill_seed=0, fmt="bf16"):
     """Decode attention over BF16 caches (the consumer of the stored rows), one step of
     `seqs` sequences at ragged positions U[0, capacity) with per-sequence caches of
     `capacity` rows: the split-K pass and the per-head merge.  Bytes: every key and value
@@ -335,26 +335,41 @@ def bench_attention(torch, steps, seqs=64, capacity=CAPACITY, fill_seed=0):
         states[i] = [1, p, capacity, 1 << 20, p, min(int(p), 1024), 0, 0]
     st = torch.from_numpy(states).cuda()
     gen = torch.Generator(device="cuda").manual_seed(fill_seed)
-    kc = (torch.randn((seqs * capacity, HKV * D), generator=gen, device="cuda")).to(
-        torch.bfloat16).view(torch.int16)
-    vc = (torch.randn((seqs * capacity, HKV * D), generator=gen, device="cuda")).to(
-        torch.bfloat16).view(torch.int16)
+    if fmt == "q8_0":
+        # valid rows: random codes, block scales 1/64 (fp16 0x2400)
+        def rows():
+            r = torch.randint(-127, 128, (seqs * capacity, 544), generator=gen, device="cuda",
+                              dtype=torch.int8)
+            r[:, :32].view(torch.int16).fill_(0x2400)
+            return r
+        kc, vc = rows(), rows()
+        row_bytes = 544
+    else:
+        kc = (torch.randn((seqs * capacity, HKV * D), generator=gen, device="cuda")).to(
+            torch.bfloat16).view(torch.int16)
+        vc = (torch.randn((seqs * capacity, HKV * D), generator=gen, device="cuda")).to(
+            torch.bfloat16).view(torch.int16)
+        row_bytes = HKV * D * 2
     q = (torch.randn((seqs, HQ, D), generator=gen, device="cuda") * 0.1).to(
         torch.bfloat16).view(torch.int16)
     out = torch.empty_like(q)
     bad = torch.zeros(1, dtype=torch.int32, device="cuda")
-    kv = ops.kv_cache(abi.KV_BF16, kc, vc, capacity, seq_stride=capacity)
+    kv = ops.kv_cache(abi.KV_Q8_0 if fmt == "q8_0" else abi.KV_BF16, kc, vc, capacity,
+                      seq_stride=capacity)
     pos = ops.positions_decode(st, maximum=capacity)
     scratch = ops.DecodeAttention(q, kv, out, pos, bad)  # allocates the scratch once
     ms = graph_time(torch, lambda i: ops.DecodeAttention(q, kv, out, pos, bad, scratch=scratch),
                     steps)
     if bad.item():
         raise SystemExit("device error flag set in the decode attention benchmark")
-    nbytes = int((positions.astype(np.int64) + 1).sum()) * HKV * D * 2 * 2 + 2 * q.numel() * 2
+    # every K and V row of the window (a q8_0 row holds all 4 KV heads: each KV head's
+    # split reads its 128 codes and 8 scale bytes of it), plus q and the output
+    per_row = HKV * D * 2 if fmt != "q8_0" else HKV * (D + 8)
+    nbytes = int((positions.astype(np.int64) + 1).sum()) * per_row * 2 + 2 * q.numel() * 2
     del kc, vc
     torch.cuda.empty_cache()
     return {"workload": f"decode attention, {seqs} sequences at ragged positions < {capacity}, "
-                        "BF16 caches (split-K + merge)",
+                        f"{fmt} caches (split-K + merge)",
             "us_per_step": round(ms * 1e3, 3), "bytes_per_step": nbytes,
             "gbs": round(nbytes / (ms * 1e-3) / 1e9, 2),
             "frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
@@ -501,7 +516,8 @@ def main():
                            "config0_gpu": bench_decode(torch, 200, 1, capacity=8192),
                            "norm_fp8": bench_norm_fp8(torch, 200),
                            "combine_norm": bench_combine_norm(torch, 100),
-                           "attention": bench_attention(torch, 10)}
+                           "attention": bench_attention(torch, 10),
+                           "attention_q8_0": bench_attention(torch, 10, fmt="q8_0")}
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(host, args.cpu_seconds, cpu_threads())
         if not args.no_configs:

@@ -342,7 +342,9 @@ template <int G> __global__ __launch_bounds__(32 * G < 64 ? 64 : 32 * G) void k_
   constexpr int NT = 32 * G < 64 ? 64 : 32 * G;
   __shared__ uint32_t kq[kQ8Tile][36]; // K codes, rows padded to 36 words
   __shared__ uint32_t vq[kQ8Tile][32]; // V codes
-  __shared__ float ksc[kQ8Tile][4], vsc[kQ8Tile][4];
+  __shared__ float ksc[kQ8Tile][4];
+  __shared__ float vsc[4][kQ8Tile];      // V block scales, by block then key
+  __shared__ float pr[G][32];            // this slice's probabilities, per head
   const int split = blockIdx.x, kv = blockIdx.y, seq = blockIdx.z, tid = threadIdx.x;
   const int hg = tid >> 5, lane = tid & 31, head = kv * G + (hg < G ? hg : G - 1);
   int n, first;
@@ -406,10 +408,10 @@ template <int G> __global__ __launch_bounds__(32 * G < 64 ? 64 : 32 * G) void k_
       ksc[key][1] = f16_bits(kd.x >> 16);
       ksc[key][2] = f16_bits(kd.y & 0xffffu);
       ksc[key][3] = f16_bits(kd.y >> 16);
-      vsc[key][0] = f16_bits(vd.x & 0xffffu);
-      vsc[key][1] = f16_bits(vd.x >> 16);
-      vsc[key][2] = f16_bits(vd.y & 0xffffu);
-      vsc[key][3] = f16_bits(vd.y >> 16);
+      vsc[0][key] = f16_bits(vd.x & 0xffffu);
+      vsc[1][key] = f16_bits(vd.x >> 16);
+      vsc[2][key] = f16_bits(vd.y & 0xffffu);
+      vsc[3][key] = f16_bits(vd.y >> 16);
     }
     __syncthreads();
     if (hg < G) {
@@ -451,13 +453,26 @@ template <int G> __global__ __launch_bounds__(32 * G < 64 ? 64 : 32 * G) void k_
 #pragma unroll
         for (int i = 0; i < 4; ++i)
           acc[sl][i] *= alpha;
-        for (int k = 0; k < 32; ++k) {
-          const float factor = __shfl(p, k, 32) * vsc[sl * 32 + k][lane >> 3];
-          const uint32_t codes = vq[sl * 32 + k][lane];
+        // The half-wave's probabilities go through LDS (its own row of pr; a half-wave
+        // executes in lockstep with its writes, so no barrier is needed for it).
+        pr[hg][lane] = p;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll 2
+        for (int k4 = 0; k4 < 32; k4 += 4) {
+          const float4 p4 = *reinterpret_cast<const float4 *>(&pr[hg][k4]);
+          const float4 s4 = *reinterpret_cast<const float4 *>(&vsc[lane >> 3][sl * 32 + k4]);
+          const float pk[4] = {p4.x, p4.y, p4.z, p4.w}, sk[4] = {s4.x, s4.y, s4.z, s4.w};
 #pragma unroll
-          for (int i = 0; i < 4; ++i)
-            acc[sl][i] = __builtin_fmaf(factor, (float)(int8_t)(codes >> (8 * i)), acc[sl][i]);
+          for (int j = 0; j < 4; ++j) {
+            const float factor = pk[j] * sk[j];
+            const uint32_t codes = vq[sl * 32 + k4 + j][lane];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              acc[sl][i] = __builtin_fmaf(factor, (float)(int8_t)(codes >> (8 * i)), acc[sl][i]);
+          }
         }
+        __builtin_amdgcn_wave_barrier(); // pr is rewritten by the next slice
       }
     }
     __syncthreads();
