@@ -340,10 +340,12 @@ __device__ __forceinline__ float f16_bits(uint32_t h) {
 
 template <int G> __global__ __launch_bounds__(32 * G < 64 ? 64 : 32 * G) void k_q8_0_split(AttnArgs a) {
   constexpr int NT = 32 * G < 64 ? 64 : 32 * G;
-  __shared__ uint32_t kq[kQ8Tile][36]; // K codes, rows padded to 36 words
-  __shared__ uint32_t vq[kQ8Tile][32]; // V codes
-  __shared__ float ksc[kQ8Tile][4];
-  __shared__ float vsc[4][kQ8Tile];      // V block scales, by block then key
+  // Half a tile (two 32-key slices) is staged at a time: 20 KB of LDS per workgroup.
+  constexpr int HK = kQ8Tile / 2;
+  __shared__ uint32_t kq[HK][36]; // K codes, rows padded to 36 words
+  __shared__ uint32_t vq[HK][32]; // V codes
+  __shared__ float ksc[HK][4];
+  __shared__ float vsc[4][HK];    // V block scales, by block then key
   __shared__ float pr[G][32];            // this slice's probabilities, per head
   const int split = blockIdx.x, kv = blockIdx.y, seq = blockIdx.z, tid = threadIdx.x;
   const int hg = tid >> 5, lane = tid & 31, head = kv * G + (hg < G ? hg : G - 1);
@@ -383,10 +385,12 @@ template <int G> __global__ __launch_bounds__(32 * G < 64 ? 64 : 32 * G) void k_
     for (int i = 0; i < 4; ++i)
       acc[sl][i] = 0.f;
   }
-  for (int tile = begin; tile < end; ++tile) {
-    // Stage the tile: codes as 16-byte chunks (8 per row and tensor), scales 8 bytes per row.
-    for (int c = tid; c < kQ8Tile * 8; c += NT) {
-      const int key = c >> 3, part = c & 7, o = tile * kQ8Tile + key;
+  for (int step = begin * 2; step < end * 2; ++step) {
+    const int tile = step >> 1, h0 = (step & 1) * HK;
+    // Stage keys h0 .. h0 + 63 of the tile: codes as 16-byte chunks (8 per row and tensor),
+    // scales 8 bytes per row.
+    for (int c = tid; c < HK * 8; c += NT) {
+      const int key = c >> 3, part = c & 7, o = tile * kQ8Tile + h0 + key;
       uint4 kw = make_uint4(0, 0, 0, 0), vw = make_uint4(0, 0, 0, 0);
       if (o < n) {
         const size_t row = (size_t)(a.local ? (first + o) & 1023 : first + o) * kRowBytes;
@@ -396,8 +400,8 @@ template <int G> __global__ __launch_bounds__(32 * G < 64 ? 64 : 32 * G) void k_
       *reinterpret_cast<uint4 *>(&kq[key][4 * part]) = kw;
       *reinterpret_cast<uint4 *>(&vq[key][4 * part]) = vw;
     }
-    for (int key = tid; key < kQ8Tile; key += NT) {
-      const int o = tile * kQ8Tile + key;
+    for (int key = tid; key < HK; key += NT) {
+      const int o = tile * kQ8Tile + h0 + key;
       uint2 kd = make_uint2(0, 0), vd = make_uint2(0, 0);
       if (o < n) {
         const size_t row = (size_t)(a.local ? (first + o) & 1023 : first + o) * kRowBytes;
@@ -416,8 +420,9 @@ template <int G> __global__ __launch_bounds__(32 * G < 64 ? 64 : 32 * G) void k_
     __syncthreads();
     if (hg < G) {
 #pragma unroll
-      for (int sl = 0; sl < 4; ++sl) {
-        const int key = sl * 32 + lane, o = tile * kQ8Tile + key;
+      for (int hs = 0; hs < 2; ++hs) {
+        const int sl = (step & 1) * 2 + hs; // the online-softmax stream of this slice
+        const int key = hs * 32 + lane, o = tile * kQ8Tile + h0 + key;
         int kw[32];
 #pragma unroll
         for (int m = 0; m < 8; ++m) {
@@ -461,12 +466,12 @@ template <int G> __global__ __launch_bounds__(32 * G < 64 ? 64 : 32 * G) void k_
 #pragma unroll 2
         for (int k4 = 0; k4 < 32; k4 += 4) {
           const float4 p4 = *reinterpret_cast<const float4 *>(&pr[hg][k4]);
-          const float4 s4 = *reinterpret_cast<const float4 *>(&vsc[lane >> 3][sl * 32 + k4]);
+          const float4 s4 = *reinterpret_cast<const float4 *>(&vsc[lane >> 3][hs * 32 + k4]);
           const float pk[4] = {p4.x, p4.y, p4.z, p4.w}, sk[4] = {s4.x, s4.y, s4.z, s4.w};
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
             const float factor = pk[j] * sk[j];
-            const uint32_t codes = vq[sl * 32 + k4 + j][lane];
+            const uint32_t codes = vq[hs * 32 + k4 + j][lane];
 #pragma unroll
             for (int i = 0; i < 4; ++i)
               acc[sl][i] = __builtin_fmaf(factor, (float)(int8_t)(codes >> (8 * i)), acc[sl][i]);
