@@ -38,6 +38,8 @@ Per oracle function, what checks it:
   po_decode_attention             float64 softmax attention over the same keys (global and
                                   local ring) within the BF16-probability error bound; the
                                   split count changes results only within that bound
+  po_decode_attention_q8_0        float64 attention of the original query over the cache's
+                                  decoded rows rotated back, within the query-coding bound
 """
 import numpy as np
 import pytest
