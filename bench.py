@@ -344,18 +344,27 @@ def bench_attention(torch, steps, seqs=64, capacity=CAPACITY, fill_seed=0, fmt="
             return r
         kc, vc = rows(), rows()
         row_bytes = 544
+        scales = None
+    elif fmt == "q8":
+        kc = torch.randint(-127, 128, (seqs * capacity, HKV * D), generator=gen, device="cuda",
+                           dtype=torch.int8)
+        vc = torch.randint(-127, 128, (seqs * capacity, HKV * D), generator=gen, device="cuda",
+                           dtype=torch.int8)
+        scales = torch.full((seqs * capacity, HKV, 2), 1.0 / 64, device="cuda")
+        row_bytes = HKV * D
     else:
         kc = (torch.randn((seqs * capacity, HKV * D), generator=gen, device="cuda")).to(
             torch.bfloat16).view(torch.int16)
         vc = (torch.randn((seqs * capacity, HKV * D), generator=gen, device="cuda")).to(
             torch.bfloat16).view(torch.int16)
         row_bytes = HKV * D * 2
+        scales = None
     q = (torch.randn((seqs, HQ, D), generator=gen, device="cuda") * 0.1).to(
         torch.bfloat16).view(torch.int16)
     out = torch.empty_like(q)
     bad = torch.zeros(1, dtype=torch.int32, device="cuda")
-    kv = ops.kv_cache(abi.KV_Q8_0 if fmt == "q8_0" else abi.KV_BF16, kc, vc, capacity,
-                      seq_stride=capacity)
+    code = {"bf16": abi.KV_BF16, "q8": abi.KV_Q8, "q8_0": abi.KV_Q8_0}[fmt]
+    kv = ops.kv_cache(code, kc, vc, capacity, scales=scales, seq_stride=capacity)
     pos = ops.positions_decode(st, maximum=capacity)
     scratch = ops.DecodeAttention(q, kv, out, pos, bad)  # allocates the scratch once
     ms = graph_time(torch, lambda i: ops.DecodeAttention(q, kv, out, pos, bad, scratch=scratch),
@@ -364,9 +373,9 @@ def bench_attention(torch, steps, seqs=64, capacity=CAPACITY, fill_seed=0, fmt="
         raise SystemExit("device error flag set in the decode attention benchmark")
     # every K and V row of the window (a q8_0 row holds all 4 KV heads: each KV head's
     # split reads its 128 codes and 8 scale bytes of it), plus q and the output
-    per_row = HKV * D * 2 if fmt != "q8_0" else HKV * (D + 8)
+    per_row = {"bf16": HKV * D * 2, "q8": HKV * (D + 4), "q8_0": HKV * (D + 8)}[fmt]
     nbytes = int((positions.astype(np.int64) + 1).sum()) * per_row * 2 + 2 * q.numel() * 2
-    del kc, vc
+    del kc, vc, scales
     torch.cuda.empty_cache()
     return {"workload": f"decode attention, {seqs} sequences at ragged positions < {capacity}, "
                         f"{fmt} caches (split-K + merge)",
@@ -517,7 +526,8 @@ def main():
                            "norm_fp8": bench_norm_fp8(torch, 200),
                            "combine_norm": bench_combine_norm(torch, 100),
                            "attention": bench_attention(torch, 10),
-                           "attention_q8_0": bench_attention(torch, 10, fmt="q8_0")}
+                           "attention_q8_0": bench_attention(torch, 10, fmt="q8_0"),
+                           "attention_q8": bench_attention(torch, 10, fmt="q8")}
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(host, args.cpu_seconds, cpu_threads())
         if not args.no_configs:

@@ -57,6 +57,7 @@ struct AttnArgs {
   // (fp32 [seqs][hq][4]), both in the scratch.
   int8_t *qcodes;
   float *qscale;
+  const float *kvscales; // q8 caches: (k, v) scale pair per row and KV head
 };
 
 // The sequence's admission and key window (Admitted, attention_gqa8_fragment_validation.cuh:
@@ -96,7 +97,29 @@ template <class T> __device__ __forceinline__ float act_value(const void *p, siz
     return static_cast<const float *>(p)[i];
 }
 
-template <int G, class T>
+// q8 cache rows decoded into the BF16 tile: bf16(code * scale) (kv_q8::Decode,
+// kv_q8.cuh:15-27); a -128 code, an invalid scale or a non-finite result raises the flag.
+__device__ __forceinline__ void q8_decode16(uint4 codes, float scale, uint4 &lo, uint4 &hi,
+                                            bool &fine) {
+  const uint32_t w[4] = {codes.x, codes.y, codes.z, codes.w};
+  uint32_t out[8];
+  bool ok = isfinite(scale) && scale > 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t x = w[i] ^ 0x80808080u; // a byte 0x80 (code -128) becomes zero
+    ok = ok && (((x - 0x01010101u) & ~x & 0x80808080u) == 0);
+    out[2 * i] = pack2((float)(int8_t)(w[i] & 0xffu) * scale, (float)(int8_t)((w[i] >> 8) & 0xffu) * scale);
+    out[2 * i + 1] = pack2((float)(int8_t)((w[i] >> 16) & 0xffu) * scale, (float)(int8_t)(w[i] >> 24) * scale);
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    ok = ok && ((out[i] & 0x7f80u) != 0x7f80u) && ((out[i] & 0x7f800000u) != 0x7f800000u);
+  lo = make_uint4(out[0], out[1], out[2], out[3]);
+  hi = make_uint4(out[4], out[5], out[6], out[7]);
+  fine = fine && ok;
+}
+
+template <int G, class T, bool Q8>
 __global__ __launch_bounds__(64) void k_attn_split(AttnArgs a) {
   __shared__ uint32_t qs[G][kD / 2];         // query rows, BF16 pairs
   // K and V tiles, BF16 pairs; K rows padded to 68 words so that the 32 key lanes' 16-byte
@@ -117,8 +140,13 @@ __global__ __launch_bounds__(64) void k_attn_split(AttnArgs a) {
     return; // block-uniform
   const int begin = tiles * split / active, end = tiles * (split + 1) / active;
   const int features = a.hkv * kD;
-  const uint16_t *kc = a.kc + (size_t)seq * a.seq_stride * features + kv * kD;
-  const uint16_t *vc = a.vc + (size_t)seq * a.seq_stride * features + kv * kD;
+  // element offset of this sequence's rows and this KV head (BF16 values or q8 codes)
+  const size_t head_off = (size_t)seq * a.seq_stride * features + kv * kD;
+  const uint16_t *kc = a.kc + head_off, *vc = a.vc + head_off;
+  const int8_t *k8 = reinterpret_cast<const int8_t *>(a.kc) + head_off;
+  const int8_t *v8 = reinterpret_cast<const int8_t *>(a.vc) + head_off;
+  const float2 *sc = reinterpret_cast<const float2 *>(a.kvscales) +
+                     (size_t)seq * a.seq_stride * a.hkv + kv;
 
   // Query rows: finite and BF16-exact, as the reference requires of its fp32 input.
   bool qfine = true;
@@ -145,25 +173,50 @@ __global__ __launch_bounds__(64) void k_attn_split(AttnArgs a) {
   // Tile loads: 16-byte chunk c = lane + 64 m of the tile's 32 key rows (key c / 16,
   // dimensions 8 (c % 16) ..), contiguous 1 KB per instruction.  Rows past the window load
   // a valid row and are zeroed (the reference zero-fills them).
+  // q8: chunk c = lane + 64 m (m < 4) holds 16 codes (key c / 8, dimensions 16 (c % 8) ..),
+  // with that key's scale pair.
+  constexpr int CH = Q8 ? 4 : 8;
+  float2 kvs[CH];
   auto load_tile = [&](int tile, uint4 (&kw)[8], uint4 (&vw)[8]) {
 #pragma unroll
-    for (int m = 0; m < 8; ++m) {
-      const int c = lane + 64 * m, o = tile * kKeys + (c >> 4);
-      const size_t r = (size_t)((first + (o < n ? o : 0)) % a.cap) * features;
-      kw[m] = ld_nt(reinterpret_cast<const uint4 *>(kc + r) + (c & 15));
-      vw[m] = ld_nt(reinterpret_cast<const uint4 *>(vc + r) + (c & 15));
+    for (int m = 0; m < CH; ++m) {
+      const int c = lane + 64 * m, o = tile * kKeys + (c >> (Q8 ? 3 : 4));
+      const size_t row = (size_t)((first + (o < n ? o : 0)) % a.cap);
+      if constexpr (Q8) {
+        kw[m] = ld_nt(reinterpret_cast<const uint4 *>(k8 + row * features) + (c & 7));
+        vw[m] = ld_nt(reinterpret_cast<const uint4 *>(v8 + row * features) + (c & 7));
+        kvs[m] = sc[row * a.hkv];
+      } else {
+        kw[m] = ld_nt(reinterpret_cast<const uint4 *>(kc + row * features) + (c & 15));
+        vw[m] = ld_nt(reinterpret_cast<const uint4 *>(vc + row * features) + (c & 15));
+      }
     }
   };
   uint4 kw[8], vw[8];
   load_tile(begin, kw, vw);
   for (int tile = begin; tile < end; ++tile) {
 #pragma unroll
-    for (int m = 0; m < 8; ++m) {
+    for (int m = 0; m < CH; ++m) {
       const int c = lane + 64 * m;
-      if (tile * kKeys + (c >> 4) >= n)
-        kw[m] = vw[m] = make_uint4(0, 0, 0, 0);
-      *reinterpret_cast<uint4 *>(&ks[c >> 4][(c & 15) * 4]) = kw[m];
-      *reinterpret_cast<uint4 *>(&vs[c >> 4][(c & 15) * 4]) = vw[m];
+      if constexpr (Q8) {
+        const int key8 = c >> 3, part = c & 7;
+        uint4 klo, khi, vlo, vhi;
+        if (tile * kKeys + key8 >= n) { // the reference stages zeros with unit scales
+          klo = khi = vlo = vhi = make_uint4(0, 0, 0, 0);
+        } else {
+          q8_decode16(kw[m], kvs[m].x, klo, khi, fine);
+          q8_decode16(vw[m], kvs[m].y, vlo, vhi, fine);
+        }
+        *reinterpret_cast<uint4 *>(&ks[key8][part * 8]) = klo;
+        *reinterpret_cast<uint4 *>(&ks[key8][part * 8 + 4]) = khi;
+        *reinterpret_cast<uint4 *>(&vs[key8][part * 8]) = vlo;
+        *reinterpret_cast<uint4 *>(&vs[key8][part * 8 + 4]) = vhi;
+      } else {
+        if (tile * kKeys + (c >> 4) >= n)
+          kw[m] = vw[m] = make_uint4(0, 0, 0, 0);
+        *reinterpret_cast<uint4 *>(&ks[c >> 4][(c & 15) * 4]) = kw[m];
+        *reinterpret_cast<uint4 *>(&vs[c >> 4][(c & 15) * 4]) = vw[m];
+      }
     }
     __syncthreads();
     // The next tile's loads are in flight during this tile's arithmetic (the last tile
@@ -570,7 +623,7 @@ template <class T> __global__ __launch_bounds__(64) void k_q8_0_merge(AttnArgs a
 extern "C" long long padra_DecodeAttentionScratch(int format, int seqs, int q_heads,
                                                   int splits) {
   if (seqs < 1 || q_heads < 1 || splits < 1 || splits > 32 ||
-      (format != PADRA_KV_BF16 && format != PADRA_KV_Q8_0))
+      (format != PADRA_KV_BF16 && format != PADRA_KV_Q8 && format != PADRA_KV_Q8_0))
     return -1;
   const long long base = (long long)seqs * splits * q_heads * (kD + 1);
   // q8_0: the coded query (128 bytes) and its 4 block scales per head
@@ -589,9 +642,11 @@ extern "C" int padra_DecodeAttention(void *stream, const void *q, const padra_KV
       (act != PADRA_ACT_BF16 && act != PADRA_ACT_F32) || !aligned16(kv->k) ||
       !aligned16(kv->v) || !aligned16(scratch) || splits < 0 || splits > 32)
     return PADRA_INVALID_ARGUMENT;
-  if (kv->format != PADRA_KV_BF16 && kv->format != PADRA_KV_Q8_0)
+  if (kv->format != PADRA_KV_BF16 && kv->format != PADRA_KV_Q8 && kv->format != PADRA_KV_Q8_0)
     return PADRA_UNSUPPORTED;
-  const bool q8 = kv->format == PADRA_KV_Q8_0;
+  if (kv->format == PADRA_KV_Q8 && !kv->scales)
+    return PADRA_INVALID_ARGUMENT;
+  const bool q8 = kv->format == PADRA_KV_Q8_0, q8s = kv->format == PADRA_KV_Q8;
   if (q8 && kv_heads * kD != 512)
     return PADRA_UNSUPPORTED; // the 544-byte q8_0 row of 4 KV heads
   if (splits == 0) // the reference's counts
@@ -619,6 +674,7 @@ extern "C" int padra_DecodeAttention(void *stream, const void *q, const padra_KV
   a.vocab = pos->vocab;
   a.seq_stride = seqs > 1 ? kv->seq_stride : 0;
   a.bad = bad;
+  a.kvscales = static_cast<const float *>(kv->scales);
   const hipStream_t s = static_cast<hipStream_t>(stream);
   const dim3 split_grid(splits, kv_heads, seqs), merge_grid(q_heads, seqs);
   const int group = q_heads / kv_heads;
@@ -645,20 +701,27 @@ extern "C" int padra_DecodeAttention(void *stream, const void *q, const padra_KV
       hipLaunchKernelGGL((k_q8_0_merge<T>), merge_grid, dim3(64), 0, s, a);
       return launched("DecodeAttention");
     }
-    switch (group) {
-    case 1:
-      hipLaunchKernelGGL((k_attn_split<1, T>), split_grid, dim3(64), 0, s, a);
-      break;
-    case 2:
-      hipLaunchKernelGGL((k_attn_split<2, T>), split_grid, dim3(64), 0, s, a);
-      break;
-    case 4:
-      hipLaunchKernelGGL((k_attn_split<4, T>), split_grid, dim3(64), 0, s, a);
-      break;
-    default:
-      hipLaunchKernelGGL((k_attn_split<8, T>), split_grid, dim3(64), 0, s, a);
-      break;
-    }
+    auto split = [&](auto q8tag) {
+      constexpr bool Q8 = decltype(q8tag)::value;
+      switch (group) {
+      case 1:
+        hipLaunchKernelGGL((k_attn_split<1, T, Q8>), split_grid, dim3(64), 0, s, a);
+        break;
+      case 2:
+        hipLaunchKernelGGL((k_attn_split<2, T, Q8>), split_grid, dim3(64), 0, s, a);
+        break;
+      case 4:
+        hipLaunchKernelGGL((k_attn_split<4, T, Q8>), split_grid, dim3(64), 0, s, a);
+        break;
+      default:
+        hipLaunchKernelGGL((k_attn_split<8, T, Q8>), split_grid, dim3(64), 0, s, a);
+        break;
+      }
+    };
+    if (q8s)
+      split(std::true_type{});
+    else
+      split(std::false_type{});
     hipLaunchKernelGGL((k_attn_merge<T>), merge_grid, dim3(64), 0, s, a);
     return launched("DecodeAttention");
   };

@@ -131,13 +131,19 @@ def test_host_validation_newer_entry_points():
     assert need == 2 * 32 * 16 * 129
     assert lib.padra_DecodeAttentionScratch(abi.KV_Q8_0, 2, 16, 32) == need + 2 * 16 * 36
     assert lib.padra_DecodeAttentionScratch(abi.KV_BF16, 2, 16, 33) == -1
-    assert lib.padra_DecodeAttentionScratch(abi.KV_Q8, 2, 16, 32) == -1
+    assert lib.padra_DecodeAttentionScratch(abi.KV_Q8, 2, 16, 32) == need
+    assert lib.padra_DecodeAttentionScratch(abi.KV_Q8_0_NOROT, 2, 16, 32) == -1
     assert lib.padra_DecodeAttention(None, _p(16), ctypes.byref(kv), _p(32), ctypes.byref(dec), 2,
                                      16, 4, 0, 0, _p(64), need - 1, bad, 0) == abi.INVALID_ARGUMENT
     assert lib.padra_DecodeAttention(None, _p(16), ctypes.byref(kv), _p(32), ctypes.byref(dec), 2,
                                      24, 4, 0, 0, _p(64), need * 2, bad, 0) == abi.UNSUPPORTED
-    q8 = abi.KVCache(format=abi.KV_Q8, k=16, v=32, scales=48, cap=4096, first=0, seq_stride=4096)
+    q8 = abi.KVCache(format=abi.KV_Q8, k=16, v=32, scales=None, cap=4096, first=0,
+                     seq_stride=4096)
     assert lib.padra_DecodeAttention(None, _p(16), ctypes.byref(q8), _p(32), ctypes.byref(dec), 2,
-                                     16, 4, 0, 0, _p(64), need, bad, 0) == abi.UNSUPPORTED
+                                     16, 4, 0, 0, _p(64), need, bad, 0) == abi.INVALID_ARGUMENT
+    norot = abi.KVCache(format=abi.KV_Q8_0_NOROT, k=16, v=32, scales=None, cap=4096, first=0,
+                        seq_stride=4096)
+    assert lib.padra_DecodeAttention(None, _p(16), ctypes.byref(norot), _p(32), ctypes.byref(dec),
+                                     2, 16, 4, 0, 0, _p(64), need, bad, 0) == abi.UNSUPPORTED
     assert lib.padra_DecodeAttention(None, _p(16), ctypes.byref(kv), _p(32), ctypes.byref(base),
                                      2, 16, 4, 0, 0, _p(64), need, bad, 0) == abi.INVALID_ARGUMENT

@@ -545,3 +545,55 @@ def test_decode_attention_q8_0(oracle, hq, local):
         worst = max(worst, int(d.max()))
         assert close.all(), (s, int(d.max()))
     print(f"  max BF16 ulp difference {worst}", flush=True)
+
+
+@pytest.mark.parametrize("local", [False, True])
+def test_decode_attention_q8(oracle, local):
+    """q8 caches (per-head fp32 scale): the split reads bf16(code * scale) rows
+    (kv_q8::Decode), so the oracle is the BF16 attention over the decoded cache; within the
+    _attn_close tolerance."""
+    print(f"[case] decode attention q8 local={local}", flush=True)
+    seqs, hq, hkv, capacity = 4, 16, 4, 4096
+    cap = 1024 if local else capacity
+    rng = np.random.default_rng(130 + local)
+    positions = rng.integers(0, capacity, seqs).astype(np.int32)
+    positions[0] = 3
+    q = synth.bf16_bits((rng.standard_normal((seqs, hq, 128)) * 2).astype(np.float32))
+    codes_k = rng.integers(-127, 128, (seqs, cap, hkv * 128)).astype(np.int8)
+    codes_v = rng.integers(-127, 128, (seqs, cap, hkv * 128)).astype(np.int8)
+    scales = (rng.uniform(0.005, 0.02, (seqs, cap, hkv, 2))).astype(np.float32)
+    dk = synth.bf16_bits(codes_k.reshape(seqs, cap, hkv, 128).astype(np.float32) *
+                         scales[..., 0:1]).reshape(seqs, cap, -1)
+    dv = synth.bf16_bits(codes_v.reshape(seqs, cap, hkv, 128).astype(np.float32) *
+                         scales[..., 1:2]).reshape(seqs, cap, -1)
+    states = np.zeros((seqs, 8), np.int32)
+    for s, p in enumerate(positions):
+        states[s] = [5, p, capacity, 10, p, min(p, 1024), 0, 0]
+    out = torch.empty((seqs, hq, 128), dtype=torch.int16, device="cuda")
+    bad = flag()
+    kv = ops.kv_cache(abi.KV_Q8, torch.from_numpy(codes_k.reshape(seqs * cap, -1)).cuda(),
+                      torch.from_numpy(codes_v.reshape(seqs * cap, -1)).cuda(), cap,
+                      scales=torch.from_numpy(scales.reshape(seqs * cap, hkv, 2)).cuda(),
+                      seq_stride=cap)
+    ops.DecodeAttention(dev(q), kv, out, ops.positions_decode(torch.from_numpy(states).cuda(),
+                                                              maximum=capacity),
+                        bad, kv_heads=hkv, local=local)
+    torch.cuda.synchronize()
+    assert bad.item() == 0
+    got = host16(out)
+    for s in range(seqs):
+        want, _, wbad = oracle.decode_attention(q[s], dk[s], dv[s], positions[s], local=local)
+        assert not wbad
+        close, d = _attn_close(got[s], want)
+        assert close.all(), (s, int(d.max()))
+    # a -128 code inside the window raises the flag
+    codes_k[1, positions[1] % cap, 5] = -128
+    kv2 = ops.kv_cache(abi.KV_Q8, torch.from_numpy(codes_k.reshape(seqs * cap, -1)).cuda(),
+                       torch.from_numpy(codes_v.reshape(seqs * cap, -1)).cuda(), cap,
+                       scales=torch.from_numpy(scales.reshape(seqs * cap, hkv, 2)).cuda(),
+                       seq_stride=cap)
+    ops.DecodeAttention(dev(q), kv2, out, ops.positions_decode(torch.from_numpy(states).cuda(),
+                                                               maximum=capacity),
+                        bad, kv_heads=hkv, local=local)
+    torch.cuda.synchronize()
+    assert bad.item() == 1
