@@ -234,6 +234,13 @@ int padra_SwiGLU(void *stream, const void *gate, const void *up, void *out, long
 int padra_Embed(void *stream, const uint16_t *table, int vocab, int hidden, const int32_t *ids,
                 const padra_Positions *src, int tokens, void *out, int *bad, int act);
 
+/* padra_QuantizeFP8: QuantizeFP8 (prefill.cuh:46-66), the E4M3 row encoding of an
+ * activation (the attention output before the O projection): per row of x [rows][cols],
+ * scales[row] = max|x|/448 (1 for a zero row) and packed[row][c] = E4M3 of the correctly
+ * rounded x/scale (saturating).  A non-finite value raises *bad (the row is still
+ * written).  cols a multiple of 8; x 16-byte aligned, packed 8-byte aligned. */
+int padra_QuantizeFP8(void *stream, const void *x, uint8_t *packed, float *scales, int rows,
+                      int cols, int *bad, int act);
 /* padra_Combine: Combine (inference.cu:580-590) and exl3_packed_activations::Combine
  * (expert_exl3_prefill_packed_activations.cuh:86-102).  For each row t and column i of
  * x [rows][hidden]: c = 0; for e = 0..experts-1: c = B(c + B(down[t][e][i] * weights[t][e]));

@@ -41,6 +41,7 @@ def lib() -> ctypes.CDLL:
             "po_fp8_encode": ([F, F, F], ctypes.c_uint8),
             "po_norm_fp8": ([P, P, P, P, P, I, I, F, P, P], None),
             "po_combine": ([P, P, P, I, I, I, I, P], None),
+            "po_quantize_fp8": ([P, P, P, I, I, P], None),
             "po_decode_attention": ([P, P, P, I, I, I, I, I, I, P, P], I),
             "po_decode_attention_q8_0": ([P, P, P, I, I, I, I, I, I, P, P], I),
             "po_kv_checkpoint_plane": ([P, P, P, I, I, I], None),
@@ -202,6 +203,17 @@ def decode_attention_q8_0(q, rows_k, rows_v, position, local=False, splits=0, hk
                                           int(position), int(bool(local)), hq, hkv, int(splits),
                                           _p(out), bad.ptr)
     return out, used, bool(bad)
+
+
+def quantize_fp8(x):
+    """x fp32 [rows][cols].  Returns (packed u8, scales [rows], bad)."""
+    x = np.ascontiguousarray(x, np.float32)
+    rows, cols = x.shape
+    packed = np.empty((rows, cols), np.uint8)
+    scales = np.empty(rows, np.float32)
+    bad = Bad()
+    lib().po_quantize_fp8(_p(x), _p(packed), _p(scales), rows, cols, bad.ptr)
+    return packed, scales, bool(bad)
 
 
 def e4m3(values) -> np.ndarray:

@@ -279,6 +279,24 @@ void po_norm_fp8(const uint16_t *x, uint16_t *normalized, const uint16_t *gamma,
   }
 }
 
+/* prefill.cuh:46-66 */
+void po_quantize_fp8(const float *x, uint8_t *packed, float *scales, int rows, int cols,
+                     int *bad) {
+  for (int r = 0; r < rows; ++r) {
+    const float *xr = x + (long long)r * cols;
+    float amax = 0.f;
+    for (int c = 0; c < cols; ++c) {
+      if (!finite_f(xr[c]))
+        set_bad(bad);
+      amax = fmaxf(amax, fabsf(xr[c]));
+    }
+    const float scale = amax == 0.f ? 1.f : amax / 448.f;
+    scales[r] = scale;
+    for (int c = 0; c < cols; ++c)
+      packed[(long long)r * cols + c] = po_e4m3(xr[c] / scale);
+  }
+}
+
 /* ---- Expert combine -------------------------------------------------------------- */
 
 /* inference.cu:580-590; expert_exl3_prefill_packed_activations.cuh:86-102 */

@@ -62,6 +62,12 @@ void po_norm_fp8(const uint16_t *x, uint16_t *normalized, const uint16_t *gamma,
                  uint8_t *packed, float *scales, int rows, int hidden, float eps, float *stats,
                  int *bad);
 
+/* QuantizeFP8 (prefill.cuh:46-66): per row, scale = max|x|/448 (1 for a zero row; fmaxf
+ * drops NaN), packed = E4M3 of x / scale (correctly rounded quotient, saturating); a
+ * non-finite value raises *bad.  x is fp32 [rows][cols]. */
+void po_quantize_fp8(const float *x, uint8_t *packed, float *scales, int rows, int cols,
+                     int *bad);
+
 /* ---- Expert combine (+ residual) and combine + RMSNorm (+ FP8) ---------------- */
 /* Combine (inference.cu:580-590) and exl3_packed_activations::Combine
  * (expert_exl3_prefill_packed_activations.cuh:86-102): per row t and column i,

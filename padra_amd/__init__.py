@@ -45,6 +45,7 @@ from .ops import (  # noqa: F401
     KvQ8_0Dequantize,
     KvQ8_0DequantizePrefix,
     NormFP8,
+    QuantizeFP8,
     ResidualNormQKRopeStore,
     ResidualPostNorm,
     QKNormRopeStore,

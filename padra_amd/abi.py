@@ -87,6 +87,7 @@ SIGNATURES = {
                                   ctypes.POINTER(KVCache), ctypes.POINTER(Positions), _I, _I, _I,
                                   _P],
     "padra_Combine": [_P, _P, _P, _P, _I, _I, _I, _I, _P, _I],
+    "padra_QuantizeFP8": [_P, _P, _P, _P, _I, _I, _P, _I],
     "padra_CombineNorm": [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, ctypes.c_float, _P, _P,
                           _I],
     "padra_NormFP8": [_P, _P, _P, _P, _P, _P, _I, _I, ctypes.c_float, _P, _P, _I],

@@ -132,6 +132,64 @@ __global__ __launch_bounds__(64) void k_combine_norm(T *x, const T *down, const 
   norm_fp8_finish<J, T, FP8>(a, row, vp, gr);
 }
 
+// QuantizeFP8 (prefill.cuh:46-66): per row of x [rows][cols], scale = max|x| / 448 (1 for a
+// zero row; fmaxf drops NaN) and codes = E4M3 of the correctly rounded x / scale; a
+// non-finite value raises the flag.  One wave per row, 8 consecutive values per lane and
+// step.  BF16 rows whose values are finite and whose maximum is >= 2^-100 take the fast
+// quotient and the hardware conversion (the identities padra_CheckFP8Paths verifies for
+// BF16 values); other rows divide.
+template <class T>
+__global__ __launch_bounds__(64) void k_quantize_fp8(const T *x, uint8_t *packed, float *scales,
+                                                     int rows, int cols, int *bad) {
+  const int row = blockIdx.x, lane = threadIdx.x;
+  if (row >= rows)
+    return;
+  const T *xr = x + (size_t)row * cols;
+  float amax = 0.f;
+  bool fine = true, exact = true;
+  for (int c = 8 * lane; c < cols; c += 512) {
+    float v[8];
+    ActIO<T>::load8(xr + c, v);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      fine = fine && isfinite(v[i]);
+      exact = exact && (__float_as_uint(v[i]) & 0xffffu) == 0;
+      amax = fmaxf(amax, fabsf(v[i]));
+    }
+  }
+#pragma unroll
+  for (int d = 32; d >= 1; d /= 2)
+    amax = fmaxf(amax, __shfl_xor(amax, d, 64));
+  const bool row_fine = __ballot(!fine) == 0, row_bf16 = __ballot(!exact) == 0;
+  if (!row_fine && lane == 0)
+    raise_bad(bad);
+  const float scale = amax == 0.f ? 1.f : amax / 448.f;
+  const float inverse = 1.f / scale;
+  if (lane == 0)
+    scales[row] = scale;
+  const bool fast = row_fine && row_bf16 && fp8_fast_ok(amax, inverse); // wave-uniform
+  for (int c = 8 * lane; c < cols; c += 512) {
+    float v[8];
+    ActIO<T>::load8(xr + c, v);
+    uint32_t w[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      uint32_t lo, hi;
+      if (fast) {
+        lo = e4m3_pair_hw(fp8_quotient(v[4 * h], scale, inverse),
+                          fp8_quotient(v[4 * h + 1], scale, inverse));
+        hi = e4m3_pair_hw(fp8_quotient(v[4 * h + 2], scale, inverse),
+                          fp8_quotient(v[4 * h + 3], scale, inverse));
+      } else {
+        lo = e4m3_code(v[4 * h] / scale) | (e4m3_code(v[4 * h + 1] / scale) << 8);
+        hi = e4m3_code(v[4 * h + 2] / scale) | (e4m3_code(v[4 * h + 3] / scale) << 8);
+      }
+      w[h] = lo | (hi << 16);
+    }
+    *reinterpret_cast<uint2 *>(packed + (size_t)row * cols + c) = make_uint2(w[0], w[1]);
+  }
+}
+
 #define PADRA_COMBINE_J(JV)                                                                  \
   case JV:                                                                                   \
     return f(std::integral_constant<int, JV>{});
@@ -212,4 +270,20 @@ extern "C" int padra_CombineNorm(void *stream, void *x, const void *down, const 
     });
   };
   return act == PADRA_ACT_BF16 ? launch(uint16_t{}) : launch(float{});
+}
+
+extern "C" int padra_QuantizeFP8(void *stream, const void *x, uint8_t *packed, float *scales,
+                                 int rows, int cols, int *bad, int act) {
+  if (!x || !packed || !scales || !bad || rows < 1 || cols < 8 || cols % 8 ||
+      (act != PADRA_ACT_BF16 && act != PADRA_ACT_F32) || !aligned16(x) ||
+      (reinterpret_cast<uintptr_t>(packed) & 7))
+    return PADRA_INVALID_ARGUMENT;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  if (act == PADRA_ACT_BF16)
+    hipLaunchKernelGGL((k_quantize_fp8<uint16_t>), dim3(rows), dim3(64), 0, s,
+                       static_cast<const uint16_t *>(x), packed, scales, rows, cols, bad);
+  else
+    hipLaunchKernelGGL((k_quantize_fp8<float>), dim3(rows), dim3(64), 0, s,
+                       static_cast<const float *>(x), packed, scales, rows, cols, bad);
+  return launched("QuantizeFP8");
 }

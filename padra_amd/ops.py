@@ -61,6 +61,14 @@ def NormFP8(x, normalized, gamma, packed, scales, bad, eps=1e-6, statistics=None
              _p(scales), rows, hidden, float(eps), _p(statistics), _p(bad), _act(x))
 
 
+def QuantizeFP8(x, packed, scales, bad):
+    """packed <- E4M3 codes of x/scale, scales[row] = max|x|/448 (QuantizeFP8,
+    prefill.cuh:46-66)."""
+    _need_cuda(x, packed, scales, bad)
+    abi.call("padra_QuantizeFP8", _stream(x), _p(x), _p(packed), _p(scales), x.shape[0],
+             x.shape[-1], _p(bad), _act(x))
+
+
 def Combine(x, down, weights, bad, residual=True):
     """x <- [B(x + c) | c], c the ordered BF16 combine of the 8 expert rows
     (Combine, inference.cu:580-590).  down [rows][8][hidden], weights [rows][8] fp32."""

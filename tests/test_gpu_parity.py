@@ -165,6 +165,33 @@ def test_fp8_fast_path_identities_exhaustive():
     assert counts.tolist() == [0, 0]
 
 
+@pytest.mark.parametrize("act", ["bf16", "f32"])
+def test_quantize_fp8(oracle, act):
+    """E4M3 row encoding of activations (the attention output): BF16 rows (fast path),
+    fp32 rows that are not BF16-exact (division path), a zero row and a NaN row."""
+    print(f"[case] quantize fp8 act={act}", flush=True)
+    rng = np.random.default_rng(140)
+    rows, cols = 40, 4096
+    xf = (rng.standard_normal((rows, cols)) * np.exp2(rng.integers(-8, 8, (rows, 1)))).astype(
+        np.float32)
+    xf[3] = 0
+    if act == "bf16":
+        xb = synth.bf16_bits(xf)
+        xf = synth.bf16_to_f32(xb)
+        x = dev(xb)
+    else:
+        x = torch.from_numpy(xf).cuda()
+    want_p, want_s, want_bad = oracle.quantize_fp8(xf)
+    packed = torch.empty((rows, cols), dtype=torch.uint8, device="cuda")
+    scales = torch.empty(rows, dtype=torch.float32, device="cuda")
+    bad = flag()
+    ops.QuantizeFP8(x, packed, scales, bad)
+    torch.cuda.synchronize()
+    assert not want_bad and bad.item() == 0
+    assert np.array_equal(scales.cpu().numpy(), want_s)
+    assert np.array_equal(packed.cpu().numpy(), want_p)
+
+
 def test_norm_fp8_nonfinite_and_extremes(oracle):
     """A NaN and an infinite input row (flag raised; bytes as the reference writes them), a
     row of tiny values (scale near the fp32 minimum) and a row whose sum of squares

@@ -29,6 +29,7 @@ Per oracle function, what checks it:
                                   float32 + torch) on values aimed at every E4M3 midpoint
   po_norm_fp8                     y = po_rmsnorm's, scale = max|y|/448, codes = torch
                                   float8 of y/scale, zero row, non-finite row
+  po_quantize_fp8                 scale = max|x|/448, codes = torch float8 of numpy's x/scale
   po_combine                      one-hot weights give B(x + down_e); power-of-two weights
                                   on small integers are exact; float64 weighted sum within
                                   the rounding bound; the expert order of the accumulation
@@ -270,6 +271,20 @@ def test_norm_fp8(oracle):
     x[5, 9] = 0x7FC0  # NaN input
     *_, bad = oracle.norm_fp8(x, d["gamma"])
     assert bad
+
+
+def test_quantize_fp8(oracle):
+    rng = np.random.default_rng(25)
+    x = (rng.standard_normal((6, 4096)) * np.exp2(rng.integers(-20, 20, (6, 1)))).astype(F32)
+    x[2] = 0
+    packed, scales, bad = oracle.quantize_fp8(x)
+    assert not bad and scales[2] == 1 and not packed[2].any()
+    amax = np.abs(x).max(axis=1)
+    want = np.where(amax == 0, F32(1), (amax / F32(448)).astype(F32))
+    assert np.array_equal(scales, want)
+    assert np.array_equal(packed, torch_e4m3(x / scales[:, None]))
+    x[4, 9] = np.inf
+    assert oracle.quantize_fp8(x)[2]
 
 
 # ---- Expert combine ---------------------------------------------------------------------
