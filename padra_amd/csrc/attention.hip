@@ -1,20 +1,17 @@
-// Decode attention over a BF16 KV cache: split-K partial softmax, then a per-head merge.
+// Decode attention over a BF16 or q8 KV cache: split-K partial softmax, then a per-head merge.
 //
 // Reference: gqa8_fragment_validation::SplitBF16 (attention_gqa8_fragment_validation.cuh:
-// 79-214) with attention_perhead_exact::Merge (attention_perhead_exact.cuh:7-38), for any
-// number of query heads per KV head (the reference fixes 8).  One token per sequence, at
-// its DecodeState position; keys are the last n positions (n = position + 1, or at most
-// 1024 for a local ring), read from cache row (first + offset) % cap.
+// 79-214) with attention_perhead_exact::Merge (attention_perhead_exact.cuh:7-38); for q8
+// caches gqa8_q8_attention::SplitBF16 (attention_gqa8_q8.cuh:112-277), which reads the
+// tiles through kv_q8::Decode.  Any number of query heads per KV head up to 8 (the
+// reference fixes 8).  One token per sequence, at its DecodeState position; keys are the
+// last n positions (n = position + 1, or at most 1024 for a local ring), read from cache
+// row (first + offset) % cap.
 //
-// Split kernel: one wave per (sequence, KV head, split), over that split's 32-key tiles.
-//  - Scores: lane l takes key l % 32 and half l / 32 of the 128 dimensions, against the
-//    G query rows held in LDS; the halves meet in one lane exchange.  scale 1/sqrt(128)
-//    after the dot product, as the reference applies it.
-//  - Online softmax per row with the reference's arithmetic: the tile maximum and the sum
-//    of probabilities are xor-butterflies over the 32 key lanes (the reference's warp
-//    order), probabilities in fp32 for the denominator (fmaf(den, alpha, total)) and
-//    rounded to BF16 for the PV product.
-//  - PV: lane l owns dimensions 2l, 2l+1 of every row; the V tile is staged in LDS.
+// Split kernel (k_attn_mx): one wave per (sequence, KV head, split), over that split's
+// 32-key tiles, QK and PV on the matrix cores; the reference's online softmax per row
+// (tile maximum, fp32 probabilities for the denominator fmaf(den, alpha, total), BF16
+// probabilities for the PV product, scale 1/sqrt(128) applied after the dot product).
 // Merge kernel: one wave per (sequence, query head): weights exp(lse_s - max) / sum, then
 // out = B(sum_s w_s * partial_s) in split order.
 //
@@ -84,12 +81,6 @@ __device__ __forceinline__ float xor_sum32(float v) {
   return v;
 }
 
-// a.lo * b.lo + a.hi * b.hi + c for BF16 pairs (v_dot2_f32_bf16).
-__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
-  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
-                                        __builtin_bit_cast(bf16x2_t, b), c, false);
-}
-
 template <class T> __device__ __forceinline__ float act_value(const void *p, size_t i) {
   if constexpr (std::is_same<T, uint16_t>::value)
     return __uint_as_float((uint32_t) static_cast<const uint16_t *>(p)[i] << 16);
@@ -97,40 +88,80 @@ template <class T> __device__ __forceinline__ float act_value(const void *p, siz
     return static_cast<const float *>(p)[i];
 }
 
-// q8 cache rows decoded into the BF16 tile: bf16(code * scale) (kv_q8::Decode,
-// kv_q8.cuh:15-27); a -128 code, an invalid scale or a non-finite result raises the flag.
-__device__ __forceinline__ void q8_decode16(uint4 codes, float scale, uint4 &lo, uint4 &hi,
-                                            bool &fine) {
-  const uint32_t w[4] = {codes.x, codes.y, codes.z, codes.w};
-  uint32_t out[8];
-  bool ok = isfinite(scale) && scale > 0.f;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint32_t x = w[i] ^ 0x80808080u; // a byte 0x80 (code -128) becomes zero
-    ok = ok && (((x - 0x01010101u) & ~x & 0x80808080u) == 0);
-    out[2 * i] = pack2((float)(int8_t)(w[i] & 0xffu) * scale, (float)(int8_t)((w[i] >> 8) & 0xffu) * scale);
-    out[2 * i + 1] = pack2((float)(int8_t)((w[i] >> 16) & 0xffu) * scale, (float)(int8_t)(w[i] >> 24) * scale);
+// ---- Split kernel on the matrix cores --------------------------------------------------
+// QK and PV on v_mfma_f32_16x16x32_bf16 (the reference runs both on tensor-core MMA).  One
+// wave per (sequence, KV head, split); query rows are the 16 MFMA columns (rows past G are
+// zero).
+//  - QK: S[key][row] = K[key][:] . Q[row][:] for the tile's two 16-key halves, 4 K-steps of
+//    32 dimensions each.  Lane l then holds row l % 16, keys 16 h + 4 (l / 16) + i.
+//  - Softmax: the row's tile maximum and probability sum are the lane's 8 values plus two
+//    exchanges between the four lanes of the row.
+//  - PV: O[row][dim] += P[row][key] V[key][dim] with P straight from the score registers
+//    (K-slot i of lane group g is key 4g + i, then 16 + 4g + i - 4) and V staged in LDS as
+//    4-key groups per dimension, so that each B operand is two 8-byte LDS reads.  Lane l
+//    holds rows 4 (l / 16) + i of dimension 16 b + l % 16.
+//  - The accumulators are rescaled only when some row's maximum moved (alpha == 1 exactly
+//    otherwise).
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ f32x4_t mfma_bf16(uint4 a, uint4 b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                 __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+}
+
+// Whether every code * scale of a q8 row is finite in BF16 and the scale is valid; rows
+// that fail it (huge or invalid scales) check each decoded value instead.
+__device__ __forceinline__ bool q8_scale_fast(float scale) {
+  return scale > 0.f && (pack2(127.f * scale, 0.f) & 0x7f80u) != 0x7f80u;
+}
+
+// 16 codes (4 words) of one row: nonzero when a byte is 0x80 (code -128), from the
+// zero-byte test of the words with the sign bits flipped.
+__device__ __forceinline__ uint32_t q8_minus128(uint4 c) {
+  const uint32_t x0 = c.x ^ 0x80808080u, x1 = c.y ^ 0x80808080u, x2 = c.z ^ 0x80808080u,
+                 x3 = c.w ^ 0x80808080u;
+  return (((x0 - 0x01010101u) & ~x0) | ((x1 - 0x01010101u) & ~x1) | ((x2 - 0x01010101u) & ~x2) |
+          ((x3 - 0x01010101u) & ~x3)) &
+         0x80808080u;
+}
+
+// The 16 values code * scale of a code chunk (kv_q8::Decode), and with `fine` cleared when
+// the row's scale fails q8_scale_fast and a value is not finite in BF16 (or the scale is
+// invalid).  Keys past the window decode zero codes with a unit scale, as the reference
+// stages them.
+__device__ __forceinline__ void q8_values16(uint4 c, float scale, bool inside, float (&f)[16],
+                                            uint32_t &m128, bool &fine) {
+  if (!inside) {
+    c = make_uint4(0, 0, 0, 0);
+    scale = 1.f;
   }
+  const uint32_t w[4] = {c.x, c.y, c.z, c.w};
 #pragma unroll
-  for (int i = 0; i < 8; ++i)
-    ok = ok && ((out[i] & 0x7f80u) != 0x7f80u) && ((out[i] & 0x7f800000u) != 0x7f800000u);
-  lo = make_uint4(out[0], out[1], out[2], out[3]);
-  hi = make_uint4(out[4], out[5], out[6], out[7]);
-  fine = fine && ok;
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+      f[4 * i + b] = (float)(int8_t)((w[i] >> (8 * b)) & 0xffu) * scale;
+  m128 |= q8_minus128(c);
+  if (!q8_scale_fast(scale)) {
+    bool ok = isfinite(scale) && scale > 0.f;
+#pragma unroll
+    for (int e = 0; e < 16; ++e)
+      ok = ok && (pack2(f[e], 0.f) & 0x7f80u) != 0x7f80u;
+    fine = fine && ok;
+  }
 }
 
 template <int G, class T, bool Q8>
-__global__ __launch_bounds__(64) void k_attn_split(AttnArgs a) {
-  __shared__ uint32_t qs[G][kD / 2];         // query rows, BF16 pairs
-  // K and V tiles, BF16 pairs; K rows padded to 68 words so that the 32 key lanes' 16-byte
-  // reads spread over the banks.
-  __shared__ uint32_t ks[kKeys][kD / 2 + 4];
-  __shared__ uint32_t vs[kKeys][kD / 2];
-  __shared__ uint16_t ps[kKeys / 2][G][2];   // BF16 probabilities, key pairs per row
+__global__ __launch_bounds__(64) void k_attn_mx(AttnArgs a) {
+  constexpr int KW = kD / 2 + 4; // K row stride in words (padding spreads the banks)
+  constexpr int VW = kD + 16;    // V group stride in uint2
+  __shared__ uint32_t ks[kKeys][KW];
+  __shared__ uint2 vq[kKeys / 4][VW]; // (V[4j][d], V[4j+1][d]), (V[4j+2][d], V[4j+3][d])
   const int split = blockIdx.x, kv = blockIdx.y, seq = blockIdx.z, lane = threadIdx.x;
+  const int col = lane & 15, grp = lane >> 4;
   int n, first;
-  const bool ok = attn_window(a, seq, n, first);
-  if (!ok) {
+  if (!attn_window(a, seq, n, first)) {
     if (split == 0 && kv == 0 && lane == 0)
       raise_bad(a.bad);
     return;
@@ -140,7 +171,6 @@ __global__ __launch_bounds__(64) void k_attn_split(AttnArgs a) {
     return; // block-uniform
   const int begin = tiles * split / active, end = tiles * (split + 1) / active;
   const int features = a.hkv * kD;
-  // element offset of this sequence's rows and this KV head (BF16 values or q8 codes)
   const size_t head_off = (size_t)seq * a.seq_stride * features + kv * kD;
   const uint16_t *kc = a.kc + head_off, *vc = a.vc + head_off;
   const int8_t *k8 = reinterpret_cast<const int8_t *>(a.kc) + head_off;
@@ -148,149 +178,200 @@ __global__ __launch_bounds__(64) void k_attn_split(AttnArgs a) {
   const float2 *sc = reinterpret_cast<const float2 *>(a.kvscales) +
                      (size_t)seq * a.seq_stride * a.hkv + kv;
 
-  // Query rows: finite and BF16-exact, as the reference requires of its fp32 input.
-  bool qfine = true;
-  for (int i = lane; i < G * kD / 2; i += 64) {
-    const size_t o = ((size_t)seq * a.hq + kv * G) * kD + 2 * i;
-    const float x0 = act_value<T>(a.q, o), x1 = act_value<T>(a.q, o + 1);
-    qfine = qfine && isfinite(x0) && isfinite(x1) && (__float_as_uint(x0) & 0xffffu) == 0 &&
-            (__float_as_uint(x1) & 0xffffu) == 0;
-    qs[i / (kD / 2)][i % (kD / 2)] = (__float_as_uint(x0) >> 16) | (__float_as_uint(x1) & 0xffff0000u);
-  }
-  if (__ballot(!qfine) != 0 && lane == 0)
-    raise_bad(a.bad);
-
-  const int key = lane & 31, half = lane >> 5;
-  float maximum[G], den[G], acc[G][2];
-#pragma unroll
-  for (int r = 0; r < G; ++r) {
-    maximum[r] = -INFINITY;
-    den[r] = 0.f;
-    acc[r][0] = acc[r][1] = 0.f;
-  }
+  // Query operand: row col (zero past G), dimensions 32 t + 8 grp + e; finite and
+  // BF16-exact, as the reference requires of its fp32 input.
+  uint4 qb[4];
   bool fine = true;
-  __syncthreads();
-  // Tile loads: 16-byte chunk c = lane + 64 m of the tile's 32 key rows (key c / 16,
-  // dimensions 8 (c % 16) ..), contiguous 1 KB per instruction.  Rows past the window load
-  // a valid row and are zeroed (the reference zero-fills them).
-  // q8: chunk c = lane + 64 m (m < 4) holds 16 codes (key c / 8, dimensions 16 (c % 8) ..),
-  // with that key's scale pair.
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    uint32_t w[4] = {0, 0, 0, 0};
+    if (col < G) {
+      const size_t o = ((size_t)seq * a.hq + kv * G + col) * kD + 32 * t + 8 * grp;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float x0 = act_value<T>(a.q, o + 2 * e), x1 = act_value<T>(a.q, o + 2 * e + 1);
+        fine = fine && isfinite(x0) && isfinite(x1) && (__float_as_uint(x0) & 0xffffu) == 0 &&
+               (__float_as_uint(x1) & 0xffffu) == 0;
+        w[e] = (__float_as_uint(x0) >> 16) | (__float_as_uint(x1) & 0xffff0000u);
+      }
+    }
+    qb[t] = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+  if (__ballot(!fine) != 0 && lane == 0)
+    raise_bad(a.bad);
+  fine = true;
+
+  // Tile loads, each instruction covering whole rows (256 B BF16 rows on 16 lanes, 128 B q8
+  // rows on 8 lanes).  K: key c / 16 (q8: c / 8) of chunk c = lane + 64 m, dimensions in
+  // chunk order.  V: lane keeps 4 consecutive keys of the same dimensions:
+  //  BF16: m = 4 h + p is key 16 h + 4 grp + p, dimensions 8 col ..;
+  //  q8:   m = p is key 4 (lane / 8) + p, dimensions 16 (lane % 8) ...
+  // Rows past the window load a valid row and are zeroed (the reference zero-fills them).
   constexpr int CH = Q8 ? 4 : 8;
-  float2 kvs[CH];
+  float ksc[CH], vsc[CH];
+  auto row_of = [&](int tile, int key) {
+    const int o = tile * kKeys + key;
+    return (size_t)((first + (o < n ? o : 0)) % a.cap);
+  };
+  auto vkey = [&](int m) { return Q8 ? 4 * (lane >> 3) + m : 16 * (m >> 2) + 4 * grp + (m & 3); };
   auto load_tile = [&](int tile, uint4 (&kw)[8], uint4 (&vw)[8]) {
 #pragma unroll
     for (int m = 0; m < CH; ++m) {
-      const int c = lane + 64 * m, o = tile * kKeys + (c >> (Q8 ? 3 : 4));
-      const size_t row = (size_t)((first + (o < n ? o : 0)) % a.cap);
+      const int c = lane + 64 * m;
+      const size_t kr = row_of(tile, c >> (Q8 ? 3 : 4)), vr = row_of(tile, vkey(m));
       if constexpr (Q8) {
-        kw[m] = ld_nt(reinterpret_cast<const uint4 *>(k8 + row * features) + (c & 7));
-        vw[m] = ld_nt(reinterpret_cast<const uint4 *>(v8 + row * features) + (c & 7));
-        kvs[m] = sc[row * a.hkv];
+        kw[m] = ld_nt(reinterpret_cast<const uint4 *>(k8 + kr * features) + (c & 7));
+        vw[m] = ld_nt(reinterpret_cast<const uint4 *>(v8 + vr * features) + (lane & 7));
+        ksc[m] = sc[kr * a.hkv].x;
+        vsc[m] = sc[vr * a.hkv].y;
       } else {
-        kw[m] = ld_nt(reinterpret_cast<const uint4 *>(kc + row * features) + (c & 15));
-        vw[m] = ld_nt(reinterpret_cast<const uint4 *>(vc + row * features) + (c & 15));
+        kw[m] = ld_nt(reinterpret_cast<const uint4 *>(kc + kr * features) + (c & 15));
+        vw[m] = ld_nt(reinterpret_cast<const uint4 *>(vc + vr * features) + col);
       }
     }
   };
+
+  float maximum = -INFINITY, den = 0.f;
+  f32x4_t o[8];
+#pragma unroll
+  for (int b = 0; b < 8; ++b)
+    o[b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   uint4 kw[8], vw[8];
   load_tile(begin, kw, vw);
   for (int tile = begin; tile < end; ++tile) {
+    const int left = n - tile * kKeys; // keys of this tile inside the window (may be >= 32)
+    // Stage K rows and V key groups as BF16.
+    if constexpr (Q8) {
+      uint32_t m128 = 0;
 #pragma unroll
-    for (int m = 0; m < CH; ++m) {
-      const int c = lane + 64 * m;
-      if constexpr (Q8) {
-        const int key8 = c >> 3, part = c & 7;
-        uint4 klo, khi, vlo, vhi;
-        if (tile * kKeys + key8 >= n) { // the reference stages zeros with unit scales
-          klo = khi = vlo = vhi = make_uint4(0, 0, 0, 0);
-        } else {
-          q8_decode16(kw[m], kvs[m].x, klo, khi, fine);
-          q8_decode16(vw[m], kvs[m].y, vlo, vhi, fine);
-        }
-        *reinterpret_cast<uint4 *>(&ks[key8][part * 8]) = klo;
-        *reinterpret_cast<uint4 *>(&ks[key8][part * 8 + 4]) = khi;
-        *reinterpret_cast<uint4 *>(&vs[key8][part * 8]) = vlo;
-        *reinterpret_cast<uint4 *>(&vs[key8][part * 8 + 4]) = vhi;
-      } else {
-        if (tile * kKeys + (c >> 4) >= n)
-          kw[m] = vw[m] = make_uint4(0, 0, 0, 0);
+      for (int m = 0; m < CH; ++m) {
+        const int c = lane + 64 * m, key = c >> 3, part = c & 7;
+        float f[16];
+        q8_values16(kw[m], ksc[m], key < left, f, m128, fine);
+        uint32_t w[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          w[e] = pack2(f[2 * e], f[2 * e + 1]);
+        *reinterpret_cast<uint4 *>(&ks[key][part * 8]) = make_uint4(w[0], w[1], w[2], w[3]);
+        *reinterpret_cast<uint4 *>(&ks[key][part * 8 + 4]) = make_uint4(w[4], w[5], w[6], w[7]);
+      }
+      float fv[4][16];
+#pragma unroll
+      for (int m = 0; m < 4; ++m)
+        q8_values16(vw[m], vsc[m], vkey(m) < left, fv[m], m128, fine);
+      fine = fine && m128 == 0;
+      uint2 *dst = &vq[lane >> 3][16 * (lane & 7)];
+#pragma unroll
+      for (int e = 0; e < 16; e += 2)
+        *reinterpret_cast<uint4 *>(dst + e) =
+            make_uint4(pack2(fv[0][e], fv[1][e]), pack2(fv[2][e], fv[3][e]),
+                       pack2(fv[0][e + 1], fv[1][e + 1]), pack2(fv[2][e + 1], fv[3][e + 1]));
+    } else {
+#pragma unroll
+      for (int m = 0; m < 8; ++m) {
+        const int c = lane + 64 * m;
+        if ((c >> 4) >= left)
+          kw[m] = make_uint4(0, 0, 0, 0);
+        if (vkey(m) >= left)
+          vw[m] = make_uint4(0, 0, 0, 0);
         *reinterpret_cast<uint4 *>(&ks[c >> 4][(c & 15) * 4]) = kw[m];
-        *reinterpret_cast<uint4 *>(&vs[c >> 4][(c & 15) * 4]) = vw[m];
+      }
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const uint4 *p = &vw[4 * h];
+        const uint32_t w0[4] = {p[0].x, p[0].y, p[0].z, p[0].w}, w1[4] = {p[1].x, p[1].y, p[1].z, p[1].w},
+                       w2[4] = {p[2].x, p[2].y, p[2].z, p[2].w}, w3[4] = {p[3].x, p[3].y, p[3].z, p[3].w};
+        uint2 *dst = &vq[4 * h + grp][8 * col];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) // dimensions 2e, 2e + 1 of the chunk
+          *reinterpret_cast<uint4 *>(dst + 2 * e) = make_uint4(
+              __builtin_amdgcn_perm(w1[e], w0[e], 0x05040100u),
+              __builtin_amdgcn_perm(w3[e], w2[e], 0x05040100u),
+              __builtin_amdgcn_perm(w1[e], w0[e], 0x07060302u),
+              __builtin_amdgcn_perm(w3[e], w2[e], 0x07060302u));
       }
     }
     __syncthreads();
     // The next tile's loads are in flight during this tile's arithmetic (the last tile
     // reloads itself, keeping the loads unconditional).
     load_tile(min(tile + 1, end - 1), kw, vw);
-    const bool valid = tile * kKeys + key < n;
-    // Scores of this lane's key for every row: dot products of BF16 pairs (each product of
-    // two BF16 values is exact in fp32).
-    float s[G];
+
+    // Scores: lane holds row col, keys 16 h + 4 grp + i.
+    f32x4_t s[2];
 #pragma unroll
-    for (int r = 0; r < G; ++r) {
-      float dot = 0.f;
+    for (int h = 0; h < 2; ++h) {
+      s[h] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int m = 0; m < 8; ++m) {
-        const uint4 qw = *reinterpret_cast<const uint4 *>(&qs[r][half * 32 + 4 * m]);
-        const uint4 kq = *reinterpret_cast<const uint4 *>(&ks[key][half * 32 + 4 * m]);
-        dot = dot2(qw.x, kq.x, dot);
-        dot = dot2(qw.y, kq.y, dot);
-        dot = dot2(qw.z, kq.z, dot);
-        dot = dot2(qw.w, kq.w, dot);
+      for (int t = 0; t < 4; ++t)
+        s[h] = mfma_bf16(*reinterpret_cast<const uint4 *>(&ks[16 * h + col][16 * t + 4 * grp]),
+                         qb[t], s[h]);
+    }
+    float sv[8], tmax = -INFINITY;
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float v = s[h][i] * kScoreScale;
+        if (16 * h + 4 * grp + i < left)
+          fine = fine && isfinite(v);
+        else
+          v = -INFINITY;
+        sv[4 * h + i] = v;
+        tmax = fmaxf(tmax, v);
       }
-      s[r] = (dot + __shfl_xor(dot, 32, 64)) * kScoreScale;
-      if (valid)
-        fine = fine && isfinite(s[r]);
-      else
-        s[r] = -INFINITY;
-    }
-    // Online softmax per row (every lane holds every row's running state).
-    float alpha[G];
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+    const float next = fmaxf(maximum, tmax);
+    const float alpha = isfinite(maximum) ? expf(maximum - next) : 0.f;
+    float p[8], total = 0.f;
 #pragma unroll
-    for (int r = 0; r < G; ++r) {
-      const float next = fmaxf(maximum[r], xor_max32(s[r]));
-      alpha[r] = isfinite(maximum[r]) ? expf(maximum[r] - next) : 0.f;
-      const float prob = isfinite(s[r]) ? expf(s[r] - next) : 0.f;
-      const float total = xor_sum32(prob);
-      if (half == 0)
-        ps[key / 2][r][key & 1] = (uint16_t)(pack2(prob, 0.f) & 0xffffu);
-      den[r] = __builtin_fmaf(den[r], alpha[r], total);
-      maximum[r] = next;
+    for (int k = 0; k < 8; ++k) {
+      p[k] = isfinite(sv[k]) ? expf(sv[k] - next) : 0.f;
+      total += p[k];
     }
-    __syncthreads();
-    // PV: dimensions 2*lane, 2*lane + 1.
+    total += __shfl_xor(total, 16, 64);
+    total += __shfl_xor(total, 32, 64);
+    den = __builtin_fmaf(den, alpha, total);
+    maximum = next;
+    const uint4 pa = make_uint4(pack2(p[0], p[1]), pack2(p[2], p[3]), pack2(p[4], p[5]),
+                                pack2(p[6], p[7]));
+    if (__ballot(alpha != 1.f) != 0) { // wave-uniform
+      float ar[4];
 #pragma unroll
-    for (int r = 0; r < G; ++r) {
-      acc[r][0] *= alpha[r];
-      acc[r][1] *= alpha[r];
+      for (int i = 0; i < 4; ++i)
+        ar[i] = __shfl(alpha, 4 * grp + i, 64);
+#pragma unroll
+      for (int b = 0; b < 8; ++b)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          o[b][i] *= ar[i];
     }
-    // Key pairs: (V[2jp][d], V[2jp+1][d]) against the row's probability pair.  A
-    // non-finite V value reaches the outputs (inf or NaN) and is flagged there.
-#pragma unroll 4
-    for (int jp = 0; jp < kKeys / 2; ++jp) {
-      const uint32_t va = vs[2 * jp][lane], vb = vs[2 * jp + 1][lane];
-      const uint32_t x0 = __builtin_amdgcn_perm(vb, va, 0x05040100u); // (va.lo, vb.lo)
-      const uint32_t x1 = __builtin_amdgcn_perm(vb, va, 0x07060302u); // (va.hi, vb.hi)
 #pragma unroll
-      for (int r = 0; r < G; ++r) {
-        const uint32_t pw = *reinterpret_cast<const uint32_t *>(ps[jp][r]);
-        acc[r][0] = dot2(pw, x0, acc[r][0]);
-        acc[r][1] = dot2(pw, x1, acc[r][1]);
-      }
+    for (int b = 0; b < 8; ++b) {
+      const uint2 v0 = vq[grp][16 * b + col], v1 = vq[4 + grp][16 * b + col];
+      o[b] = mfma_bf16(pa, make_uint4(v0.x, v0.y, v1.x, v1.y), o[b]);
     }
     __syncthreads();
   }
+  // Rows 4 grp + i: this lane's dimension 16 b + col of each.
   const int head0 = kv * G;
 #pragma unroll
-  for (int r = 0; r < G; ++r) {
-    float *dst = a.partial + (((size_t)seq * a.splits + split) * a.hq + head0 + r) * kD;
-    const float v0 = acc[r][0] / den[r], v1 = acc[r][1] / den[r];
-    fine = fine && isfinite(v0) && isfinite(v1);
-    *reinterpret_cast<float2 *>(dst + 2 * lane) = make_float2(v0, v1);
-    if (lane == 0) {
-      const float l = maximum[r] + logf(den[r]);
-      fine = fine && isfinite(l);
-      a.lse[((size_t)seq * a.splits + split) * a.hq + head0 + r] = l;
+  for (int i = 0; i < 4; ++i) {
+    const int r = 4 * grp + i;
+    const float d = __shfl(den, r, 64), mx = __shfl(maximum, r, 64);
+    if (r < G) {
+      float *dst = a.partial + (((size_t)seq * a.splits + split) * a.hq + head0 + r) * kD + col;
+#pragma unroll
+      for (int b = 0; b < 8; ++b) {
+        const float v = o[b][i] / d;
+        fine = fine && isfinite(v);
+        dst[16 * b] = v;
+      }
+      if (col == 0) {
+        const float l = mx + logf(d);
+        fine = fine && isfinite(l);
+        a.lse[((size_t)seq * a.splits + split) * a.hq + head0 + r] = l;
+      }
     }
   }
   if (__ballot(!fine) != 0 && lane == 0)
@@ -705,16 +786,16 @@ extern "C" int padra_DecodeAttention(void *stream, const void *q, const padra_KV
       constexpr bool Q8 = decltype(q8tag)::value;
       switch (group) {
       case 1:
-        hipLaunchKernelGGL((k_attn_split<1, T, Q8>), split_grid, dim3(64), 0, s, a);
+        hipLaunchKernelGGL((k_attn_mx<1, T, Q8>), split_grid, dim3(64), 0, s, a);
         break;
       case 2:
-        hipLaunchKernelGGL((k_attn_split<2, T, Q8>), split_grid, dim3(64), 0, s, a);
+        hipLaunchKernelGGL((k_attn_mx<2, T, Q8>), split_grid, dim3(64), 0, s, a);
         break;
       case 4:
-        hipLaunchKernelGGL((k_attn_split<4, T, Q8>), split_grid, dim3(64), 0, s, a);
+        hipLaunchKernelGGL((k_attn_mx<4, T, Q8>), split_grid, dim3(64), 0, s, a);
         break;
       default:
-        hipLaunchKernelGGL((k_attn_split<8, T, Q8>), split_grid, dim3(64), 0, s, a);
+        hipLaunchKernelGGL((k_attn_mx<8, T, Q8>), split_grid, dim3(64), 0, s, a);
         break;
       }
     };

@@ -597,3 +597,58 @@ def test_decode_attention_q8(oracle, local):
                         bad, kv_heads=hkv, local=local)
     torch.cuda.synchronize()
     assert bad.item() == 1
+
+
+def test_decode_attention_q8_scales(oracle):
+    """kv_q8::Decode's checks (kv_q8.cuh:15-27) on the rows the split reads: a scale whose
+    127 * scale overflows BF16 decodes its smaller codes to finite values (no flag) and its
+    overflowing ones to a flag; a zero scale in the window is flagged; a NaN scale outside
+    the window is never read."""
+    print("[case] decode attention q8 scales", flush=True)
+    seqs, hq, hkv, cap = 2, 16, 4, 1024
+    rng = np.random.default_rng(141)
+    positions = np.array([3, 700], np.int32)
+    q = synth.bf16_bits((rng.standard_normal((seqs, hq, 128)) * 2).astype(np.float32))
+    codes_k = rng.integers(-127, 128, (seqs, cap, hkv * 128)).astype(np.int8)
+    codes_v = rng.integers(-127, 128, (seqs, cap, hkv * 128)).astype(np.int8)
+    scales = (rng.uniform(0.005, 0.02, (seqs, cap, hkv, 2))).astype(np.float32)
+    # sequence 1, row 17, V of every head: scale 3e36, codes within +-100 (3e38 < BF16 max)
+    codes_v[1, 17] = rng.integers(-100, 101, hkv * 128)
+    scales[1, 17, :, 1] = 3e36
+    scales[0, 500, :, 0] = np.nan  # outside sequence 0's window (positions 0..3)
+    states = np.zeros((seqs, 8), np.int32)
+    for s, p in enumerate(positions):
+        states[s] = [5, p, cap, 10, p, min(p, 1024), 0, 0]
+
+    def run(ck, sc):
+        out = torch.empty((seqs, hq, 128), dtype=torch.int16, device="cuda")
+        bad = flag()
+        kv = ops.kv_cache(abi.KV_Q8, torch.from_numpy(ck.reshape(seqs * cap, -1)).cuda(),
+                          torch.from_numpy(codes_v.reshape(seqs * cap, -1)).cuda(), cap,
+                          scales=torch.from_numpy(sc.reshape(seqs * cap, hkv, 2)).cuda(),
+                          seq_stride=cap)
+        ops.DecodeAttention(dev(q), kv, out,
+                            ops.positions_decode(torch.from_numpy(states).cuda(), maximum=cap),
+                            bad, kv_heads=hkv)
+        torch.cuda.synchronize()
+        return host16(out), bad.item()
+
+    got, bad = run(codes_k, scales)
+    assert bad == 0
+    with np.errstate(over="ignore", invalid="ignore"):
+        dk = synth.bf16_bits(codes_k.reshape(seqs, cap, hkv, 128).astype(np.float32) *
+                             scales[..., 0:1]).reshape(seqs, cap, -1)
+        dv = synth.bf16_bits(codes_v.reshape(seqs, cap, hkv, 128).astype(np.float32) *
+                             scales[..., 1:2]).reshape(seqs, cap, -1)
+    for s in range(seqs):
+        want, _, wbad = oracle.decode_attention(q[s], dk[s], dv[s], positions[s])
+        assert not wbad
+        close, d = _attn_close(got[s], want)
+        assert close.all(), (s, int(d.max()))
+    # code 127 at scale 3e36 rounds to a BF16 infinity
+    codes_v[1, 17, 3] = 127
+    assert run(codes_k, scales)[1] == 1
+    codes_v[1, 17, 3] = 0
+    sc = scales.copy()
+    sc[1, 650, 2, 0] = 0.0  # zero K scale inside sequence 1's window
+    assert run(codes_k, sc)[1] == 1
