@@ -152,12 +152,27 @@ __device__ __forceinline__ void q8_values16(uint4 c, float scale, bool inside, f
   }
 }
 
+// Slot of dimension d in a staged V row.  Each staging lane writes its dimension pairs at
+// slots rotated by its chunk index (q8: 16-dimension chunks, rotation by the chunk; BF16:
+// 8-dimension chunks, rotation by chunk / 4), which spreads a quarter-wave's 16-byte writes
+// over all 64 banks.
+template <bool Q8> __device__ __forceinline__ int vq_slot(int d) {
+  if constexpr (Q8) {
+    const int t = d >> 4;
+    return 16 * t + 2 * (((d >> 1) + t) & 7) + (d & 1);
+  } else {
+    const int c = d >> 3;
+    return 8 * c + 2 * (((d >> 1) + (c >> 2)) & 3) + (d & 1);
+  }
+}
+
 template <int G, class T, bool Q8>
 __global__ __launch_bounds__(64) void k_attn_mx(AttnArgs a) {
   constexpr int KW = kD / 2 + 4; // K row stride in words (padding spreads the banks)
   constexpr int VW = kD + 16;    // V group stride in uint2
-  __shared__ uint32_t ks[kKeys][KW];
-  __shared__ uint2 vq[kKeys / 4][VW]; // (V[4j][d], V[4j+1][d]), (V[4j+2][d], V[4j+3][d])
+  __shared__ __align__(16) uint32_t ks[kKeys][KW];
+  // (V[4j][d], V[4j+1][d]), (V[4j+2][d], V[4j+3][d]) at slot vq_slot(d)
+  __shared__ __align__(16) uint2 vq[kKeys / 4][VW];
   const int split = blockIdx.x, kv = blockIdx.y, seq = blockIdx.z, lane = threadIdx.x;
   const int col = lane & 15, grp = lane >> 4;
   int n, first;
@@ -201,19 +216,26 @@ __global__ __launch_bounds__(64) void k_attn_mx(AttnArgs a) {
     raise_bad(a.bad);
   fine = true;
 
-  // Tile loads, each instruction covering whole rows (256 B BF16 rows on 16 lanes, 128 B q8
-  // rows on 8 lanes).  K: key c / 16 (q8: c / 8) of chunk c = lane + 64 m, dimensions in
-  // chunk order.  V: lane keeps 4 consecutive keys of the same dimensions:
-  //  BF16: m = 4 h + p is key 16 h + 4 grp + p, dimensions 8 col ..;
-  //  q8:   m = p is key 4 (lane / 8) + p, dimensions 16 (lane % 8) ...
+  // Tile loads, each instruction covering whole rows of the head (BF16: 256 B on 16 lanes;
+  // q8: 128 codes on 8 lanes).
+  //  BF16 K: chunk c = lane + 64 m is key c / 16, dimensions 8 (c % 16) ..; V: m = 4 h + p
+  //  is key 16 h + 4 grp + p, dimensions 8 col ...
+  //  q8 K: chunk c = lane + 64 m is key c / 8, dimensions 16 (c % 8) ..; V: m = p is key
+  //  4 (lane / 8) + p, dimensions 16 (lane % 8) ..; each with its key's scale.
   // Rows past the window load a valid row and are zeroed (the reference zero-fills them).
   constexpr int CH = Q8 ? 4 : 8;
   float ksc[CH], vsc[CH];
+  // Cache row of window offset tile * 32 + key: the tile's first row (one modulo per tile)
+  // plus the key, wrapped once (the window holds at most cap keys); keys past the window
+  // read the window's first row.
+  const int first_row = first % a.cap;
   auto row_of = [&](int tile, int key) {
-    const int o = tile * kKeys + key;
-    return (size_t)((first + (o < n ? o : 0)) % a.cap);
+    const int base = (first + tile * kKeys) % a.cap, r = base + key;
+    return (size_t)(tile * kKeys + key < n ? (r >= a.cap ? r - a.cap : r) : first_row);
   };
-  auto vkey = [&](int m) { return Q8 ? 4 * (lane >> 3) + m : 16 * (m >> 2) + 4 * grp + (m & 3); };
+  auto vkey = [&](int m) {
+    return Q8 ? 4 * (lane >> 3) + m : 16 * (m >> 2) + 4 * grp + (m & 3);
+  };
   auto load_tile = [&](int tile, uint4 (&kw)[8], uint4 (&vw)[8]) {
 #pragma unroll
     for (int m = 0; m < CH; ++m) {
@@ -253,17 +275,19 @@ __global__ __launch_bounds__(64) void k_attn_mx(AttnArgs a) {
         for (int e = 0; e < 8; ++e)
           w[e] = pack2(f[2 * e], f[2 * e + 1]);
         *reinterpret_cast<uint4 *>(&ks[key][part * 8]) = make_uint4(w[0], w[1], w[2], w[3]);
-        *reinterpret_cast<uint4 *>(&ks[key][part * 8 + 4]) = make_uint4(w[4], w[5], w[6], w[7]);
+        *reinterpret_cast<uint4 *>(&ks[key][part * 8 + 4]) =
+            make_uint4(w[4], w[5], w[6], w[7]);
       }
       float fv[4][16];
 #pragma unroll
       for (int m = 0; m < 4; ++m)
         q8_values16(vw[m], vsc[m], vkey(m) < left, fv[m], m128, fine);
       fine = fine && m128 == 0;
-      uint2 *dst = &vq[lane >> 3][16 * (lane & 7)];
+      const int t7 = lane & 7;
+      uint2 *dst = &vq[lane >> 3][16 * t7];
 #pragma unroll
       for (int e = 0; e < 16; e += 2)
-        *reinterpret_cast<uint4 *>(dst + e) =
+        *reinterpret_cast<uint4 *>(dst + 2 * ((e / 2 + t7) & 7)) =
             make_uint4(pack2(fv[0][e], fv[1][e]), pack2(fv[2][e], fv[3][e]),
                        pack2(fv[0][e + 1], fv[1][e + 1]), pack2(fv[2][e + 1], fv[3][e + 1]));
     } else {
@@ -284,7 +308,7 @@ __global__ __launch_bounds__(64) void k_attn_mx(AttnArgs a) {
         uint2 *dst = &vq[4 * h + grp][8 * col];
 #pragma unroll
         for (int e = 0; e < 4; ++e) // dimensions 2e, 2e + 1 of the chunk
-          *reinterpret_cast<uint4 *>(dst + 2 * e) = make_uint4(
+          *reinterpret_cast<uint4 *>(dst + 2 * ((e + (col >> 2)) & 3)) = make_uint4(
               __builtin_amdgcn_perm(w1[e], w0[e], 0x05040100u),
               __builtin_amdgcn_perm(w3[e], w2[e], 0x05040100u),
               __builtin_amdgcn_perm(w1[e], w0[e], 0x07060302u),
@@ -348,7 +372,8 @@ __global__ __launch_bounds__(64) void k_attn_mx(AttnArgs a) {
     }
 #pragma unroll
     for (int b = 0; b < 8; ++b) {
-      const uint2 v0 = vq[grp][16 * b + col], v1 = vq[4 + grp][16 * b + col];
+      const int d = vq_slot<Q8>(16 * b + col);
+      const uint2 v0 = vq[grp][d], v1 = vq[4 + grp][d];
       o[b] = mfma_bf16(pa, make_uint4(v0.x, v0.y, v1.x, v1.y), o[b]);
     }
     __syncthreads();
@@ -425,8 +450,8 @@ template <class T> __global__ __launch_bounds__(64) void k_attn_merge(AttnArgs a
 // 128-key tile runs as four 32-key online-softmax streams (slice s: keys 32 s .. 32 s + 31),
 // each key lane keeping its own denominator; PV multiplies V codes by p * v_scale.  The four
 // streams join per split; the merge rotates the result back (two 64-point transforms).
-// Here one half-wave (32 lanes) serves one query head: lane = key for the scores, lane =
-// four dimensions for PV; the tile of 128 K and V rows is staged in LDS once for the G heads.
+// Here (k_q8_0_mx) each stream is its own partial entry and the merge joins the 4 * splits
+// entries; scores and PV run on the matrix cores.
 
 constexpr int kQ8Tile = 128, kRowBytes = 544;
 
@@ -472,20 +497,80 @@ __device__ __forceinline__ float f16_bits(uint32_t h) {
   return __half2float(__ushort_as_half((unsigned short)h));
 }
 
-template <int G> __global__ __launch_bounds__(32 * G < 64 ? 64 : 32 * G) void k_q8_0_split(AttnArgs a) {
-  constexpr int NT = 32 * G < 64 ? 64 : 32 * G;
-  // Half a tile (two 32-key slices) is staged at a time: 20 KB of LDS per workgroup.
-  constexpr int HK = kQ8Tile / 2;
-  __shared__ uint32_t kq[HK][36]; // K codes, rows padded to 36 words
-  __shared__ uint32_t vq[HK][32]; // V codes
-  __shared__ float ksc[HK][4];
-  __shared__ float vsc[4][HK];    // V block scales, by block then key
-  __shared__ float pr[G][32];            // this slice's probabilities, per head
-  const int split = blockIdx.x, kv = blockIdx.y, seq = blockIdx.z, tid = threadIdx.x;
-  const int hg = tid >> 5, lane = tid & 31, head = kv * G + (hg < G ? hg : G - 1);
+// ---- q8_0 split on the matrix cores -----------------------------------------------------
+// One workgroup per (sequence, split): four waves, one per KV head, each serving its G query
+// heads; the slice's 544-byte rows are staged whole, once for the four heads.  The reference keeps four
+// online-softmax streams per split (stream s: keys 32 s .. 32 s + 31 of every 128-key tile);
+// here each stream runs on its own, over the split's tiles, and ends as its own partial
+// entry (normalized output and log-sum-exp), so the merge combines 4 entries per split.
+// Per 32-key slice:
+//  - QK on v_mfma_i32_16x16x64_i8: rows are (head 4 j + r, block b) pairs of a head group j,
+//    whose A operand is the head's query codes masked to block b, so that each result is the
+//    exact integer dot product of one block; the score is then
+//    fma(float(dot_b), RN(k_scale_b * q_scale_b), ..) in block order, times 1/sqrt(128) (the
+//    reference sums the same products with its own grouping of the fp32 additions).  Lane l
+//    holds head 4 j + l / 16 of key 16 k + l % 16.
+//  - Softmax per head with the reference's recurrences (den = fmaf(den, alpha, p) per key
+//    position), maxima over the 16 key lanes by DPP row rotations.
+//  - PV on v_mfma_f32_16x16x32_bf16: O[head][dim] += (p * v_scale)[head][key] code[key][dim].
+//    Codes are exact in BF16; the fp32 factor enters as two BF16 terms (hi + lo, 2^-17
+//    relative).  The factor depends on the dimension's block, so rows are (head, block of a
+//    block pair): lane l holds rows 4 (l / 16) + i of dimension 16 t + l % 16, of which the
+//    rows of the tile's own block are kept.
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kStreams = 4;
+
+__device__ __forceinline__ i32x4_t mfma_i8(uint4 a, uint4 b, i32x4_t c) {
+  return __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i32x4_t, a),
+                                               __builtin_bit_cast(i32x4_t, b), c, 0, 0, 0);
+}
+
+// v from lane (l + N) % 16 of the lane's 16-lane row.
+template <int N> __device__ __forceinline__ float row_ror(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x120 + N, 0xf, 0xf, false));
+}
+// The maximum (fmaxf: NaN operands dropped) and the sum over a 16-lane row; every lane of
+// the row gets the same value (each step adds the lane's value to its half-row partner's).
+__device__ __forceinline__ float row_max16(float v) {
+  v = fmaxf(v, row_ror<8>(v));
+  v = fmaxf(v, row_ror<4>(v));
+  v = fmaxf(v, row_ror<2>(v));
+  return fmaxf(v, row_ror<1>(v));
+}
+__device__ __forceinline__ float row_sum16(float v) {
+  v = v + row_ror<8>(v);
+  v = v + row_ror<4>(v);
+  v = v + row_ror<2>(v);
+  return v + row_ror<1>(v);
+}
+
+// x as a BF16 pair hi + lo (hi = RN(x), lo = RN(x - hi)): the packed hi and lo words of
+// two values.
+__device__ __forceinline__ void bf16_split2(float x0, float x1, uint32_t &hi, uint32_t &lo) {
+  hi = pack2(x0, x1);
+  lo = pack2(x0 - lo16(hi), x1 - hi16(hi));
+}
+
+template <int G> __global__ __launch_bounds__(256) void k_q8_0_mx(AttnArgs a) {
+  // The 4 KV heads of a row, one wave each: the slice's rows are staged together, whole.
+  // K codes of the slice (rows padded to 36 words) and V codes as BF16 (4 keys per dimension
+  // and group, at slot vq_slot<true>(d)); head strides padded to 32 words modulo the banks.
+  __shared__ __align__(16) struct { uint32_t r[32][36]; uint32_t pad[32]; } kq_all[4];
+  __shared__ __align__(16) struct { uint2 r[8][kD + 8]; uint2 pad[16]; } vq_all[4];
+  __shared__ float ksc_all[4][32][4];    // K block scales by key
+  __shared__ float vsc_all[4][4][32];    // V block scales by block
+  __shared__ float ps_all[4][8][36];     // probabilities by head (rows padded)
+  const int split = blockIdx.x, seq = blockIdx.z, tid = threadIdx.x, kv = tid >> 6;
+  const int lane = tid & 63, col = lane & 15, grp = lane >> 4;
+  auto &kq = kq_all[kv].r;
+  auto &vq = vq_all[kv].r;
+  auto &ksc = ksc_all[kv];
+  auto &vsc = vsc_all[kv];
+  auto &ps = ps_all[kv];
   int n, first;
   if (!attn_window(a, seq, n, first) || (a.local && a.cap != 1024)) {
-    if (split == 0 && kv == 0 && tid == 0)
+    if (split == 0 && tid == 0)
       raise_bad(a.bad);
     return;
   }
@@ -498,182 +583,274 @@ template <int G> __global__ __launch_bounds__(32 * G < 64 ? 64 : 32 * G) void k_
                          (size_t)seq * a.seq_stride * kRowBytes;
   const uint8_t *vrows = static_cast<const uint8_t *>(static_cast<const void *>(a.vc)) +
                          (size_t)seq * a.seq_stride * kRowBytes;
-  // this head's coded query
-  int qi[32];
-  float qd[4];
-  {
-    const int *src = reinterpret_cast<const int *>(a.qcodes + ((size_t)seq * a.hq + head) * kD);
+  const int head0 = kv * G;
+
+  // Query A operands: row col = (head 4 j + col / 4, block col % 4); K-slot group grp of
+  // step h covers dimensions 64 h + 16 grp .. + 15, of block 2 h + grp / 2.
+  uint4 aq[2][2];
+  float qd[2][4]; // block scales of head 4 j + grp
 #pragma unroll
-    for (int i = 0; i < 32; ++i)
-      qi[i] = src[i];
+  for (int j = 0; j < 2; ++j) {
+    const int hh = 4 * j + (col >> 2);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      aq[j][h] = make_uint4(0, 0, 0, 0);
+      if (hh < G && (col & 3) == 2 * h + (grp >> 1))
+        aq[j][h] = *reinterpret_cast<const uint4 *>(
+            a.qcodes + ((size_t)seq * a.hq + head0 + hh) * kD + 64 * h + 16 * grp);
+    }
+    const int hq = 4 * j + grp;
 #pragma unroll
     for (int b = 0; b < 4; ++b)
-      qd[b] = a.qscale[((size_t)seq * a.hq + head) * 4 + b];
+      qd[j][b] = hq < G ? a.qscale[((size_t)seq * a.hq + head0 + hq) * 4 + b] : 0.f;
   }
-  float mx[4], den[4], acc[4][4];
+
+  // Slice loads over whole rows (512 codes = 32 chunks of 16 bytes): K chunk c = tid + 256 m
+  // is key c / 32, part c % 32 (head part / 8, codes 16 (part % 8) ..); V chunk m is key
+  // 4 (tid / 32) + m, part tid % 32.  Threads 0..127 load the 32-byte scale headers: half
+  // tid % 2 (heads 2 (tid % 2), + 1) of K row tid / 2 (tid < 64) or V row tid / 2 - 32.
+  // Keys past the window load the window's first row and are zeroed (the reference
+  // zero-fills them).
+  auto row_at = [&](int o) {
+    const int r = o < n ? o : 0;
+    return (size_t)(a.local ? (first + r) & 1023 : first + r) * kRowBytes;
+  };
+  uint4 kw[4], vw[4], hw = make_uint4(0, 0, 0, 0);
+  const int hrow = (tid >> 1) & 31;
+  auto load_slice = [&](int tile, int s) {
+    const int o0 = tile * kQ8Tile + 32 * s;
 #pragma unroll
-  for (int sl = 0; sl < 4; ++sl) {
-    mx[sl] = -INFINITY;
-    den[sl] = 0.f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      acc[sl][i] = 0.f;
-  }
-  for (int step = begin * 2; step < end * 2; ++step) {
-    const int tile = step >> 1, h0 = (step & 1) * HK;
-    // Stage keys h0 .. h0 + 63 of the tile: codes as 16-byte chunks (8 per row and tensor),
-    // scales 8 bytes per row.
-    for (int c = tid; c < HK * 8; c += NT) {
-      const int key = c >> 3, part = c & 7, o = tile * kQ8Tile + h0 + key;
-      uint4 kw = make_uint4(0, 0, 0, 0), vw = make_uint4(0, 0, 0, 0);
-      if (o < n) {
-        const size_t row = (size_t)(a.local ? (first + o) & 1023 : first + o) * kRowBytes;
-        kw = ld_nt(reinterpret_cast<const uint4 *>(krows + row + dbytes + kv * kD) + part);
-        vw = ld_nt(reinterpret_cast<const uint4 *>(vrows + row + dbytes + kv * kD) + part);
-      }
-      *reinterpret_cast<uint4 *>(&kq[key][4 * part]) = kw;
-      *reinterpret_cast<uint4 *>(&vq[key][4 * part]) = vw;
+    for (int m = 0; m < 4; ++m) {
+      const int c = tid + 256 * m;
+      kw[m] = ld_nt(reinterpret_cast<const uint4 *>(krows + row_at(o0 + (c >> 5)) + dbytes) +
+                    (c & 31));
+      vw[m] = ld_nt(reinterpret_cast<const uint4 *>(vrows + row_at(o0 + 4 * (tid >> 5) + m) +
+                                                    dbytes) + (tid & 31));
     }
-    for (int key = tid; key < HK; key += NT) {
-      const int o = tile * kQ8Tile + h0 + key;
-      uint2 kd = make_uint2(0, 0), vd = make_uint2(0, 0);
-      if (o < n) {
-        const size_t row = (size_t)(a.local ? (first + o) & 1023 : first + o) * kRowBytes;
-        kd = *reinterpret_cast<const uint2 *>(krows + row + 8 * kv);
-        vd = *reinterpret_cast<const uint2 *>(vrows + row + 8 * kv);
+    if (tid < 128)
+      hw = *reinterpret_cast<const uint4 *>((tid < 64 ? krows : vrows) + row_at(o0 + hrow) +
+                                            16 * (tid & 1));
+  };
+
+  bool fine = true;
+  float lses[kStreams][2];
+  const int slices = end - begin;
+  load_slice(begin, 0);
+  for (int s = 0; s < kStreams; ++s) {
+    float mx[2] = {-INFINITY, -INFINITY}, den[2][2] = {{0.f, 0.f}, {0.f, 0.f}};
+    f32x4_t o[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t)
+      o[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int it = 0; it < slices; ++it) {
+      const int tile = begin + it, o0 = tile * kQ8Tile + 32 * s;
+      // Stage the slice.
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        const int c = tid + 256 * m;
+        const uint4 w = o0 + (c >> 5) < n ? kw[m] : make_uint4(0, 0, 0, 0);
+        *reinterpret_cast<uint4 *>(&kq_all[(c >> 3) & 3].r[c >> 5][4 * (c & 7)]) = w;
       }
-      ksc[key][0] = f16_bits(kd.x & 0xffffu);
-      ksc[key][1] = f16_bits(kd.x >> 16);
-      ksc[key][2] = f16_bits(kd.y & 0xffffu);
-      ksc[key][3] = f16_bits(kd.y >> 16);
-      vsc[0][key] = f16_bits(vd.x & 0xffffu);
-      vsc[1][key] = f16_bits(vd.x >> 16);
-      vsc[2][key] = f16_bits(vd.y & 0xffffu);
-      vsc[3][key] = f16_bits(vd.y >> 16);
-    }
-    __syncthreads();
-    if (hg < G) {
+      {
+        float f[4][16];
 #pragma unroll
-      for (int hs = 0; hs < 2; ++hs) {
-        const int sl = (step & 1) * 2 + hs; // the online-softmax stream of this slice
-        const int key = hs * 32 + lane, o = tile * kQ8Tile + h0 + key;
-        int kw[32];
+        for (int m = 0; m < 4; ++m) {
+          const bool inside = o0 + 4 * (tid >> 5) + m < n;
+          const uint32_t w[4] = {vw[m].x, vw[m].y, vw[m].z, vw[m].w};
 #pragma unroll
-        for (int m = 0; m < 8; ++m) {
-          const uint4 w = *reinterpret_cast<const uint4 *>(&kq[key][4 * m]);
-          kw[4 * m] = (int)w.x;
-          kw[4 * m + 1] = (int)w.y;
-          kw[4 * m + 2] = (int)w.z;
-          kw[4 * m + 3] = (int)w.w;
+          for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int b = 0; b < 4; ++b)
+              f[m][4 * i + b] = inside ? (float)(int8_t)((w[i] >> (8 * b)) & 0xffu) : 0.f;
         }
-        float part[4];
+        const int t7 = tid & 7;
+        uint2 *dst = &vq_all[(tid >> 3) & 3].r[tid >> 5][16 * t7];
 #pragma unroll
-        for (int sub = 0; sub < 4; ++sub) {
-          float dot = 0.f;
+        for (int e = 0; e < 16; e += 2)
+          *reinterpret_cast<uint4 *>(dst + 2 * ((e / 2 + t7) & 7)) =
+              make_uint4(pack2(f[0][e], f[1][e]), pack2(f[2][e], f[3][e]),
+                         pack2(f[0][e + 1], f[1][e + 1]), pack2(f[2][e + 1], f[3][e + 1]));
+      }
+      if (tid < 128) {
+        const bool inside = o0 + hrow < n;
+        const uint32_t hv[4] = {hw.x, hw.y, hw.z, hw.w};
+#pragma unroll
+        for (int h2 = 0; h2 < 2; ++h2) { // heads 2 (tid % 2) + h2
+          const int hd = 2 * (tid & 1) + h2;
+          float d[4];
 #pragma unroll
           for (int b = 0; b < 4; ++b) {
-            int sum = __builtin_amdgcn_sdot4(kw[b * 8 + sub], qi[b * 8 + sub], 0, false);
-            sum = __builtin_amdgcn_sdot4(kw[b * 8 + sub + 4], qi[b * 8 + sub + 4], sum, false);
-            dot = __builtin_fmaf((float)sum, ksc[key][b] * qd[b], dot);
+            const uint32_t word = hv[2 * h2 + (b >> 1)];
+            d[b] = inside ? f16_bits((b & 1) ? word >> 16 : word & 0xffffu) : 0.f;
           }
-          part[sub] = dot;
-        }
-        const float dot = (part[0] + part[1]) + (part[2] + part[3]);
-        const float own = o < n ? dot * kScoreScale : -INFINITY;
-        float top = own;
+          if (tid < 64) {
+            *reinterpret_cast<float4 *>(&ksc_all[hd][hrow][0]) = make_float4(d[0], d[1], d[2], d[3]);
+          } else {
 #pragma unroll
-        for (int d = 16; d >= 1; d /= 2)
-          top = fmaxf(top, __shfl_xor(top, d, 32));
-        const float next = fmaxf(mx[sl], top);
-        const float alpha = isfinite(mx[sl]) ? expf(mx[sl] - next) : 0.f;
-        const float p = isfinite(own) ? expf(own - next) : 0.f;
-        mx[sl] = next;
-        den[sl] = __builtin_fmaf(den[sl], alpha, p);
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          acc[sl][i] *= alpha;
-        // The half-wave's probabilities go through LDS (its own row of pr; a half-wave
-        // executes in lockstep with its writes, so no barrier is needed for it).
-        pr[hg][lane] = p;
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-#pragma unroll 2
-        for (int k4 = 0; k4 < 32; k4 += 4) {
-          const float4 p4 = *reinterpret_cast<const float4 *>(&pr[hg][k4]);
-          const float4 s4 = *reinterpret_cast<const float4 *>(&vsc[lane >> 3][hs * 32 + k4]);
-          const float pk[4] = {p4.x, p4.y, p4.z, p4.w}, sk[4] = {s4.x, s4.y, s4.z, s4.w};
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const float factor = pk[j] * sk[j];
-            const uint32_t codes = vq[hs * 32 + k4 + j][lane];
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-              acc[sl][i] = __builtin_fmaf(factor, (float)(int8_t)(codes >> (8 * i)), acc[sl][i]);
+            for (int b = 0; b < 4; ++b)
+              vsc_all[hd][b][hrow] = d[b];
           }
         }
-        __builtin_amdgcn_wave_barrier(); // pr is rewritten by the next slice
+      }
+      __syncthreads();
+      // The next slice's loads are in flight during this slice's arithmetic (the last one
+      // reloads the first slice, keeping the loads unconditional).
+      {
+        const bool last_tile = it + 1 == slices;
+        load_slice(last_tile ? begin : tile + 1, last_tile ? (s + 1) & 3 : s);
+      }
+
+      // Scores: head 4 j + grp, key 16 k + col.
+      float sc[2][2];
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        const uint4 b0 = *reinterpret_cast<const uint4 *>(&kq[16 * k + col][4 * grp]);
+        const uint4 b1 = *reinterpret_cast<const uint4 *>(&kq[16 * k + col][16 + 4 * grp]);
+        const float4 kd = *reinterpret_cast<const float4 *>(&ksc[16 * k + col][0]);
+        const bool valid = o0 + 16 * k + col < n;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          i32x4_t d = mfma_i8(aq[j][0], b0, i32x4_t{0, 0, 0, 0});
+          d = mfma_i8(aq[j][1], b1, d);
+          float dot = 0.f;
+          dot = __builtin_fmaf((float)d[0], kd.x * qd[j][0], dot);
+          dot = __builtin_fmaf((float)d[1], kd.y * qd[j][1], dot);
+          dot = __builtin_fmaf((float)d[2], kd.z * qd[j][2], dot);
+          dot = __builtin_fmaf((float)d[3], kd.w * qd[j][3], dot);
+          sc[k][j] = valid ? dot * kScoreScale : -INFINITY;
+        }
+      }
+      float alpha[2];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const float next = fmaxf(mx[j], row_max16(fmaxf(sc[0][j], sc[1][j])));
+        alpha[j] = isfinite(mx[j]) ? expf(mx[j] - next) : 0.f;
+        mx[j] = next;
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+          const float p = isfinite(sc[k][j]) ? expf(sc[k][j] - next) : 0.f;
+          den[k][j] = __builtin_fmaf(den[k][j], alpha[j], p);
+          ps[4 * j + grp][16 * k + col] = p;
+        }
+      }
+      // Rows 4 grp + i of the PV accumulators are head (4 grp + i) % 8, whose alpha lane 16 i
+      // holds (alpha[0] for heads 0..3, alpha[1] for 4..7).
+      if (__ballot(alpha[0] != 1.f || alpha[1] != 1.f) != 0) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float a0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha[0]), 16 * i));
+          const float a1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha[1]), 16 * i));
+          const float ar = (grp & 1) ? a1 : a0;
+#pragma unroll
+          for (int t = 0; t < 8; ++t)
+            o[t][i] *= ar;
+        }
+      }
+      __syncthreads();
+      // PV A operands: row col = (head col % 8, block 2 c + col / 8); K-slots of group grp are
+      // keys 8 grp .. 8 grp + 7.
+      uint4 ahi[2], alo[2];
+      {
+        const int hh = col & 7;
+        const float4 p0 = *reinterpret_cast<const float4 *>(&ps[hh][8 * grp]);
+        const float4 p1 = *reinterpret_cast<const float4 *>(&ps[hh][8 * grp + 4]);
+        const float pv[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+          const int b = 2 * c + (col >> 3);
+          const float4 v0 = *reinterpret_cast<const float4 *>(&vsc[b][8 * grp]);
+          const float4 v1 = *reinterpret_cast<const float4 *>(&vsc[b][8 * grp + 4]);
+          const float vv[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+          uint32_t hi[4], lo[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float f0 = hh < G ? pv[2 * e] * vv[2 * e] : 0.f;
+            const float f1 = hh < G ? pv[2 * e + 1] * vv[2 * e + 1] : 0.f;
+            bf16_split2(f0, f1, hi[e], lo[e]);
+          }
+          ahi[c] = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+          alo[c] = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        const int d = vq_slot<true>(16 * t + col);
+        const uint2 v0 = vq[2 * grp][d], v1 = vq[2 * grp + 1][d];
+        const uint4 bv = make_uint4(v0.x, v0.y, v1.x, v1.y);
+        o[t] = mfma_bf16(ahi[t >> 2], bv, o[t]);
+        o[t] = mfma_bf16(alo[t >> 2], bv, o[t]);
+      }
+      __syncthreads(); // the next slice restages the tiles
+    }
+    // The stream's entry: den over the 32 key positions, lse = max + log(den), and the
+    // normalized output (zero for an empty stream).
+    float dsum[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      dsum[j] = row_sum16(den[0][j] + den[1][j]);
+      lses[s][j] = dsum[j] > 0.f ? mx[j] + logf(dsum[j]) : -INFINITY;
+    }
+    const size_t entry = ((size_t)seq * a.splits + split) * kStreams + s;
+    if (col == 0) {
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        if (4 * j + grp < G)
+          a.lse[entry * a.hq + head0 + 4 * j + grp] = lses[s][j];
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int hh = (4 * grp + i) & 7;
+      const float d0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(dsum[0]), 16 * i));
+      const float d1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(dsum[1]), 16 * i));
+      const float d = (grp & 1) ? d1 : d0;
+      if (hh < G) {
+        float *dst = a.partial + (entry * a.hq + head0 + hh) * kD + col;
+#pragma unroll
+        for (int t = 0; t < 8; ++t)
+          if (((t >> 1) & 1) == (grp >> 1))
+            dst[16 * t] = d > 0.f ? o[t][i] / d : 0.f;
       }
     }
-    __syncthreads();
   }
-  if (hg >= G)
-    return;
-  float top = -INFINITY;
+  // The reference's check of the split's combined weight (per head).
 #pragma unroll
-  for (int sl = 0; sl < 4; ++sl) {
-    float d = den[sl];
+  for (int j = 0; j < 2; ++j) {
+    const float top = fmaxf(fmaxf(lses[0][j], lses[1][j]), fmaxf(lses[2][j], lses[3][j]));
+    float total = 0.f;
 #pragma unroll
-    for (int o = 16; o >= 1; o /= 2)
-      d = d + __shfl_xor(d, o, 32);
-    mx[sl] = d > 0.f ? mx[sl] + logf(d) : -INFINITY;
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      acc[sl][i] = d > 0.f ? acc[sl][i] / d : 0.f;
-    top = fmaxf(top, mx[sl]);
+    for (int s = 0; s < kStreams; ++s)
+      total += isfinite(lses[s][j]) ? expf(lses[s][j] - top) : 0.f;
+    if (4 * j + grp < G)
+      fine = fine && total > 0.f && isfinite(total);
   }
-  top = fmaxf(fmaxf(mx[0], mx[1]), fmaxf(mx[2], mx[3]));
-  float total = 0.f, sum[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int sl = 0; sl < 4; ++sl) {
-    const float w = isfinite(mx[sl]) ? expf(mx[sl] - top) : 0.f;
-    total += w;
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      sum[i] = __builtin_fmaf(w, acc[sl][i], sum[i]);
-  }
-  if (!(total > 0.f) || !isfinite(total)) {
-    if (lane == 0)
-      raise_bad(a.bad);
-    return;
-  }
-  float *dst = a.partial + (((size_t)seq * a.splits + split) * a.hq + head) * kD + 4 * lane;
-  *reinterpret_cast<float4 *>(dst) =
-      make_float4(sum[0] / total, sum[1] / total, sum[2] / total, sum[3] / total);
-  if (lane == 0)
-    a.lse[((size_t)seq * a.splits + split) * a.hq + head] = top + logf(total);
+  if (__ballot(!fine) != 0 && lane == 0)
+    raise_bad(a.bad);
 }
 
-template <class T> __global__ __launch_bounds__(64) void k_q8_0_merge(AttnArgs a) {
+template <class T> __global__ __launch_bounds__(64) void k_q8_0_mx_merge(AttnArgs a) {
   const int head = blockIdx.x, seq = blockIdx.y, lane = threadIdx.x;
   int n, first;
   if (!attn_window(a, seq, n, first) || (a.local && a.cap != 1024))
     return; // the split kernel raised the flag
-  const int active = min(a.splits, (n + kQ8Tile - 1) / kQ8Tile), l32 = lane & 31;
-  const float v = l32 < active ? a.lse[((size_t)seq * a.splits + l32) * a.hq + head] : -INFINITY;
-  float mxv = v;
+  // Entries e = 4 split + stream, two per lane (e = lane, lane + 64).
+  const int entries = kStreams * min(a.splits, (n + kQ8Tile - 1) / kQ8Tile);
+  const size_t base = (size_t)seq * a.splits * kStreams;
+  const float v0 = lane < entries ? a.lse[(base + lane) * a.hq + head] : -INFINITY;
+  const float v1 = lane + 64 < entries ? a.lse[(base + lane + 64) * a.hq + head] : -INFINITY;
+  float mxv = fmaxf(v0, v1);
 #pragma unroll
-  for (int d = 16; d >= 1; d /= 2)
-    mxv = fmaxf(mxv, __shfl_xor(mxv, d, 32));
-  const float p = l32 < active ? expf(v - mxv) : 0.f;
-  float den = p;
+  for (int d = 32; d >= 1; d /= 2)
+    mxv = fmaxf(mxv, __shfl_xor(mxv, d, 64));
+  const float p0 = isfinite(v0) ? expf(v0 - mxv) : 0.f, p1 = isfinite(v1) ? expf(v1 - mxv) : 0.f;
+  float den = p0 + p1;
 #pragma unroll
-  for (int d = 16; d >= 1; d /= 2)
-    den = den + __shfl_xor(den, d, 32);
-  const float weight = p / den;
+  for (int d = 32; d >= 1; d /= 2)
+    den = den + __shfl_xor(den, d, 64);
+  const float w0 = p0 / den, w1 = p1 / den;
   float x0 = 0.f, x1 = 0.f;
-  for (int sp = 0; sp < active; ++sp) {
-    const float w = __shfl(weight, sp, 64);
-    const float *src = a.partial + (((size_t)seq * a.splits + sp) * a.hq + head) * kD;
+  for (int e = 0; e < entries; ++e) {
+    const float w = e < 64 ? __shfl(w0, e, 64) : __shfl(w1, e - 64, 64);
+    const float *src = a.partial + ((base + e) * a.hq + head) * kD;
     x0 = __builtin_fmaf(w, src[lane], x0);
     x1 = __builtin_fmaf(w, src[64 + lane], x1);
   }
@@ -687,7 +864,7 @@ template <class T> __global__ __launch_bounds__(64) void k_q8_0_merge(AttnArgs a
   x0 *= .125f;
   x1 *= .125f;
   const uint32_t word = pack2(x0, x1); // lo: feature lane, hi: feature lane + 64
-  if (__ballot(!isfinite(x0) || !isfinite(x1)) != 0 && lane == 0)
+  if (__ballot(!isfinite(x0) || !isfinite(x1) || !(den > 0.f)) != 0 && lane == 0)
     raise_bad(a.bad);
   const size_t o = ((size_t)seq * a.hq + head) * kD;
   if constexpr (std::is_same<T, uint16_t>::value) {
@@ -706,7 +883,9 @@ extern "C" long long padra_DecodeAttentionScratch(int format, int seqs, int q_he
   if (seqs < 1 || q_heads < 1 || splits < 1 || splits > 32 ||
       (format != PADRA_KV_BF16 && format != PADRA_KV_Q8 && format != PADRA_KV_Q8_0))
     return -1;
-  const long long base = (long long)seqs * splits * q_heads * (kD + 1);
+  // partial outputs and log-sum-exps per entry (q8_0: one entry per split and stream)
+  const long long base =
+      (long long)seqs * splits * (format == PADRA_KV_Q8_0 ? kStreams : 1) * q_heads * (kD + 1);
   // q8_0: the coded query (128 bytes) and its 4 block scales per head
   return format == PADRA_KV_Q8_0 ? base + (long long)seqs * q_heads * (kD / 4 + 4) : base;
 }
@@ -740,10 +919,13 @@ extern "C" int padra_DecodeAttention(void *stream, const void *q, const padra_KV
   a.kc = static_cast<const uint16_t *>(kv->k);
   a.vc = static_cast<const uint16_t *>(kv->v);
   a.out = out;
+  // scratch: partial [entries][128], coded query [seqs][hq][128] bytes (16-byte aligned),
+  // query block scales [seqs][hq][4], lse [entries]
+  const long long entries = (long long)seqs * splits * (q8 ? kStreams : 1) * q_heads;
   a.partial = scratch;
-  a.lse = scratch + (long long)seqs * splits * q_heads * kD;
-  a.qscale = a.lse + (long long)seqs * splits * q_heads;
-  a.qcodes = reinterpret_cast<int8_t *>(a.qscale + (long long)seqs * q_heads * 4);
+  a.qcodes = reinterpret_cast<int8_t *>(scratch + entries * kD);
+  a.qscale = scratch + entries * kD + (long long)seqs * q_heads * (kD / 4);
+  a.lse = a.qscale + (q8 ? (long long)seqs * q_heads * 4 : 0);
   a.decode = pos->decode;
   a.seqs = seqs;
   a.hq = q_heads;
@@ -767,19 +949,19 @@ extern "C" int padra_DecodeAttention(void *stream, const void *q, const padra_KV
       hipLaunchKernelGGL((k_q8_0_query<T>), merge_grid, dim3(64), 0, s, a);
       switch (group) {
       case 1:
-        hipLaunchKernelGGL((k_q8_0_split<1>), split_grid, dim3(64), 0, s, a);
+        hipLaunchKernelGGL((k_q8_0_mx<1>), dim3(splits, 1, seqs), dim3(256), 0, s, a);
         break;
       case 2:
-        hipLaunchKernelGGL((k_q8_0_split<2>), split_grid, dim3(64), 0, s, a);
+        hipLaunchKernelGGL((k_q8_0_mx<2>), dim3(splits, 1, seqs), dim3(256), 0, s, a);
         break;
       case 4:
-        hipLaunchKernelGGL((k_q8_0_split<4>), split_grid, dim3(128), 0, s, a);
+        hipLaunchKernelGGL((k_q8_0_mx<4>), dim3(splits, 1, seqs), dim3(256), 0, s, a);
         break;
       default:
-        hipLaunchKernelGGL((k_q8_0_split<8>), split_grid, dim3(256), 0, s, a);
+        hipLaunchKernelGGL((k_q8_0_mx<8>), dim3(splits, 1, seqs), dim3(256), 0, s, a);
         break;
       }
-      hipLaunchKernelGGL((k_q8_0_merge<T>), merge_grid, dim3(64), 0, s, a);
+      hipLaunchKernelGGL((k_q8_0_mx_merge<T>), merge_grid, dim3(64), 0, s, a);
       return launched("DecodeAttention");
     }
     auto split = [&](auto q8tag) {
