@@ -18,6 +18,10 @@
 // Not bit-identical to the reference: its QK and PV products run on tensor-core MMA with an
 // unspecified accumulation order, and its expf/logf are CUDA's.  Products of two BF16
 // values are exact in fp32, so only the order of the fp32 sums and the exp/log ulps differ.
+// The split kernels take their probabilities from the hardware exponential
+// (v_exp_f32(x * log2 e), __expf): for x = score - maximum <= 0 its relative error grows
+// with |x| (about 2^-24 |x| from rounding x * log2 e), so it is a few fp32 ulps where the
+// probability matters and larger only for probabilities below e^-16.
 #include <stdio.h>
 
 #include <algorithm>
@@ -110,46 +114,54 @@ __device__ __forceinline__ f32x4_t mfma_bf16(uint4 a, uint4 b, f32x4_t c) {
                                                  __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
 }
 
-// Whether every code * scale of a q8 row is finite in BF16 and the scale is valid; rows
-// that fail it (huge or invalid scales) check each decoded value instead.
+// Whether every code * scale of a q8 row is finite in BF16 and the scale is valid:
+// 0 < scale and 127 * scale below 0x1.ffp127, the least fp32 value that BF16 rounds to
+// infinity (|code| <= 127, and rounding is monotonic).  Tiles with a row that fails it
+// check each decoded value (q8_check16).
 __device__ __forceinline__ bool q8_scale_fast(float scale) {
-  return scale > 0.f && (pack2(127.f * scale, 0.f) & 0x7f80u) != 0x7f80u;
+  return scale > 0.f && 127.f * scale < 0x1.ffp127f;
 }
 
-// 16 codes (4 words) of one row: nonzero when a byte is 0x80 (code -128), from the
-// zero-byte test of the words with the sign bits flipped.
-__device__ __forceinline__ uint32_t q8_minus128(uint4 c) {
-  const uint32_t x0 = c.x ^ 0x80808080u, x1 = c.y ^ 0x80808080u, x2 = c.z ^ 0x80808080u,
-                 x3 = c.w ^ 0x80808080u;
-  return (((x0 - 0x01010101u) & ~x0) | ((x1 - 0x01010101u) & ~x1) | ((x2 - 0x01010101u) & ~x2) |
-          ((x3 - 0x01010101u) & ~x3)) &
-         0x80808080u;
+// Nonzero in bit 7 of a byte when the word holds a 0x80 byte (code -128): the zero-byte
+// test of x = w ^ 0x80808080, (x - 0x01010101) & ~x & 0x80808080, where the bits 7 of ~x
+// are those of w.  Accumulated over words; the caller masks with 0x80808080.
+__device__ __forceinline__ uint32_t q8_minus128(uint32_t w) {
+  return ((w ^ 0x80808080u) + 0xfefefeffu) & w;
 }
 
-// The 16 values code * scale of a code chunk (kv_q8::Decode), and with `fine` cleared when
-// the row's scale fails q8_scale_fast and a value is not finite in BF16 (or the scale is
-// invalid).  Keys past the window decode zero codes with a unit scale, as the reference
-// stages them.
+// The 16 values code * scale of a code chunk (kv_q8::Decode), accumulating the -128 test
+// and whether the scale passes q8_scale_fast.  Keys past the window decode zero codes with
+// a unit scale, as the reference stages them.
 __device__ __forceinline__ void q8_values16(uint4 c, float scale, bool inside, float (&f)[16],
-                                            uint32_t &m128, bool &fine) {
+                                            uint32_t &m128, bool &slow) {
   if (!inside) {
     c = make_uint4(0, 0, 0, 0);
     scale = 1.f;
   }
   const uint32_t w[4] = {c.x, c.y, c.z, c.w};
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < 4; ++i) {
 #pragma unroll
     for (int b = 0; b < 4; ++b)
       f[4 * i + b] = (float)(int8_t)((w[i] >> (8 * b)) & 0xffu) * scale;
-  m128 |= q8_minus128(c);
-  if (!q8_scale_fast(scale)) {
-    bool ok = isfinite(scale) && scale > 0.f;
-#pragma unroll
-    for (int e = 0; e < 16; ++e)
-      ok = ok && (pack2(f[e], 0.f) & 0x7f80u) != 0x7f80u;
-    fine = fine && ok;
+    m128 |= q8_minus128(w[i]);
   }
+  slow = slow || !q8_scale_fast(scale);
+}
+
+// kv_q8::Decode's checks on a chunk whose scale failed q8_scale_fast: a valid scale and
+// every code * scale finite in BF16.
+__device__ __forceinline__ bool q8_check16(uint4 c, float scale) {
+  const uint32_t w[4] = {c.x, c.y, c.z, c.w};
+  bool ok = isfinite(scale) && scale > 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const float v = (float)(int8_t)((w[i] >> (8 * b)) & 0xffu) * scale;
+      ok = ok & ((pack2(v, 0.f) & 0x7f80u) != 0x7f80u);
+    }
+  return ok;
 }
 
 // Slot of dimension d in a staged V row.  Each staging lane writes its dimension pairs at
@@ -265,24 +277,33 @@ __global__ __launch_bounds__(64) void k_attn_mx(AttnArgs a) {
     // Stage K rows and V key groups as BF16.
     if constexpr (Q8) {
       uint32_t m128 = 0;
+      bool slow = false;
 #pragma unroll
       for (int m = 0; m < CH; ++m) {
         const int c = lane + 64 * m, key = c >> 3, part = c & 7;
         float f[16];
-        q8_values16(kw[m], ksc[m], key < left, f, m128, fine);
+        q8_values16(kw[m], ksc[m], key < left, f, m128, slow);
         uint32_t w[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e)
           w[e] = pack2(f[2 * e], f[2 * e + 1]);
         *reinterpret_cast<uint4 *>(&ks[key][part * 8]) = make_uint4(w[0], w[1], w[2], w[3]);
-        *reinterpret_cast<uint4 *>(&ks[key][part * 8 + 4]) =
-            make_uint4(w[4], w[5], w[6], w[7]);
+        *reinterpret_cast<uint4 *>(&ks[key][part * 8 + 4]) = make_uint4(w[4], w[5], w[6], w[7]);
       }
       float fv[4][16];
 #pragma unroll
       for (int m = 0; m < 4; ++m)
-        q8_values16(vw[m], vsc[m], vkey(m) < left, fv[m], m128, fine);
-      fine = fine && m128 == 0;
+        q8_values16(vw[m], vsc[m], vkey(m) < left, fv[m], m128, slow);
+      fine = fine && (m128 & 0x80808080u) == 0;
+      if (__ballot(slow) != 0) { // rare: huge or invalid scales
+#pragma unroll
+        for (int m = 0; m < CH; ++m) {
+          if (((lane + 64 * m) >> 3) < left && !q8_scale_fast(ksc[m]))
+            fine = fine && q8_check16(kw[m], ksc[m]);
+          if (vkey(m) < left && !q8_scale_fast(vsc[m]))
+            fine = fine && q8_check16(vw[m], vsc[m]);
+        }
+      }
       const int t7 = lane & 7;
       uint2 *dst = &vq[lane >> 3][16 * t7];
 #pragma unroll
@@ -346,11 +367,11 @@ __global__ __launch_bounds__(64) void k_attn_mx(AttnArgs a) {
     tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
     tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
     const float next = fmaxf(maximum, tmax);
-    const float alpha = isfinite(maximum) ? expf(maximum - next) : 0.f;
+    const float alpha = isfinite(maximum) ? __expf(maximum - next) : 0.f;
     float p[8], total = 0.f;
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
-      p[k] = isfinite(sv[k]) ? expf(sv[k] - next) : 0.f;
+      p[k] = isfinite(sv[k]) ? __expf(sv[k] - next) : 0.f;
       total += p[k];
     }
     total += __shfl_xor(total, 16, 64);
@@ -655,13 +676,13 @@ template <int G> __global__ __launch_bounds__(256) void k_q8_0_mx(AttnArgs a) {
         float f[4][16];
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
-          const bool inside = o0 + 4 * (tid >> 5) + m < n;
-          const uint32_t w[4] = {vw[m].x, vw[m].y, vw[m].z, vw[m].w};
+          const uint4 c = o0 + 4 * (tid >> 5) + m < n ? vw[m] : make_uint4(0, 0, 0, 0);
+          const uint32_t w[4] = {c.x, c.y, c.z, c.w};
 #pragma unroll
           for (int i = 0; i < 4; ++i)
 #pragma unroll
             for (int b = 0; b < 4; ++b)
-              f[m][4 * i + b] = inside ? (float)(int8_t)((w[i] >> (8 * b)) & 0xffu) : 0.f;
+              f[m][4 * i + b] = (float)(int8_t)((w[i] >> (8 * b)) & 0xffu);
         }
         const int t7 = tid & 7;
         uint2 *dst = &vq_all[(tid >> 3) & 3].r[tid >> 5][16 * t7];
@@ -724,11 +745,11 @@ template <int G> __global__ __launch_bounds__(256) void k_q8_0_mx(AttnArgs a) {
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
         const float next = fmaxf(mx[j], row_max16(fmaxf(sc[0][j], sc[1][j])));
-        alpha[j] = isfinite(mx[j]) ? expf(mx[j] - next) : 0.f;
+        alpha[j] = isfinite(mx[j]) ? __expf(mx[j] - next) : 0.f;
         mx[j] = next;
 #pragma unroll
         for (int k = 0; k < 2; ++k) {
-          const float p = isfinite(sc[k][j]) ? expf(sc[k][j] - next) : 0.f;
+          const float p = isfinite(sc[k][j]) ? __expf(sc[k][j] - next) : 0.f;
           den[k][j] = __builtin_fmaf(den[k][j], alpha[j], p);
           ps[4 * j + grp][16 * k + col] = p;
         }
