@@ -520,10 +520,10 @@ __device__ __forceinline__ float f16_bits(uint32_t h) {
 
 // ---- q8_0 split on the matrix cores -----------------------------------------------------
 // One workgroup per (sequence, split): four waves, one per KV head, each serving its G query
-// heads; the slice's 544-byte rows are staged whole, once for the four heads.  The reference keeps four
-// online-softmax streams per split (stream s: keys 32 s .. 32 s + 31 of every 128-key tile);
-// here each stream runs on its own, over the split's tiles, and ends as its own partial
-// entry (normalized output and log-sum-exp), so the merge combines 4 entries per split.
+// heads; the slice's 544-byte rows are staged whole, once for the four heads.  The reference
+// keeps four online-softmax streams per split (stream s: keys 32 s .. 32 s + 31 of every
+// 128-key tile) and weighs them by exp(lse_s - max) at the end; here each stream runs on its
+// own over the split's tiles and is folded into the split's combination when it ends.
 // Per 32-key slice:
 //  - QK on v_mfma_i32_16x16x64_i8: rows are (head 4 j + r, block b) pairs of a head group j,
 //    whose A operand is the head's query codes masked to block b, so that each result is the
@@ -654,7 +654,19 @@ template <int G> __global__ __launch_bounds__(256) void k_q8_0_mx(AttnArgs a) {
   };
 
   bool fine = true;
-  float lses[kStreams][2];
+  // The split's combination of its streams, for rows 4 grp + i of the PV layout (head
+  // (4 grp + i) % 8): the largest stream log-sum-exp, the total weight, and the weighted
+  // outputs of this lane's four dimension tiles t = 4 u + 2 (grp / 2) + v.
+  float cm[4], ct[4], cs[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    cm[i] = -INFINITY;
+    ct[i] = 0.f;
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      cs[u][i] = 0.f;
+  }
+  bool has[2] = {false, false}; // a stream of head 4 j + grp with a finite log-sum-exp
   const int slices = end - begin;
   load_slice(begin, 0);
   for (int s = 0; s < kStreams; ++s) {
@@ -803,47 +815,63 @@ template <int G> __global__ __launch_bounds__(256) void k_q8_0_mx(AttnArgs a) {
       }
       __syncthreads(); // the next slice restages the tiles
     }
-    // The stream's entry: den over the 32 key positions, lse = max + log(den), and the
-    // normalized output (zero for an empty stream).
-    float dsum[2];
+    // The stream's log-sum-exp (den over the 32 key positions), folded into the split's
+    // combination with weight exp(lse - max): the reference weighs its four streams the
+    // same way once all are done; online here, in stream order.  Streams without a finite
+    // log-sum-exp carry no weight, as there.
+    float dsum[2], lse[2];
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       dsum[j] = row_sum16(den[0][j] + den[1][j]);
-      lses[s][j] = dsum[j] > 0.f ? mx[j] + logf(dsum[j]) : -INFINITY;
-    }
-    const size_t entry = ((size_t)seq * a.splits + split) * kStreams + s;
-    if (col == 0) {
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-        if (4 * j + grp < G)
-          a.lse[entry * a.hq + head0 + 4 * j + grp] = lses[s][j];
+      lse[j] = dsum[j] > 0.f ? mx[j] + logf(dsum[j]) : -INFINITY;
+      has[j] = has[j] || isfinite(lse[j]);
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int hh = (4 * grp + i) & 7;
+      // head (4 grp + i) % 8 is head 4 (grp % 2) + i, whose values lane 16 i holds (in
+      // dsum[grp % 2] and lse[grp % 2]: read both, then select per lane)
       const float d0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(dsum[0]), 16 * i));
       const float d1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(dsum[1]), 16 * i));
-      const float d = (grp & 1) ? d1 : d0;
-      if (hh < G) {
-        float *dst = a.partial + (entry * a.hq + head0 + hh) * kD + col;
+      const float l0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(lse[0]), 16 * i));
+      const float l1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(lse[1]), 16 * i));
+      const float d = (grp & 1) ? d1 : d0, l = (grp & 1) ? l1 : l0;
+      if (isfinite(l)) {
+        const float m2 = fmaxf(cm[i], l);
+        const float wa = isfinite(cm[i]) ? expf(cm[i] - m2) : 0.f, wb = expf(l - m2);
+        ct[i] = __builtin_fmaf(ct[i], wa, wb);
 #pragma unroll
-        for (int t = 0; t < 8; ++t)
-          if (((t >> 1) & 1) == (grp >> 1))
-            dst[16 * t] = d > 0.f ? o[t][i] / d : 0.f;
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+          for (int v = 0; v < 2; ++v) {
+            const float x = (grp >> 1) ? o[4 * u + 2 + v][i] : o[4 * u + v][i];
+            cs[2 * u + v][i] = __builtin_fmaf(cs[2 * u + v][i], wa, wb * (x / d));
+          }
+        cm[i] = m2;
       }
     }
   }
-  // The reference's check of the split's combined weight (per head).
+  // The split's entry: the combined output and log-sum-exp of each head.
+  const size_t entry = (size_t)seq * a.splits + split;
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const float top = fmaxf(fmaxf(lses[0][j], lses[1][j]), fmaxf(lses[2][j], lses[3][j]));
-    float total = 0.f;
+  for (int i = 0; i < 4; ++i) {
+    const int hh = (4 * grp + i) & 7;
+    if (hh < G) {
+      float *dst = a.partial + (entry * a.hq + head0 + hh) * kD + col;
 #pragma unroll
-    for (int s = 0; s < kStreams; ++s)
-      total += isfinite(lses[s][j]) ? expf(lses[s][j] - top) : 0.f;
-    if (4 * j + grp < G)
-      fine = fine && total > 0.f && isfinite(total);
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int v = 0; v < 2; ++v)
+          dst[16 * (4 * u + 2 * (grp >> 1) + v)] = ct[i] > 0.f ? cs[2 * u + v][i] / ct[i] : 0.f;
+      if (col == 0 && grp < 2)
+        a.lse[entry * a.hq + head0 + hh] = ct[i] > 0.f ? cm[i] + logf(ct[i]) : -INFINITY;
+    }
   }
+  // The reference's check of the split's combined weight: it fails when no stream of a
+  // head has a finite log-sum-exp (a stream's is finite or -inf).
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+    if (4 * j + grp < G)
+      fine = fine && has[j];
   if (__ballot(!fine) != 0 && lane == 0)
     raise_bad(a.bad);
 }
@@ -853,25 +881,24 @@ template <class T> __global__ __launch_bounds__(64) void k_q8_0_mx_merge(AttnArg
   int n, first;
   if (!attn_window(a, seq, n, first) || (a.local && a.cap != 1024))
     return; // the split kernel raised the flag
-  // Entries e = 4 split + stream, two per lane (e = lane, lane + 64).
-  const int entries = kStreams * min(a.splits, (n + kQ8Tile - 1) / kQ8Tile);
-  const size_t base = (size_t)seq * a.splits * kStreams;
-  const float v0 = lane < entries ? a.lse[(base + lane) * a.hq + head] : -INFINITY;
-  const float v1 = lane + 64 < entries ? a.lse[(base + lane + 64) * a.hq + head] : -INFINITY;
-  float mxv = fmaxf(v0, v1);
+  // One entry per active split (at most 32: lanes 0..31).
+  const int active = min(a.splits, (n + kQ8Tile - 1) / kQ8Tile), l32 = lane & 31;
+  const size_t base = (size_t)seq * a.splits;
+  const float v = l32 < active ? a.lse[(base + l32) * a.hq + head] : -INFINITY;
+  float mxv = v;
 #pragma unroll
-  for (int d = 32; d >= 1; d /= 2)
-    mxv = fmaxf(mxv, __shfl_xor(mxv, d, 64));
-  const float p0 = isfinite(v0) ? expf(v0 - mxv) : 0.f, p1 = isfinite(v1) ? expf(v1 - mxv) : 0.f;
-  float den = p0 + p1;
+  for (int d = 16; d >= 1; d /= 2)
+    mxv = fmaxf(mxv, __shfl_xor(mxv, d, 32));
+  const float p = isfinite(v) ? expf(v - mxv) : 0.f;
+  float den = p;
 #pragma unroll
-  for (int d = 32; d >= 1; d /= 2)
-    den = den + __shfl_xor(den, d, 64);
-  const float w0 = p0 / den, w1 = p1 / den;
+  for (int d = 16; d >= 1; d /= 2)
+    den = den + __shfl_xor(den, d, 32);
+  const float weight = p / den;
   float x0 = 0.f, x1 = 0.f;
-  for (int e = 0; e < entries; ++e) {
-    const float w = e < 64 ? __shfl(w0, e, 64) : __shfl(w1, e - 64, 64);
-    const float *src = a.partial + ((base + e) * a.hq + head) * kD;
+  for (int sp = 0; sp < active; ++sp) {
+    const float w = __shfl(weight, sp, 64);
+    const float *src = a.partial + ((base + sp) * a.hq + head) * kD;
     x0 = __builtin_fmaf(w, src[lane], x0);
     x1 = __builtin_fmaf(w, src[64 + lane], x1);
   }
@@ -904,9 +931,8 @@ extern "C" long long padra_DecodeAttentionScratch(int format, int seqs, int q_he
   if (seqs < 1 || q_heads < 1 || splits < 1 || splits > 32 ||
       (format != PADRA_KV_BF16 && format != PADRA_KV_Q8 && format != PADRA_KV_Q8_0))
     return -1;
-  // partial outputs and log-sum-exps per entry (q8_0: one entry per split and stream)
-  const long long base =
-      (long long)seqs * splits * (format == PADRA_KV_Q8_0 ? kStreams : 1) * q_heads * (kD + 1);
+  // partial outputs and log-sum-exps per split
+  const long long base = (long long)seqs * splits * q_heads * (kD + 1);
   // q8_0: the coded query (128 bytes) and its 4 block scales per head
   return format == PADRA_KV_Q8_0 ? base + (long long)seqs * q_heads * (kD / 4 + 4) : base;
 }
@@ -940,9 +966,9 @@ extern "C" int padra_DecodeAttention(void *stream, const void *q, const padra_KV
   a.kc = static_cast<const uint16_t *>(kv->k);
   a.vc = static_cast<const uint16_t *>(kv->v);
   a.out = out;
-  // scratch: partial [entries][128], coded query [seqs][hq][128] bytes (16-byte aligned),
-  // query block scales [seqs][hq][4], lse [entries]
-  const long long entries = (long long)seqs * splits * (q8 ? kStreams : 1) * q_heads;
+  // scratch: partial [seqs][splits][hq][128], coded query [seqs][hq][128] bytes (16-byte
+  // aligned), query block scales [seqs][hq][4], lse [seqs][splits][hq]
+  const long long entries = (long long)seqs * splits * q_heads;
   a.partial = scratch;
   a.qcodes = reinterpret_cast<int8_t *>(scratch + entries * kD);
   a.qscale = scratch + entries * kD + (long long)seqs * q_heads * (kD / 4);

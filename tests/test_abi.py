@@ -129,8 +129,7 @@ def test_host_validation_newer_entry_points():
                      seq_stride=4096)
     need = lib.padra_DecodeAttentionScratch(abi.KV_BF16, 2, 16, 32)
     assert need == 2 * 32 * 16 * 129
-    # q8_0: four stream entries per split, plus the coded query
-    assert lib.padra_DecodeAttentionScratch(abi.KV_Q8_0, 2, 16, 32) == 4 * need + 2 * 16 * 36
+    assert lib.padra_DecodeAttentionScratch(abi.KV_Q8_0, 2, 16, 32) == need + 2 * 16 * 36
     assert lib.padra_DecodeAttentionScratch(abi.KV_BF16, 2, 16, 33) == -1
     assert lib.padra_DecodeAttentionScratch(abi.KV_Q8, 2, 16, 32) == need
     assert lib.padra_DecodeAttentionScratch(abi.KV_Q8_0_NOROT, 2, 16, 32) == -1
