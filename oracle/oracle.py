@@ -42,6 +42,7 @@ def lib() -> ctypes.CDLL:
             "po_norm_fp8": ([P, P, P, P, P, I, I, F, P, P], None),
             "po_combine": ([P, P, P, I, I, I, I, P], None),
             "po_quantize_fp8": ([P, P, P, I, I, P], None),
+            "po_round_away_mismatches": ([ctypes.c_uint64, ctypes.c_uint64], ctypes.c_ulonglong),
             "po_decode_attention": ([P, P, P, I, I, I, I, I, I, P, P], I),
             "po_decode_attention_q8_0": ([P, P, P, I, I, I, I, I, I, P, P], I),
             "po_kv_checkpoint_plane": ([P, P, P, I, I, I], None),
@@ -203,6 +204,11 @@ def decode_attention_q8_0(q, rows_k, rows_v, position, local=False, splits=0, hk
                                           int(position), int(bool(local)), hq, hkv, int(splits),
                                           _p(out), bad.ptr)
     return out, used, bool(bad)
+
+
+def round_away_mismatches(lo=0, hi=1 << 32):
+    """Floats in bit range [lo, hi) where the GPU's three-instruction roundf differs."""
+    return int(lib().po_round_away_mismatches(lo, hi))
 
 
 def quantize_fp8(x):

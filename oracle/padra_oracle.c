@@ -297,6 +297,20 @@ void po_quantize_fp8(const float *x, uint8_t *packed, float *scales, int rows, i
   }
 }
 
+unsigned long long po_round_away_mismatches(uint64_t lo, uint64_t hi) {
+  unsigned long long bad = 0;
+  for (uint64_t b = lo; b < hi; ++b) {
+    const uint32_t u = (uint32_t)b;
+    float x;
+    memcpy(&x, &u, 4);
+    if (!finite_f(x) || fabsf(x) >= 8388608.f)
+      continue;
+    volatile float s = x + copysignf(0.49999997f, x); /* one float addition, RNE */
+    bad += (int)s != (int)roundf(x);
+  }
+  return bad;
+}
+
 /* ---- Expert combine -------------------------------------------------------------- */
 
 /* inference.cu:580-590; expert_exl3_prefill_packed_activations.cuh:86-102 */

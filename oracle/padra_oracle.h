@@ -68,6 +68,11 @@ void po_norm_fp8(const uint16_t *x, uint16_t *normalized, const uint16_t *gamma,
 void po_quantize_fp8(const float *x, uint8_t *packed, float *scales, int rows, int cols,
                      int *bad);
 
+/* Checker for the GPU's rounding of q8_0 codes: the number of floats with bit patterns in
+ * [lo, hi) (finite, |x| < 2^23) where (int)(x + copysignf(0.49999997f, x)) differs from
+ * (int)roundf(x). */
+unsigned long long po_round_away_mismatches(uint64_t lo, uint64_t hi);
+
 /* ---- Expert combine (+ residual) and combine + RMSNorm (+ FP8) ---------------- */
 /* Combine (inference.cu:580-590) and exl3_packed_activations::Combine
  * (expert_exl3_prefill_packed_activations.cuh:86-102): per row t and column i,

@@ -145,8 +145,13 @@ __device__ __forceinline__ uint32_t q8_code(float value, float scale) {
   return (uint32_t)(c & 0xff);
 }
 // q8_0 code (kv_q8_native.cuh:46-48): roundf (half away from zero) of v * inverse.
+// roundf(v) (half away from zero) is (int)(v + copysign(0.49999997, v)) with the float
+// sum rounded to nearest even and the conversion truncating, for every finite |v| < 2^23
+// (0.49999997 is the float below 0.5; the oracle's po_round_away_mismatches checks all of
+// them): three instructions instead of roundf's seven.
 __device__ __forceinline__ uint32_t q8_0_code(float value, float inverse) {
-  const int c = max(-127, min(127, (int)roundf(value * inverse)));
+  const float v = value * inverse;
+  const int c = max(-127, min(127, (int)(v + __builtin_copysignf(0.49999997f, v))));
   return (uint32_t)(c & 0xff);
 }
 // A 32-byte control record read as eight words issued together: the checks below then

@@ -737,3 +737,11 @@ def test_decode_attention_q8_0_float64(oracle, position, local):
         w = np.exp(s - s.max())
         ref = (w / w.sum()) @ vf[rows, h // g]
         assert np.max(np.abs(got[h] - ref)) <= 0.02 * np.abs(vf).max(), h
+
+
+def test_round_away_identity(oracle):
+    """The GPU rounds q8_0 codes as (int)(v + copysign(0.49999997, v)) in place of roundf:
+    equal on every finite float with |v| < 2^23 (all 2^32 bit patterns scanned, ~10 s), and
+    the plain v + 0.5 it avoids is not (0.49999997 + 0.5 rounds up to 1)."""
+    assert oracle.round_away_mismatches() == 0
+    assert np.float32(0.49999997) + np.float32(0.5) == np.float32(1.0)
