@@ -438,7 +438,7 @@ def _ulp_diff(got_bits, want_bits):
 
 
 @pytest.mark.parametrize("hq,local,splits", [(16, False, 0), (32, False, 0), (16, True, 0),
-                                             (16, False, 5)])
+                                             (16, False, 5), (4, False, 0), (8, True, 0)])
 def test_decode_attention(oracle, hq, local, splits):
     """Ragged decode batch against the oracle's attention at each sequence's position,
     within the _attn_close tolerance (the reference's tensor-core order and CUDA expf/logf
@@ -508,7 +508,8 @@ def test_decode_attention_f32_and_invalid(oracle):
         assert _attn_close(synth.bf16_bits(got[s]), want)[0].all()
 
 
-@pytest.mark.parametrize("hq,local", [(16, False), (32, False), (16, True)])
+@pytest.mark.parametrize("hq,local", [(16, False), (32, False), (16, True), (4, False),
+                                      (8, True)])
 def test_decode_attention_q8_0(oracle, hq, local):
     """q8_0 caches (rotated v2) against the oracle's EncodeQuery/Split/Merge, within the
     _attn_close tolerance (CUDA expf/logf against any other implementation)."""
@@ -547,13 +548,13 @@ def test_decode_attention_q8_0(oracle, hq, local):
     print(f"  max BF16 ulp difference {worst}", flush=True)
 
 
-@pytest.mark.parametrize("local", [False, True])
-def test_decode_attention_q8(oracle, local):
+@pytest.mark.parametrize("hq,local", [(16, False), (16, True), (4, False), (8, True)])
+def test_decode_attention_q8(oracle, hq, local):
     """q8 caches (per-head fp32 scale): the split reads bf16(code * scale) rows
     (kv_q8::Decode), so the oracle is the BF16 attention over the decoded cache; within the
     _attn_close tolerance."""
-    print(f"[case] decode attention q8 local={local}", flush=True)
-    seqs, hq, hkv, capacity = 4, 16, 4, 4096
+    print(f"[case] decode attention q8 hq={hq} local={local}", flush=True)
+    seqs, hkv, capacity = 4, 4, 4096
     cap = 1024 if local else capacity
     rng = np.random.default_rng(130 + local)
     positions = rng.integers(0, capacity, seqs).astype(np.int32)
