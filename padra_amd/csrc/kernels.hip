@@ -19,6 +19,9 @@ using namespace padra;
 // Occupancy hint for the Q/K and chain kernels.  Forcing 4 waves per SIMD (<= 128 VGPRs)
 // makes the compiler spill the Q/K working set to scratch; measured on MI355X, the
 // unconstrained allocation (2-3 waves per SIMD) is 20% faster for a 2048-token chunk.
+#ifndef PADRA_CHAIN_ORDER
+#define PADRA_CHAIN_ORDER 0
+#endif
 #ifndef PADRA_WAVES_PER_EU
 #define PADRA_WAVES_PER_EU
 #endif
@@ -94,10 +97,18 @@ template <int VT, int J, int FMT>
 __global__ __launch_bounds__(64) PADRA_WAVES_PER_EU void k_chain(NormArgs<uint16_t> n, QKArgs<uint16_t> q,
                                               long long norm_waves, long long waves) {
   const long long b = blockIdx.x;
+#if PADRA_CHAIN_ORDER == 1
+  const long long qw = waves - norm_waves;
+  if (b < qw)
+    qk_heads_wave<uint16_t, FMT>(q, b);
+  else if (b < waves)
+    norm_row_wave<VT, J, uint16_t, true>(n, (int)(b - qw));
+#else
   if (b < norm_waves)
     norm_row_wave<VT, J, uint16_t, true>(n, (int)b);
   else if (b < waves)
     qk_heads_wave<uint16_t, FMT>(q, b - norm_waves);
+#endif
 }
 
 // Launch tuning (padra_Tune): waves per CU for the pipelined row kernel, 0 = one wave

@@ -218,8 +218,8 @@ __device__ __forceinline__ void norm_compute(const NormArgs<T> &a, int row,
     uint32_t out[K / 2];
 #pragma unroll
     for (int w = 0; w < K / 2; ++w) {
-      const uint32_t p = pack2(lo16(vp[j][w]) * inv, hi16(vp[j][w]) * inv);
-      const float y0 = lo16(p) * gr[j].get(2 * w), y1 = hi16(p) * gr[j].get(2 * w + 1);
+      const float y0 = B(lo16(vp[j][w]) * inv) * gr[j].get(2 * w);
+      const float y1 = B(hi16(vp[j][w]) * inv) * gr[j].get(2 * w + 1);
       if constexpr (CHECK_Y)
         fine = fine && bf16_finite_after_round(y0) && bf16_finite_after_round(y1);
       out[w] = pack2(y0, y1);

@@ -277,8 +277,11 @@ template <> struct Act32<float> {
 struct Bf8 {
   uint4 w;
   __device__ __forceinline__ void load(const uint16_t *p) { w = *reinterpret_cast<const uint4 *>(p); }
+  __device__ __forceinline__ uint32_t word(int i) const {
+    return i == 0 ? w.x : i == 1 ? w.y : i == 2 ? w.z : w.w;
+  }
   __device__ __forceinline__ float get(int i) const {
-    const uint32_t v = (i / 2) == 0 ? w.x : (i / 2) == 1 ? w.y : (i / 2) == 2 ? w.z : w.w;
+    const uint32_t v = word(i / 2);
     return i & 1 ? hi16(v) : lo16(v);
   }
 };

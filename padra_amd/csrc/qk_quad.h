@@ -6,7 +6,7 @@
 //  - The tree over the four warp partials, (w0 + w2) + (w1 + w3), is two DPP quad
 //    exchanges (lanes g^2, then g^1), then a broadcast from lane g = 0.
 //  - RoPE pairs feature f < 64 with f + 64, i.e. lane g with lane g^2: the partner's
-//    normalized values arrive packed, sixteen DPP moves per lane.
+//    normalized values arrive by DPP, one move per feature.
 // Loads and stores of the 4 KB block are four coalesced 1 KB instructions, transposed
 // through LDS as in the lane-pair path.
 #pragma once
@@ -269,27 +269,24 @@ __device__ __forceinline__ void qk_heads_wave_quad(const QKArgs<uint16_t> &a, lo
     }
     const float sum = fquad_first(S + E);
     const float inv = 1.f / sqrtf(sum / (float)D + a.eps);
-    // Normalized group, packed: A = B(B(x * inv) * w) (qk_rope_store_exact.cuh:39).
-    uint32_t an[16];
+    // Normalized group: A = B(B(x * inv) * w) (qk_rope_store_exact.cuh:39), as floats.
+    float an[32];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const uint32_t p1 = pack2(x.get(2 * i) * inv, x.get(2 * i + 1) * inv);
-      an[i] = pack2(lo16(p1) * w8[i / 4].get((2 * i) & 7), hi16(p1) * w8[i / 4].get((2 * i + 1) & 7));
-    }
-    // Partner group (features f +- 64): lower lanes rotate lo = A c - P s, upper lanes
-    // hi = A c + P s (c, s of the pair index).
-    // B(-P s) = -B(P s): the lower lanes flip the partner's sign bits.
+    for (int f = 0; f < 32; ++f)
+      an[f] = B(B(x.get(f) * inv) * w8[f / 8].get(f & 7));
+    // Partner group (features f +- 64, lane g ^ 2): lower lanes rotate lo = A c - P s,
+    // upper lanes hi = A c + P s (c, s of the pair index).  B(-P s) = B(P (-s)): the lower
+    // lanes flip the sign bits of their s words.
     const uint32_t sgn = g < 2 ? 0x80008000u : 0u;
     bool fine = isfinite(sum);
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      const uint32_t pw = quad_xor2(an[i]) ^ sgn;
       const int k0 = 2 * i, k1 = 2 * i + 1;
       const float c0 = c8[k0 / 8].get(k0 & 7), c1 = c8[k1 / 8].get(k1 & 7);
-      const float s0 = s8[k0 / 8].get(k0 & 7), s1 = s8[k1 / 8].get(k1 & 7);
-      const uint32_t p3 = pack2(lo16(an[i]) * c0, hi16(an[i]) * c1);
-      const uint32_t p4 = pack2(lo16(pw) * s0, hi16(pw) * s1);
-      const float r0 = lo16(p3) + lo16(p4), r1 = hi16(p3) + hi16(p4);
+      const uint32_t sword = s8[k0 / 8].word((k0 & 7) / 2) ^ sgn;
+      const float s0 = lo16(sword), s1 = hi16(sword);
+      const float r0 = B(an[k0] * c0) + B(fquad_xor2(an[k0]) * s0);
+      const float r1 = B(an[k1] * c1) + B(fquad_xor2(an[k1]) * s1);
       fine = fine && bf16_finite_after_round(r0) && bf16_finite_after_round(r1);
       out[i] = pack2(r0, r1);
     }
