@@ -134,6 +134,14 @@ __device__ __forceinline__ bool bf16_finite(float x) {
   return fabsf(x) < __uint_as_float(0x7f7f8000u);
 }
 
+// Ring slot of a non-negative position: the division runs only when the position has
+// wrapped (pos >= cap), which a global cache (cap = capacity > pos) never does.
+__device__ __forceinline__ int ring_slot(int pos, int cap) {
+  if (pos >= cap)
+    pos %= cap;
+  return pos;
+}
+
 // Sets the caller's sticky error flag (reference: atomicExch(bad, 1)).
 __device__ __forceinline__ void raise_bad(int *bad) {
   if (bad)

@@ -19,9 +19,6 @@ using namespace padra;
 // Occupancy hint for the Q/K and chain kernels.  Forcing 4 waves per SIMD (<= 128 VGPRs)
 // makes the compiler spill the Q/K working set to scratch; measured on MI355X, the
 // unconstrained allocation (2-3 waves per SIMD) is 20% faster for a 2048-token chunk.
-#ifndef PADRA_CHAIN_ORDER
-#define PADRA_CHAIN_ORDER 0
-#endif
 #ifndef PADRA_WAVES_PER_EU
 #define PADRA_WAVES_PER_EU
 #endif
@@ -92,23 +89,16 @@ template <int J, class T> __global__ __launch_bounds__(64) void k_norm_fp8(NormF
 // Residual-norm waves first, then the Q/K waves.  Measured on MI355X for a 2048-token
 // chunk, this order is 10% faster than spreading the norm rows evenly over the grid
 // (Bresenham interleave) or over its first half: the early grid streams the four norm
-// tensors alone, and the VALU-heavier Q/K waves follow as norm waves retire.
+// tensors alone, and the VALU-heavier Q/K waves follow as norm waves retire.  Putting the
+// Q/K waves first measured 15% slower.
 template <int VT, int J, int FMT>
 __global__ __launch_bounds__(64) PADRA_WAVES_PER_EU void k_chain(NormArgs<uint16_t> n, QKArgs<uint16_t> q,
                                               long long norm_waves, long long waves) {
   const long long b = blockIdx.x;
-#if PADRA_CHAIN_ORDER == 1
-  const long long qw = waves - norm_waves;
-  if (b < qw)
-    qk_heads_wave<uint16_t, FMT>(q, b);
-  else if (b < waves)
-    norm_row_wave<VT, J, uint16_t, true>(n, (int)(b - qw));
-#else
   if (b < norm_waves)
     norm_row_wave<VT, J, uint16_t, true>(n, (int)b);
   else if (b < waves)
     qk_heads_wave<uint16_t, FMT>(q, b - norm_waves);
-#endif
 }
 
 // Launch tuning (padra_Tune): waves per CU for the pipelined row kernel, 0 = one wave

@@ -42,21 +42,36 @@ __device__ __forceinline__ void v_rows_copy16(const A &a, unsigned block0, unsig
                                               unsigned nk) {
   constexpr int D = 128;
   const int lane = threadIdx.x & 63, features = a.hkv * D;
+  // Piece m of this lane is chunk (lane & 15) of head 4m + (lane >> 4) of the block; its
+  // (token, KV head) pair advances by 4 heads per piece, without a division.
+  const unsigned idx0 = block0 - nq - nk + (unsigned)(lane >> 4);
+  const unsigned hk = (unsigned)a.hkv;
+  unsigned tm[4], hm[4];
+  tm[0] = idx0 / hk;
+  hm[0] = idx0 - tm[0] * hk;
+#pragma unroll
+  for (int m = 1; m < 4; ++m) {
+    tm[m] = tm[m - 1];
+    hm[m] = hm[m - 1] + 4u;
+    while (hm[m] >= hk) {
+      hm[m] -= hk;
+      ++tm[m];
+    }
+  }
   uint4 d[4];
   PosState ps[4];
 #pragma unroll
   for (int m = 0; m < 4; ++m) {
-    const unsigned idx = min(block0 + (unsigned)((64 * m + lane) >> 4) - nq - nk, nk - 1u);
-    ps[m] = fetch_state(a.pos, (int)(idx / (unsigned)a.hkv));
-    d[m] = ld_nt(reinterpret_cast<const uint4 *>(a.v + (size_t)idx * D) + ((64 * m + lane) & 15));
+    const unsigned idx = min(idx0 + 4u * m, nk - 1u);
+    ps[m] = fetch_state(a.pos, (int)min(tm[m], (unsigned)a.tokens - 1u));
+    d[m] = ld_nt(reinterpret_cast<const uint4 *>(a.v + (size_t)idx * D) + (lane & 15));
   }
 #pragma unroll
   for (int m = 0; m < 4; ++m) {
-    const int c = 64 * m + lane;
-    const unsigned idx = block0 + (unsigned)(c >> 4) - nq - nk;
+    const unsigned idx = idx0 + 4u * m;
     if (idx >= nk)
       continue;
-    const int t = (int)(idx / (unsigned)a.hkv), h = (int)(idx % (unsigned)a.hkv), ci = c & 15;
+    const int t = (int)tm[m], h = (int)hm[m], ci = lane & 15;
     bool ok;
     const int pos = resolve_position(a.pos, ps[m], t, a.cap, a.first, false, ok);
     if (!ok || pos < 0 || pos >= a.table_rows) {
@@ -67,7 +82,7 @@ __device__ __forceinline__ void v_rows_copy16(const A &a, unsigned block0, unsig
     if (t < a.first)
       continue;
     const long long seq = a.pos.mode == PADRA_POS_DECODE ? t : 0;
-    const long long slot = seq * a.seq_stride + pos % a.cap;
+    const long long slot = seq * a.seq_stride + ring_slot(pos, a.cap);
     st_nt(reinterpret_cast<uint4 *>(static_cast<uint16_t *>(a.vc) + slot * features + h * D) + ci, d[m]);
   }
 }
@@ -195,7 +210,10 @@ template <int FMT>
 __device__ __forceinline__ void qk_heads_wave_quad(const QKArgs<uint16_t> &a, long long wave) {
   constexpr int D = 128;
   __shared__ uint4 stage[256];
-  __shared__ int head_pos[16]; // per head of the block: cache position, -1 = write nothing
+  // Per head of the block: 1 = write the activation, 0 = write nothing; and the element
+  // offset of its BF16 cache row (-1 = no cache write).
+  __shared__ int head_live[16];
+  __shared__ long long head_row[16];
   const int lane = threadIdx.x & 63, g = lane & 3;
   const unsigned block0 = (unsigned)wave * 16u;
   const unsigned nq = (unsigned)a.tokens * (unsigned)a.hq;
@@ -297,7 +315,7 @@ __device__ __forceinline__ void qk_heads_wave_quad(const QKArgs<uint16_t> &a, lo
     // K heads encode their rotated values, V heads their inputs (quad-uniform roles).
     const bool enc = live && ok && role >= 1 && t >= a.first;
     const long long seq = a.pos.mode == PADRA_POS_DECODE ? t : 0;
-    const long long slot = seq * a.seq_stride + (ok ? pos % max(a.cap, 1) : 0);
+    const long long slot = seq * a.seq_stride + (ok ? ring_slot(pos, max(a.cap, 1)) : 0);
     uint32_t w16[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i)
@@ -316,39 +334,35 @@ __device__ __forceinline__ void qk_heads_wave_quad(const QKArgs<uint16_t> &a, lo
       stage[quad_slot(lane, p)] = make_uint4(out[4 * p], out[4 * p + 1], out[4 * p + 2], out[4 * p + 3]);
   }
   const bool vcopy = FMT == PADRA_KV_BF16 && live && ok && role == 2 && t >= a.first;
-  if (g == 0)
-    head_pos[lane >> 2] = (qk || vcopy) ? pos : -1;
-  __syncthreads();
   const int features = a.hkv * D;
+  if (g == 0) {
+    head_live[lane >> 2] = (qk || vcopy) ? 1 : 0;
+    long long r = -1;
+    if (FMT == PADRA_KV_BF16 && live && ok && role >= 1 && t >= a.first) {
+      const long long seq = a.pos.mode == PADRA_POS_DECODE ? t : 0;
+      r = (seq * a.seq_stride + ring_slot(pos, a.cap)) * features + hh * D;
+    }
+    head_row[lane >> 2] = r;
+  }
+  __syncthreads();
 #pragma unroll
   for (int m = 0; m < 4; ++m) {
     const int c = 64 * m + lane, j = c >> 4, ci = c & 15;
     const unsigned hc = block0 + (unsigned)j;
-    const int hp = head_pos[j];
-    if (hp < 0)
+    if (!head_live[j])
       continue; // past the end, or a head that writes nothing
     const uint4 d = stage[quad_slot(4 * j + (ci >> 2), ci & 3)];
     if constexpr (FMT == PADRA_KV_BF16) {
+      const long long r = head_row[j];
       if (hc >= nq + nk) { // V head: cache only
-        const unsigned vi = hc - nq - nk;
-        const int tc = (int)(vi / (unsigned)a.hkv), hh = (int)(vi % (unsigned)a.hkv);
-        const long long sq = a.pos.mode == PADRA_POS_DECODE ? tc : 0;
-        const long long sl = sq * a.seq_stride + hp % a.cap;
-        st_nt(reinterpret_cast<uint4 *>(static_cast<uint16_t *>(a.vc) + sl * features + hh * D) + ci, d);
+        st_nt(reinterpret_cast<uint4 *>(static_cast<uint16_t *>(a.vc) + r) + ci, d);
         continue;
       }
-    }
-    st_nt(reinterpret_cast<uint4 *>(const_cast<uint16_t *>(head_src(a, hc, nq, nk))) + ci, d);
-    if constexpr (FMT == PADRA_KV_BF16) {
-      if (hc >= nq) {
-        const unsigned kvi = hc - nq;
-        const int tc = (int)(kvi / (unsigned)a.hkv), hh = (int)(kvi % (unsigned)a.hkv);
-        if (tc >= a.first) {
-          const long long sq = a.pos.mode == PADRA_POS_DECODE ? tc : 0;
-          const long long sl = sq * a.seq_stride + hp % a.cap;
-          st_nt(reinterpret_cast<uint4 *>(static_cast<uint16_t *>(a.kc) + sl * features + hh * D) + ci, d);
-        }
-      }
+      st_nt(reinterpret_cast<uint4 *>(const_cast<uint16_t *>(head_src(a, hc, nq, nk))) + ci, d);
+      if (r >= 0)
+        st_nt(reinterpret_cast<uint4 *>(static_cast<uint16_t *>(a.kc) + r) + ci, d);
+    } else {
+      st_nt(reinterpret_cast<uint4 *>(const_cast<uint16_t *>(head_src(a, hc, nq, nk))) + ci, d);
     }
   }
 }
