@@ -236,7 +236,7 @@ __device__ __forceinline__ void qk_heads_wave_quad(const QKArgs<uint16_t> &a, lo
   const int hh = live ? (int)(idx - (unsigned)t * heads) : 0;
   const PosState ps = fetch_state(a.pos, t);
 
-  // 1. Four coalesced loads per lane (clamped, unconditional), into the LDS image.
+  // 1. Four coalesced loads per lane (clamped, unconditional), for the LDS image.
   uint4 in[4];
 #pragma unroll
   for (int m = 0; m < 4; ++m) {
@@ -244,13 +244,8 @@ __device__ __forceinline__ void qk_heads_wave_quad(const QKArgs<uint16_t> &a, lo
     const unsigned hc = min(block0 + (unsigned)(c >> 4), total - 1u);
     in[m] = ld_nt(reinterpret_cast<const uint4 *>(head_src(a, hc, nq, nk)) + (c & 15));
   }
-#pragma unroll
-  for (int m = 0; m < 4; ++m) {
-    const int c = 64 * m + lane;
-    stage[quad_slot(4 * (c >> 4) + ((c & 15) >> 2), c & 3)] = in[m];
-  }
-
-  // 2. The head's position.
+  // 2. The head's position (its control record was requested first), then the weight and
+  // table loads, so that they are in flight with the data loads.
   bool ok = false;
   int pos = resolve_position(a.pos, ps, t, FMT >= 0 ? a.cap : 0, a.first, FMT > PADRA_KV_BF16,
                              ok);
@@ -266,6 +261,12 @@ __device__ __forceinline__ void qk_heads_wave_quad(const QKArgs<uint16_t> &a, lo
     w8[m].load(wsrc + 8 * m);
     c8[m].load(row + 8 * m);
     s8[m].load(row + 64 + 8 * m);
+  }
+  // 3. The data into the image.
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const int c = 64 * m + lane;
+    stage[quad_slot(4 * (c >> 4) + ((c & 15) >> 2), c & 3)] = in[m];
   }
   __syncthreads();
   Act32<uint16_t> x;
@@ -327,7 +328,7 @@ __device__ __forceinline__ void qk_heads_wave_quad(const QKArgs<uint16_t> &a, lo
   }
   __syncthreads(); // every lane has read its input pieces: the image can be overwritten
 
-  // 3. Outputs back into the image, then four coalesced stores per lane.
+  // 4. Outputs back into the image, then four coalesced stores per lane.
   if (qk) {
 #pragma unroll
     for (int p = 0; p < 4; ++p)
