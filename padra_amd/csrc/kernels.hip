@@ -42,10 +42,11 @@ template <class T, int FMT> __global__ __launch_bounds__(64) PADRA_WAVES_PER_EU 
 }
 
 // Self-check of the two fast-path identities, over their whole domains:
-//   A. e4m3_pair_hw(x) == e4m3_code(x) for every float with |x| <= 480 (2.28e9 inputs);
+//   A. e4m3_pair_hw(x) == e4m3_code(x) for every float with |x| <= 480 (2.28e9 inputs),
+//      and the unclamped e4m3_pair_fast(x) == e4m3_code(x) for |x| <= 460;
 //   B. for every BF16 maximum m >= 2^-100 (scale = m/448, inverse normal) and every BF16
-//      v with |v| <= m, both signs: code of fp8_quotient == code of the correctly rounded
-//      division (2.1e9 pairs).
+//      v with |v| <= m, both signs: the code of fp8_quotient, through either conversion,
+//      == the code of the correctly rounded division (2.1e9 pairs).
 // Mismatches are added to counts[0] (A) and counts[1] (B).
 __global__ __launch_bounds__(256) void k_check_fp8_hw(unsigned long long n,
                                                       unsigned long long *counts) {
@@ -54,7 +55,10 @@ __global__ __launch_bounds__(256) void k_check_fp8_hw(unsigned long long n,
   for (unsigned long long i = blockIdx.x * (unsigned long long)blockDim.x + threadIdx.x; i < n;
        i += stride) {
     const float x = __uint_as_float((uint32_t)(i >> 1) | ((uint32_t)(i & 1) << 31));
-    bad += (e4m3_pair_hw(x, 0.f) & 0xffu) != e4m3_code(x);
+    const uint32_t code = e4m3_code(x);
+    bad += (e4m3_pair_hw(x, 0.f) & 0xffu) != code;
+    if ((__float_as_uint(x) & 0x7fffffffu) <= 0x43e60000u) // |x| <= 460
+      bad += (e4m3_pair_fast(x, 0.f) & 0xffu) != code;
   }
   if (bad)
     atomicAdd(&counts[0], bad);
@@ -70,7 +74,9 @@ __global__ __launch_bounds__(256) void k_check_fp8_quotient(unsigned long long *
 #pragma unroll
     for (int sg = 0; sg < 2; ++sg) {
       const float v = __uint_as_float((vb << 16) | (sg ? 0x80000000u : 0u));
-      bad += (e4m3_pair_hw(fp8_quotient(v, scale, inverse), 0.f) & 0xffu) != e4m3_code(v / scale);
+      const float q = fp8_quotient(v, scale, inverse);
+      const uint32_t code = e4m3_code(v / scale);
+      bad += ((e4m3_pair_hw(q, 0.f) & 0xffu) != code) + ((e4m3_pair_fast(q, 0.f) & 0xffu) != code);
     }
   }
   if (bad)

@@ -11,6 +11,8 @@
 //              it is computed here
 // The maximum is order-independent, so the wave reduces it with any exchange pattern.
 #pragma once
+#include <type_traits>
+
 #include "norm_rows.h"
 
 namespace padra {
@@ -53,6 +55,15 @@ __device__ __forceinline__ uint32_t e4m3_pair_hw(float q0, float q1) {
                                                    false) & 0xffffu;
 }
 
+// The same conversion without the clamp, for the row fast path: there |q| is within one
+// ulp of |y| / scale <= amax / RN(amax / 448) < 448.001, which the conversion rounds to
+// at most 448 (the overflow threshold is 464).  padra_CheckFP8Paths compares it with
+// e4m3_code on every float up to 460 and, through fp8_quotient, on every BF16 (maximum,
+// value) pair of the fast path.
+__device__ __forceinline__ uint32_t e4m3_pair_fast(float q0, float q1) {
+  return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(q0, q1, 0, false) & 0xffffu;
+}
+
 // The quotient v / scale from the cached reciprocal plus one exact-remainder correction:
 // q = v * inverse, r = v - q * scale (one fused multiply-add), q + r * inverse, with v's
 // sign restored (a zero v would otherwise come back +0).  For BF16 v and a scale derived
@@ -81,8 +92,8 @@ __device__ __forceinline__ void fp8_encode_pairs(const uint32_t (&w)[J], float s
 #pragma unroll
   for (int j = 0; j < J; ++j) {
     if constexpr (FAST)
-      codes[j] = e4m3_pair_hw(fp8_quotient(lo16(w[j]), scale, inverse),
-                              fp8_quotient(hi16(w[j]), scale, inverse));
+      codes[j] = e4m3_pair_fast(fp8_quotient(lo16(w[j]), scale, inverse),
+                                fp8_quotient(hi16(w[j]), scale, inverse));
     else
       codes[j] = e4m3_code(lo16(w[j]) / scale) | (e4m3_code(hi16(w[j]) / scale) << 8);
   }
@@ -124,8 +135,7 @@ __device__ __forceinline__ void norm_fp8_finish(const NormFP8Args<T> &a, int row
   u16x2_t mag2 = {0, 0};
 #pragma unroll
   for (int j = 0; j < J; ++j) {
-    const uint32_t p = pack2(lo16(vp[j]) * inv, hi16(vp[j]) * inv);
-    yw[j] = pack2(lo16(p) * gr[j].get(0), hi16(p) * gr[j].get(1));
+    yw[j] = pack2(B(lo16(vp[j]) * inv) * gr[j].get(0), B(hi16(vp[j]) * inv) * gr[j].get(1));
     mag2 = __builtin_elementwise_max(mag2, __builtin_bit_cast(u16x2_t, yw[j] & 0x7fff7fffu));
     Lanes<T, K>::store(a.y + off + VT * j, &yw[j]);
   }
@@ -185,8 +195,12 @@ __device__ __forceinline__ void norm_fp8_row_wave(const NormFP8Args<T> &a, int r
   // Thread 2l+k owns elements 2l + k + 128 j, summed in j order.
   uint32_t vp[J];
 #pragma unroll
-  for (int j = 0; j < J; ++j)
-    vp[j] = pack2(x[j].get(0), x[j].get(1));
+  for (int j = 0; j < J; ++j) {
+    if constexpr (std::is_same<T, uint16_t>::value)
+      vp[j] = x[j].w[0]; // BF16 input: the pair is the loaded word
+    else
+      vp[j] = pack2(x[j].get(0), x[j].get(1));
+  }
   norm_fp8_finish<J, T, true>(a, row, vp, gr);
 }
 
