@@ -65,14 +65,16 @@ __device__ __forceinline__ uint32_t e4m3_pair_fast(float q0, float q1) {
 }
 
 // The quotient v / scale from the cached reciprocal plus one exact-remainder correction:
-// q = v * inverse, r = v - q * scale (one fused multiply-add), q + r * inverse, with v's
-// sign restored (a zero v would otherwise come back +0).  For BF16 v and a scale derived
-// from a BF16 maximum of at least 2^-100 (inverse normal), its E4M3 code equals the code of
-// the correctly rounded quotient for every such pair, as padra_CheckFP8Paths verifies.
+// q = v * inverse, r = q * scale - v (one fused multiply-add), q - r * inverse.  Written
+// with r of that sign, a zero v keeps its sign through both steps (-0: q = -0, r = +0,
+// -0 * inverse + -0 = -0), and the negations are free operand modifiers.  For BF16 v and
+// a scale derived from a BF16 maximum of at least 2^-100 (inverse normal), its E4M3 code
+// equals the code of the correctly rounded quotient for every such pair, as
+// padra_CheckFP8Paths verifies.
 __device__ __forceinline__ float fp8_quotient(float v, float scale, float inverse) {
   const float q = v * inverse;
-  const float r = __builtin_fmaf(-q, scale, v);
-  return __builtin_copysignf(__builtin_fmaf(r, inverse, q), v);
+  const float r = __builtin_fmaf(q, scale, -v);
+  return __builtin_fmaf(-r, inverse, q);
 }
 
 // Whether a row may take the fast path: finite values, maximum >= 2^-100, normal inverse.
