@@ -287,6 +287,13 @@ long long padra_DecodeAttentionScratch(int format, int seqs, int q_heads, int sp
  * (device memory, 2 x u64; both 0 when the fast path is exact).  About 4.4e9 evaluations,
  * a few milliseconds. */
 int padra_CheckFP8Paths(void *stream, unsigned long long *counts);
+/* padra_CheckQ8Path: no counterpart in the reference.  Checks the reciprocal form of the q8
+ * KV code (kv_q8::Encode's RNE(x / scale), kv_q8.cuh:12-14) that the store kernels use on
+ * heads whose scale is at least 2^-100: for every such BF16 maximum and every BF16
+ * value up to it, both signs, the code equals the correctly rounded division's.  Writes the
+ * mismatch count to counts[0] (device memory, u64; 0 when exact).  About 2.1e9
+ * evaluations, a few milliseconds. */
+int padra_CheckQ8Path(void *stream, unsigned long long *counts);
 /* ---- launch tuning ------------------------------------------------------------------
  * No counterpart in the reference (its launch shapes are fixed).  Process-wide launch
  * parameters for measurement sweeps; defaults need no call.

@@ -80,6 +80,7 @@ SIGNATURES = {
     "padra_KvQ8_0DequantizePrefix": [_P, _P, _P, _P, _P, ctypes.POINTER(Positions), _I, _I, _I,
                                      _P],
     "padra_CheckFP8Paths": [_P, _P],
+    "padra_CheckQ8Path": [_P, _P],
     "padra_DecodeAttentionScratch": [_I, _I, _I, _I],
     "padra_DecodeAttention": [_P, _P, ctypes.POINTER(KVCache), _P, ctypes.POINTER(Positions), _I,
                               _I, _I, _I, _I, _P, ctypes.c_longlong, _P, _I],

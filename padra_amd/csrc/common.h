@@ -153,6 +153,21 @@ __device__ __forceinline__ uint32_t q8_code(float value, float scale) {
   const int c = max(-127, min(127, (int)rintf(value / scale)));
   return (uint32_t)(c & 0xff);
 }
+// The same code through the head's cached reciprocal: q = v * inverse, r = q * scale - v
+// (one fused multiply-add), q - r * inverse, then RNE and the clamp; three instructions
+// where the correctly rounded division takes ten.  For every BF16 value v with |v| <= amax,
+// amax a BF16 maximum whose scale = amax / 127 is at least 2^-100 (q8_fast_ok: then r,
+// whose size is about 2^-24 |v|, loses at most 2^-150 to the subnormal range, which moves
+// q - r * inverse by at most 2^-43), its code equals q8_code's: padra_CheckQ8Path compares
+// the two on every such (amax, v) pair on the device.  With smaller scales the two differ
+// (a scale of 2^-125 puts an exact 63.5 quotient at 63.499996).
+__device__ __forceinline__ uint32_t q8_code_fast(float value, float scale, float inverse) {
+  const float q = value * inverse;
+  const float r = __builtin_fmaf(q, scale, -value);
+  const int c = max(-127, min(127, (int)rintf(__builtin_fmaf(-r, inverse, q))));
+  return (uint32_t)(c & 0xff);
+}
+__device__ __forceinline__ bool q8_fast_ok(float scale) { return scale >= 0x1p-100f; }
 // q8_0 code (kv_q8_native.cuh:46-48): roundf (half away from zero) of v * inverse.
 // roundf(v) (half away from zero) is (int)(v + copysign(0.49999997, v)) with the float
 // sum rounded to nearest even and the conversion truncating, for every finite |v| < 2^23

@@ -352,6 +352,37 @@ extern "C" int padra_NormFP8(void *stream, const void *x, void *normalized,
   return act == PADRA_ACT_BF16 ? launch(uint16_t{}) : launch(float{});
 }
 
+// Device self-check of q8_code_fast: for every positive finite BF16 maximum amax whose
+// scale amax / 127 passes q8_fast_ok (scale >= 2^-100), and every BF16 v with
+// |v| <= amax (both signs), the code through the reciprocal equals the code of the correctly rounded quotient
+// (2.1e9 pairs).  Mismatches are added to counts[0].
+__global__ __launch_bounds__(256) void k_check_q8(unsigned long long *counts) {
+  const uint32_t mb = blockIdx.x + 1; // BF16 bits of the maximum, 0x0001 .. 0x7f7f
+  const float amax = __uint_as_float(mb << 16);
+  const float scale = amax / 127.f, inverse = 1.f / scale;
+  if (!q8_fast_ok(scale))
+    return; // block-uniform
+  unsigned long long bad = 0;
+  for (uint32_t vb = threadIdx.x; vb <= mb; vb += blockDim.x) {
+#pragma unroll
+    for (int sg = 0; sg < 2; ++sg) {
+      const float v = __uint_as_float((vb << 16) | (sg ? 0x80000000u : 0u));
+      bad += q8_code_fast(v, scale, inverse) != q8_code(v, scale);
+    }
+  }
+  if (bad)
+    atomicAdd(&counts[0], bad);
+}
+
+extern "C" int padra_CheckQ8Path(void *stream, unsigned long long *counts) {
+  if (!counts)
+    return PADRA_INVALID_ARGUMENT;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(k_zero_u64, dim3(1), dim3(64), 0, s, counts, 1);
+  hipLaunchKernelGGL(k_check_q8, dim3(0x7f7f), dim3(256), 0, s, counts);
+  return launched();
+}
+
 extern "C" int padra_CheckFP8Paths(void *stream, unsigned long long *counts) {
   if (!counts)
     return PADRA_INVALID_ARGUMENT;

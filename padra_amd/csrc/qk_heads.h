@@ -145,14 +145,16 @@ __device__ __forceinline__ void encode_head_q(const A &a, float (&xa)[32], float
     m = fmaxf(m, shfl_xor(m, 1));
     const float scale = m == 0.f ? 1.f : m / 127.f;
     int8_t *codes = static_cast<int8_t *>(ISV ? a.vc : a.kc) + slot * features + h * D;
+    const float inverse = 1.f / scale;
+    const bool fast = q8_fast_ok(scale); // pair-uniform
     uint32_t w0[8], w1[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       w0[i] = w1[i] = 0u;
 #pragma unroll
       for (int b = 0; b < 4; ++b) {
-        w0[i] |= q8_code(xa[4 * i + b], scale) << (8 * b);
-        w1[i] |= q8_code(xb[4 * i + b], scale) << (8 * b);
+        w0[i] |= (fast ? q8_code_fast(xa[4 * i + b], scale, inverse) : q8_code(xa[4 * i + b], scale)) << (8 * b);
+        w1[i] |= (fast ? q8_code_fast(xb[4 * i + b], scale, inverse) : q8_code(xb[4 * i + b], scale)) << (8 * b);
       }
     }
     store_codes32(codes + 32 * half, w0);

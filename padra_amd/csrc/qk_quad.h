@@ -142,13 +142,23 @@ __device__ __forceinline__ void encode_quad(const QKArgs<uint16_t> &a, const uin
         raise_bad(a.bad);
       return;
     }
-    const float scale = m == 0.f ? 1.f : m / 127.f;
+    const float scale = m == 0.f ? 1.f : m / 127.f, inverse = 1.f / scale;
+    if (q8_fast_ok(scale)) { // quad-uniform
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      cw[i] = 0u;
+      for (int i = 0; i < 8; ++i) {
+        cw[i] = 0u;
 #pragma unroll
-      for (int b = 0; b < 4; ++b)
-        cw[i] |= q8_code(x[4 * i + b], scale) << (8 * b);
+        for (int b = 0; b < 4; ++b)
+          cw[i] |= q8_code_fast(x[4 * i + b], scale, inverse) << (8 * b);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        cw[i] = 0u;
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+          cw[i] |= q8_code(x[4 * i + b], scale) << (8 * b);
+      }
     }
     int8_t *codes = static_cast<int8_t *>(ISV ? a.vc : a.kc) + slot * features + h * D + 32 * g;
     st_nt(reinterpret_cast<uint4 *>(codes), make_uint4(cw[0], cw[1], cw[2], cw[3]));

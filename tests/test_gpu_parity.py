@@ -165,6 +165,17 @@ def test_fp8_fast_path_identities_exhaustive():
     assert counts.tolist() == [0, 0]
 
 
+def test_q8_reciprocal_code_exhaustive():
+    """The q8 KV code through the scale's reciprocal (the store kernels' form) equals the
+    code of the correctly rounded division for every BF16 (maximum, value) pair whose scale
+    is at least 2^-100."""
+    print("[case] q8 reciprocal code", flush=True)
+    counts = torch.full((1,), -1, dtype=torch.int64, device="cuda")
+    abi.call("padra_CheckQ8Path", None, counts.data_ptr())
+    torch.cuda.synchronize()
+    assert counts.tolist() == [0]
+
+
 @pytest.mark.parametrize("act", ["bf16", "f32"])
 def test_quantize_fp8(oracle, act):
     """E4M3 row encoding of activations (the attention output): BF16 rows (fast path),
