@@ -89,13 +89,14 @@ __device__ __forceinline__ void v_rows_copy16(const A &a, unsigned block0, unsig
 
 // Hadamard stage across lanes of the quad: this lane's features pair with lane (lane ^ D)'s
 // (D = 1: feature bit 5, D = 2: bit 6); the lower lane keeps lower + upper, the upper lane
-// lower - upper.
+// lower - upper.  Both are one fused multiply-add other + s * x with s = +-1: s * x is
+// exact, so it rounds once, as the sum or difference does.
 template <int D> __device__ __forceinline__ void hadamard_quad(float (&x)[32], int g) {
+  const float sgn = (g & D) ? -1.f : 1.f;
 #pragma unroll
   for (int f = 0; f < 32; ++f) {
     const uint32_t o = D == 1 ? quad_xor1(__float_as_uint(x[f])) : quad_xor2(__float_as_uint(x[f]));
-    const float other = __uint_as_float(o);
-    x[f] = (g & D) ? other - x[f] : x[f] + other;
+    x[f] = __builtin_fmaf(sgn, x[f], __uint_as_float(o));
   }
 }
 
@@ -171,10 +172,11 @@ __device__ __forceinline__ void encode_quad(const QKArgs<uint16_t> &a, const uin
       hadamard_quad<1>(x, g);
       if constexpr (!ISV) {
         // the last K stage (bit 6) with the 1/sqrt(128) scale
+        const float sgn = (g & 2) ? -1.f : 1.f;
 #pragma unroll
         for (int f = 0; f < 32; ++f) {
           const float other = __uint_as_float(quad_xor2(__float_as_uint(x[f])));
-          x[f] = ((g & 2) ? other - x[f] : x[f] + other) * .08838834764831845f;
+          x[f] = __builtin_fmaf(sgn, x[f], other) * .08838834764831845f;
         }
       } else {
 #pragma unroll
