@@ -27,7 +27,8 @@ namespace {
 
 template <int VT, int J, class T, bool RES>
 __global__ __launch_bounds__(64) void k_norm(NormArgs<T> a) {
-  norm_row_wave<VT, J, T, RES>(a, blockIdx.x);
+  __shared__ uint4 lds[VT * J / 8];
+  norm_row_wave<VT, J, T, RES>(a, blockIdx.x, lds);
 }
 
 // Fewer waves than rows, each pipelining its rows (row loads in flight during the
@@ -38,7 +39,8 @@ __global__ __launch_bounds__(64) void k_norm_pipe(NormArgs<T> a) {
 }
 
 template <class T, int FMT> __global__ __launch_bounds__(64) PADRA_WAVES_PER_EU void k_qk(QKArgs<T> a) {
-  qk_heads_wave<T, FMT>(a, blockIdx.x);
+  __shared__ uint4 lds[256];
+  qk_heads_wave<T, FMT>(a, blockIdx.x, lds);
 }
 
 // Self-check of the two fast-path identities, over their whole domains:
@@ -100,11 +102,12 @@ template <int J, class T> __global__ __launch_bounds__(64) void k_norm_fp8(NormF
 template <int VT, int J, int FMT>
 __global__ __launch_bounds__(64) PADRA_WAVES_PER_EU void k_chain(NormArgs<uint16_t> n, QKArgs<uint16_t> q,
                                               long long norm_waves, long long waves) {
+  __shared__ uint4 lds[256];
   const long long b = blockIdx.x;
   if (b < norm_waves)
-    norm_row_wave<VT, J, uint16_t, true>(n, (int)b);
+    norm_row_wave<VT, J, uint16_t, true, false>(n, (int)b, nullptr);
   else if (b < waves)
-    qk_heads_wave<uint16_t, FMT>(q, b - norm_waves);
+    qk_heads_wave<uint16_t, FMT>(q, b - norm_waves, lds);
 }
 
 // Launch tuning (padra_Tune): waves per CU for the pipelined row kernel, 0 = one wave

@@ -17,6 +17,8 @@
 // store to x may alias the residual for all the compiler knows, which would otherwise
 // pin each load behind the previous store).
 #pragma once
+#include <type_traits>
+
 #include "common.h"
 
 namespace padra {
@@ -230,11 +232,115 @@ __device__ __forceinline__ void norm_compute(const NormArgs<T> &a, int row,
     raise_bad(a.bad);
 }
 
-// One row per wave: all loads of the row, then compute and stores.
-template <int VT, int J, class T, bool RES>
-__device__ __forceinline__ void norm_row_wave(const NormArgs<T> &a, int row) {
+// BF16 rows with 16-byte accesses.  Piece c of lane L is elements 512c + 8L .. 512c + 8L + 7
+// of x, the residual, gamma and the outputs: every load and store of the row is a 1 KB
+// coalesced instruction (4 per tensor at H = 2048, instead of 16 of 4 or 8 bytes).  Only
+// the sum of squares needs the reference's thread ownership (thread t: elements t + VT j,
+// summed in j order): v = B(x + r) crosses LDS once, packed, and each lane reads back the
+// words of its K threads.  The outputs are elementwise and stay in the piece layout.
+template <int VT, int J, bool RES>
+__device__ __forceinline__ void norm_row_wave_wide(const NormArgs<uint16_t> &a, int row,
+                                                   uint4 *vlds) {
+  constexpr int K = VT / 64, H = VT * J, C = (H + 511) / 512, LPW = 32 / K, WARPS = VT / 32;
+  constexpr bool CHECK_Y = VT == 256 || !RES;
+  const int lane = threadIdx.x & 63;
+  const size_t base = (size_t)row * H;
+  uint4 xin[C], rin[C], gin[C];
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+    const int e = (512 * c + 8 * lane < H) ? 512 * c + 8 * lane : 0; // clamped, unconditional
+    xin[c] = ld_nt(reinterpret_cast<const uint4 *>(a.x + base + e));
+    if constexpr (RES)
+      rin[c] = ld_nt(reinterpret_cast<const uint4 *>(a.residual + base + e));
+    gin[c] = *reinterpret_cast<const uint4 *>(a.gamma + e);
+  }
+  // v = B(x + r), packed, into x and LDS.
+  uint4 vw[C];
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+    if constexpr (RES) {
+      const uint32_t xw[4] = {xin[c].x, xin[c].y, xin[c].z, xin[c].w};
+      const uint32_t rw[4] = {rin[c].x, rin[c].y, rin[c].z, rin[c].w};
+      uint32_t o[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        o[k] = pack2(lo16(xw[k]) + lo16(rw[k]), hi16(xw[k]) + hi16(rw[k]));
+      vw[c] = make_uint4(o[0], o[1], o[2], o[3]);
+    } else {
+      vw[c] = xin[c];
+    }
+    if (512 * c + 8 * lane < H) {
+      if constexpr (RES)
+        st_nt(reinterpret_cast<uint4 *>(a.x + base + 512 * c + 8 * lane), vw[c]);
+      vlds[64 * c + lane] = vw[c];
+    }
+  }
+  __syncthreads();
+  // The reference's per-thread sums: lane l owns threads K l .. K l + K - 1, i.e. the K / 2
+  // words K l / 2 + (VT / 2) j of the packed row.
+  const uint32_t *vwords = reinterpret_cast<const uint32_t *>(vlds);
+  float s[K], e[K];
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    s[k] = 0.f;
+    e[k] = 0.f;
+  }
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+#pragma unroll
+    for (int w = 0; w < K / 2; ++w) {
+      const uint32_t word = vwords[(K / 2) * lane + w + (VT / 2) * j];
+      const float v0 = lo16(word), v1 = hi16(word);
+      acc_pos(v0 * v0, s[2 * w], e[2 * w]);
+      acc_pos(v1 * v1, s[2 * w + 1], e[2 * w + 1]);
+    }
+  }
+  warp_tree<K>(s, e);
+  float S = s[0], E = e[0];
+  partials_tree<WARPS, LPW>(S, E);
+  const float total = __shfl(S + E, 0, 64);
+  const float variance = total / (float)H;
+  const float inv = 1.f / sqrtf(variance + a.eps);
+  if (a.stats && lane == 0) {
+    a.stats[2 * row] = variance;
+    a.stats[2 * row + 1] = inv;
+  }
+  // Error flag as in norm_compute.
+  bool fine = !RES || isfinite(total);
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+    const uint32_t vv[4] = {vw[c].x, vw[c].y, vw[c].z, vw[c].w};
+    const uint32_t gg[4] = {gin[c].x, gin[c].y, gin[c].z, gin[c].w};
+    uint32_t o[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const float y0 = B(lo16(vv[k]) * inv) * lo16(gg[k]);
+      const float y1 = B(hi16(vv[k]) * inv) * hi16(gg[k]);
+      if constexpr (CHECK_Y)
+        fine = fine && bf16_finite_after_round(y0) && bf16_finite_after_round(y1);
+      o[k] = pack2(y0, y1);
+    }
+    if (512 * c + 8 * lane < H)
+      st_nt(reinterpret_cast<uint4 *>(a.y + base + 512 * c + 8 * lane), make_uint4(o[0], o[1], o[2], o[3]));
+  }
+  if (__ballot(!fine) != 0 && lane == 0)
+    raise_bad(a.bad);
+}
+
+// One row per wave: all loads of the row, then compute and stores.  WIDE (BF16 rows): the
+// 16-byte layout of norm_row_wave_wide, with `lds` (VT * J / 8 uint4 of LDS owned by the
+// caller); otherwise every access is in the reference's thread-ownership layout.  Alone
+// (padra_ResidualPostNorm) the wide form is faster (2048 x 2048: 7.3 -> 7.0 us); inside the
+// fused chain, where the Q/K waves follow, it measured slower (12.75 -> 13.15 us), so the
+// chain keeps the ownership layout.
+template <int VT, int J, class T, bool RES, bool WIDE = true>
+__device__ __forceinline__ void norm_row_wave(const NormArgs<T> &a, int row, uint4 *lds) {
   if (row >= a.rows)
     return; // wave-uniform
+  if constexpr (WIDE && std::is_same<T, uint16_t>::value) {
+    norm_row_wave_wide<VT, J, RES>(a, row, lds);
+    return;
+  }
   RowIn<VT, J, T> in;
   Lanes<uint16_t, VT / 64> gr[J];
   norm_load<VT, J, T, RES>(a, row, in);

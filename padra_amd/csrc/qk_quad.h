@@ -219,9 +219,10 @@ __device__ __forceinline__ void encode_quad(const QKArgs<uint16_t> &a, const uin
 
 // FMT: -1 (no cache), PADRA_KV_BF16, or a quantized cache format.
 template <int FMT>
-__device__ __forceinline__ void qk_heads_wave_quad(const QKArgs<uint16_t> &a, long long wave) {
+// `stage`: 256 uint4 of LDS (the block's transposition image), owned by the caller.
+__device__ __forceinline__ void qk_heads_wave_quad(const QKArgs<uint16_t> &a, long long wave,
+                                                   uint4 *stage) {
   constexpr int D = 128;
-  __shared__ uint4 stage[256];
   // Per head of the block: 1 = write the activation, 0 = write nothing; and the element
   // offset of its BF16 cache row (-1 = no cache write).
   __shared__ int head_live[16];
@@ -387,9 +388,9 @@ template <class T, int FMT> constexpr int qk_heads_per_wave() {
 
 // BF16 activations: four lanes per head; fp32 activations: two lanes per head.
 template <class T, int FMT>
-__device__ __forceinline__ void qk_heads_wave(const QKArgs<T> &a, long long wave) {
+__device__ __forceinline__ void qk_heads_wave(const QKArgs<T> &a, long long wave, uint4 *lds) {
   if constexpr (std::is_same<T, uint16_t>::value) {
-    qk_heads_wave_quad<FMT>(a, wave);
+    qk_heads_wave_quad<FMT>(a, wave, lds);
   } else {
     qk_heads_wave_direct<T, FMT>(a, wave);
   }
