@@ -301,6 +301,11 @@ int padra_CheckQ8Path(void *stream, unsigned long long *counts);
  * pipeline their rows (0, the default: one wave per row). */
 enum { PADRA_TUNE_NORM_WAVES_PER_CU = 0 };
 int padra_Tune(int knob, int value);
+/* padra_StreamCopy: no counterpart in the reference.  Copies `bytes` (a multiple of 16;
+ * 16-byte aligned pointers) with the best one-pass streaming kernel found for MI355X
+ * (16-byte non-temporal loads, all before the stores); the bench times it at the chain's
+ * byte count as the practical HBM ceiling. */
+int padra_StreamCopy(void *stream, void *dst, const void *src, long long bytes);
 
 /* ---- version / capability ----------------------------------------------------------- */
 const char *padra_version(void);

@@ -97,6 +97,7 @@ SIGNATURES = {
     "padra_SwiGLU": [_P, _P, _P, _P, ctypes.c_longlong, _P, _P, _I],
     "padra_Embed": [_P, _P, _I, _I, _P, ctypes.POINTER(Positions), _I, _P, _P, _I],
     "padra_Tune": [_I, _I],
+    "padra_StreamCopy": [_P, _P, _P, ctypes.c_longlong],
     "padra_version": [],
 }
 RESTYPES = {"padra_version": ctypes.c_char_p, "padra_DecodeAttentionScratch": ctypes.c_longlong}
