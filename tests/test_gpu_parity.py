@@ -462,6 +462,39 @@ def test_config1_full_chunk(oracle):
     assert not kc[tokens:].any().item()
 
 
+@pytest.mark.parametrize("fmt", [abi.KV_Q8, abi.KV_Q8_0, abi.KV_Q8_0_NOROT])
+def test_config2_full_chunk(oracle, fmt):
+    """Config 2 at full size: the 2048-token chunk with quantized KV (q8, q8_0 rotated and
+    unrotated), cap 131072, outliers in K and V; every output and code bit-exact."""
+    print(f"[case] config2 full fmt={fmt}", flush=True)
+    tokens, capacity = 2048, 131072
+    d = synth.chain_inputs(tokens, outliers=True, seed=2)
+    tb = table_bits(oracle, tokens)
+    positions = np.arange(tokens, dtype=np.int32)
+    wx, wy, _, _ = oracle.residual_rmsnorm(d["x"], d["residual"], d["gamma"], threads=128)
+    wq, wk, _ = _qk_oracle(oracle, d, tb, positions)
+    # slots of positions < tokens: the expected rows of a cache `tokens` rows long
+    ek, ev, es = _expected_cache(oracle, fmt, wk, d["v"], positions, tokens, 0)
+    x, r, g = dev(d["x"]), dev(d["residual"]), dev(d["gamma"])
+    y = torch.empty_like(x)
+    q, k = dev(d["q"]), dev(d["k"])
+    kc, vc, sc = _alloc_cache(fmt, capacity)
+    state = _prefill_state(0, tokens, capacity)
+    bad = flag()
+    ops.ResidualNormQKRopeStore(x, r, y, g, q, k, dev(d["v"]), dev(d["qn"]), dev(d["kn"]),
+                                dev(tb), ops.positions_prefill(state),
+                                ops.kv_cache(fmt, kc, vc, capacity, scales=sc), bad)
+    torch.cuda.synchronize()
+    assert not bad.item()
+    assert np.array_equal(host16(x), wx) and np.array_equal(host16(y), wy)
+    assert np.array_equal(host16(q), wq) and np.array_equal(host16(k), wk)
+    assert np.array_equal(_np(kc[:tokens], fmt), ek) and np.array_equal(_np(vc[:tokens], fmt), ev)
+    assert not kc[tokens:].any().item() and not vc[tokens:].any().item()
+    if es is not None:
+        assert np.array_equal(sc[:tokens].cpu().numpy(), es)
+        assert not sc[tokens:].any().item()
+
+
 @pytest.mark.parametrize("fmt", FORMATS)
 @pytest.mark.parametrize("tree", [128, 256])
 def test_reference_geometry_chain(oracle, fmt, tree):
