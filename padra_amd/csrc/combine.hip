@@ -115,7 +115,7 @@ __global__ __launch_bounds__(64) void k_combine_norm(T *x, const T *down, const 
       bool f;
       combine8<T, true>(xr, down + (size_t)row * kExperts * H + col, (size_t)H,
                         weights + (size_t)row * kExperts, out, f);
-      ActIO<T>::store8(xr, out);
+      ActIO<T>::template store8<true>(xr, out);
       fine = fine && f;
 #pragma unroll
       for (int k = 0; k < 4; ++k)
@@ -129,7 +129,7 @@ __global__ __launch_bounds__(64) void k_combine_norm(T *x, const T *down, const 
 #pragma unroll
   for (int j = 0; j < J; ++j)
     vp[j] = v_lds[64 * j + lane];
-  norm_fp8_finish<J, T, FP8>(a, row, vp, gr);
+  norm_fp8_finish<J, T, FP8, true>(a, row, vp, gr);
 }
 
 // QuantizeFP8 (prefill.cuh:46-66): per row of x [rows][cols], scale = max|x| / 448 (1 for a

@@ -92,6 +92,28 @@ __device__ __forceinline__ void st_nt(uint4 *p, uint4 v) {
   const u32x4_t t = {v.x, v.y, v.z, v.w};
   __builtin_nontemporal_store(t, reinterpret_cast<u32x4_t *>(p));
 }
+// Stores written through with the sc1 cache policy (global_store ... sc1).  For a kernel
+// that streams each byte once this measured faster than non-temporal stores in some
+// kernels (the expert combine + norm: 22.8 -> 21.5 us) and slower in others (the fused
+// chain), so the choice is made per kernel.
+__device__ __forceinline__ void st_wt(uint32_t *p, uint32_t v) {
+  asm volatile("global_store_dword %0, %1, off sc1" : : "v"(p), "v"(v) : "memory");
+}
+__device__ __forceinline__ void st_wt(uint2 *p, uint2 v) {
+  const u32x2_t t = {v.x, v.y};
+  asm volatile("global_store_dwordx2 %0, %1, off sc1" : : "v"(p), "v"(t) : "memory");
+}
+__device__ __forceinline__ void st_wt(uint4 *p, uint4 v) {
+  const u32x4_t t = {v.x, v.y, v.z, v.w};
+  asm volatile("global_store_dwordx4 %0, %1, off sc1" : : "v"(p), "v"(t) : "memory");
+}
+// Non-temporal (WT false) or written-through (WT true) streaming store.
+template <bool WT, class P, class V> __device__ __forceinline__ void st_stream(P *p, V v) {
+  if constexpr (WT)
+    st_wt(p, v);
+  else
+    st_nt(p, v);
+}
 __device__ __forceinline__ float ld_nt(const float *p) { return __builtin_nontemporal_load(p); }
 __device__ __forceinline__ void st_nt(float *p, float v) { __builtin_nontemporal_store(v, p); }
 
@@ -104,8 +126,9 @@ template <> struct ActIO<uint16_t> {
     v[0] = lo16(w.x); v[1] = hi16(w.x); v[2] = lo16(w.y); v[3] = hi16(w.y);
     v[4] = lo16(w.z); v[5] = hi16(w.z); v[6] = lo16(w.w); v[7] = hi16(w.w);
   }
+  template <bool WT = false>
   static __device__ __forceinline__ void store8(uint16_t *p, const uint32_t (&w)[4]) {
-    st_nt(reinterpret_cast<uint4 *>(p), make_uint4(w[0], w[1], w[2], w[3]));
+    st_stream<WT>(reinterpret_cast<uint4 *>(p), make_uint4(w[0], w[1], w[2], w[3]));
   }
 };
 template <> struct ActIO<float> {
@@ -117,11 +140,12 @@ template <> struct ActIO<float> {
     v[4] = __uint_as_float(b.x); v[5] = __uint_as_float(b.y);
     v[6] = __uint_as_float(b.z); v[7] = __uint_as_float(b.w);
   }
+  template <bool WT = false>
   static __device__ __forceinline__ void store8(float *p, const uint32_t (&w)[4]) {
-    st_nt(reinterpret_cast<uint4 *>(p), make_uint4(w[0] << 16, w[0] & 0xffff0000u, w[1] << 16,
-                                                   w[1] & 0xffff0000u));
-    st_nt(reinterpret_cast<uint4 *>(p + 4), make_uint4(w[2] << 16, w[2] & 0xffff0000u,
-                                                       w[3] << 16, w[3] & 0xffff0000u));
+    st_stream<WT>(reinterpret_cast<uint4 *>(p), make_uint4(w[0] << 16, w[0] & 0xffff0000u,
+                                                           w[1] << 16, w[1] & 0xffff0000u));
+    st_stream<WT>(reinterpret_cast<uint4 *>(p + 4), make_uint4(w[2] << 16, w[2] & 0xffff0000u,
+                                                               w[3] << 16, w[3] & 0xffff0000u));
   }
 };
 __device__ __forceinline__ void load8_bf16(const uint16_t *p, float (&v)[8]) {

@@ -104,7 +104,7 @@ __device__ __forceinline__ void fp8_encode_pairs(const uint32_t (&w)[J], float s
 // Everything after the row's values are in registers: lane l holds v_{2l+k+128j} (k = 0, 1)
 // in vp[j] (BF16 pair) and the matching gamma pairs.  The 128-thread tree, the normalized
 // row, and with FP8 the scale and codes.
-template <int J, class T, bool FP8>
+template <int J, class T, bool FP8, bool WT = false>
 __device__ __forceinline__ void norm_fp8_finish(const NormFP8Args<T> &a, int row,
                                                 const uint32_t (&vp)[J],
                                                 const Lanes<uint16_t, 2> (&gr)[J]) {
@@ -139,7 +139,7 @@ __device__ __forceinline__ void norm_fp8_finish(const NormFP8Args<T> &a, int row
   for (int j = 0; j < J; ++j) {
     yw[j] = pack2(B(lo16(vp[j]) * inv) * gr[j].get(0), B(hi16(vp[j]) * inv) * gr[j].get(1));
     mag2 = __builtin_elementwise_max(mag2, __builtin_bit_cast(u16x2_t, yw[j] & 0x7fff7fffu));
-    Lanes<T, K>::store(a.y + off + VT * j, &yw[j]);
+    Lanes<T, K>::template store<WT>(a.y + off + VT * j, &yw[j]);
   }
   uint32_t mag = max((uint32_t)mag2.x, (uint32_t)mag2.y);
 #pragma unroll

@@ -54,11 +54,12 @@ template <int K> struct Lanes<uint16_t, K> {
     }
   }
   __device__ __forceinline__ float get(int i) const { return i & 1 ? hi16(w[i / 2]) : lo16(w[i / 2]); }
+  template <bool WT = false>
   static __device__ __forceinline__ void store(uint16_t *p, const uint32_t *w) {
     if constexpr (K == 2)
-      st_nt(reinterpret_cast<uint32_t *>(p), w[0]);
+      st_stream<WT>(reinterpret_cast<uint32_t *>(p), w[0]);
     else
-      st_nt(reinterpret_cast<uint2 *>(p), make_uint2(w[0], w[1]));
+      st_stream<WT>(reinterpret_cast<uint2 *>(p), make_uint2(w[0], w[1]));
   }
 };
 template <int K> struct Lanes<float, K> {
@@ -77,11 +78,12 @@ template <int K> struct Lanes<float, K> {
     }
   }
   __device__ __forceinline__ float get(int i) const { return f[i]; }
+  template <bool WT = false>
   static __device__ __forceinline__ void store(float *p, const uint32_t *w) {
     if constexpr (K == 2)
-      st_nt(reinterpret_cast<uint2 *>(p), make_uint2(w[0] << 16, w[0] & 0xffff0000u));
+      st_stream<WT>(reinterpret_cast<uint2 *>(p), make_uint2(w[0] << 16, w[0] & 0xffff0000u));
     else
-      st_nt(reinterpret_cast<uint4 *>(p), make_uint4(w[0] << 16, w[0] & 0xffff0000u, w[1] << 16,
+      st_stream<WT>(reinterpret_cast<uint4 *>(p), make_uint4(w[0] << 16, w[0] & 0xffff0000u, w[1] << 16,
                                                      w[1] & 0xffff0000u));
   }
 };
