@@ -203,7 +203,7 @@ __device__ __forceinline__ void norm_fp8_row_wave(const NormFP8Args<T> &a, int r
     else
       vp[j] = pack2(x[j].get(0), x[j].get(1));
   }
-  norm_fp8_finish<J, T, true>(a, row, vp, gr);
+  norm_fp8_finish<J, T, true, true>(a, row, vp, gr); // written-through: 6.34 -> 6.25 us
 }
 
 } // namespace padra
