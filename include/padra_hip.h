@@ -263,6 +263,8 @@ int padra_CombineNorm(void *stream, void *x, const void *down, const float *weig
  * {1, 2, 4, 8} query heads per KV head.
  *  - BF16 cache: gqa8_fragment_validation::SplitBF16 (attention_gqa8_fragment_validation.cuh:
  *    79-214) and attention_perhead_exact::Merge (attention_perhead_exact.cuh:7-38).
+ *  - q8 cache: gqa8_q8_attention::SplitBF16 (attention_gqa8_q8.cuh:112-277), its tiles
+ *    decoded by kv_q8::Decode, with the per-head merge above.
  *  - q8_0 cache (rotated v2, 4 KV heads): q8_native::EncodeQuery, Split and Merge
  *    (kv_q8_native.cuh:103-148, 198-363); a local ring must have cap 1024.
  * q [seqs][q_heads][128] (BF16-exact), out likewise; kv: the cache binding (cap rows per
@@ -278,6 +280,17 @@ int padra_DecodeAttention(void *stream, const void *q, const padra_KVCache *kv, 
                           const padra_Positions *pos, int seqs, int q_heads, int kv_heads,
                           int local, int splits, float *scratch, long long scratch_floats,
                           int *bad, int act);
+/* padra_DecodeAttentionFP8: padra_DecodeAttention (BF16 or q8 cache) whose merge also
+ * writes the E4M3 encoding of each sequence's output row, as
+ * attention_o_wide_exact::MergeQuantize (attention_merge_quantize_wide_exact.cuh:9-66)
+ * does after the reference's q8 split (attention_gqa8_q8.cuh:278-300): packed
+ * [seqs][q_heads * 128] codes of the correctly rounded quotient out / scale, scales [seqs]
+ * = max|out row| / 448 (1 for a zero row); the same bytes padra_QuantizeFP8 writes for out.
+ * q_heads <= 32.  A q8_0 cache is PADRA_UNSUPPORTED (its reference merge has no FP8 form). */
+int padra_DecodeAttentionFP8(void *stream, const void *q, const padra_KVCache *kv, void *out,
+                             uint8_t *packed, float *scales, const padra_Positions *pos,
+                             int seqs, int q_heads, int kv_heads, int local, int splits,
+                             float *scratch, long long scratch_floats, int *bad, int act);
 /* Floats of scratch padra_DecodeAttention needs for a cache format (splits as passed,
  * 1..32); -1 if invalid. */
 long long padra_DecodeAttentionScratch(int format, int seqs, int q_heads, int splits);

@@ -84,6 +84,9 @@ SIGNATURES = {
     "padra_DecodeAttentionScratch": [_I, _I, _I, _I],
     "padra_DecodeAttention": [_P, _P, ctypes.POINTER(KVCache), _P, ctypes.POINTER(Positions), _I,
                               _I, _I, _I, _I, _P, ctypes.c_longlong, _P, _I],
+    "padra_DecodeAttentionFP8": [_P, _P, ctypes.POINTER(KVCache), _P, _P, _P,
+                                 ctypes.POINTER(Positions), _I, _I, _I, _I, _I, _P,
+                                 ctypes.c_longlong, _P, _I],
     "padra_KVCheckpointCapture": [_P, ctypes.POINTER(KVCache), ctypes.POINTER(KVCache),
                                   ctypes.POINTER(KVCache), ctypes.POINTER(Positions), _I, _I, _I,
                                   _P],

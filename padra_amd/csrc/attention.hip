@@ -27,6 +27,7 @@
 #include <algorithm>
 
 #include "common.h"
+#include "norm_fp8.h"
 
 using namespace padra;
 
@@ -460,6 +461,91 @@ template <class T> __global__ __launch_bounds__(64) void k_attn_merge(AttnArgs a
     raise_bad(a.bad);
 }
 
+
+// MergeQuantize (attention_merge_quantize_wide_exact.cuh:9-66), the merge the reference
+// runs after its q8 split (attention_gqa8_q8.cuh:278-300) and, with the FP8 output, after
+// the BF16 one: the per-head merge of k_attn_merge for every head of a sequence in one
+// workgroup, then the E4M3 encoding of the whole output row (q_heads x 128 values) with
+// scale = max|out| / 448 (1 for a zero row), as padra_QuantizeFP8 writes it.  Waves take
+// heads wave, wave + 4, ...; lane l holds dimensions 2l, 2l + 1 of each.
+template <class T>
+__global__ __launch_bounds__(256) void k_attn_merge_fp8(AttnArgs a, uint8_t *packed,
+                                                        float *scales) {
+  constexpr int kWaves = 4, kHeads = 32;
+  __shared__ float weights[kHeads][32];
+  __shared__ float maxima[kWaves];
+  const int seq = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int n, first;
+  if (!attn_window(a, seq, n, first))
+    return; // block-uniform; the split kernel raised the flag
+  const int active = min(a.splits, (n + kKeys - 1) / kKeys);
+  bool fine = true;
+  for (int head = wave; head < a.hq; head += kWaves) {
+    const float v =
+        lane < active ? a.lse[((size_t)seq * a.splits + lane) * a.hq + head] : -INFINITY;
+    const float mx = xor_max32(v);
+    const float w = lane < active ? expf(v - mx) : 0.f;
+    const float total = xor_sum32(w);
+    if (lane < active) {
+      weights[head][lane] = w / total;
+      fine = fine && isfinite(weights[head][lane]);
+    }
+  }
+  __syncthreads();
+  uint32_t words[kHeads / kWaves];
+  float amax = 0.f;
+#pragma unroll
+  for (int k = 0; k < kHeads / kWaves; ++k) {
+    const int head = wave + kWaves * k;
+    words[k] = 0u;
+    if (head >= a.hq)
+      continue;
+    float s0 = 0.f, s1 = 0.f;
+    for (int sp = 0; sp < active; ++sp) {
+      const float2 p = *reinterpret_cast<const float2 *>(
+          a.partial + (((size_t)seq * a.splits + sp) * a.hq + head) * kD + 2 * lane);
+      s0 = __builtin_fmaf(weights[head][sp], p.x, s0);
+      s1 = __builtin_fmaf(weights[head][sp], p.y, s1);
+    }
+    const uint32_t word = pack2(s0, s1);
+    words[k] = word;
+    fine = fine && ((word & 0x7f80u) != 0x7f80u) && ((word & 0x7f800000u) != 0x7f800000u);
+    amax = fmaxf(amax, fmaxf(fabsf(lo16(word)), fabsf(hi16(word))));
+    const size_t o = ((size_t)seq * a.hq + head) * kD + 2 * lane;
+    if constexpr (std::is_same<T, uint16_t>::value)
+      static_cast<uint32_t *>(a.out)[o / 2] = word;
+    else
+      *reinterpret_cast<float2 *>(static_cast<float *>(a.out) + o) =
+          make_float2(lo16(word), hi16(word));
+  }
+#pragma unroll
+  for (int d = 32; d >= 1; d /= 2)
+    amax = fmaxf(amax, __shfl_xor(amax, d, 64));
+  if (lane == 0)
+    maxima[wave] = amax;
+  const bool row_fine = !__syncthreads_or(!fine);
+  amax = fmaxf(fmaxf(maxima[0], maxima[1]), fmaxf(maxima[2], maxima[3]));
+  if (!row_fine && threadIdx.x == 0)
+    raise_bad(a.bad);
+  const float scale = amax == 0.f ? 1.f : amax / 448.f;
+  const float inverse = 1.f / scale;
+  if (threadIdx.x == 0)
+    scales[seq] = scale;
+  const bool fast = row_fine && fp8_fast_ok(amax, inverse); // block-uniform
+#pragma unroll
+  for (int k = 0; k < kHeads / kWaves; ++k) {
+    const int head = wave + kWaves * k;
+    if (head >= a.hq)
+      continue;
+    const uint32_t word = words[k];
+    const uint32_t code =
+        fast ? e4m3_pair_fast(fp8_quotient(lo16(word), scale, inverse),
+                              fp8_quotient(hi16(word), scale, inverse))
+             : e4m3_code(lo16(word) / scale) | (e4m3_code(hi16(word) / scale) << 8);
+    *reinterpret_cast<uint16_t *>(packed + ((size_t)seq * a.hq + head) * kD + 2 * lane) =
+        (uint16_t)code;
+  }
+}
 
 // ---- q8_0 caches ------------------------------------------------------------------------
 //
@@ -937,11 +1023,12 @@ extern "C" long long padra_DecodeAttentionScratch(int format, int seqs, int q_he
   return format == PADRA_KV_Q8_0 ? base + (long long)seqs * q_heads * (kD / 4 + 4) : base;
 }
 
-extern "C" int padra_DecodeAttention(void *stream, const void *q, const padra_KVCache *kv,
-                                     void *out, const padra_Positions *pos, int seqs,
-                                     int q_heads, int kv_heads, int local, int splits,
-                                     float *scratch, long long scratch_floats, int *bad,
-                                     int act) {
+namespace {
+// Both entry points: packed/scales non-null selects the merge with the FP8 encoding.
+int decode_attention(void *stream, const void *q, const padra_KVCache *kv, void *out,
+                     uint8_t *packed, float *scales, const padra_Positions *pos, int seqs,
+                     int q_heads, int kv_heads, int local, int splits, float *scratch,
+                     long long scratch_floats, int *bad, int act) {
   if (!q || !kv || !out || !pos || !bad || !scratch || seqs < 1 || q_heads < 1 ||
       kv_heads < 1 || q_heads % kv_heads || !kv->k || !kv->v || kv->cap < 1 ||
       kv->cap > 131072 || pos->mode != PADRA_POS_DECODE || !pos->decode || pos->maximum < 1 ||
@@ -953,6 +1040,11 @@ extern "C" int padra_DecodeAttention(void *stream, const void *q, const padra_KV
     return PADRA_UNSUPPORTED;
   if (kv->format == PADRA_KV_Q8 && !kv->scales)
     return PADRA_INVALID_ARGUMENT;
+  const bool fp8 = packed != nullptr;
+  if (fp8 && (!scales || q_heads > 32))
+    return PADRA_INVALID_ARGUMENT;
+  if (fp8 && kv->format == PADRA_KV_Q8_0)
+    return PADRA_UNSUPPORTED; // the reference's q8_0 merge has no FP8 form
   const bool q8 = kv->format == PADRA_KV_Q8_0, q8s = kv->format == PADRA_KV_Q8;
   if (q8 && kv_heads * kD != 512)
     return PADRA_UNSUPPORTED; // the 544-byte q8_0 row of 4 KV heads
@@ -1032,8 +1124,32 @@ extern "C" int padra_DecodeAttention(void *stream, const void *q, const padra_KV
       split(std::true_type{});
     else
       split(std::false_type{});
-    hipLaunchKernelGGL((k_attn_merge<T>), merge_grid, dim3(64), 0, s, a);
+    if (fp8)
+      hipLaunchKernelGGL((k_attn_merge_fp8<T>), dim3(seqs), dim3(256), 0, s, a, packed, scales);
+    else
+      hipLaunchKernelGGL((k_attn_merge<T>), merge_grid, dim3(64), 0, s, a);
     return launched("DecodeAttention");
   };
   return act == PADRA_ACT_BF16 ? launch(uint16_t{}) : launch(float{});
+}
+} // namespace
+
+extern "C" int padra_DecodeAttention(void *stream, const void *q, const padra_KVCache *kv,
+                                     void *out, const padra_Positions *pos, int seqs,
+                                     int q_heads, int kv_heads, int local, int splits,
+                                     float *scratch, long long scratch_floats, int *bad,
+                                     int act) {
+  return decode_attention(stream, q, kv, out, nullptr, nullptr, pos, seqs, q_heads, kv_heads,
+                          local, splits, scratch, scratch_floats, bad, act);
+}
+
+extern "C" int padra_DecodeAttentionFP8(void *stream, const void *q, const padra_KVCache *kv,
+                                        void *out, uint8_t *packed, float *scales,
+                                        const padra_Positions *pos, int seqs, int q_heads,
+                                        int kv_heads, int local, int splits, float *scratch,
+                                        long long scratch_floats, int *bad, int act) {
+  if (!packed)
+    return PADRA_INVALID_ARGUMENT;
+  return decode_attention(stream, q, kv, out, packed, scales, pos, seqs, q_heads, kv_heads,
+                          local, splits, scratch, scratch_floats, bad, act);
 }

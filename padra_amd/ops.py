@@ -226,11 +226,13 @@ def KVCheckpointCapture(ring: abi.KVCache, chunk: abi.KVCache, saved: abi.KVCach
 
 
 def DecodeAttention(q, kv: abi.KVCache, out, positions: abi.Positions, bad, kv_heads=4,
-                    local=False, splits=0, scratch=None):
+                    local=False, splits=0, scratch=None, packed=None, scales=None):
     """Decode attention over a BF16 or q8_0 cache for q [seqs][q_heads][128]
     (SplitBF16 + per-head Merge, attention_gqa8_fragment_validation.cuh:79-214,
     attention_perhead_exact.cuh:7-38; q8_native EncodeQuery/Split/Merge,
-    kv_q8_native.cuh:103-363).  Allocates the fp32 scratch when none is given."""
+    kv_q8_native.cuh:103-363).  Allocates the fp32 scratch when none is given.  With packed
+    ([seqs][q_heads * 128] uint8) and scales ([seqs] fp32), the merge also writes each
+    output row's E4M3 encoding (MergeQuantize, attention_merge_quantize_wide_exact.cuh:9-66)."""
     _need_cuda(q, out, bad, scratch)
     seqs, q_heads = q.shape[0], q.shape[1]
     if kv.format == abi.KV_Q8_0:
@@ -240,9 +242,15 @@ def DecodeAttention(q, kv: abi.KVCache, out, positions: abi.Positions, bad, kv_h
     need = abi.lib().padra_DecodeAttentionScratch(kv.format, seqs, q_heads, used)
     if scratch is None:
         scratch = torch.empty(need, dtype=torch.float32, device=q.device)
-    abi.call("padra_DecodeAttention", _stream(q), _p(q), ctypes.byref(kv), _p(out),
-             ctypes.byref(positions), seqs, q_heads, int(kv_heads), int(bool(local)), int(splits),
-             _p(scratch), scratch.numel(), _p(bad), _act(q))
+    if packed is None:
+        abi.call("padra_DecodeAttention", _stream(q), _p(q), ctypes.byref(kv), _p(out),
+                 ctypes.byref(positions), seqs, q_heads, int(kv_heads), int(bool(local)),
+                 int(splits), _p(scratch), scratch.numel(), _p(bad), _act(q))
+    else:
+        _need_cuda(packed, scales)
+        abi.call("padra_DecodeAttentionFP8", _stream(q), _p(q), ctypes.byref(kv), _p(out),
+                 _p(packed), _p(scales), ctypes.byref(positions), seqs, q_heads, int(kv_heads),
+                 int(bool(local)), int(splits), _p(scratch), scratch.numel(), _p(bad), _act(q))
     return scratch
 
 

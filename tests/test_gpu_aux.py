@@ -600,6 +600,60 @@ def test_decode_attention_q8(oracle, hq, local):
     assert bad.item() == 1
 
 
+@pytest.mark.parametrize("fmt", [abi.KV_BF16, abi.KV_Q8])
+@pytest.mark.parametrize("hq", [16, 32])
+def test_decode_attention_fp8_merge(fmt, hq):
+    """The merge with the FP8 output (MergeQuantize): out identical to padra_DecodeAttention's
+    and the codes and scales identical to padra_QuantizeFP8 of that output (both pinned by
+    their own tests), for BF16 and q8 caches; a zero query row gives scale 1 and zero
+    codes; a q8_0 cache is refused."""
+    print(f"[case] decode attention fp8 merge fmt={fmt} hq={hq}", flush=True)
+    seqs, hkv, capacity = 5, 4, 4096
+    rng = np.random.default_rng(150 + hq + fmt)
+    positions = rng.integers(0, capacity, seqs).astype(np.int32)
+    positions[0] = 0
+    q = synth.bf16_bits((rng.standard_normal((seqs, hq, 128)) * 2).astype(np.float32))
+    if fmt == abi.KV_BF16:
+        kc = dev(synth.bf16_bits(rng.standard_normal((seqs * capacity, hkv * 128)).astype(np.float32)))
+        vc = dev(synth.bf16_bits(rng.standard_normal((seqs * capacity, hkv * 128)).astype(np.float32)))
+        vc[capacity * 2:capacity * 3] = 0  # sequence 2: all-zero values, a zero output row
+        kv = ops.kv_cache(fmt, kc, vc, capacity, seq_stride=capacity)
+    else:
+        codes_k = torch.from_numpy(rng.integers(-127, 128, (seqs * capacity, hkv * 128)).astype(np.int8)).cuda()
+        codes_v = torch.from_numpy(rng.integers(-127, 128, (seqs * capacity, hkv * 128)).astype(np.int8)).cuda()
+        codes_v[capacity * 2:capacity * 3] = 0
+        sc = torch.from_numpy(rng.uniform(0.005, 0.02, (seqs * capacity, hkv, 2)).astype(np.float32)).cuda()
+        kv = ops.kv_cache(fmt, codes_k, codes_v, capacity, scales=sc, seq_stride=capacity)
+    states = np.zeros((seqs, 8), np.int32)
+    for s, p in enumerate(positions):
+        states[s] = [5, p, capacity, 10, p, min(p, 1024), 0, 0]
+    pos = ops.positions_decode(torch.from_numpy(states).cuda(), maximum=capacity)
+    out_a = torch.empty((seqs, hq, 128), dtype=torch.int16, device="cuda")
+    out_b = torch.empty_like(out_a)
+    packed_a = torch.empty((seqs, hq * 128), dtype=torch.uint8, device="cuda")
+    packed_b = torch.empty_like(packed_a)
+    scales_a = torch.empty(seqs, dtype=torch.float32, device="cuda")
+    scales_b = torch.empty_like(scales_a)
+    bad = flag()
+    ops.DecodeAttention(dev(q), kv, out_a, pos, bad, kv_heads=hkv)
+    ops.QuantizeFP8(out_a.view(seqs, hq * 128), packed_a, scales_a, bad)
+    ops.DecodeAttention(dev(q), kv, out_b, pos, bad, kv_heads=hkv, packed=packed_b,
+                        scales=scales_b)
+    torch.cuda.synchronize()
+    assert bad.item() == 0
+    assert torch.equal(out_a, out_b)
+    assert torch.equal(packed_a, packed_b)
+    assert torch.equal(scales_a, scales_b)
+    assert scales_b[2].item() == 1.0 and not packed_b[2].any().item()
+    q8_0 = ops.kv_cache(abi.KV_Q8_0, torch.zeros((seqs * capacity, 544), dtype=torch.uint8,
+                                                 device="cuda"),
+                        torch.zeros((seqs * capacity, 544), dtype=torch.uint8, device="cuda"),
+                        capacity, seq_stride=capacity)
+    with pytest.raises(abi.PadraError):
+        ops.DecodeAttention(dev(q), q8_0, out_b, pos, bad, kv_heads=hkv, packed=packed_b,
+                            scales=scales_b)
+
+
 def test_decode_attention_q8_scales(oracle):
     """kv_q8::Decode's checks (kv_q8.cuh:15-27) on the rows the split reads: a scale whose
     127 * scale overflows BF16 decodes its smaller codes to finite values (no flag) and its
