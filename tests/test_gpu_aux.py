@@ -707,3 +707,17 @@ def test_decode_attention_q8_scales(oracle):
     sc = scales.copy()
     sc[1, 650, 2, 0] = 0.0  # zero K scale inside sequence 1's window
     assert run(codes_k, sc)[1] == 1
+
+
+def test_stream_copy():
+    """The bench's ceiling kernel copies exactly (whole and partial last workgroups) and
+    refuses misaligned sizes."""
+    print("[case] stream copy", flush=True)
+    for n in (16, 16 * 1023, 16 * 1024 * 5 + 48):
+        src = torch.randint(0, 256, (n,), dtype=torch.uint8, device="cuda")
+        dst = torch.zeros_like(src)
+        abi.call("padra_StreamCopy", None, dst.data_ptr(), src.data_ptr(), n)
+        torch.cuda.synchronize()
+        assert torch.equal(src, dst), n
+    with pytest.raises(abi.PadraError):
+        abi.call("padra_StreamCopy", None, dst.data_ptr(), src.data_ptr(), 24)
