@@ -346,6 +346,42 @@ def test_qk_rope_store_prefill(oracle, fmt, tokens, base, cap):
         assert np.array_equal(sc.cpu().numpy(), es)
 
 
+@pytest.mark.parametrize("fmt", [abi.KV_Q8, abi.KV_Q8_0, abi.KV_Q8_0_NOROT])
+def test_store_extreme_value_scales(oracle, fmt):
+    """V heads of tiny and huge magnitude (q8: scales below 2^-100, where the store takes
+    the division instead of the reciprocal form, and near the top of the fp32 range; q8_0:
+    fp16 block scales from subnormal to near their top), bit-exact against the oracle's
+    codes and scales."""
+    print(f"[case] store extreme scales fmt={fmt}", flush=True)
+    tokens, capacity = 48, 4096
+    d = synth.chain_inputs(tokens, outliers=False, seed=77 + fmt)
+    v = d["v"].view(np.uint16).reshape(tokens, -1).astype(np.uint32) << 16
+    vf = v.view(np.float32).copy()
+    # q8_0 scales are fp16 (amax / 127 must stay finite there), q8 scales fp32
+    factors = np.array([1e-36, 3e-33, 1e-30, 1.0, 1e30, 1e36] if fmt == abi.KV_Q8 else
+                       [1e-36, 1e-20, 1e-6, 1.0, 1e3, 1e5], np.float32)
+    vf *= factors[np.arange(tokens) % len(factors)][:, None]
+    d["v"] = synth.bf16_bits(vf).reshape(d["v"].shape)
+    tb = table_bits(oracle, capacity)
+    positions = np.arange(tokens, dtype=np.int32)
+    wq, wk, _ = _qk_oracle(oracle, d, tb, positions)
+    ek, ev, es = _expected_cache(oracle, fmt, wk, d["v"], positions, capacity, 0)
+    kc, vc, sc = _alloc_cache(fmt, capacity)
+    q, k = dev(d["q"]), dev(d["k"])
+    bad = flag()
+    kv = ops.kv_cache(fmt, kc, vc, capacity, scales=sc)
+    ops.QKNormRopeStore(q, k, dev(d["qn"]), dev(d["kn"]), dev(tb), ops.positions_base(0), bad,
+                        v=dev(d["v"]), kv=kv)
+    torch.cuda.synchronize()
+    assert not bad.item()
+    assert np.array_equal(_np(kc, fmt), ek)
+    assert np.array_equal(_np(vc, fmt), ev)
+    if es is not None:
+        assert np.array_equal(sc.cpu().numpy(), es)
+        small = es[..., 1][es[..., 1] > 0]
+        assert small.min() < 2.0 ** -100  # the division path ran
+
+
 @pytest.mark.parametrize("fmt", FORMATS)
 def test_qk_rope_store_decode_batch(oracle, fmt):
     """Ragged positions, one token per sequence, per-sequence caches (seq_stride rows)."""
