@@ -95,8 +95,10 @@ class ChainSet:
                                          self.qn, self.kn, self.table, self.pos, self.kv, self.bad)
 
 
-def time_graph(torch, sets, steps, warmup):
-    """Captures `steps` launches (rotating over sets) into one graph; returns ms/launch."""
+def time_graph(torch, sets, steps, warmup, replays=None):
+    """Captures `steps` launches (rotating over sets) into one graph; returns ms/launch of
+    one timed replay.  With `replays` (a list), that many further replays are timed the
+    same way and their ms/launch appended to it (for the spread of the figure)."""
     for i in range(warmup):
         sets[i % len(sets)].launch()
     torch.cuda.synchronize()
@@ -115,7 +117,16 @@ def time_graph(torch, sets, steps, warmup):
         graph.replay()
         end.record(stream)
     torch.cuda.synchronize()
-    return start.elapsed_time(end) / steps
+    ms = start.elapsed_time(end) / steps
+    if replays is not None:
+        for _ in range(9):
+            with torch.cuda.stream(stream):
+                start.record(stream)
+                graph.replay()
+                end.record(stream)
+            torch.cuda.synchronize()
+            replays.append(start.elapsed_time(end) / steps)
+    return ms
 
 
 def warm_graph(torch, graph, seconds=0.03, most=50):
@@ -258,7 +269,16 @@ def graph_time(torch, step, steps, warmup=3):
         graph.replay()
         end.record(stream)
     torch.cuda.synchronize()
-    return start.elapsed_time(end) / steps
+    ms = start.elapsed_time(end) / steps
+    if replays is not None:
+        for _ in range(9):
+            with torch.cuda.stream(stream):
+                start.record(stream)
+                graph.replay()
+                end.record(stream)
+            torch.cuda.synchronize()
+            replays.append(start.elapsed_time(end) / steps)
+    return ms
 
 
 def bench_swiglu(torch, steps, sets=4):
@@ -496,11 +516,12 @@ def main():
     results = {}
     for fmt in formats:
         sets = [ChainSet(torch, host, table, fmt) for _ in range(args.sets)]
-        ms = time_graph(torch, sets, args.steps, args.warmup)
+        spread = []
+        ms = time_graph(torch, sets, args.steps, args.warmup, spread)
         eager = time_eager(torch, sets, min(args.steps, 50))
         nbytes = chain_bytes(fmt) * TOKENS
         results[fmt] = {"ms": ms, "eager_ms": eager, "bytes": nbytes,
-                        "gbs": nbytes / (ms * 1e-3) / 1e9}
+                        "gbs": nbytes / (ms * 1e-3) / 1e9, "spread": sorted([ms] + spread)}
         bad = sum(int(s.bad.item()) for s in sets)
         if bad:
             raise SystemExit(f"device error flag set for format {fmt}")
@@ -540,6 +561,9 @@ def main():
                          "torch_copy_64MB_gbs": round(ceiling, 1)},
         "formats": {f: {"gbs": round(r["gbs"], 2), "us_per_launch": round(r["ms"] * 1e3, 3),
                         "eager_us_per_launch": round(r["eager_ms"] * 1e3, 3),
+                        "replays_us_p10_median_p90": [
+                            round(float(np.percentile(r["spread"], q)) * 1e3, 3)
+                            for q in (10, 50, 90)],
                         "bytes_per_launch": r["bytes"],
                         "frac": round(r["gbs"] / HBM_PEAK_GBS, 4)} for f, r in results.items()},
     }
