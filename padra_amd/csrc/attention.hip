@@ -1041,7 +1041,8 @@ int decode_attention(void *stream, const void *q, const padra_KVCache *kv, void 
   if (kv->format == PADRA_KV_Q8 && !kv->scales)
     return PADRA_INVALID_ARGUMENT;
   const bool fp8 = packed != nullptr;
-  if (fp8 && (!scales || q_heads > 32))
+  if (fp8 && (!scales || q_heads > 32 || (reinterpret_cast<uintptr_t>(packed) & 1) ||
+              (reinterpret_cast<uintptr_t>(scales) & 3)))
     return PADRA_INVALID_ARGUMENT;
   if (fp8 && kv->format == PADRA_KV_Q8_0)
     return PADRA_UNSUPPORTED; // the reference's q8_0 merge has no FP8 form
