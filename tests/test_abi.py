@@ -147,3 +147,23 @@ def test_host_validation_newer_entry_points():
                                      2, 16, 4, 0, 0, _p(64), need, bad, 0) == abi.UNSUPPORTED
     assert lib.padra_DecodeAttention(None, _p(16), ctypes.byref(kv), _p(32), ctypes.byref(base),
                                      2, 16, 4, 0, 0, _p(64), need, bad, 0) == abi.INVALID_ARGUMENT
+    # the FP8 merge: both outputs required and aligned, at most 32 query heads, no q8_0
+    fp8 = lib.padra_DecodeAttentionFP8
+    assert fp8(None, _p(16), ctypes.byref(kv), _p(32), None, _p(96), ctypes.byref(dec), 2, 16,
+               4, 0, 0, _p(64), need, bad, 0) == abi.INVALID_ARGUMENT
+    assert fp8(None, _p(16), ctypes.byref(kv), _p(32), _p(80), None, ctypes.byref(dec), 2, 16,
+               4, 0, 0, _p(64), need, bad, 0) == abi.INVALID_ARGUMENT
+    assert fp8(None, _p(16), ctypes.byref(kv), _p(32), _p(81), _p(96), ctypes.byref(dec), 2, 16,
+               4, 0, 0, _p(64), need, bad, 0) == abi.INVALID_ARGUMENT
+    big = lib.padra_DecodeAttentionScratch(abi.KV_BF16, 2, 64, 32)
+    assert fp8(None, _p(16), ctypes.byref(kv), _p(32), _p(80), _p(96), ctypes.byref(dec), 2, 64,
+               8, 0, 0, _p(64), big, bad, 0) == abi.INVALID_ARGUMENT
+    q8_0 = abi.KVCache(format=abi.KV_Q8_0, k=16, v=32, scales=None, cap=4096, first=0,
+                       seq_stride=4096)
+    assert fp8(None, _p(16), ctypes.byref(q8_0), _p(32), _p(80), _p(96), ctypes.byref(dec), 2,
+               16, 4, 0, 0, _p(64), need * 2, bad, 0) == abi.UNSUPPORTED
+    # the self-checks need their count buffers; the streaming copy whole 16-byte units
+    assert lib.padra_CheckQ8Path(None, None) == abi.INVALID_ARGUMENT
+    assert lib.padra_CheckFP8Paths(None, None) == abi.INVALID_ARGUMENT
+    assert lib.padra_StreamCopy(None, _p(16), _p(32), 24) == abi.INVALID_ARGUMENT
+    assert lib.padra_StreamCopy(None, _p(16), _p(40), 32) == abi.INVALID_ARGUMENT
