@@ -269,16 +269,7 @@ def graph_time(torch, step, steps, warmup=3):
         graph.replay()
         end.record(stream)
     torch.cuda.synchronize()
-    ms = start.elapsed_time(end) / steps
-    if replays is not None:
-        for _ in range(9):
-            with torch.cuda.stream(stream):
-                start.record(stream)
-                graph.replay()
-                end.record(stream)
-            torch.cuda.synchronize()
-            replays.append(start.elapsed_time(end) / steps)
-    return ms
+    return start.elapsed_time(end) / steps
 
 
 def bench_swiglu(torch, steps, sets=4):
