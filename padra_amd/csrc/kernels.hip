@@ -39,7 +39,8 @@ __global__ __launch_bounds__(64) void k_norm_pipe(NormArgs<T> a) {
 }
 
 template <class T, int FMT> __global__ __launch_bounds__(64) PADRA_WAVES_PER_EU void k_qk(QKArgs<T> a) {
-  __shared__ uint4 lds[256];
+  // the BF16 quad layout's image (4 KB), or the fp32 path's (16 KB)
+  __shared__ uint4 lds[std::is_same<T, uint16_t>::value ? 256 : 1024];
   qk_heads_wave<T, FMT>(a, blockIdx.x, lds);
 }
 

@@ -392,7 +392,7 @@ __device__ __forceinline__ void qk_heads_wave(const QKArgs<T> &a, long long wave
   if constexpr (std::is_same<T, uint16_t>::value) {
     qk_heads_wave_quad<FMT>(a, wave, lds);
   } else {
-    qk_heads_wave_direct<T, FMT>(a, wave);
+    qk_heads_wave_direct<T, FMT>(a, wave, lds);
   }
 }
 

@@ -383,6 +383,38 @@ def test_store_extreme_value_scales(oracle, fmt):
 
 
 @pytest.mark.parametrize("fmt", FORMATS)
+@pytest.mark.parametrize("tokens,base,cap", [(300, 1000, 4096), (1500, 100, 1024)])
+def test_qk_rope_store_f32_activations(oracle, fmt, tokens, base, cap):
+    """The reference's own activation form (fp32 buffers of BF16-exact values) through the
+    Q/K path, every KV format, a global cache and a local ring narrower than the chunk:
+    q and k in place, cache rows, codes and scales bit-exact against the oracle."""
+    print(f"[case] store f32 fmt={fmt} tokens={tokens} cap={cap}", flush=True)
+    d = synth.chain_inputs(tokens, outliers=True, seed=fmt * 11 + tokens)
+    capacity = 4096
+    first = 0 if cap == capacity else max(0, tokens - cap)
+    tb = table_bits(oracle, capacity)
+    positions = np.arange(base, base + tokens, dtype=np.int32)
+    wq, wk, _ = _qk_oracle(oracle, d, tb, positions)
+    ek, ev, es = _expected_cache(oracle, fmt, wk, d["v"], positions, cap, first)
+    kc, vc, sc = _alloc_cache(fmt, cap)
+    f32 = lambda a: torch.from_numpy(synth.bf16_to_f32(a)).cuda()
+    q, k, v = f32(d["q"]), f32(d["k"]), f32(d["v"])
+    state = _prefill_state(base, tokens, capacity)
+    bad = flag()
+    kv = ops.kv_cache(fmt, kc, vc, cap, scales=sc, first=first)
+    ops.QKNormRopeStore(q, k, dev(d["qn"]), dev(d["kn"]), dev(tb),
+                        ops.positions_prefill(state, maximum=capacity), bad, v=v, kv=kv)
+    torch.cuda.synchronize()
+    assert not bad.item()
+    assert np.array_equal(q.cpu().numpy(), synth.bf16_to_f32(wq))
+    assert np.array_equal(k.cpu().numpy(), synth.bf16_to_f32(wk))
+    assert np.array_equal(_np(kc, fmt), ek)
+    assert np.array_equal(_np(vc, fmt), ev)
+    if es is not None:
+        assert np.array_equal(sc.cpu().numpy(), es)
+
+
+@pytest.mark.parametrize("fmt", FORMATS)
 def test_qk_rope_store_decode_batch(oracle, fmt):
     """Ragged positions, one token per sequence, per-sequence caches (seq_stride rows)."""
     print(f"[case] decode batch fmt={fmt}", flush=True)
