@@ -2,8 +2,7 @@
 // residual-norm, Q/K-norm + RoPE + KV-store and fused chain paths.
 //
 // Launch geometry: one 64-lane wavefront per workgroup.  A residual-norm wave covers one
-// row; a Q/K wave covers 16 head vectors (BF16, four lanes each) or 32 (fp32 activations
-// and the quantized caches, two lanes each).  Every wave issues its loads before any
+// row; a Q/K wave covers 16 head vectors, four lanes each.  Every wave issues its loads before any
 // arithmetic, and there is no inter-wave communication, so the grid is a flat list of
 // independent waves (thousands for a 2048-token chunk: >> 256 CUs).
 #include <stdio.h>
@@ -40,7 +39,7 @@ __global__ __launch_bounds__(64) void k_norm_pipe(NormArgs<T> a) {
 
 template <class T, int FMT> __global__ __launch_bounds__(64) PADRA_WAVES_PER_EU void k_qk(QKArgs<T> a) {
   // the BF16 quad layout's image (4 KB), or the fp32 path's (16 KB)
-  __shared__ uint4 lds[std::is_same<T, uint16_t>::value ? 256 : 1024];
+  __shared__ uint4 lds[quad_image_slots<T>()];
   qk_heads_wave<T, FMT>(a, blockIdx.x, lds);
 }
 

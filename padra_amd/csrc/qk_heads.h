@@ -1,20 +1,15 @@
-// Per-head Q/K RMSNorm + NeoX RoPE, and the KV-cache store of the rotated K row and
-// the V row in BF16, q8 or q8_0 form, with two lanes per 128-wide head vector and 32 head
-// vectors per wavefront: the fp32-activation path, and the lane-pair encoders the
-// store-only kernel (padra_KVStore) uses.  BF16 activations take the four-lane layout of
-// qk_quad.h, which builds on the helpers here.
+// Helpers of the per-head Q/K RMSNorm + NeoX RoPE + KV-cache store: the in-lane warp
+// tree, the Hadamard stages, and the lane-pair K/V encoders of the store-only kernel
+// (padra_KVStore), which holds a head in two lanes.  The Q/K kernels themselves hold a
+// head in four lanes (qk_quad.h).
 //
 // Reference: QKNormRopeStoreControlled (qk_rope_store_exact.cuh:4-49), QKNormRope
 // (qknorm_rope.cuh:4-50), QKNormRopePair64 (qknorm_rope_pair64.cuh:3-83).  The reference
 // block has 128 threads, one feature each; warp w (features 32w..32w+31) reduces its
 // squares with a shuffle-down tree and the four warp partials reduce as
-// ((w0 + w2) + (w1 + w3)).  Here lane `half` of a pair holds the features of warps
-// `half` and `half + 2` (features 32*half + i and 64 + 32*half + i, i < 32), so:
-//  - each warp's whole tree runs inside one lane;
-//  - w0 + w2 and w1 + w3 are also in-lane, and the last fold is one lane exchange;
-//  - every RoPE pair (i, i + 64) is in one lane, with no exchange at all.
-// The first tree level adds two squares with zero error terms; it is written out
-// directly (its error fold is an exact no-op).
+// ((w0 + w2) + (w1 + w3)).  A lane holding warp w's 32 features runs that warp's whole
+// tree in-lane (warp_sumsq32).  The first tree level adds two squares with zero error
+// terms; it is written out directly (its error fold is an exact no-op).
 #pragma once
 #include <type_traits>
 
@@ -297,211 +292,9 @@ __device__ __forceinline__ void group_sumsq(const X &x, float &S, float &E) {
   warp_sumsq32(v, S, E);
 }
 
-// One wave = 32 head vectors, two lanes each (the fp32-activation path).  The flat index
-// space is the T*Hq query heads, then the T*Hkv key heads, then (with a cache binding) the
-// T*Hkv value heads, whose lanes only move the V row into the cache.
-//
-// The wave's 32 heads (16 KB of fp32) move through an LDS image: sixteen coalesced 1 KB
-// loads per lane in, each lane reads its two 128-byte halves (features 32*half .. and
-// 64 + 32*half ..), and the rotated query and key heads go back through the image to
-// sixteen coalesced 1 KB stores.  (Reading the halves straight from memory, each
-// instruction touched 64 separate 16-byte pieces 128 or 512 bytes apart: 47 us for a
-// 2048-token chunk, against 10 us through the image.)  Chunk ci (16 bytes) of head jj sits
-// at slot 32*jj + ((ci + jj) & 31): both the transposing writes and the half reads are
-// free of bank conflicts.
-__device__ __forceinline__ int direct_slot(int jj, int ci) { return 32 * jj + ((ci + jj) & 31); }
-
-template <class T, int FMT>
-__device__ __forceinline__ void qk_heads_wave_direct(const QKArgs<T> &a, long long wave,
-                                                     uint4 *image) {
-  static_assert(std::is_same<T, float>::value, "BF16 activations take the quad layout");
-  constexpr int D = 128;
-  __shared__ int head_live[32]; // 1: the head's rotated values go back to its activation
-  const int lane = threadIdx.x & 63, half = lane & 1, jj = lane >> 1;
-  const unsigned block0 = (unsigned)wave * 32u;
-  const unsigned hv = block0 + (unsigned)jj;
-  const unsigned nq = (unsigned)a.tokens * (unsigned)a.hq;
-  const unsigned nk = (unsigned)a.tokens * (unsigned)a.hkv;
-  const unsigned total = nq + nk + (FMT >= 0 ? nk : 0u);
-  const bool live = hv < total;
-  const int role = hv < nq ? 0 : (hv < nq + nk ? 1 : 2); // 0 q, 1 k, 2 v
-  const unsigned idx = role == 0 ? hv : (role == 1 ? hv - nq : hv - nq - nk);
-  const unsigned heads = role == 0 ? (unsigned)a.hq : (unsigned)a.hkv;
-  const int t = live ? (int)(idx / heads) : 0, h = live ? (int)(idx % heads) : 0;
-  const PosState ps = fetch_state(a.pos, t);
-  auto src_of = [&](unsigned hc) -> const float * {
-    return hc < nq ? a.q + (size_t)hc * D
-                   : (hc < nq + nk ? a.k + (size_t)(hc - nq) * D : a.v + (size_t)(hc - nq - nk) * D);
-  };
-
-  // 1. The block into the image: sixteen 1 KB loads per lane, in two batches of eight.
-#pragma unroll
-  for (int b = 0; b < 2; ++b) {
-    uint4 in[8];
-#pragma unroll
-    for (int m = 0; m < 8; ++m) {
-      const int c = 64 * (8 * b + m) + lane;
-      const unsigned hc = min(block0 + (unsigned)(c >> 5), total - 1u);
-      in[m] = ld_nt(reinterpret_cast<const uint4 *>(src_of(hc)) + (c & 31));
-    }
-#pragma unroll
-    for (int m = 0; m < 8; ++m) {
-      const int c = 64 * (8 * b + m) + lane;
-      image[direct_slot(c >> 5, c & 31)] = in[m];
-    }
-  }
-  bool ok = false;
-  const int pos = resolve_position(a.pos, ps, t, FMT >= 0 ? a.cap : 0, a.first,
-                                   FMT > PADRA_KV_BF16, ok);
-  ok = ok && live && pos >= 0 && pos < a.table_rows;
-  if (live && !ok && half == 0)
-    raise_bad(a.bad);
-  __syncthreads();
-  // This lane's halves: chunks 8*half .. (xa) and 16 + 8*half .. (xb) of its head.
-  Act32<T> xa, xb;
-#pragma unroll
-  for (int p = 0; p < 8; ++p) {
-    const uint4 va = image[direct_slot(jj, 8 * half + p)];
-    const uint4 vb = image[direct_slot(jj, 16 + 8 * half + p)];
-    xa.f[p] = make_float4(__uint_as_float(va.x), __uint_as_float(va.y), __uint_as_float(va.z),
-                          __uint_as_float(va.w));
-    xb.f[p] = make_float4(__uint_as_float(vb.x), __uint_as_float(vb.y), __uint_as_float(vb.z),
-                          __uint_as_float(vb.w));
-  }
-  const long long seq = a.pos.mode == PADRA_POS_DECODE ? t : 0;
-  const long long slot = seq * a.seq_stride + (ok ? ring_slot(pos, max(a.cap, 1)) : 0);
-  bool store_act = false;
-  uint32_t lo[16], hi[16];
-
-  if (FMT >= 0 && role == 2) {
-    // V row: the unchanged values go to the cache (StorePrefillControlled,
-    // prefill_control.cuh:36-37; QKNormRopeStoreControlled, qk_rope_store_exact.cuh:47).
-    if constexpr (FMT >= 0) {
-      if (ok && t >= a.first) {
-        if constexpr (FMT == PADRA_KV_BF16) {
-          uint16_t *vc = static_cast<uint16_t *>(a.vc) + slot * (a.hkv * D) + h * D;
-          uint32_t pa[16], pb[16];
-#pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            pa[i] = pack2(xa.get(2 * i), xa.get(2 * i + 1));
-            pb[i] = pack2(xb.get(2 * i), xb.get(2 * i + 1));
-          }
-          store32_bf16(vc + 32 * half, pa);
-          store32_bf16(vc + 64 + 32 * half, pb);
-        } else {
-          float fa[32], fb[32];
-#pragma unroll
-          for (int i = 0; i < 32; ++i) {
-            fa[i] = xa.get(i);
-            fb[i] = xb.get(i);
-          }
-          encode_head_q<FMT, true>(a, fa, fb, slot, h, half);
-        }
-      }
-    }
-  } else if (ok) {
-    const bool isk = role == 1;
-    const uint16_t *w = isk ? a.kn : a.qn;
-    const uint16_t *row = a.table + (size_t)pos * D;
-
-    float S, E, S2, E2;
-    group_sumsq(xa, S, E);
-    group_sumsq(xb, S2, E2);
-    fold(S2, E2, S, E); // w_half + w_{half+2}
-    const float So = shfl_xor(S, 1), Eo = shfl_xor(E, 1);
-    float bs = half ? So : S, be = half ? Eo : E;
-    fold(half ? S : So, half ? E : Eo, bs, be); // (w0 + w2) + (w1 + w3)
-    const float sum = bs + be;
-    const float inv = 1.f / sqrtf(sum / (float)D + a.eps);
-
-    // Normalize and rotate pairs (i, i + 64), eight at a time: every BF16 rounding of the
-    // reference is one half of a packed conversion of the pair.
-    bool fine = isfinite(sum);
-#pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      Bf8 wa, wb, c8, s8;
-      wa.load(w + 32 * half + 8 * m);
-      wb.load(w + 64 + 32 * half + 8 * m);
-      c8.load(row + 32 * half + 8 * m);
-      s8.load(row + 64 + 32 * half + 8 * m);
-#pragma unroll
-      for (int q = 0; q < 8; q += 2) {
-        float l2[2], h2[2];
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          const int i = 8 * m + q + u;
-          const uint32_t p1 = pack2(xa.get(i) * inv, xb.get(i) * inv);
-          const uint32_t p2 = pack2(lo16(p1) * wa.get(q + u), hi16(p1) * wb.get(q + u));
-          const float A = lo16(p2), Bv = hi16(p2), c = c8.get(q + u), sn = s8.get(q + u);
-          const uint32_t p3 = pack2(A * c, Bv * c);
-          const uint32_t p4 = pack2((-Bv) * sn, A * sn);
-          l2[u] = lo16(p3) + lo16(p4);
-          h2[u] = hi16(p3) + hi16(p4);
-          fine = fine && bf16_finite_after_round(l2[u]) && bf16_finite_after_round(h2[u]);
-        }
-        lo[(8 * m + q) / 2] = pack2(l2[0], l2[1]);
-        hi[(8 * m + q) / 2] = pack2(h2[0], h2[1]);
-      }
-    }
-    store_act = true;
-    if (!fine)
-      raise_bad(a.bad);
-
-    if constexpr (FMT >= 0) {
-      if (isk && t >= a.first) {
-        if constexpr (FMT == PADRA_KV_BF16) {
-          uint16_t *kc = static_cast<uint16_t *>(a.kc) + slot * (a.hkv * D) + h * D;
-          store32_bf16(kc + 32 * half, lo);
-          store32_bf16(kc + 64 + 32 * half, hi);
-        } else {
-          float ka[32], kb[32];
-#pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            ka[2 * i] = lo16(lo[i]);
-            ka[2 * i + 1] = hi16(lo[i]);
-            kb[2 * i] = lo16(hi[i]);
-            kb[2 * i + 1] = hi16(hi[i]);
-          }
-          encode_head_q<FMT, false>(a, ka, kb, slot, h, half);
-        }
-      }
-    }
-  }
-
-  // 2. Rotated query and key heads back through the image (as fp32), then sixteen 1 KB
-  // stores per lane.  Each lane rewrites only the slots it read.
-  if (store_act) {
-#pragma unroll
-    for (int p = 0; p < 4; ++p) {
-      const uint32_t *l = lo + 4 * p, *g = hi + 4 * p;
-      image[direct_slot(jj, 8 * half + 2 * p)] =
-          make_uint4(l[0] << 16, l[0] & 0xffff0000u, l[1] << 16, l[1] & 0xffff0000u);
-      image[direct_slot(jj, 8 * half + 2 * p + 1)] =
-          make_uint4(l[2] << 16, l[2] & 0xffff0000u, l[3] << 16, l[3] & 0xffff0000u);
-      image[direct_slot(jj, 16 + 8 * half + 2 * p)] =
-          make_uint4(g[0] << 16, g[0] & 0xffff0000u, g[1] << 16, g[1] & 0xffff0000u);
-      image[direct_slot(jj, 16 + 8 * half + 2 * p + 1)] =
-          make_uint4(g[2] << 16, g[2] & 0xffff0000u, g[3] << 16, g[3] & 0xffff0000u);
-    }
-  }
-  if (half == 0)
-    head_live[jj] = store_act ? 1 : 0;
-  __syncthreads();
-#pragma unroll
-  for (int m = 0; m < 16; ++m) {
-    const int c = 64 * m + lane, j = c >> 5;
-    if (!head_live[j])
-      continue;
-    const unsigned hc = block0 + (unsigned)j;
-    float *dst = const_cast<float *>(src_of(hc));
-    st_nt(reinterpret_cast<uint4 *>(dst) + (c & 31), image[direct_slot(j, c & 31)]);
-  }
-}
-
 // The source row of head vector hv of the flat index space (q heads, k heads, v heads).
 template <class A>
-__device__ __forceinline__ const uint16_t *head_src(const A &a, unsigned hv, unsigned nq,
-                                                    unsigned nk) {
+__device__ __forceinline__ auto head_src(const A &a, unsigned hv, unsigned nq, unsigned nk) {
   constexpr int D = 128;
   return hv < nq ? a.q + (size_t)hv * D
                  : (hv < nq + nk ? a.k + (size_t)(hv - nq) * D : a.v + (size_t)(hv - nq - nk) * D);

@@ -100,49 +100,50 @@ template <int D> __device__ __forceinline__ void hadamard_quad(float (&x)[32], i
   }
 }
 
-// Encodes one K or V head vector held by a quad (lane g: features 32g .. 32g+31, BF16
-// pairs in w) into a quantized cache row.  `active` is quad-uniform; every lane runs the
-// quad exchanges.
-//  - q8 (kv_q8::Encode, kv_q8.cuh:41-73): a head with a non-finite value raises the flag
-//    and writes nothing; scale = amax/127 (1 for a zero head), codes RNE(x / scale)
-//    clamped to +-127, scale into the (k, v) pair of the row's head.
+// Encodes one K or V head vector held by a quad (lane g: features 32g .. 32g+31 in x)
+// into a quantized cache row.  `active` is quad-uniform; every lane runs the quad
+// exchanges.
+//  - A head with a non-finite value (q8: or a value that is not BF16-exact) raises the
+//    flag and writes nothing (kv_q8.cuh:49-54, kv_q8_native.cuh:70-79).
+//  - q8 (kv_q8::Encode, kv_q8.cuh:41-73): scale = amax/127 (1 for a zero head), codes
+//    RNE(x / scale) clamped to +-127, scale into the (k, v) pair of the row's head.
 //  - q8_0 (q8_native::EncodeKV, kv_q8_native.cuh:52-101): the rotation (K 128-point,
 //    V two 64-point; stages on feature bits 0-4 inside the lane, bits 5 and 6 across the
 //    quad), then block g = this lane's 32 features: d = half(amax/127), codes
 //    roundf(x * (1/d_fp32)) clamped.  Blocks from the first failing one (non-finite amax
 //    or d) on are not written, and the flag is raised.
-template <int FMT, bool ISV>
-__device__ __forceinline__ void encode_quad(const QKArgs<uint16_t> &a, const uint32_t (&w)[16],
-                                            long long slot, int h, int g, bool active) {
+template <int FMT, bool ISV, class A>
+__device__ __forceinline__ void encode_quad(const A &a, float (&x)[32], long long slot, int h,
+                                            int g, bool active) {
   constexpr int D = 128;
   const int features = a.hkv * D;
-  float x[32];
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    x[2 * i] = lo16(w[i]);
-    x[2 * i + 1] = hi16(w[i]);
-  }
-  uint32_t cw[8];
-  if constexpr (FMT == PADRA_KV_Q8) {
-    bool finite = true;
-    float m = 0.f;
+  {
+    bool valid = true;
 #pragma unroll
     for (int i = 0; i < 32; ++i) {
-      finite = finite && isfinite(x[i]);
-      m = fmaxf(m, fabsf(x[i]));
+      valid = valid && isfinite(x[i]);
+      if constexpr (FMT == PADRA_KV_Q8)
+        valid = valid && (__float_as_uint(x[i]) & 0xffffu) == 0u;
     }
-    uint32_t fin = finite ? 1u : 0u;
-    fin &= quad_xor1(fin);
-    fin &= quad_xor2(fin);
-    m = fmaxf(m, __uint_as_float(quad_xor1(__float_as_uint(m))));
-    m = fmaxf(m, __uint_as_float(quad_xor2(__float_as_uint(m))));
+    uint32_t v = valid ? 1u : 0u;
+    v &= quad_xor1(v);
+    v &= quad_xor2(v);
     if (!active)
       return;
-    if (!fin) {
+    if (!v) {
       if (g == 0)
         raise_bad(a.bad);
       return;
     }
+  }
+  uint32_t cw[8];
+  if constexpr (FMT == PADRA_KV_Q8) {
+    float m = 0.f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i)
+      m = fmaxf(m, fabsf(x[i]));
+    m = fmaxf(m, __uint_as_float(quad_xor1(__float_as_uint(m))));
+    m = fmaxf(m, __uint_as_float(quad_xor2(__float_as_uint(m))));
     const float scale = m == 0.f ? 1.f : m / 127.f, inverse = 1.f / scale;
     if (q8_fast_ok(scale)) { // quad-uniform
 #pragma unroll
@@ -194,8 +195,6 @@ __device__ __forceinline__ void encode_quad(const QKArgs<uint16_t> &a, const uin
     uint32_t stop = fail ? (uint32_t)g : 4u; // first failing block of the head, 4 = none
     stop = min(stop, quad_xor1(stop));
     stop = min(stop, quad_xor2(stop));
-    if (!active)
-      return;
     if (stop < 4u && g == 0)
       raise_bad(a.bad);
     if ((uint32_t)g >= stop)
@@ -217,12 +216,32 @@ __device__ __forceinline__ void encode_quad(const QKArgs<uint16_t> &a, const uin
   }
 }
 
+// LDS image of a quad block: the activation pieces (BF16: 4 per lane, slots 0..255;
+// fp32: 8 per lane, slots 0..511) and, for fp32 activations, the BF16 cache rows of the
+// block's heads behind them (slots 512..767).  The fp32 pieces of one lane are 64 slots
+// apart, rotated by 2 per piece: the eight lanes writing one owner's pieces and the eight
+// writing the next owner's fall into sixteen different slots mod 16, and so do sixteen
+// lanes reading their own piece p.
+template <class T> constexpr int quad_image_slots() {
+  return std::is_same<T, uint16_t>::value ? 256 : 768;
+}
+template <class T> __device__ __forceinline__ int quad_piece_slot(int owner, int p) {
+  if constexpr (std::is_same<T, uint16_t>::value)
+    return quad_slot(owner, p);
+  else
+    return p * 64 + ((owner + 2 * p) & 63);
+}
+
 // FMT: -1 (no cache), PADRA_KV_BF16, or a quantized cache format.
-template <int FMT>
-// `stage`: 256 uint4 of LDS (the block's transposition image), owned by the caller.
-__device__ __forceinline__ void qk_heads_wave_quad(const QKArgs<uint16_t> &a, long long wave,
+// `stage`: quad_image_slots<T>() uint4 of LDS (the block's transposition image), owned by
+// the caller.
+template <class T, int FMT>
+__device__ __forceinline__ void qk_heads_wave_quad(const QKArgs<T> &a, long long wave,
                                                    uint4 *stage) {
   constexpr int D = 128;
+  constexpr bool F32 = std::is_same<T, float>::value;
+  constexpr int PL = F32 ? 8 : 4; // 16-byte pieces per lane
+  constexpr int CH = 4 * PL;      // 16-byte chunks per head
   // Per head of the block: 1 = write the activation, 0 = write nothing; and the element
   // offset of its BF16 cache row (-1 = no cache write).
   __shared__ int head_live[16];
@@ -232,7 +251,7 @@ __device__ __forceinline__ void qk_heads_wave_quad(const QKArgs<uint16_t> &a, lo
   const unsigned nq = (unsigned)a.tokens * (unsigned)a.hq;
   const unsigned nk = (unsigned)a.tokens * (unsigned)a.hkv;
   const unsigned total = nq + nk + (FMT >= 0 ? nk : 0u);
-  if constexpr (FMT == PADRA_KV_BF16) {
+  if constexpr (FMT == PADRA_KV_BF16 && !F32) {
     if (block0 >= nq + nk) { // wave-uniform
       v_rows_copy16(a, block0, nq, nk);
       return;
@@ -249,13 +268,13 @@ __device__ __forceinline__ void qk_heads_wave_quad(const QKArgs<uint16_t> &a, lo
   const int hh = live ? (int)(idx - (unsigned)t * heads) : 0;
   const PosState ps = fetch_state(a.pos, t);
 
-  // 1. Four coalesced loads per lane (clamped, unconditional), for the LDS image.
-  uint4 in[4];
+  // 1. PL coalesced loads per lane (clamped, unconditional), for the LDS image.
+  uint4 in[PL];
 #pragma unroll
-  for (int m = 0; m < 4; ++m) {
+  for (int m = 0; m < PL; ++m) {
     const int c = 64 * m + lane;
-    const unsigned hc = min(block0 + (unsigned)(c >> 4), total - 1u);
-    in[m] = ld_nt(reinterpret_cast<const uint4 *>(head_src(a, hc, nq, nk)) + (c & 15));
+    const unsigned hc = min(block0 + (unsigned)(c / CH), total - 1u);
+    in[m] = ld_nt(reinterpret_cast<const uint4 *>(head_src(a, hc, nq, nk)) + (c % CH));
   }
   // 2. The head's position (its control record was requested first), then the weight and
   // table loads, so that they are in flight with the data loads.
@@ -277,15 +296,21 @@ __device__ __forceinline__ void qk_heads_wave_quad(const QKArgs<uint16_t> &a, lo
   }
   // 3. The data into the image.
 #pragma unroll
-  for (int m = 0; m < 4; ++m) {
+  for (int m = 0; m < PL; ++m) {
     const int c = 64 * m + lane;
-    stage[quad_slot(4 * (c >> 4) + ((c & 15) >> 2), c & 3)] = in[m];
+    stage[quad_piece_slot<T>(4 * (c / CH) + (c % CH) / PL, c % PL)] = in[m];
   }
   __syncthreads();
-  Act32<uint16_t> x;
+  Act32<T> x;
 #pragma unroll
-  for (int p = 0; p < 4; ++p)
-    x.w[p] = stage[quad_slot(lane, p)];
+  for (int p = 0; p < PL; ++p) {
+    const uint4 v = stage[quad_piece_slot<T>(lane, p)];
+    if constexpr (F32)
+      x.f[p] = make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z),
+                           __uint_as_float(v.w));
+    else
+      x.w[p] = v;
+  }
 
   uint32_t out[16];
   const bool qk = live && ok && role < 2;
@@ -330,24 +355,48 @@ __device__ __forceinline__ void qk_heads_wave_quad(const QKArgs<uint16_t> &a, lo
     const bool enc = live && ok && role >= 1 && t >= a.first;
     const long long seq = a.pos.mode == PADRA_POS_DECODE ? t : 0;
     const long long slot = seq * a.seq_stride + (ok ? ring_slot(pos, max(a.cap, 1)) : 0);
-    uint32_t w16[16];
+    float xe[32];
 #pragma unroll
-    for (int i = 0; i < 16; ++i)
-      w16[i] = role == 1 ? out[i] : x.word(i);
+    for (int i = 0; i < 16; ++i) {
+      xe[2 * i] = role == 1 ? lo16(out[i]) : x.get(2 * i);
+      xe[2 * i + 1] = role == 1 ? hi16(out[i]) : x.get(2 * i + 1);
+    }
     if (role == 2)
-      encode_quad<FMT, true>(a, w16, slot, hh, g, enc);
+      encode_quad<FMT, true>(a, xe, slot, hh, g, enc);
     else
-      encode_quad<FMT, false>(a, w16, slot, hh, g, enc && role == 1);
+      encode_quad<FMT, false>(a, xe, slot, hh, g, enc && role == 1);
   }
   __syncthreads(); // every lane has read its input pieces: the image can be overwritten
 
-  // 4. Outputs back into the image, then four coalesced stores per lane.
+  // 4. Outputs back into the image, then coalesced stores.
+  const bool vcopy = FMT == PADRA_KV_BF16 && live && ok && role == 2 && t >= a.first;
   if (qk) {
 #pragma unroll
-    for (int p = 0; p < 4; ++p)
-      stage[quad_slot(lane, p)] = make_uint4(out[4 * p], out[4 * p + 1], out[4 * p + 2], out[4 * p + 3]);
+    for (int p = 0; p < PL; ++p) {
+      if constexpr (F32) {
+        const uint32_t l = out[2 * p], u = out[2 * p + 1];
+        stage[quad_piece_slot<T>(lane, p)] =
+            make_uint4(l << 16, l & 0xffff0000u, u << 16, u & 0xffff0000u);
+      } else {
+        stage[quad_piece_slot<T>(lane, p)] =
+            make_uint4(out[4 * p], out[4 * p + 1], out[4 * p + 2], out[4 * p + 3]);
+      }
+    }
   }
-  const bool vcopy = FMT == PADRA_KV_BF16 && live && ok && role == 2 && t >= a.first;
+  if constexpr (F32 && FMT == PADRA_KV_BF16) {
+    // The BF16 cache rows: rotated K, or V rounded to BF16 (the reference stores
+    // bf16(v), prefill_control.cuh:36-37).
+    if (role == 1 ? qk : vcopy) {
+#pragma unroll
+      for (int p = 0; p < 4; ++p) {
+        uint32_t w[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          w[i] = role == 1 ? out[4 * p + i] : pack2(x.get(8 * p + 2 * i), x.get(8 * p + 2 * i + 1));
+        stage[512 + quad_slot(lane, p)] = make_uint4(w[0], w[1], w[2], w[3]);
+      }
+    }
+  }
   const int features = a.hkv * D;
   if (g == 0) {
     head_live[lane >> 2] = (qk || vcopy) ? 1 : 0;
@@ -359,41 +408,62 @@ __device__ __forceinline__ void qk_heads_wave_quad(const QKArgs<uint16_t> &a, lo
     head_row[lane >> 2] = r;
   }
   __syncthreads();
+  if constexpr (F32) {
+    // fp32 activations of the Q and K heads: eight 1 KB stores per lane.
 #pragma unroll
-  for (int m = 0; m < 4; ++m) {
-    const int c = 64 * m + lane, j = c >> 4, ci = c & 15;
-    const unsigned hc = block0 + (unsigned)j;
-    if (!head_live[j])
-      continue; // past the end, or a head that writes nothing
-    const uint4 d = stage[quad_slot(4 * j + (ci >> 2), ci & 3)];
-    if constexpr (FMT == PADRA_KV_BF16) {
-      const long long r = head_row[j];
-      if (hc >= nq + nk) { // V head: cache only
-        st_nt(reinterpret_cast<uint4 *>(static_cast<uint16_t *>(a.vc) + r) + ci, d);
+    for (int m = 0; m < PL; ++m) {
+      const int c = 64 * m + lane, j = c / CH, ci = c % CH;
+      const unsigned hc = block0 + (unsigned)j;
+      if (!head_live[j] || hc >= nq + nk)
         continue;
+      const uint4 d = stage[quad_piece_slot<T>(4 * j + ci / PL, ci % PL)];
+      st_nt(reinterpret_cast<uint4 *>(const_cast<T *>(head_src(a, hc, nq, nk))) + ci, d);
+    }
+    if constexpr (FMT == PADRA_KV_BF16) {
+      // BF16 cache rows of the K and V heads: four 1 KB stores per lane.
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        const int c = 64 * m + lane, j = c >> 4, ci = c & 15;
+        const long long r = head_row[j];
+        if (!head_live[j] || r < 0)
+          continue;
+        const unsigned hc = block0 + (unsigned)j;
+        const uint4 d = stage[512 + quad_slot(4 * j + (ci >> 2), ci & 3)];
+        uint16_t *cache = static_cast<uint16_t *>(hc >= nq + nk ? a.vc : a.kc);
+        st_nt(reinterpret_cast<uint4 *>(cache + r) + ci, d);
       }
-      st_nt(reinterpret_cast<uint4 *>(const_cast<uint16_t *>(head_src(a, hc, nq, nk))) + ci, d);
-      if (r >= 0)
-        st_nt(reinterpret_cast<uint4 *>(static_cast<uint16_t *>(a.kc) + r) + ci, d);
-    } else {
-      st_nt(reinterpret_cast<uint4 *>(const_cast<uint16_t *>(head_src(a, hc, nq, nk))) + ci, d);
+    }
+  } else {
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const int c = 64 * m + lane, j = c >> 4, ci = c & 15;
+      const unsigned hc = block0 + (unsigned)j;
+      if (!head_live[j])
+        continue; // past the end, or a head that writes nothing
+      const uint4 d = stage[quad_slot(4 * j + (ci >> 2), ci & 3)];
+      if constexpr (FMT == PADRA_KV_BF16) {
+        const long long r = head_row[j];
+        if (hc >= nq + nk) { // V head: cache only
+          st_nt(reinterpret_cast<uint4 *>(static_cast<uint16_t *>(a.vc) + r) + ci, d);
+          continue;
+        }
+        st_nt(reinterpret_cast<uint4 *>(const_cast<uint16_t *>(head_src(a, hc, nq, nk))) + ci, d);
+        if (r >= 0)
+          st_nt(reinterpret_cast<uint4 *>(static_cast<uint16_t *>(a.kc) + r) + ci, d);
+      } else {
+        st_nt(reinterpret_cast<uint4 *>(const_cast<uint16_t *>(head_src(a, hc, nq, nk))) + ci, d);
+      }
     }
   }
 }
 
 // Head vectors per wave of each Q/K kernel variant.
-template <class T, int FMT> constexpr int qk_heads_per_wave() {
-  return std::is_same<T, uint16_t>::value ? 16 : 32;
-}
+template <class T, int FMT> constexpr int qk_heads_per_wave() { return 16; }
 
-// BF16 activations: four lanes per head; fp32 activations: two lanes per head.
+// Four lanes per head for both activation types.
 template <class T, int FMT>
 __device__ __forceinline__ void qk_heads_wave(const QKArgs<T> &a, long long wave, uint4 *lds) {
-  if constexpr (std::is_same<T, uint16_t>::value) {
-    qk_heads_wave_quad<FMT>(a, wave, lds);
-  } else {
-    qk_heads_wave_direct<T, FMT>(a, wave, lds);
-  }
+  qk_heads_wave_quad<T, FMT>(a, wave, lds);
 }
 
 } // namespace padra

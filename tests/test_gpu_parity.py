@@ -382,6 +382,67 @@ def test_store_extreme_value_scales(oracle, fmt):
         assert small.min() < 2.0 ** -100  # the division path ran
 
 
+@pytest.mark.parametrize("act", ["bf16", "f32"])
+@pytest.mark.parametrize("fmt", [abi.KV_Q8, abi.KV_Q8_0, abi.KV_Q8_0_NOROT])
+def test_store_nonfinite_heads(oracle, fmt, act):
+    """Non-finite K and V heads in the quantized stores (kv_q8.cuh:49-54,
+    kv_q8_native.cuh:70-79): the flag is raised and the head's codes and scales are not
+    written.  Token 3 head 1 has a NaN in K and V, token 10 head 2 infinities in both,
+    token 17 head 0 a NaN in V only.  The reference encodes K and V of a head together and
+    writes neither when one is invalid; the store here writes the valid K head of token 17,
+    so that K row is left out of the comparison.  The caches start filled with a pattern,
+    so that a row written with zero codes and scales differs from a row left alone; a
+    second launch with only the V head of token 17 invalid must raise the flag by itself."""
+    print(f"[case] store nonfinite fmt={fmt} act={act}", flush=True)
+    tokens, capacity = 40, 4096
+    d0 = synth.chain_inputs(tokens, outliers=False, seed=91 + fmt)
+    tb = table_bits(oracle, capacity)
+    positions = np.arange(tokens, dtype=np.int32)
+    conv = (lambda a: torch.from_numpy(synth.bf16_to_f32(a)).cuda()) if act == "f32" else dev
+    fill_code, fill_scale = 0x5A, 7.0
+
+    def run(both):
+        d = dict(d0)
+        k, v = d0["k"].view(np.uint16).copy(), d0["v"].view(np.uint16).copy()
+        if both:
+            k[3, 1, 5], v[3, 1, 77] = 0x7FC0, 0x7FC0
+            k[10, 2, 0], v[10, 2, 127] = 0x7F80, 0xFF80
+        v[17, 0, 64] = 0x7FC0
+        d["k"], d["v"] = k.view(d0["k"].dtype), v.view(d0["v"].dtype)
+        _, wk, _ = _qk_oracle(oracle, d, tb, positions)
+        width = 512 if fmt == abi.KV_Q8 else 544
+        kind = np.int8 if fmt == abi.KV_Q8 else np.uint8
+        ek, ev = np.full((capacity, width), fill_code, kind), np.full((capacity, width), fill_code, kind)
+        es = None
+        if fmt == abi.KV_Q8:
+            es = np.full((capacity, 4, 2), fill_scale, np.float32)
+            assert oracle.kv_q8_encode(wk, d["v"], ek, ev, es, positions, capacity, 0)
+        else:
+            assert oracle.kv_q8_0_encode(wk, d["v"], ek, ev, positions, capacity, 0,
+                                         rotate=(fmt == abi.KV_Q8_0))
+        kc, vc, sc = _alloc_cache(fmt, capacity)
+        kc.fill_(fill_code)
+        vc.fill_(fill_code)
+        if sc is not None:
+            sc.fill_(fill_scale)
+        bad = flag()
+        kv = ops.kv_cache(fmt, kc, vc, capacity, scales=sc)
+        ops.QKNormRopeStore(conv(d["q"]), conv(d["k"]), dev(d["qn"]), dev(d["kn"]), dev(tb),
+                            ops.positions_base(0), bad, v=conv(d["v"]), kv=kv)
+        torch.cuda.synchronize()
+        assert bad.item()
+        rows = np.arange(capacity) != 17
+        assert np.array_equal(_np(vc, fmt), ev)
+        assert np.array_equal(_np(kc, fmt)[rows], ek[rows])
+        if es is not None:
+            got = sc.cpu().numpy()
+            assert np.array_equal(got[..., 1], es[..., 1])
+            assert np.array_equal(got[rows, :, 0], es[rows, :, 0])
+
+    run(True)
+    run(False)
+
+
 @pytest.mark.parametrize("fmt", FORMATS)
 @pytest.mark.parametrize("tokens,base,cap", [(300, 1000, 4096), (1500, 100, 1024)])
 def test_qk_rope_store_f32_activations(oracle, fmt, tokens, base, cap):
