@@ -294,6 +294,42 @@ def bench_swiglu(torch, steps, sets=4):
             "rows_per_s": round(d["gate"].shape[0] / (ms * 1e-3), 1)}
 
 
+def bench_f32_layer(torch, steps, sets=8):
+    """The config-1 chunk in the reference's own activation form (fp32 buffers holding
+    BF16-exact values, PADRA_ACT_F32), launched as the reference launches it: the residual
+    + RMSNorm, then the Q/K norm + RoPE + BF16 KV store.  Each launch is timed alone."""
+    from padra_amd import abi, ops, synth
+    host = synth.chain_inputs(TOKENS, HIDDEN, HQ, HKV, D, outliers=True, seed=0)
+    f32 = lambda a: torch.from_numpy(synth.bf16_to_f32(a)).cuda()
+    b16 = lambda a: torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).cuda()
+    table = torch.from_numpy(ops.RopeTable(TOKENS, D, 1e6).view(torch.int16).numpy()).cuda()
+    g, qn, kn = b16(host["gamma"]), b16(host["qn"]), b16(host["kn"])
+    bad = torch.zeros(1, dtype=torch.int32, device="cuda")
+    bufs = []
+    for _ in range(sets):
+        x = f32(host["x"])
+        kc = torch.empty((CAPACITY, HKV * D), dtype=torch.int16, device="cuda")
+        bufs.append((x, f32(host["residual"]), torch.empty_like(x), f32(host["q"]),
+                     f32(host["k"]), f32(host["v"]), ops.kv_cache(abi.KV_BF16, kc, torch.empty_like(kc),
+                                                                  CAPACITY), kc))
+    norm_ms = graph_time(torch, lambda i: ops.ResidualPostNorm(*bufs[i % sets][:3], g, bad), steps)
+    qk_ms = graph_time(torch, lambda i: ops.QKNormRopeStore(
+        bufs[i % sets][3], bufs[i % sets][4], qn, kn, table, ops.positions_base(0), bad,
+        v=bufs[i % sets][5], kv=bufs[i % sets][6]), steps)
+    if bad.item():
+        raise SystemExit("device error flag set in the fp32-activation benchmark")
+    norm_bytes = TOKENS * HIDDEN * 4 * 4
+    qk_bytes = TOKENS * (((HQ + 2 * HKV) + (HQ + HKV)) * D * 4 + 2 * HKV * D * 2 + 2 * D)
+    rate = lambda b, ms: round(b / (ms * 1e-3) / 1e9, 2)
+    return {"workload": "config1 chunk with fp32 activations: residual+RMSNorm, then "
+                        "QK-norm+RoPE+BF16 KV store (two launches)",
+            "norm_us": round(norm_ms * 1e3, 3), "norm_bytes": norm_bytes,
+            "norm_gbs": rate(norm_bytes, norm_ms),
+            "qk_us": round(qk_ms * 1e3, 3), "qk_bytes": qk_bytes, "qk_gbs": rate(qk_bytes, qk_ms),
+            "gbs": rate(norm_bytes + qk_bytes, norm_ms + qk_ms),
+            "frac": round((norm_bytes + qk_bytes) / ((norm_ms + qk_ms) * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+
+
 def bench_norm_fp8(torch, steps, sets=8):
     """The input RMSNorm with its FP8 E4M3 row encoding (the QKV GEMM's input) over the
     config-1 chunk: 2048 rows of 2048; reads x, writes normalized (BF16) and codes."""
@@ -563,6 +599,7 @@ def main():
         line["configs"] = {"config3": bench_swiglu(torch, 50),
                            "config4": bench_decode(torch, 100, 64),
                            "config0_gpu": bench_decode(torch, 200, 1, capacity=8192),
+                           "config1_f32_activations": bench_f32_layer(torch, 200),
                            "norm_fp8": bench_norm_fp8(torch, 200),
                            "combine_norm": bench_combine_norm(torch, 100),
                            "attention": bench_attention(torch, 10),
