@@ -483,13 +483,20 @@ def bench_decode(torch, steps, seqs, vocab=131072, capacity=CAPACITY):
     def step(i):
         ops.Embed(tbl, x, bad, positions=pos)
         ops.ResidualNormQKRopeStore(x, r, y, g, q, k, v, qn, kn, rope, pos, kv, bad, tree=256)
+
+    def fused_step(i):
+        ops.EmbedResidualNormQKRopeStore(tbl, None, x, r, y, g, q, k, v, qn, kn, rope, pos, kv,
+                                         bad, tree=256)
     ms = graph_time(torch, step, steps)
+    fused_ms = graph_time(torch, fused_step, steps)
     if bad.item():
         raise SystemExit("device error flag set in the decode benchmark")
     nbytes = seqs * (2 * 2 * HIDDEN + chain_bytes("bf16"))
     return {"workload": f"{'config4' if seqs > 1 else 'config0'}: decode step of {seqs} "
                         "sequence(s): gather + fused chain (256-thread tree), ragged positions",
             "us_per_step": round(ms * 1e3, 3), "tokens_per_s": round(seqs / (ms * 1e-3), 1),
+            "fused_us_per_step": round(fused_ms * 1e3, 3),
+            "fused_tokens_per_s": round(seqs / (fused_ms * 1e-3), 1),
             "bytes_per_step": nbytes, "gbs": round(nbytes / (ms * 1e-3) / 1e9, 2)}
 
 

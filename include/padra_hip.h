@@ -179,6 +179,21 @@ int padra_ResidualNormQKRopeStore(void *stream, void *x, const void *residual,
                                   const padra_Positions *pos, int tokens, int q_heads,
                                   int kv_heads, int head_dim, float eps,
                                   const padra_KVCache *kv, int *bad);
+/* padra_EmbedResidualNormQKRopeStore: padra_Embed (BF16 output into x, same positions)
+ * followed by padra_ResidualNormQKRopeStore, in one launch: the norm rows read row t of x
+ * from embed[token_t] instead of from x.  The layer-0 decode step, EmbedControlled
+ * (decode_control.cuh:68-79) then the residual norm and QKNormRopeStoreControlled;
+ * exact-fusions-v1 runs them as separate kernels.  Results, including x and the flag for
+ * an invalid token (that row reads x as it was), are bit-identical to the two calls. */
+int padra_EmbedResidualNormQKRopeStore(void *stream, const uint16_t *embed, int vocab,
+                                       const int32_t *ids, void *x, const void *residual,
+                                       void *normalized, const uint16_t *gamma, int hidden,
+                                       int tree, float *statistics, void *q, void *k,
+                                       const void *v, const uint16_t *qn, const uint16_t *kn,
+                                       const uint16_t *table, int table_rows,
+                                       const padra_Positions *pos, int tokens, int q_heads,
+                                       int kv_heads, int head_dim, float eps,
+                                       const padra_KVCache *kv, int *bad);
 
 /* ---- KV store, commit, decode ---------------------------------------------------------
  * padra_KVStore: the cache writers without the Q/K norm -- StorePrefillControlled /

@@ -72,6 +72,9 @@ SIGNATURES = {
     "padra_ResidualNormQKRopeStore": [_P, _P, _P, _P, _P, _I, _I, _P, _P, _P, _P, _P, _P, _P, _I,
                                       ctypes.POINTER(Positions), _I, _I, _I, _I, _F,
                                       ctypes.POINTER(KVCache), _P],
+    "padra_EmbedResidualNormQKRopeStore": [_P, _P, _I, _P, _P, _P, _P, _P, _I, _I, _P, _P, _P,
+                                           _P, _P, _P, _P, _I, ctypes.POINTER(Positions), _I,
+                                           _I, _I, _I, _F, ctypes.POINTER(KVCache), _P],
     "padra_KVStore": [_P, _P, _P, ctypes.POINTER(Positions), _I, _I, _I, ctypes.POINTER(KVCache),
                       _P, _I],
     "padra_KVCommit": [_P, ctypes.POINTER(KVCache), ctypes.POINTER(KVCache),

@@ -244,6 +244,29 @@ struct PosSrc {
   const padra_DecodeState *decode;
 };
 
+// The token of embedding row t (Embed / EmbedPrefillControlled / EmbedControlled,
+// inference.cu:181-187, prefill_control.cuh:3-22, decode_control.cuh:68-79): ids[t]
+// (PADRA_POS_BASE), ids[prompt_offset + t] under a valid PrefillState, or the ready
+// DecodeState t's token.  ok is false for an invalid state or a token outside [0, vocab).
+__device__ __forceinline__ int embed_token(const PosSrc &src, const int32_t *ids, int t,
+                                           int vocab, bool &ok) {
+  int token = -1;
+  ok = true;
+  if (src.mode == PADRA_POS_BASE) {
+    token = ids[t];
+  } else if (src.mode == PADRA_POS_PREFILL) {
+    const padra_PrefillState s = load_state(src.prefill);
+    ok = prefill_valid(s, src.tokens, s.capacity, src.epoch, src.maximum);
+    token = ok ? ids[s.prompt_offset + t] : -1;
+  } else {
+    const padra_DecodeState s = load_state(src.decode + t);
+    ok = decode_ready(s, src.maximum, src.vocab);
+    token = ok ? s.token : -1;
+  }
+  ok = ok && token >= 0 && token < vocab;
+  return token;
+}
+
 // The control record token t's position depends on (PADRA_POS_PREFILL: the chunk's
 // PrefillState; PADRA_POS_DECODE: sequence t's DecodeState).  Fetched apart from
 // resolve_position so that a kernel can put the load in flight before its data loads.

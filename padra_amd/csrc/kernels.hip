@@ -99,13 +99,14 @@ template <int J, class T> __global__ __launch_bounds__(64) void k_norm_fp8(NormF
 // (Bresenham interleave) or over its first half: the early grid streams the four norm
 // tensors alone, and the VALU-heavier Q/K waves follow as norm waves retire.  Putting the
 // Q/K waves first measured 15% slower.
-template <int VT, int J, int FMT>
+// GATHER: the norm rows read their x from the embedding table (the fused decode step).
+template <int VT, int J, int FMT, bool GATHER = false>
 __global__ __launch_bounds__(64) PADRA_WAVES_PER_EU void k_chain(NormArgs<uint16_t> n, QKArgs<uint16_t> q,
                                               long long norm_waves, long long waves) {
   __shared__ uint4 lds[256];
   const long long b = blockIdx.x;
   if (b < norm_waves)
-    norm_row_wave<VT, J, uint16_t, true, false>(n, (int)b, nullptr);
+    norm_row_wave<VT, J, uint16_t, true, false, GATHER>(n, (int)b, nullptr);
   else if (b < waves) {
     // Rotated q8_0: the K and V blocks (Hadamard rotation + encoding, the heaviest Q/K
     // waves) are dispatched before the Q blocks instead of last, so they do not form the
@@ -432,12 +433,16 @@ extern "C" int padra_QKNormRopeStore(void *stream, void *q, void *k, const void 
   return act == PADRA_ACT_BF16 ? launch(uint16_t{}) : launch(float{});
 }
 
-extern "C" int padra_ResidualNormQKRopeStore(
-    void *stream, void *x, const void *residual, void *normalized, const uint16_t *gamma,
-    int hidden, int tree, float *statistics, void *q, void *k, const void *v,
-    const uint16_t *qn, const uint16_t *kn, const uint16_t *table, int table_rows,
-    const padra_Positions *pos, int tokens, int q_heads, int kv_heads, int head_dim, float eps,
-    const padra_KVCache *kv, int *bad) {
+namespace {
+
+// The fused chain launch; with `gather` (non-null) the norm rows take x from the embedding
+// table as padra_Embed would have written it.
+int chain(hipStream_t s, const uint16_t *gather, int vocab, const int32_t *ids, void *x,
+          const void *residual, void *normalized, const uint16_t *gamma, int hidden, int tree,
+          float *statistics, void *q, void *k, const void *v, const uint16_t *qn,
+          const uint16_t *kn, const uint16_t *table, int table_rows, const padra_Positions *pos,
+          int tokens, int q_heads, int kv_heads, int head_dim, float eps,
+          const padra_KVCache *kv, int *bad) {
   int st = check_norm(x, normalized, gamma, tokens, hidden, eps, tree, bad, PADRA_ACT_BF16);
   if (st)
     return st;
@@ -447,7 +452,6 @@ extern "C" int padra_ResidualNormQKRopeStore(
                 kv, bad, PADRA_ACT_BF16);
   if (st)
     return st;
-  const hipStream_t s = static_cast<hipStream_t>(stream);
   NormArgs<uint16_t> n;
   n.x = static_cast<uint16_t *>(x);
   n.residual = static_cast<const uint16_t *>(residual);
@@ -457,6 +461,25 @@ extern "C" int padra_ResidualNormQKRopeStore(
   n.bad = bad;
   n.rows = tokens;
   n.eps = eps;
+  if (gather) {
+    // padra_Embed's token source for the same positions.
+    if (vocab < 1 || !aligned16(gather))
+      return PADRA_INVALID_ARGUMENT;
+    n.gather = gather;
+    n.ids = ids;
+    n.vocab = vocab;
+    n.src.mode = pos ? pos->mode : PADRA_POS_BASE;
+    n.src.tokens = tokens;
+    if (pos) {
+      n.src.maximum = pos->maximum;
+      n.src.vocab = pos->vocab;
+      n.src.epoch = pos->binding_epoch;
+      n.src.prefill = pos->prefill;
+      n.src.decode = pos->decode;
+    }
+    if ((n.src.mode == PADRA_POS_BASE || n.src.mode == PADRA_POS_PREFILL) && !ids)
+      return PADRA_INVALID_ARGUMENT;
+  }
   const QKArgs<uint16_t> a = make_qk<uint16_t>(q, k, v, qn, kn, table, table_rows, pos, tokens,
                                                q_heads, kv_heads, eps, kv, bad);
   const long long norm_waves = (tokens + rows_per_wave(tree) - 1) / rows_per_wave(tree);
@@ -466,20 +489,54 @@ extern "C" int padra_ResidualNormQKRopeStore(
   return with_format(kv, [&](auto fmt) -> int {
     const long long waves = norm_waves + qk_waves(tokens, q_heads, kv_heads, kv != nullptr,
                                                   qk_heads_per_wave<uint16_t, fmt.value>());
-    if (tree == 128 && j == 16)
-      hipLaunchKernelGGL((k_chain<128, 16, fmt.value>), dim3((unsigned)waves), dim3(64), 0, s, n, a,
-                         norm_waves, waves);
-    else if (tree == 128)
-      hipLaunchKernelGGL((k_chain<128, 18, fmt.value>), dim3((unsigned)waves), dim3(64), 0, s, n, a,
-                         norm_waves, waves);
-    else if (j == 8)
-      hipLaunchKernelGGL((k_chain<256, 8, fmt.value>), dim3((unsigned)waves), dim3(64), 0, s, n, a,
-                         norm_waves, waves);
-    else
-      hipLaunchKernelGGL((k_chain<256, 9, fmt.value>), dim3((unsigned)waves), dim3(64), 0, s, n, a,
-                         norm_waves, waves);
+    const dim3 grid((unsigned)waves), block(64);
+    if (gather) {
+      if (tree == 128 && j == 16)
+        hipLaunchKernelGGL((k_chain<128, 16, fmt.value, true>), grid, block, 0, s, n, a, norm_waves, waves);
+      else if (tree == 128)
+        hipLaunchKernelGGL((k_chain<128, 18, fmt.value, true>), grid, block, 0, s, n, a, norm_waves, waves);
+      else if (j == 8)
+        hipLaunchKernelGGL((k_chain<256, 8, fmt.value, true>), grid, block, 0, s, n, a, norm_waves, waves);
+      else
+        hipLaunchKernelGGL((k_chain<256, 9, fmt.value, true>), grid, block, 0, s, n, a, norm_waves, waves);
+    } else {
+      if (tree == 128 && j == 16)
+        hipLaunchKernelGGL((k_chain<128, 16, fmt.value>), grid, block, 0, s, n, a, norm_waves, waves);
+      else if (tree == 128)
+        hipLaunchKernelGGL((k_chain<128, 18, fmt.value>), grid, block, 0, s, n, a, norm_waves, waves);
+      else if (j == 8)
+        hipLaunchKernelGGL((k_chain<256, 8, fmt.value>), grid, block, 0, s, n, a, norm_waves, waves);
+      else
+        hipLaunchKernelGGL((k_chain<256, 9, fmt.value>), grid, block, 0, s, n, a, norm_waves, waves);
+    }
     return launched();
   });
+}
+
+} // namespace
+
+extern "C" int padra_ResidualNormQKRopeStore(
+    void *stream, void *x, const void *residual, void *normalized, const uint16_t *gamma,
+    int hidden, int tree, float *statistics, void *q, void *k, const void *v,
+    const uint16_t *qn, const uint16_t *kn, const uint16_t *table, int table_rows,
+    const padra_Positions *pos, int tokens, int q_heads, int kv_heads, int head_dim, float eps,
+    const padra_KVCache *kv, int *bad) {
+  return chain(static_cast<hipStream_t>(stream), nullptr, 0, nullptr, x, residual, normalized,
+               gamma, hidden, tree, statistics, q, k, v, qn, kn, table, table_rows, pos, tokens,
+               q_heads, kv_heads, head_dim, eps, kv, bad);
+}
+
+extern "C" int padra_EmbedResidualNormQKRopeStore(
+    void *stream, const uint16_t *embed, int vocab, const int32_t *ids, void *x,
+    const void *residual, void *normalized, const uint16_t *gamma, int hidden, int tree,
+    float *statistics, void *q, void *k, const void *v, const uint16_t *qn, const uint16_t *kn,
+    const uint16_t *table, int table_rows, const padra_Positions *pos, int tokens, int q_heads,
+    int kv_heads, int head_dim, float eps, const padra_KVCache *kv, int *bad) {
+  if (!embed)
+    return PADRA_INVALID_ARGUMENT;
+  return chain(static_cast<hipStream_t>(stream), embed, vocab, ids, x, residual, normalized,
+               gamma, hidden, tree, statistics, q, k, v, qn, kn, table, table_rows, pos, tokens,
+               q_heads, kv_heads, head_dim, eps, kv, bad);
 }
 
 extern "C" int padra_Tune(int knob, int value) {

@@ -32,6 +32,13 @@ template <class T> struct NormArgs {
   int *bad;
   int rows;
   float eps;
+  // Embedding gather in front of the residual add (the fused decode step): row t's x is
+  // gather[token_t] ([vocab][H] BF16); a row whose token is invalid raises the flag and
+  // reads x as it is, as the separate gather launch would have left it.
+  const uint16_t *gather = nullptr;
+  const int32_t *ids = nullptr;
+  int vocab = 0;
+  PosSrc src{};
 };
 
 // Largest |y| whose BF16 rounding stays finite: 0x7f7f8000 is the midpoint between the
@@ -157,6 +164,27 @@ __device__ __forceinline__ void norm_load(const NormArgs<T> &a, int row, RowIn<V
     if constexpr (RES)
       in.r[j].load(a.residual + off + VT * j);
   }
+}
+
+// norm_load with the embedding gather: the residual loads first, then the token (its
+// control record) and the embedding row.
+template <int VT, int J>
+__device__ __forceinline__ void norm_load_gather(const NormArgs<uint16_t> &a, int row,
+                                                 RowIn<VT, J, uint16_t> &in) {
+  constexpr int K = VT / 64, H = VT * J;
+  const int lane = threadIdx.x & 63;
+  const size_t off = (size_t)row * H + K * lane;
+#pragma unroll
+  for (int j = 0; j < J; ++j)
+    in.r[j].load(a.residual + off + VT * j);
+  bool ok;
+  const int token = embed_token(a.src, a.ids, row, a.vocab, ok);
+  if (!ok && lane == 0)
+    raise_bad(a.bad);
+  const uint16_t *src = ok ? a.gather + (size_t)token * H + K * lane : a.x + off;
+#pragma unroll
+  for (int j = 0; j < J; ++j)
+    in.x[j].load(src + VT * j);
 }
 
 template <int VT, int J>
@@ -335,7 +363,7 @@ __device__ __forceinline__ void norm_row_wave_wide(const NormArgs<uint16_t> &a, 
 // (padra_ResidualPostNorm) the wide form is faster (2048 x 2048: 7.3 -> 7.0 us); inside the
 // fused chain, where the Q/K waves follow, it measured slower (12.75 -> 13.15 us), so the
 // chain keeps the ownership layout.
-template <int VT, int J, class T, bool RES, bool WIDE = true>
+template <int VT, int J, class T, bool RES, bool WIDE = true, bool GATHER = false>
 __device__ __forceinline__ void norm_row_wave(const NormArgs<T> &a, int row, uint4 *lds) {
   if (row >= a.rows)
     return; // wave-uniform
@@ -345,7 +373,12 @@ __device__ __forceinline__ void norm_row_wave(const NormArgs<T> &a, int row, uin
   }
   RowIn<VT, J, T> in;
   Lanes<uint16_t, VT / 64> gr[J];
-  norm_load<VT, J, T, RES>(a, row, in);
+  if constexpr (GATHER) {
+    static_assert(RES && std::is_same<T, uint16_t>::value, "gather: BF16 residual rows");
+    norm_load_gather<VT, J>(a, row, in);
+  } else {
+    norm_load<VT, J, T, RES>(a, row, in);
+  }
   norm_load_gamma<VT, J>(a.gamma, gr);
   norm_compute<VT, J, T, RES>(a, row, in, gr);
 }

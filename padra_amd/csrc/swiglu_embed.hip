@@ -105,20 +105,9 @@ template <class O>
 __global__ __launch_bounds__(64) void k_embed(const uint16_t *table, const int32_t *ids, O *out,
                                               int hidden, int vocab, PosSrc src, int *bad) {
   const int t = blockIdx.x, lane = threadIdx.x & 63;
-  int token = -1;
-  bool ok = true;
-  if (src.mode == PADRA_POS_BASE) {
-    token = ids[t];
-  } else if (src.mode == PADRA_POS_PREFILL) {
-    const padra_PrefillState s = load_state(src.prefill);
-    ok = prefill_valid(s, src.tokens, s.capacity, src.epoch, src.maximum);
-    token = ok ? ids[s.prompt_offset + t] : -1;
-  } else {
-    const padra_DecodeState s = load_state(src.decode + t);
-    ok = decode_ready(s, src.maximum, src.vocab);
-    token = ok ? s.token : -1;
-  }
-  if (!ok || token < 0 || token >= vocab) {
+  bool ok;
+  const int token = embed_token(src, ids, t, vocab, ok);
+  if (!ok) {
     if (lane == 0)
       raise_bad(bad);
     return;

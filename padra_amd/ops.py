@@ -185,6 +185,21 @@ def ResidualNormQKRopeStore(x, residual, normalized, gamma, q, k, v, qn, kn, tab
              kv_heads, head_dim, float(eps), None if kv is None else ctypes.byref(kv), _p(bad))
 
 
+def EmbedResidualNormQKRopeStore(embed, ids, x, residual, normalized, gamma, q, k, v, qn, kn,
+                                 table, positions: abi.Positions, kv: abi.KVCache | None, bad,
+                                 eps=1e-6, tree=abi.TREE_256, statistics=None):
+    """Embed (x <- embed[token]) then ResidualNormQKRopeStore, in one launch."""
+    _need_cuda(embed, ids, x, residual, normalized, gamma, q, k, v, qn, kn, table, bad, statistics)
+    tokens, q_heads, kv_heads, head_dim = _shape_qk(q, k)
+    if x.shape[0] != tokens or embed.shape[-1] != x.shape[-1]:
+        raise ValueError("x rows must equal the token count and embed rows x's width")
+    abi.call("padra_EmbedResidualNormQKRopeStore", _stream(x), _p(embed), embed.shape[0],
+             _p(ids), _p(x), _p(residual), _p(normalized), _p(gamma), x.shape[-1], int(tree),
+             _p(statistics), _p(q), _p(k), _p(v), _p(qn), _p(kn), _p(table), table.shape[0],
+             ctypes.byref(positions), tokens, q_heads, kv_heads, head_dim, float(eps),
+             None if kv is None else ctypes.byref(kv), _p(bad))
+
+
 def KVStore(k, v, positions: abi.Positions, kv: abi.KVCache, bad):
     """Store / encode K [T][Hkv][D] (already rotated) and V rows into the cache."""
     _need_cuda(k, v, bad)

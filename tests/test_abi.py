@@ -165,5 +165,12 @@ def test_host_validation_newer_entry_points():
     # the self-checks need their count buffers; the streaming copy whole 16-byte units
     assert lib.padra_CheckQ8Path(None, None) == abi.INVALID_ARGUMENT
     assert lib.padra_CheckFP8Paths(None, None) == abi.INVALID_ARGUMENT
+    # fused gather + chain: the embedding table is required
+    base = abi.Positions(mode=abi.POS_BASE, base=0, prefill=None, decode=None, maximum=4096,
+                         vocab=1000, binding_epoch=1)
+    assert lib.padra_EmbedResidualNormQKRopeStore(
+        None, None, 1000, _p(160), _p(16), _p(32), _p(48), _p(64), 2048, 256, None, _p(80),
+        _p(96), None, _p(112), _p(128), _p(144), 4096, ctypes.byref(base), 1, 16, 4, 128, 1e-6,
+        None, bad) == abi.INVALID_ARGUMENT
     assert lib.padra_StreamCopy(None, _p(16), _p(32), 24) == abi.INVALID_ARGUMENT
     assert lib.padra_StreamCopy(None, _p(16), _p(40), 32) == abi.INVALID_ARGUMENT

@@ -721,3 +721,67 @@ def test_stream_copy():
         assert torch.equal(src, dst), n
     with pytest.raises(abi.PadraError):
         abi.call("padra_StreamCopy", None, dst.data_ptr(), src.data_ptr(), 24)
+
+
+@pytest.mark.parametrize("mode,fmt", [("decode", abi.KV_BF16), ("decode", abi.KV_Q8_0),
+                                      ("base", abi.KV_BF16)])
+def test_embed_chain_matches_gather_then_chain(oracle, mode, fmt):
+    """padra_EmbedResidualNormQKRopeStore against padra_Embed followed by
+    padra_ResidualNormQKRopeStore on the same inputs: x, normalized, q, k, the caches and
+    the flag bit-identical; x and normalized also against the oracle's residual norm of the
+    gathered rows.  Decode: 64 sequences at ragged positions with per-sequence caches, one
+    of them holding a token outside the vocabulary (the flag is raised and that row reads
+    x as it was); base: token ids from an array."""
+    print(f"[case] embed chain mode={mode} fmt={fmt}", flush=True)
+    seqs, capacity, vocab, hidden = 64, 2048, 1000, 2048
+    rng = np.random.default_rng(123)
+    d = synth.chain_inputs(seqs, outliers=True, seed=124)
+    emb = synth.bf16_bits((rng.standard_normal((vocab, hidden)) * 0.5).astype(np.float32))
+    ids = rng.integers(0, vocab, seqs).astype(np.int32)
+    positions = rng.integers(0, capacity, seqs).astype(np.int32)
+    tb = ops.RopeTable(capacity, 128, 1e6).view(torch.int16).numpy().view(np.uint16)
+    states = np.zeros((seqs, 8), np.int32)
+    for i, p in enumerate(positions):
+        states[i] = [ids[i], p, capacity, 10, p, min(int(p), 1024), 0, 0]
+    invalid = 5 if mode == "decode" else None
+    if invalid is not None:
+        states[invalid, 0] = vocab  # outside [0, vocab)
+
+    def run(fused):
+        x, r, y = dev(d["x"]), dev(d["residual"]), torch.empty((seqs, hidden), dtype=torch.int16, device="cuda")
+        q, k = dev(d["q"]), dev(d["k"])
+        rows = seqs * capacity if mode == "decode" else capacity
+        kc, vc, sc = _cache(fmt, rows)
+        st = dev(states)
+        bad = flag()
+        if mode == "decode":
+            pos = ops.positions_decode(st, maximum=capacity, vocab=vocab)
+            kv = ops.kv_cache(fmt, kc, vc, capacity, scales=sc, seq_stride=capacity)
+        else:
+            pos = ops.positions_base(100)
+            kv = ops.kv_cache(fmt, kc, vc, capacity, scales=sc)
+        args = (x, dev(d["residual"]), y, dev(d["gamma"]), q, k, dev(d["v"]), dev(d["qn"]),
+                dev(d["kn"]), dev(tb), pos, kv, bad)
+        table, idt = dev(emb), dev(ids)
+        if fused:
+            ops.EmbedResidualNormQKRopeStore(table, idt, *args, tree=abi.TREE_256)
+        else:
+            ops.Embed(table, x, bad, ids=idt, positions=pos)
+            ops.ResidualNormQKRopeStore(*args, tree=abi.TREE_256)
+        torch.cuda.synchronize()
+        out = [host16(x), host16(y), host16(q), host16(k), kc.cpu().numpy(), vc.cpu().numpy(),
+               int(bad.item())]
+        if sc is not None:
+            out.append(sc.cpu().numpy())
+        return out
+
+    fused, split = run(True), run(False)
+    for a, b in zip(fused, split):
+        assert np.array_equal(a, b)
+    assert fused[6] == (1 if invalid is not None else 0)
+    xin = emb[ids].copy()
+    if invalid is not None:
+        xin[invalid] = d["x"].reshape(seqs, hidden)[invalid]
+    wx, wy, _, _ = oracle.residual_rmsnorm(xin, d["residual"].reshape(seqs, hidden),
+                                           d["gamma"], threads=256)
+    assert np.array_equal(fused[0], wx) and np.array_equal(fused[1], wy)
