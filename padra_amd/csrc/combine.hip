@@ -91,25 +91,34 @@ __global__ __launch_bounds__(256) void k_combine(T *x, const T *down, const floa
     raise_bad(bad);
 }
 
-// Combine + RMSNorm (+ FP8): one wave per row.  The combine runs in the natural layout
-// (lane l takes columns 8l..8l+7 of each 512-column chunk, 16-byte accesses), its BF16
-// results go through LDS, and the norm reads them back in the 128-thread ownership layout
-// (lane l: columns 2l, 2l+1 of each 128).
-template <int J, class T, bool FP8>
-__global__ __launch_bounds__(64) void k_combine_norm(T *x, const T *down, const float *weights,
-                                                     NormFP8Args<T> a) {
+// Waves per row of the combine + norm kernel.  The row's 36 sixteen-byte loads per lane
+// (8 expert rows and x, four 512-column chunks at H = 2048) do not fit one wave's registers
+// at once, so one wave per row loaded them in dependent rounds; four waves, one chunk
+// each, put them all in flight: 2048 x 2048 with FP8, 21.1 -> 19.3 us.  Finishing the
+// norm in every wave (each storing a quarter of the row after the same reductions)
+// measured slower (22.6 us), so wave 0 finishes the row alone.
+constexpr int kCombineWaves = 4;
+
+// Combine + RMSNorm (+ FP8): W waves per row.  The combine runs in the natural layout
+// (lane l takes columns 8l..8l+7 of each 512-column chunk, 16-byte accesses; wave w takes
+// chunks w, w + W, ...), its BF16 results go through LDS, and wave 0 reads them back in
+// the 128-thread ownership layout (lane l: columns 2l, 2l+1 of each 128) for the norm.
+template <int J, class T, bool FP8, int W>
+__global__ __launch_bounds__(64 * W) void k_combine_norm(T *x, const T *down, const float *weights,
+                                                         NormFP8Args<T> a) {
   constexpr int H = 128 * J, CHUNKS = (H + 511) / 512;
   __shared__ uint32_t v_lds[H / 2];
-  const int row = blockIdx.x, lane = threadIdx.x & 63;
+  const int row = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   if (row >= a.rows)
-    return;
+    return; // block-uniform
   Lanes<uint16_t, 2> gr[J];
-  norm_load_gamma<128, J>(a.gamma, gr);
+  if (wave == 0)
+    norm_load_gamma<128, J>(a.gamma, gr);
   bool fine = true;
 #pragma unroll
-  for (int ch = 0; ch < CHUNKS; ++ch) {
-    const int col = ch * 512 + 8 * lane;
-    if (col < H) {
+  for (int i = 0; i < (CHUNKS + W - 1) / W; ++i) {
+    const int ch = wave + W * i, col = ch * 512 + 8 * lane;
+    if (ch < CHUNKS && col < H) {
       T *xr = x + (size_t)row * H + col;
       uint32_t out[4];
       bool f;
@@ -125,6 +134,8 @@ __global__ __launch_bounds__(64) void k_combine_norm(T *x, const T *down, const 
   if (__ballot(!fine) != 0 && lane == 0)
     raise_bad(a.bad);
   __syncthreads();
+  if (wave != 0)
+    return;
   uint32_t vp[J];
 #pragma unroll
   for (int j = 0; j < J; ++j)
@@ -261,10 +272,12 @@ extern "C" int padra_CombineNorm(void *stream, void *x, const void *down, const 
     a.eps = eps;
     return combine_shape(hidden, [&](auto j) -> int {
       if (packed)
-        hipLaunchKernelGGL((k_combine_norm<j.value, T, true>), dim3(rows), dim3(64), 0, s,
+        hipLaunchKernelGGL((k_combine_norm<j.value, T, true, kCombineWaves>), dim3(rows),
+                           dim3(64 * kCombineWaves), 0, s,
                            static_cast<T *>(x), static_cast<const T *>(down), weights, a);
       else
-        hipLaunchKernelGGL((k_combine_norm<j.value, T, false>), dim3(rows), dim3(64), 0, s,
+        hipLaunchKernelGGL((k_combine_norm<j.value, T, false, kCombineWaves>), dim3(rows),
+                           dim3(64 * kCombineWaves), 0, s,
                            static_cast<T *>(x), static_cast<const T *>(down), weights, a);
       return launched("CombineNorm");
     });
