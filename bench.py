@@ -587,7 +587,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": traffic_from_profiles(formats[0]),
-                     "kernel": "k_chain<128,16,fmt>", "bytes_per_launch": head["bytes"]},
+                     "kernel": "k_chain<128,16,fmt,false>", "bytes_per_launch": head["bytes"]},
         "copy_ceiling_gbs": round(stream_gbs, 1),
         "copy_ceiling": {"kernel": "padra_StreamCopy", "bytes_per_launch": 2 * (head["bytes"] // 2 // 16 * 16),
                          "us_per_launch": round(stream_ms * 1e3, 3), "gbs": round(stream_gbs, 1),
@@ -619,7 +619,7 @@ def main():
     print(json.dumps(line), flush=True)
 
 
-CHAIN_KERNEL = "k_chain<128, 16, 0>"  # the config-1 instantiation (tree 128, H 2048, BF16 KV)
+CHAIN_KERNEL = "k_chain<128, 16, 0, false>"  # config 1: tree 128, H 2048, BF16 KV, no gather
 
 
 def summarize(outdir: str, command: str) -> None:
