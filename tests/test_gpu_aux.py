@@ -724,20 +724,23 @@ def test_stream_copy():
 
 
 @pytest.mark.parametrize("mode,fmt", [("decode", abi.KV_BF16), ("decode", abi.KV_Q8_0),
-                                      ("base", abi.KV_BF16)])
+                                      ("base", abi.KV_BF16), ("prefill", abi.KV_Q8)])
 def test_embed_chain_matches_gather_then_chain(oracle, mode, fmt):
     """padra_EmbedResidualNormQKRopeStore against padra_Embed followed by
     padra_ResidualNormQKRopeStore on the same inputs: x, normalized, q, k, the caches and
     the flag bit-identical; x and normalized also against the oracle's residual norm of the
     gathered rows.  Decode: 64 sequences at ragged positions with per-sequence caches, one
     of them holding a token outside the vocabulary (the flag is raised and that row reads
-    x as it was); base: token ids from an array."""
+    x as it was); base: token ids from an array; prefill: the prompt ids from the
+    PrefillState's prompt offset."""
     print(f"[case] embed chain mode={mode} fmt={fmt}", flush=True)
     seqs, capacity, vocab, hidden = 64, 2048, 1000, 2048
     rng = np.random.default_rng(123)
     d = synth.chain_inputs(seqs, outliers=True, seed=124)
     emb = synth.bf16_bits((rng.standard_normal((vocab, hidden)) * 0.5).astype(np.float32))
-    ids = rng.integers(0, vocab, seqs).astype(np.int32)
+    offset = 7 if mode == "prefill" else 0
+    prompt = rng.integers(0, vocab, seqs + offset).astype(np.int32)
+    ids = prompt[offset:]
     positions = rng.integers(0, capacity, seqs).astype(np.int32)
     tb = ops.RopeTable(capacity, 128, 1e6).view(torch.int16).numpy().view(np.uint16)
     states = np.zeros((seqs, 8), np.int32)
@@ -757,12 +760,17 @@ def test_embed_chain_matches_gather_then_chain(oracle, mode, fmt):
         if mode == "decode":
             pos = ops.positions_decode(st, maximum=capacity, vocab=vocab)
             kv = ops.kv_cache(fmt, kc, vc, capacity, scales=sc, seq_stride=capacity)
+        elif mode == "prefill":
+            pst = torch.tensor([100, offset, seqs, capacity, 100, 1, 1, 1], dtype=torch.int32,
+                               device="cuda")
+            pos = ops.positions_prefill(pst, maximum=capacity)
+            kv = ops.kv_cache(fmt, kc, vc, capacity, scales=sc)
         else:
             pos = ops.positions_base(100)
             kv = ops.kv_cache(fmt, kc, vc, capacity, scales=sc)
         args = (x, dev(d["residual"]), y, dev(d["gamma"]), q, k, dev(d["v"]), dev(d["qn"]),
                 dev(d["kn"]), dev(tb), pos, kv, bad)
-        table, idt = dev(emb), dev(ids)
+        table, idt = dev(emb), dev(prompt if mode == "prefill" else ids)
         if fused:
             ops.EmbedResidualNormQKRopeStore(table, idt, *args, tree=abi.TREE_256)
         else:
