@@ -57,17 +57,6 @@ __device__ __forceinline__ void warp_sumsq32(const float (&x)[32], float &S, flo
 }
 
 template <class T>
-__device__ __forceinline__ void load32(const T *p, float (&x)[32]) {
-#pragma unroll
-  for (int m = 0; m < 4; ++m) {
-    float c[8];
-    ActIO<T>::load8(p + 8 * m, c);
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-      x[8 * m + i] = c[i];
-  }
-}
-template <class T>
 __device__ __forceinline__ void store32(T *p, const uint32_t (&w)[16]) {
 #pragma unroll
   for (int m = 0; m < 4; ++m) {

@@ -1,4 +1,4 @@
-// Q/K RMSNorm + NeoX RoPE (+ BF16 KV store) with four lanes per head: lane 4j + g owns
+// Q/K RMSNorm + NeoX RoPE (+ KV store) with four lanes per head: lane 4j + g owns
 // features 32g .. 32g+31 of head j, i.e. exactly reference warp g of the head's 128-thread
 // block (qk_rope_store_exact.cuh:28-44, inference.cu:110-135).  A wave covers 16 heads.
 //
@@ -7,8 +7,8 @@
 //    exchanges (lanes g^2, then g^1), then a broadcast from lane g = 0.
 //  - RoPE pairs feature f < 64 with f + 64, i.e. lane g with lane g^2: the partner's
 //    normalized values arrive by DPP, one move per feature.
-// Loads and stores of the 4 KB block are four coalesced 1 KB instructions, transposed
-// through LDS as in the lane-pair path.
+// The block's head vectors (4 KB of BF16 or 8 KB of fp32 activations) are loaded and
+// stored as coalesced 1 KB instructions and transposed through an LDS image.
 #pragma once
 #include <type_traits>
 
