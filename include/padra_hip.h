@@ -322,13 +322,6 @@ int padra_CheckFP8Paths(void *stream, unsigned long long *counts);
  * mismatch count to counts[0] (device memory, u64; 0 when exact).  About 2.1e9
  * evaluations, a few milliseconds. */
 int padra_CheckQ8Path(void *stream, unsigned long long *counts);
-/* ---- launch tuning ------------------------------------------------------------------
- * No counterpart in the reference (its launch shapes are fixed).  Process-wide launch
- * parameters for measurement sweeps; defaults need no call.
- * PADRA_TUNE_NORM_WAVES_PER_CU: residual-norm rows run on value * CU-count waves that
- * pipeline their rows (0, the default: one wave per row). */
-enum { PADRA_TUNE_NORM_WAVES_PER_CU = 0 };
-int padra_Tune(int knob, int value);
 /* padra_StreamCopy: no counterpart in the reference.  Copies `bytes` (a multiple of 16;
  * 16-byte aligned pointers) with the best one-pass streaming kernel found for MI355X
  * (16-byte non-temporal loads, all before the stores); the bench times it at the chain's

@@ -102,7 +102,6 @@ SIGNATURES = {
     "padra_SiluTableBuild": [_P, _P],
     "padra_SwiGLU": [_P, _P, _P, _P, ctypes.c_longlong, _P, _P, _I],
     "padra_Embed": [_P, _P, _I, _I, _P, ctypes.POINTER(Positions), _I, _P, _P, _I],
-    "padra_Tune": [_I, _I],
     "padra_StreamCopy": [_P, _P, _P, ctypes.c_longlong],
     "padra_version": [],
 }

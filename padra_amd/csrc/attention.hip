@@ -1017,9 +1017,9 @@ extern "C" long long padra_DecodeAttentionScratch(int format, int seqs, int q_he
   if (seqs < 1 || q_heads < 1 || splits < 1 || splits > 32 ||
       (format != PADRA_KV_BF16 && format != PADRA_KV_Q8 && format != PADRA_KV_Q8_0))
     return -1;
-  // partial outputs and log-sum-exps per split
-  const long long base = (long long)seqs * splits * q_heads * (kD + 1);
-  // q8_0: the coded query (128 bytes) and its 4 block scales per head
+  // partial outputs and log-sum-exps per split, rounded up to 16 bytes
+  const long long base = ((long long)seqs * splits * q_heads * (kD + 1) + 3) & ~3ll;
+  // q8_0: the coded query (128 bytes) and its 4 block scales per head, after the lse
   return format == PADRA_KV_Q8_0 ? base + (long long)seqs * q_heads * (kD / 4 + 4) : base;
 }
 
@@ -1059,13 +1059,15 @@ int decode_attention(void *stream, const void *q, const padra_KVCache *kv, void 
   a.kc = static_cast<const uint16_t *>(kv->k);
   a.vc = static_cast<const uint16_t *>(kv->v);
   a.out = out;
-  // scratch: partial [seqs][splits][hq][128], coded query [seqs][hq][128] bytes (16-byte
-  // aligned), query block scales [seqs][hq][4], lse [seqs][splits][hq]
+  // scratch: partial [seqs][splits][hq][128], lse [seqs][splits][hq], then (q8_0 only,
+  // from the next 16-byte boundary) coded query [seqs][hq][128] bytes and query block
+  // scales [seqs][hq][4]; the end is exactly padra_DecodeAttentionScratch's count
   const long long entries = (long long)seqs * splits * q_heads;
+  const long long qbase = (entries * (kD + 1) + 3) & ~3ll;
   a.partial = scratch;
-  a.qcodes = reinterpret_cast<int8_t *>(scratch + entries * kD);
-  a.qscale = scratch + entries * kD + (long long)seqs * q_heads * (kD / 4);
-  a.lse = a.qscale + (q8 ? (long long)seqs * q_heads * 4 : 0);
+  a.lse = scratch + entries * kD;
+  a.qcodes = reinterpret_cast<int8_t *>(scratch + qbase);
+  a.qscale = scratch + qbase + (long long)seqs * q_heads * (kD / 4);
   a.decode = pos->decode;
   a.seqs = seqs;
   a.hq = q_heads;

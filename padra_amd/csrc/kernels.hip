@@ -15,13 +15,6 @@
 
 using namespace padra;
 
-// Occupancy hint for the Q/K and chain kernels.  Forcing 4 waves per SIMD (<= 128 VGPRs)
-// makes the compiler spill the Q/K working set to scratch; measured on MI355X, the
-// unconstrained allocation (2-3 waves per SIMD) is 20% faster for a 2048-token chunk.
-#ifndef PADRA_WAVES_PER_EU
-#define PADRA_WAVES_PER_EU
-#endif
-
 namespace {
 
 template <int VT, int J, class T, bool RES>
@@ -30,21 +23,15 @@ __global__ __launch_bounds__(64) void k_norm(NormArgs<T> a) {
   norm_row_wave<VT, J, T, RES>(a, blockIdx.x, lds);
 }
 
-// Fewer waves than rows, each pipelining its rows (row loads in flight during the
-// previous row's arithmetic).
-template <int VT, int J, class T, bool RES>
-__global__ __launch_bounds__(64) void k_norm_pipe(NormArgs<T> a) {
-  norm_rows_pipelined<VT, J, T, RES>(a, blockIdx.x, gridDim.x);
-}
-
-template <class T, int FMT> __global__ __launch_bounds__(64) PADRA_WAVES_PER_EU void k_qk(QKArgs<T> a) {
-  // the quad layout's image: 4 KB (BF16 activations) or 12 KB (fp32)
-  __shared__ uint4 lds[quad_image_slots<T>()];
-  // Rotated q8_0: K and V blocks first, as in k_chain (2048-token chunk, BF16
-  // activations: 9.65 -> 8.98 us; fp32: 11.6 -> 11.0 us).
+template <class T, int FMT> __global__ __launch_bounds__(64) void k_qk(QKArgs<T> a) {
+  // the quad layout's image: 4 KB (BF16 activations) or 12 KB (fp32), twice the
+  // activation pieces with a quantized cache (the K waves stage their V heads)
+  __shared__ uint4 lds[quad_image_slots_fmt<T, FMT>()];
+  // Quantized caches: the K waves (K heads with their V heads, the heaviest waves)
+  // first, as in k_chain.
   long long w = blockIdx.x;
-  if constexpr (FMT == PADRA_KV_Q8_0) {
-    w += ((long long)a.tokens * a.hq) / 16;
+  if constexpr (FMT > PADRA_KV_BF16) {
+    w += qk_q_waves(a.tokens, a.hq);
     if (w >= (long long)gridDim.x)
       w -= gridDim.x;
   }
@@ -109,42 +96,24 @@ template <int J, class T> __global__ __launch_bounds__(64) void k_norm_fp8(NormF
 // Q/K waves first measured 15% slower.
 // GATHER: the norm rows read their x from the embedding table (the fused decode step).
 template <int VT, int J, int FMT, bool GATHER = false>
-__global__ __launch_bounds__(64) PADRA_WAVES_PER_EU void k_chain(NormArgs<uint16_t> n, QKArgs<uint16_t> q,
+__global__ __launch_bounds__(64) void k_chain(NormArgs<uint16_t> n, QKArgs<uint16_t> q,
                                               long long norm_waves, long long waves) {
-  __shared__ uint4 lds[256];
+  __shared__ uint4 lds[quad_image_slots_fmt<uint16_t, FMT>()];
   const long long b = blockIdx.x;
   if (b < norm_waves)
     norm_row_wave<VT, J, uint16_t, true, false, GATHER>(n, (int)b, nullptr);
   else if (b < waves) {
-    // Rotated q8_0: the K and V blocks (Hadamard rotation + encoding, the heaviest Q/K
-    // waves) are dispatched before the Q blocks instead of last, so they do not form the
-    // grid's tail: 14.75 -> 13.84 us for the 2048-token chunk.  The same order measured
-    // 0.5-1% slower for q8 and unrotated q8_0, which keep Q, K, V order.
+    // Quantized caches: the K waves (K norm + RoPE, then the K and V encodings: the
+    // heaviest waves) are dispatched before the Q waves instead of last, so they do not
+    // form the grid's tail.
     long long w = b - norm_waves;
-    if constexpr (FMT == PADRA_KV_Q8_0) {
-      w += ((long long)q.tokens * q.hq) / 16;
+    if constexpr (FMT > PADRA_KV_BF16) {
+      w += qk_q_waves(q.tokens, q.hq);
       if (w >= waves - norm_waves)
         w -= waves - norm_waves;
     }
     qk_heads_wave<uint16_t, FMT>(q, w, lds);
   }
-}
-
-// Launch tuning (padra_Tune): waves per CU for the pipelined row kernel, 0 = one wave
-// per row.
-int g_norm_waves_per_cu = 0;
-int g_cu_count = 0;
-
-int cu_count() {
-  if (!g_cu_count) {
-    int dev = 0, n = 0;
-    if (hipGetDevice(&dev) == hipSuccess &&
-        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess)
-      g_cu_count = n;
-    else
-      g_cu_count = 256;
-  }
-  return g_cu_count;
 }
 
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -299,11 +268,6 @@ template <class F> int with_format(const padra_KVCache *kv, F &&f) {
   return PADRA_INVALID_ARGUMENT;
 }
 
-// Q/K waves plus, with a cache binding, the V-row waves (`per` head vectors per wave).
-long long qk_waves(int tokens, int q_heads, int kv_heads, bool store, int per) {
-  return ((long long)tokens * (q_heads + kv_heads * (store ? 2 : 1)) + per - 1) / per;
-}
-
 } // namespace
 
 extern "C" int padra_ResidualPostNorm(void *stream, void *x, const void *residual,
@@ -328,14 +292,8 @@ extern "C" int padra_ResidualPostNorm(void *stream, void *x, const void *residua
     a.bad = bad;
     a.rows = rows;
     a.eps = eps;
-    const int pipe_waves = g_norm_waves_per_cu * cu_count();
     return norm_shape(tree, hidden / tree, [&](auto vt, auto j) -> int {
-      if (pipe_waves > 0 && pipe_waves < rows) {
-        if (residual)
-          hipLaunchKernelGGL((k_norm_pipe<vt.value, j.value, T, true>), dim3(pipe_waves), dim3(64), 0, s, a);
-        else
-          hipLaunchKernelGGL((k_norm_pipe<vt.value, j.value, T, false>), dim3(pipe_waves), dim3(64), 0, s, a);
-      } else if (residual) {
+      if (residual) {
         hipLaunchKernelGGL((k_norm<vt.value, j.value, T, true>), dim3(grid), dim3(64), 0, s, a);
       } else {
         hipLaunchKernelGGL((k_norm<vt.value, j.value, T, false>), dim3(grid), dim3(64), 0, s, a);
@@ -432,8 +390,7 @@ extern "C" int padra_QKNormRopeStore(void *stream, void *q, void *k, const void 
     const QKArgs<T> a =
         make_qk<T>(q, k, v, qn, kn, table, table_rows, pos, tokens, q_heads, kv_heads, eps, kv, bad);
     return with_format(kv, [&](auto fmt) -> int {
-      const long long grid = qk_waves(tokens, q_heads, kv_heads, kv != nullptr,
-                                      qk_heads_per_wave<T, fmt.value>());
+      const long long grid = qk_wave_count<fmt.value>(tokens, q_heads, kv_heads);
       hipLaunchKernelGGL((k_qk<T, fmt.value>), dim3((unsigned)grid), dim3(64), 0, s, a);
       return launched();
     });
@@ -495,8 +452,7 @@ int chain(hipStream_t s, const uint16_t *gather, int vocab, const int32_t *ids, 
   if (!((tree == 128 && (j == 16 || j == 18)) || (tree == 256 && (j == 8 || j == 9))))
     return PADRA_UNSUPPORTED;
   return with_format(kv, [&](auto fmt) -> int {
-    const long long waves = norm_waves + qk_waves(tokens, q_heads, kv_heads, kv != nullptr,
-                                                  qk_heads_per_wave<uint16_t, fmt.value>());
+    const long long waves = norm_waves + qk_wave_count<fmt.value>(tokens, q_heads, kv_heads);
     const dim3 grid((unsigned)waves), block(64);
     if (gather) {
       if (tree == 128 && j == 16)
@@ -545,14 +501,6 @@ extern "C" int padra_EmbedResidualNormQKRopeStore(
   return chain(static_cast<hipStream_t>(stream), embed, vocab, ids, x, residual, normalized,
                gamma, hidden, tree, statistics, q, k, v, qn, kn, table, table_rows, pos, tokens,
                q_heads, kv_heads, head_dim, eps, kv, bad);
-}
-
-extern "C" int padra_Tune(int knob, int value) {
-  if (knob == PADRA_TUNE_NORM_WAVES_PER_CU && value >= 0 && value <= 64) {
-    g_norm_waves_per_cu = value;
-    return PADRA_OK;
-  }
-  return PADRA_INVALID_ARGUMENT;
 }
 
 // Streaming copy for the practical-ceiling measurement: 16 rows of 16 bytes per lane, all

@@ -56,18 +56,19 @@ int check_positions(const padra_Positions *pos, int tokens) {
 
 // ---- store / encode of K and V rows ----------------------------------------------------
 //
-// Head vectors 0 .. T*Hkv-1 are K heads, T*Hkv .. 2*T*Hkv-1 V heads; 32 per wave, two
-// lanes each (the lane-pair layout of the quantizers).  BF16 rows are a plain copy.
+// A wave covers 16 (token, KV head) pairs, two lanes per head vector (the lane-pair
+// layout of the quantizers): lanes 0-31 the K vectors, lanes 32-63 the V vectors of the
+// same pairs, so the encoder sees both halves of a head (lane ^ 32).  BF16 rows are a
+// plain copy.
 template <class T, int FMT>
 __global__ __launch_bounds__(64) void k_kv_store(QKArgs<T> a) {
   constexpr int D = 128;
   const int lane = threadIdx.x & 63, half = lane & 1;
   const unsigned nk = (unsigned)a.tokens * (unsigned)a.hkv;
-  const unsigned hv = blockIdx.x * 32u + (unsigned)(lane >> 1);
-  if (hv >= 2 * nk)
-    return;
-  const bool isv = hv >= nk;
-  const unsigned idx = isv ? hv - nk : hv;
+  const unsigned idx = blockIdx.x * 16u + (unsigned)((lane >> 1) & 15);
+  if (idx >= nk)
+    return; // both halves of the pair
+  const bool isv = lane >= 32;
   const int t = (int)(idx / (unsigned)a.hkv), h = (int)(idx % (unsigned)a.hkv);
   const T *src = (isv ? a.v : a.k) + (size_t)idx * D;
   const PosState ps = fetch_state(a.pos, t);
@@ -102,10 +103,7 @@ __global__ __launch_bounds__(64) void k_kv_store(QKArgs<T> a) {
       fa[i] = xa.get(i);
       fb[i] = xb.get(i);
     }
-    if (isv)
-      encode_head_q<FMT, true>(a, fa, fb, slot, h, half);
-    else
-      encode_head_q<FMT, false>(a, fa, fb, slot, h, half);
+    encode_head_q<FMT>(a, fa, fb, slot, h, half, isv);
   }
 }
 
@@ -341,7 +339,7 @@ extern "C" int padra_KVStore(void *stream, const void *k, const void *v,
       (pos->mode != PADRA_POS_DECODE && tokens - kv->first > kv->cap))
     return PADRA_INVALID_ARGUMENT;
   const hipStream_t s = static_cast<hipStream_t>(stream);
-  const long long grid = (2ll * tokens * kv_heads + 31) / 32;
+  const long long grid = ((long long)tokens * kv_heads + 15) / 16;
   auto launch = [&](auto tag) -> int {
     using T = decltype(tag);
     QKArgs<T> a{};

@@ -383,24 +383,4 @@ __device__ __forceinline__ void norm_row_wave(const NormArgs<T> &a, int row, uin
   norm_compute<VT, J, T, RES>(a, row, in, gr);
 }
 
-// Rows first, first + stride, ... with the next row's loads in flight while the current
-// row computes (software pipelining across the wave's rows).
-template <int VT, int J, class T, bool RES>
-__device__ __forceinline__ void norm_rows_pipelined(const NormArgs<T> &a, int first, int stride) {
-  if (first >= a.rows)
-    return;
-  Lanes<uint16_t, VT / 64> gr[J];
-  RowIn<VT, J, T> cur;
-  norm_load<VT, J, T, RES>(a, first, cur);
-  norm_load_gamma<VT, J>(a.gamma, gr);
-  for (int row = first; row < a.rows; row += stride) {
-    RowIn<VT, J, T> nxt;
-    const int next = row + stride;
-    if (next < a.rows)
-      norm_load<VT, J, T, RES>(a, next, nxt);
-    norm_compute<VT, J, T, RES>(a, row, cur, gr);
-    cur = nxt;
-  }
-}
-
 } // namespace padra

@@ -98,12 +98,14 @@ __device__ __forceinline__ void store_codes32(int8_t *p, const uint32_t (&w)[8])
 // Q8 / Q8_0 encoding of one head vector of the K cache (ISV false: the rotated K row)
 // or the V cache (ISV true), held by the two lanes of a pair: this lane has features
 // 32*half + i in xa and 64 + 32*half + i in xb.  Writes codes and scales to row `slot`.
-// The reference encodes K and V of a head in one warp (kv_q8.cuh:41-73,
-// kv_q8_native.cuh:70-100); here they are encoded by different waves, so when one of them
-// is invalid (non-finite input, the error flag is raised) the other is still written.
-template <int FMT, bool ISV, class A>
+// The pair at lane ^ 32 holds the same head's other vector and is active with this one.
+// As in the reference's one warp per (token, head) (kv_q8.cuh:41-73,
+// kv_q8_native.cuh:70-100), an invalid K or V vector (non-finite, or for q8 not
+// BF16-exact) raises the flag and writes neither, and a q8_0 block that fails in K or in
+// V ends the writes of both.
+template <int FMT, class A>
 __device__ __forceinline__ void encode_head_q(const A &a, float (&xa)[32], float (&xb)[32],
-                                              long long slot, int h, int half) {
+                                              long long slot, int h, int half, bool isv) {
   constexpr int D = 128;
   const int features = a.hkv * D;
   bool invalid = false;
@@ -113,7 +115,12 @@ __device__ __forceinline__ void encode_head_q(const A &a, float (&xa)[32], float
     if constexpr (FMT == PADRA_KV_Q8) // q8 also rejects values that are not BF16-exact
       invalid |= (__float_as_uint(xa[i]) & 0xffffu) != 0 || (__float_as_uint(xb[i]) & 0xffffu) != 0;
   }
-  invalid = invalid || __shfl_xor((int)invalid, 1, 64);
+  // Both exchanges run in every lane (a lane that skipped one would leave its value
+  // unreadable to the partner).
+  const int pair_bad = __shfl_xor((int)invalid, 1, 64);
+  invalid = invalid || pair_bad != 0;
+  const int other_bad = __shfl_xor((int)invalid, 32, 64);
+  invalid = invalid || other_bad != 0;
   if (invalid) {
     if (half == 0)
       raise_bad(a.bad);
@@ -128,7 +135,7 @@ __device__ __forceinline__ void encode_head_q(const A &a, float (&xa)[32], float
       m = fmaxf(m, fmaxf(fabsf(xa[i]), fabsf(xb[i])));
     m = fmaxf(m, shfl_xor(m, 1));
     const float scale = m == 0.f ? 1.f : m / 127.f;
-    int8_t *codes = static_cast<int8_t *>(ISV ? a.vc : a.kc) + slot * features + h * D;
+    int8_t *codes = static_cast<int8_t *>(isv ? a.vc : a.kc) + slot * features + h * D;
     const float inverse = 1.f / scale;
     const bool fast = q8_fast_ok(scale); // pair-uniform
     uint32_t w0[8], w1[8];
@@ -144,7 +151,7 @@ __device__ __forceinline__ void encode_head_q(const A &a, float (&xa)[32], float
     store_codes32(codes + 32 * half, w0);
     store_codes32(codes + 64 + 32 * half, w1);
     if (half == 0)
-      reinterpret_cast<float *>(a.scales)[(slot * a.hkv + h) * 2 + (ISV ? 1 : 0)] = scale;
+      reinterpret_cast<float *>(a.scales)[(slot * a.hkv + h) * 2 + (isv ? 1 : 0)] = scale;
   } else {
     if constexpr (FMT == PADRA_KV_Q8_0) {
       // q8_native::Rotate (kv_q8_native.cuh:22-45): stages on feature bits 0..4 in lane,
@@ -153,19 +160,16 @@ __device__ __forceinline__ void encode_head_q(const A &a, float (&xa)[32], float
       hadamard32(xb);
       hadamard_cross(xa, half);
       hadamard_cross(xb, half);
-      if constexpr (!ISV) {
+      // K: the stage on feature bit 6 (xa with xb) and the 1/sqrt(128) scale; V: the 1/8
+      // scale.  Lanes of both halves run this loop with per-lane operands: for V,
+      // lower + 0 and lower - 0 leave each value (a zero's sign aside, which no code or
+      // scale sees).
+      const float sc = isv ? .125f : .08838834764831845f;
 #pragma unroll
-        for (int i = 0; i < 32; ++i) {
-          const float lower = xa[i], upper = xb[i];
-          xa[i] = (lower + upper) * .08838834764831845f;
-          xb[i] = (lower - upper) * .08838834764831845f;
-        }
-      } else {
-#pragma unroll
-        for (int i = 0; i < 32; ++i) {
-          xa[i] = xa[i] * .125f;
-          xb[i] = xb[i] * .125f;
-        }
+      for (int i = 0; i < 32; ++i) {
+        const float lower = xa[i], upper = isv ? 0.f : xb[i];
+        xa[i] = (lower + upper) * sc;
+        xb[i] = (isv ? xb[i] : lower - upper) * sc;
       }
     }
     // Blocks (kv_q8_native.cuh:84-99): this lane holds block `half` (xa) and block
@@ -183,11 +187,12 @@ __device__ __forceinline__ void encode_head_q(const A &a, float (&xa)[32], float
     const bool fa = !isfinite(am) || !isfinite(__half2float(ah));
     const bool fb = !isfinite(bm) || !isfinite(__half2float(bh));
     const int mine = fa ? half : (fb ? half + 2 : 4);
-    const int stop = min(mine, __shfl_xor(mine, 1, 64)); // first failing block, 4 = none
+    int stop = min(mine, __shfl_xor(mine, 1, 64)); // first failing block, 4 = none
+    stop = min(stop, __shfl_xor(stop, 32, 64));      // of K and V together
     if (stop < 4 && half == 0)
       raise_bad(a.bad);
     const int row_bytes = ((2 * (features / 32) + features) + 15) / 16 * 16;
-    uint8_t *row = static_cast<uint8_t *>(ISV ? a.vc : a.kc) + slot * row_bytes;
+    uint8_t *row = static_cast<uint8_t *>(isv ? a.vc : a.kc) + slot * row_bytes;
     int8_t *qs = reinterpret_cast<int8_t *>(row + 2 * (features / 32) + h * D);
     uint16_t *d = reinterpret_cast<uint16_t *>(row) + h * 4;
     const float ai = ad == 0.f ? 0.f : 1.f / ad, bi = bd == 0.f ? 0.f : 1.f / bd;

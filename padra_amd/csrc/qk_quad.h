@@ -100,43 +100,27 @@ template <int D> __device__ __forceinline__ void hadamard_quad(float (&x)[32], i
   }
 }
 
-// Encodes one K or V head vector held by a quad (lane g: features 32g .. 32g+31 in x)
-// into a quantized cache row.  `active` is quad-uniform; every lane runs the quad
-// exchanges.
-//  - A head with a non-finite value (q8: or a value that is not BF16-exact) raises the
-//    flag and writes nothing (kv_q8.cuh:49-54, kv_q8_native.cuh:70-79).
-//  - q8 (kv_q8::Encode, kv_q8.cuh:41-73): scale = amax/127 (1 for a zero head), codes
-//    RNE(x / scale) clamped to +-127, scale into the (k, v) pair of the row's head.
-//  - q8_0 (q8_native::EncodeKV, kv_q8_native.cuh:52-101): the rotation (K 128-point,
-//    V two 64-point; stages on feature bits 0-4 inside the lane, bits 5 and 6 across the
-//    quad), then block g = this lane's 32 features: d = half(amax/127), codes
-//    roundf(x * (1/d_fp32)) clamped.  Blocks from the first failing one (non-finite amax
-//    or d) on are not written, and the flag is raised.
-template <int FMT, bool ISV, class A>
-__device__ __forceinline__ void encode_quad(const A &a, float (&x)[32], long long slot, int h,
-                                            int g, bool active) {
-  constexpr int D = 128;
-  const int features = a.hkv * D;
-  {
-    bool valid = true;
-#pragma unroll
-    for (int i = 0; i < 32; ++i) {
-      valid = valid && isfinite(x[i]);
-      if constexpr (FMT == PADRA_KV_Q8)
-        valid = valid && (__float_as_uint(x[i]) & 0xffffu) == 0u;
-    }
-    uint32_t v = valid ? 1u : 0u;
-    v &= quad_xor1(v);
-    v &= quad_xor2(v);
-    if (!active)
-      return;
-    if (!v) {
-      if (g == 0)
-        raise_bad(a.bad);
-      return;
-    }
-  }
+// The codes of one quantized head vector held by a quad (lane g: features 32g..32g+31 in
+// x), computed but not stored.
+//  - q8 (kv_q8::Encode, kv_q8.cuh:56-73): scale = amax/127 over the head (1 for a zero
+//    head), codes RNE(x / scale) clamped to +-127.
+//  - q8_0 (q8_native::EncodeKV, kv_q8_native.cuh:76-100): the rotation when FMT is the
+//    rotated format (K: 128-point, stages on feature bits 0-4 in the lane, bits 5 and 6
+//    across the quad, scale 1/sqrt(128); V: two 64-point transforms, no bit-6 stage,
+//    scale 1/8), then block g = this lane's 32 values: d = half(amax/127), codes
+//    roundf(x * (1/d_fp32)) clamped; `fail` when amax or d is not finite.
+struct QuadCodes {
   uint32_t cw[8];
+  float scale;   // q8: the head's scale
+  uint16_t d;    // q8_0: this lane's block scale (fp16 bits)
+  bool fail;     // q8_0: this lane's block cannot be encoded
+};
+template <int FMT, bool ISV>
+__device__ __forceinline__ QuadCodes quad_codes(float (&x)[32], int g) {
+  QuadCodes r;
+  r.fail = false;
+  r.d = 0;
+  r.scale = 1.f;
   if constexpr (FMT == PADRA_KV_Q8) {
     float m = 0.f;
 #pragma unroll
@@ -145,34 +129,29 @@ __device__ __forceinline__ void encode_quad(const A &a, float (&x)[32], long lon
     m = fmaxf(m, __uint_as_float(quad_xor1(__float_as_uint(m))));
     m = fmaxf(m, __uint_as_float(quad_xor2(__float_as_uint(m))));
     const float scale = m == 0.f ? 1.f : m / 127.f, inverse = 1.f / scale;
+    r.scale = scale;
     if (q8_fast_ok(scale)) { // quad-uniform
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        cw[i] = 0u;
+        r.cw[i] = 0u;
 #pragma unroll
         for (int b = 0; b < 4; ++b)
-          cw[i] |= q8_code_fast(x[4 * i + b], scale, inverse) << (8 * b);
+          r.cw[i] |= q8_code_fast(x[4 * i + b], scale, inverse) << (8 * b);
       }
     } else {
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        cw[i] = 0u;
+        r.cw[i] = 0u;
 #pragma unroll
         for (int b = 0; b < 4; ++b)
-          cw[i] |= q8_code(x[4 * i + b], scale) << (8 * b);
+          r.cw[i] |= q8_code(x[4 * i + b], scale) << (8 * b);
       }
     }
-    int8_t *codes = static_cast<int8_t *>(ISV ? a.vc : a.kc) + slot * features + h * D + 32 * g;
-    st_nt(reinterpret_cast<uint4 *>(codes), make_uint4(cw[0], cw[1], cw[2], cw[3]));
-    st_nt(reinterpret_cast<uint4 *>(codes) + 1, make_uint4(cw[4], cw[5], cw[6], cw[7]));
-    if (g == 0)
-      reinterpret_cast<float *>(a.scales)[(slot * a.hkv + h) * 2 + (ISV ? 1 : 0)] = scale;
   } else {
     if constexpr (FMT == PADRA_KV_Q8_0) {
       hadamard32(x);
       hadamard_quad<1>(x, g);
       if constexpr (!ISV) {
-        // the last K stage (bit 6) with the 1/sqrt(128) scale
         const float sgn = (g & 2) ? -1.f : 1.f;
 #pragma unroll
         for (int f = 0; f < 32; ++f) {
@@ -191,28 +170,87 @@ __device__ __forceinline__ void encode_quad(const A &a, float (&x)[32], long lon
       am = fmaxf(am, fabsf(x[i]));
     const float ad = am / 127.f;
     const __half dh = __float2half(ad);
-    const bool fail = !isfinite(am) || !isfinite(__half2float(dh));
-    uint32_t stop = fail ? (uint32_t)g : 4u; // first failing block of the head, 4 = none
+    r.fail = !isfinite(am) || !isfinite(__half2float(dh));
+    r.d = __half_as_ushort(dh);
+    const float inverse = ad == 0.f ? 0.f : 1.f / ad;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      r.cw[i] = 0u;
+#pragma unroll
+      for (int b = 0; b < 4; ++b)
+        r.cw[i] |= q8_0_code(x[4 * i + b], inverse) << (8 * b);
+    }
+  }
+  return r;
+}
+
+// Encodes one (token, KV head) pair held by a quad: the rotated K head (xk) and the V
+// head (xv), as the reference's one warp per pair does (kv_q8.cuh:41-73,
+// kv_q8_native.cuh:52-101).
+//  - A non-finite value in K or V (q8: or a value that is not BF16-exact) raises the flag
+//    and neither row is written (kv_q8.cuh:49-54, kv_q8_native.cuh:70-79).
+//  - q8: codes of both, then the (k, v) scale pair as one 8-byte store.
+//  - q8_0: block r of K and of V are written for every r before the first block whose
+//    K or V scale fails (kv_q8_native.cuh:82-99); the flag is raised at a failing block.
+// `active` is quad-uniform; DPP quad exchanges need only the quad's own lanes.
+template <int FMT, class T, class A>
+__device__ __forceinline__ void encode_pair_quad(const A &a, float (&xk)[32], const Act32<T> &xv,
+                                                 long long slot, int h, int g, bool active) {
+  constexpr int D = 128;
+  const int features = a.hkv * D;
+  float x[32];
+#pragma unroll
+  for (int i = 0; i < 32; ++i)
+    x[i] = xv.get(i);
+  {
+    bool valid = true;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+      valid = valid && isfinite(xk[i]) && isfinite(x[i]);
+      if constexpr (FMT == PADRA_KV_Q8)
+        valid = valid && (__float_as_uint(xk[i]) & 0xffffu) == 0u &&
+                (__float_as_uint(x[i]) & 0xffffu) == 0u;
+    }
+    uint32_t v = valid ? 1u : 0u;
+    v &= quad_xor1(v);
+    v &= quad_xor2(v);
+    if (!active)
+      return;
+    if (!v) {
+      if (g == 0)
+        raise_bad(a.bad);
+      return;
+    }
+  }
+  const QuadCodes cv = quad_codes<FMT, true>(x, g);
+  const QuadCodes ck = quad_codes<FMT, false>(xk, g);
+  if constexpr (FMT == PADRA_KV_Q8) {
+    int8_t *kq = static_cast<int8_t *>(a.kc) + slot * features + h * D + 32 * g;
+    int8_t *vq = static_cast<int8_t *>(a.vc) + slot * features + h * D + 32 * g;
+    st_nt(reinterpret_cast<uint4 *>(kq), make_uint4(ck.cw[0], ck.cw[1], ck.cw[2], ck.cw[3]));
+    st_nt(reinterpret_cast<uint4 *>(kq) + 1, make_uint4(ck.cw[4], ck.cw[5], ck.cw[6], ck.cw[7]));
+    st_nt(reinterpret_cast<uint4 *>(vq), make_uint4(cv.cw[0], cv.cw[1], cv.cw[2], cv.cw[3]));
+    st_nt(reinterpret_cast<uint4 *>(vq) + 1, make_uint4(cv.cw[4], cv.cw[5], cv.cw[6], cv.cw[7]));
+    if (g == 0)
+      reinterpret_cast<float2 *>(a.scales)[slot * a.hkv + h] = make_float2(ck.scale, cv.scale);
+  } else {
+    uint32_t stop = (ck.fail || cv.fail) ? (uint32_t)g : 4u; // first failing block, 4 = none
     stop = min(stop, quad_xor1(stop));
     stop = min(stop, quad_xor2(stop));
     if (stop < 4u && g == 0)
       raise_bad(a.bad);
     if ((uint32_t)g >= stop)
       return;
-    const float inverse = ad == 0.f ? 0.f : 1.f / ad;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      cw[i] = 0u;
-#pragma unroll
-      for (int b = 0; b < 4; ++b)
-        cw[i] |= q8_0_code(x[4 * i + b], inverse) << (8 * b);
-    }
     const int row_bytes = ((2 * (features / 32) + features) + 15) / 16 * 16;
-    uint8_t *row = static_cast<uint8_t *>(ISV ? a.vc : a.kc) + slot * row_bytes;
-    int8_t *qs = reinterpret_cast<int8_t *>(row + 2 * (features / 32) + h * D + 32 * g);
-    st_nt(reinterpret_cast<uint4 *>(qs), make_uint4(cw[0], cw[1], cw[2], cw[3]));
-    st_nt(reinterpret_cast<uint4 *>(qs) + 1, make_uint4(cw[4], cw[5], cw[6], cw[7]));
-    reinterpret_cast<uint16_t *>(row)[h * 4 + g] = __half_as_ushort(dh);
+    const long long qoff = slot * row_bytes + 2 * (features / 32) + h * D + 32 * g;
+    const long long doff = slot * row_bytes + 2 * (h * 4 + g);
+    uint8_t *kc = static_cast<uint8_t *>(a.kc), *vc = static_cast<uint8_t *>(a.vc);
+    st_nt(reinterpret_cast<uint4 *>(kc + qoff), make_uint4(ck.cw[0], ck.cw[1], ck.cw[2], ck.cw[3]));
+    st_nt(reinterpret_cast<uint4 *>(kc + qoff) + 1, make_uint4(ck.cw[4], ck.cw[5], ck.cw[6], ck.cw[7]));
+    st_nt(reinterpret_cast<uint4 *>(vc + qoff), make_uint4(cv.cw[0], cv.cw[1], cv.cw[2], cv.cw[3]));
+    st_nt(reinterpret_cast<uint4 *>(vc + qoff) + 1, make_uint4(cv.cw[4], cv.cw[5], cv.cw[6], cv.cw[7]));
+    *reinterpret_cast<uint16_t *>(kc + doff) = ck.d;
+    *reinterpret_cast<uint16_t *>(vc + doff) = cv.d;
   }
 }
 
@@ -224,6 +262,11 @@ __device__ __forceinline__ void encode_quad(const A &a, float (&x)[32], long lon
 // lanes reading their own piece p.
 template <class T> constexpr int quad_image_slots() {
   return std::is_same<T, uint16_t>::value ? 256 : 768;
+}
+// With a quantized cache the K waves also stage their V heads, behind the K pieces.
+template <class T, int FMT> constexpr int quad_image_slots_fmt() {
+  return FMT > PADRA_KV_BF16 ? (std::is_same<T, uint16_t>::value ? 512 : 1024)
+                             : quad_image_slots<T>();
 }
 template <class T> __device__ __forceinline__ int quad_piece_slot(int owner, int p) {
   if constexpr (std::is_same<T, uint16_t>::value)
@@ -251,6 +294,26 @@ __device__ __forceinline__ void qk_heads_wave_quad(const QKArgs<T> &a, long long
   const unsigned nq = (unsigned)a.tokens * (unsigned)a.hq;
   const unsigned nk = (unsigned)a.tokens * (unsigned)a.hkv;
   const unsigned total = nq + nk + (FMT >= 0 ? nk : 0u);
+  // Flat head index (q heads, k heads, v heads) of block slot j, or `total` for none.
+  // Quantized caches: the Q heads fill the first qk_q_waves waves, 16 per wave; every
+  // later wave takes 16 K heads and stages their 16 V heads too, so that one quad holds
+  // both vectors of a (token, KV head) pair, as the encoder needs.  Otherwise slots
+  // follow the flat order.
+  const unsigned nqw = (nq + 15u) / 16u;
+  const bool kv_wave = FMT > PADRA_KV_BF16 && (unsigned)wave >= nqw; // wave-uniform
+  auto slot_head = [&](unsigned j) -> unsigned {
+    if constexpr (FMT > PADRA_KV_BF16) {
+      if ((unsigned)wave < nqw) {
+        const unsigned h = (unsigned)wave * 16u + j;
+        return h < nq ? h : total;
+      }
+      const unsigned kvi = ((unsigned)wave - nqw) * 16u + j;
+      return kvi < nk ? nq + kvi : total;
+    } else {
+      const unsigned h = block0 + j;
+      return h < total ? h : total;
+    }
+  };
   if constexpr (FMT == PADRA_KV_BF16 && !F32) {
     if (block0 >= nq + nk) { // wave-uniform
       v_rows_copy16(a, block0, nq, nk);
@@ -259,7 +322,7 @@ __device__ __forceinline__ void qk_heads_wave_quad(const QKArgs<T> &a, long long
   }
 
   // This lane's head and warp group; its control record is requested first.
-  const unsigned hv = block0 + (unsigned)(lane >> 2);
+  const unsigned hv = slot_head((unsigned)(lane >> 2));
   const bool live = hv < total;
   const int role = hv < nq ? 0 : (hv < nq + nk ? 1 : 2); // 0 q, 1 k, 2 v
   const unsigned idx = role == 0 ? hv : (role == 1 ? hv - nq : hv - nq - nk);
@@ -273,8 +336,20 @@ __device__ __forceinline__ void qk_heads_wave_quad(const QKArgs<T> &a, long long
 #pragma unroll
   for (int m = 0; m < PL; ++m) {
     const int c = 64 * m + lane;
-    const unsigned hc = min(block0 + (unsigned)(c / CH), total - 1u);
+    const unsigned hc = min(slot_head((unsigned)(c / CH)), total - 1u);
     in[m] = ld_nt(reinterpret_cast<const uint4 *>(head_src(a, hc, nq, nk)) + (c % CH));
+  }
+  // The V heads of a K wave (quantized cache), the same pieces of a.v.
+  uint4 inv_[FMT > PADRA_KV_BF16 ? PL : 1];
+  if constexpr (FMT > PADRA_KV_BF16) {
+    if (kv_wave) {
+#pragma unroll
+      for (int m = 0; m < PL; ++m) {
+        const int c = 64 * m + lane;
+        const unsigned hc = min(slot_head((unsigned)(c / CH)), nq + nk - 1u) - nq;
+        inv_[m] = ld_nt(reinterpret_cast<const uint4 *>(a.v + (size_t)hc * D) + (c % CH));
+      }
+    }
   }
   // 2. The head's position (its control record was requested first), then the weight and
   // table loads, so that they are in flight with the data loads.
@@ -299,6 +374,16 @@ __device__ __forceinline__ void qk_heads_wave_quad(const QKArgs<T> &a, long long
   for (int m = 0; m < PL; ++m) {
     const int c = 64 * m + lane;
     stage[quad_piece_slot<T>(4 * (c / CH) + (c % CH) / PL, c % PL)] = in[m];
+  }
+  constexpr int VIMG = 64 * PL; // V pieces behind the K pieces
+  if constexpr (FMT > PADRA_KV_BF16) {
+    if (kv_wave) {
+#pragma unroll
+      for (int m = 0; m < PL; ++m) {
+        const int c = 64 * m + lane;
+        stage[VIMG + quad_piece_slot<T>(4 * (c / CH) + (c % CH) / PL, c % PL)] = inv_[m];
+      }
+    }
   }
   __syncthreads();
   Act32<T> x;
@@ -351,20 +436,30 @@ __device__ __forceinline__ void qk_heads_wave_quad(const QKArgs<T> &a, long long
       raise_bad(a.bad);
   }
   if constexpr (FMT > PADRA_KV_BF16) {
-    // K heads encode their rotated values, V heads their inputs (quad-uniform roles).
-    const bool enc = live && ok && role >= 1 && t >= a.first;
-    const long long seq = a.pos.mode == PADRA_POS_DECODE ? t : 0;
-    const long long slot = seq * a.seq_stride + (ok ? ring_slot(pos, max(a.cap, 1)) : 0);
-    float xe[32];
+    if (kv_wave) {
+      // Each quad encodes its K head (the rotated values) with the V head of the same
+      // (token, KV head) from the V image.
+      Act32<T> xv;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      xe[2 * i] = role == 1 ? lo16(out[i]) : x.get(2 * i);
-      xe[2 * i + 1] = role == 1 ? hi16(out[i]) : x.get(2 * i + 1);
+      for (int p = 0; p < PL; ++p) {
+        const uint4 v = stage[VIMG + quad_piece_slot<T>(lane, p)];
+        if constexpr (F32)
+          xv.f[p] = make_float4(__uint_as_float(v.x), __uint_as_float(v.y),
+                                __uint_as_float(v.z), __uint_as_float(v.w));
+        else
+          xv.w[p] = v;
+      }
+      const bool enc = live && ok && t >= a.first;
+      const long long seq = a.pos.mode == PADRA_POS_DECODE ? t : 0;
+      const long long slot = seq * a.seq_stride + (ok ? ring_slot(pos, max(a.cap, 1)) : 0);
+      float xe[32];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        xe[2 * i] = lo16(out[i]);
+        xe[2 * i + 1] = hi16(out[i]);
+      }
+      encode_pair_quad<FMT>(a, xe, xv, slot, hh, g, enc);
     }
-    if (role == 2)
-      encode_quad<FMT, true>(a, xe, slot, hh, g, enc);
-    else
-      encode_quad<FMT, false>(a, xe, slot, hh, g, enc && role == 1);
   }
   __syncthreads(); // every lane has read its input pieces: the image can be overwritten
 
@@ -413,7 +508,7 @@ __device__ __forceinline__ void qk_heads_wave_quad(const QKArgs<T> &a, long long
 #pragma unroll
     for (int m = 0; m < PL; ++m) {
       const int c = 64 * m + lane, j = c / CH, ci = c % CH;
-      const unsigned hc = block0 + (unsigned)j;
+      const unsigned hc = slot_head((unsigned)j);
       if (!head_live[j] || hc >= nq + nk)
         continue;
       const uint4 d = stage[quad_piece_slot<T>(4 * j + ci / PL, ci % PL)];
@@ -427,7 +522,7 @@ __device__ __forceinline__ void qk_heads_wave_quad(const QKArgs<T> &a, long long
         const long long r = head_row[j];
         if (!head_live[j] || r < 0)
           continue;
-        const unsigned hc = block0 + (unsigned)j;
+        const unsigned hc = slot_head((unsigned)j);
         const uint4 d = stage[512 + quad_slot(4 * j + (ci >> 2), ci & 3)];
         uint16_t *cache = static_cast<uint16_t *>(hc >= nq + nk ? a.vc : a.kc);
         st_nt(reinterpret_cast<uint4 *>(cache + r) + ci, d);
@@ -437,7 +532,7 @@ __device__ __forceinline__ void qk_heads_wave_quad(const QKArgs<T> &a, long long
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
       const int c = 64 * m + lane, j = c >> 4, ci = c & 15;
-      const unsigned hc = block0 + (unsigned)j;
+      const unsigned hc = slot_head((unsigned)j);
       if (!head_live[j])
         continue; // past the end, or a head that writes nothing
       const uint4 d = stage[quad_slot(4 * j + (ci >> 2), ci & 3)];
@@ -457,8 +552,20 @@ __device__ __forceinline__ void qk_heads_wave_quad(const QKArgs<T> &a, long long
   }
 }
 
-// Head vectors per wave of each Q/K kernel variant.
-template <class T, int FMT> constexpr int qk_heads_per_wave() { return 16; }
+// Waves of a Q/K launch: 16 head vectors per wave in the flat order (no cache, BF16
+// cache), or the Q waves and then the K waves (16 K heads with their V heads) of a
+// quantized cache.
+template <int FMT>
+__host__ __device__ inline long long qk_wave_count(int tokens, int q_heads, int kv_heads) {
+  const long long nq = (long long)tokens * q_heads, nk = (long long)tokens * kv_heads;
+  if (FMT > PADRA_KV_BF16)
+    return (nq + 15) / 16 + (nk + 15) / 16;
+  return (nq + nk * (FMT >= 0 ? 2 : 1) + 15) / 16;
+}
+// The waves holding Q heads only, before the K-with-V waves of a quantized cache.
+__host__ __device__ inline long long qk_q_waves(int tokens, int q_heads) {
+  return ((long long)tokens * q_heads + 15) / 16;
+}
 
 // Four lanes per head for both activation types.
 template <class T, int FMT>

@@ -133,6 +133,9 @@ def test_host_validation_newer_entry_points():
     assert lib.padra_DecodeAttentionScratch(abi.KV_BF16, 2, 16, 33) == -1
     assert lib.padra_DecodeAttentionScratch(abi.KV_Q8, 2, 16, 32) == need
     assert lib.padra_DecodeAttentionScratch(abi.KV_Q8_0_NOROT, 2, 16, 32) == -1
+    # the lse ends on a 16-byte boundary before the q8_0 query region
+    assert lib.padra_DecodeAttentionScratch(abi.KV_BF16, 1, 1, 1) == 132
+    assert lib.padra_DecodeAttentionScratch(abi.KV_Q8_0, 1, 1, 1) == 132 + 36
     assert lib.padra_DecodeAttention(None, _p(16), ctypes.byref(kv), _p(32), ctypes.byref(dec), 2,
                                      16, 4, 0, 0, _p(64), need - 1, bad, 0) == abi.INVALID_ARGUMENT
     assert lib.padra_DecodeAttention(None, _p(16), ctypes.byref(kv), _p(32), ctypes.byref(dec), 2,

@@ -104,6 +104,46 @@ def test_kv_store_then_commit(oracle, fmt):
         assert np.array_equal(rs.cpu().numpy()[slots], es[first:])
 
 
+@pytest.mark.parametrize("fmt", [abi.KV_Q8, abi.KV_Q8_0, abi.KV_Q8_0_NOROT])
+def test_kv_store_nonfinite_pairs(oracle, fmt):
+    """The store-only encoder writes a (token, head) pair's K and V rows together or not
+    at all (kv_q8.cuh:49-54, kv_q8_native.cuh:70-92): a NaN in K only (token 2 head 1),
+    an infinity in V only (token 9 head 3), and a V value of 1e9 whose q8_0 block scale
+    overflows fp16 (token 20 head 0, block 2: blocks 0-1 of both written, 2-3 of
+    neither).  Caches start filled with a pattern; every byte is compared with the
+    oracle's encoders, which follow the reference."""
+    print(f"[case] kv store nonfinite pairs fmt={fmt}", flush=True)
+    tokens = 37
+    d = synth.chain_inputs(tokens, outliers=True, seed=61 + fmt)
+    k, v = d["k"].view(np.uint16).copy(), d["v"].view(np.uint16).copy()
+    k[2, 1, 40] = 0x7FC0
+    v[9, 3, 3] = 0x7F80
+    v[20, 0, 70] = 0x4E6E
+    ek, ev, es = (np.full_like(a, 0x5A) if a is not None else None
+                  for a in _expected(oracle, fmt, k, v, np.arange(tokens, dtype=np.int32),
+                                     tokens, 0))
+    if es is not None:
+        es[:] = 7.0
+    pos = np.arange(tokens, dtype=np.int32)
+    if fmt == abi.KV_Q8:
+        assert oracle.kv_q8_encode(k, v, ek, ev, es, pos, tokens, 0)
+    else:
+        assert oracle.kv_q8_0_encode(k, v, ek, ev, pos, tokens, 0, rotate=fmt == abi.KV_Q8_0)
+    ck, cv, cs = _cache(fmt, tokens)
+    ck.fill_(0x5A)
+    cv.fill_(0x5A)
+    if cs is not None:
+        cs.fill_(7.0)
+    bad = flag()
+    ops.KVStore(dev(k), dev(v), ops.positions_base(0), ops.kv_cache(fmt, ck, cv, tokens, scales=cs),
+                bad)
+    torch.cuda.synchronize()
+    assert bad.item() == 1
+    assert np.array_equal(_np(ck, fmt), ek) and np.array_equal(_np(cv, fmt), ev)
+    if es is not None:
+        assert np.array_equal(cs.cpu().numpy(), es)
+
+
 def test_kv_store_decode_states(oracle):
     seqs, cap = 8, 128
     rng = np.random.default_rng(3)
@@ -793,3 +833,59 @@ def test_embed_chain_matches_gather_then_chain(oracle, mode, fmt):
     wx, wy, _, _ = oracle.residual_rmsnorm(xin, d["residual"].reshape(seqs, hidden),
                                            d["gamma"], threads=256)
     assert np.array_equal(fused[0], wx) and np.array_equal(fused[1], wy)
+
+
+@pytest.mark.parametrize("fmt,fp8", [(abi.KV_BF16, False), (abi.KV_Q8, False),
+                                     (abi.KV_Q8_0, False), (abi.KV_BF16, True),
+                                     (abi.KV_Q8, True)])
+def test_decode_attention_scratch_bounds(oracle, fmt, fp8):
+    """The split and merge kernels stay inside the padra_DecodeAttentionScratch floats: a
+    scratch of exactly that size followed by sentinel floats keeps every sentinel, and the
+    output equals the one computed with an oversized scratch."""
+    print(f"[case] decode attention scratch bounds fmt={fmt} fp8={fp8}", flush=True)
+    seqs, hq, hkv, cap, splits = 3, 4, 4, 512, 5
+    rng = np.random.default_rng(150 + fmt)
+    positions = np.array([0, 300, 511], np.int32)
+    q = dev(synth.bf16_bits(rng.standard_normal((seqs, hq, 128)).astype(np.float32)))
+    scales = None
+    if fmt == abi.KV_BF16:
+        kc = dev(synth.bf16_bits(rng.standard_normal((seqs * cap, 512)).astype(np.float32)))
+        vc = dev(synth.bf16_bits(rng.standard_normal((seqs * cap, 512)).astype(np.float32)))
+    elif fmt == abi.KV_Q8:
+        kc = torch.from_numpy(rng.integers(-127, 128, (seqs * cap, 512)).astype(np.int8)).cuda()
+        vc = torch.from_numpy(rng.integers(-127, 128, (seqs * cap, 512)).astype(np.int8)).cuda()
+        scales = torch.from_numpy(rng.uniform(0.005, 0.02, (seqs * cap, hkv, 2))
+                                  .astype(np.float32)).cuda()
+    else:
+        rk = np.zeros((seqs * cap, 544), np.uint8)
+        rv = np.zeros((seqs * cap, 544), np.uint8)
+        d = synth.chain_inputs(seqs * cap, outliers=True, seed=151)
+        oracle.kv_q8_0_encode(d["k"], d["v"], rk, rv, np.arange(seqs * cap, dtype=np.int32),
+                              seqs * cap)
+        kc, vc = dev(rk), dev(rv)
+    kv = ops.kv_cache(fmt, kc, vc, cap, scales=scales, seq_stride=cap)
+    states = np.zeros((seqs, 8), np.int32)
+    for s, p in enumerate(positions):
+        states[s] = [5, p, cap, 10, p, min(p, 1024), 0, 0]
+    pos = ops.positions_decode(torch.from_numpy(states).cuda(), maximum=cap)
+    need = abi.lib().padra_DecodeAttentionScratch(fmt, seqs, hq, splits)
+    assert need > 0 and need % 4 == 0
+    guard = 4096
+    sentinel = -12345.678
+    outs = []
+    for extra in (guard, 1 << 20):
+        scratch = torch.full((need + extra,), sentinel, dtype=torch.float32, device="cuda")
+        out = torch.empty((seqs, hq, 128), dtype=torch.int16, device="cuda")
+        bad = flag()
+        packed = scl = None
+        if fp8:
+            packed = torch.empty((seqs, hq * 128), dtype=torch.uint8, device="cuda")
+            scl = torch.empty(seqs, dtype=torch.float32, device="cuda")
+        ops.DecodeAttention(q, kv, out, pos, bad, kv_heads=hkv, splits=splits,
+                            scratch=scratch[:need], packed=packed, scales=scl)
+        torch.cuda.synchronize()
+        assert bad.item() == 0
+        tail = scratch[need:].cpu().numpy()
+        assert np.all(tail == np.float32(sentinel)), int(np.argmax(tail != np.float32(sentinel)))
+        outs.append(host16(out))
+    assert np.array_equal(outs[0], outs[1])

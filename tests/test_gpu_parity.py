@@ -388,11 +388,13 @@ def test_store_nonfinite_heads(oracle, fmt, act):
     """Non-finite K and V heads in the quantized stores (kv_q8.cuh:49-54,
     kv_q8_native.cuh:70-79): the flag is raised and the head's codes and scales are not
     written.  Token 3 head 1 has a NaN in K and V, token 10 head 2 infinities in both,
-    token 17 head 0 a NaN in V only.  The reference encodes K and V of a head together and
-    writes neither when one is invalid; the store here writes the valid K head of token 17,
-    so that K row is left out of the comparison.  The caches start filled with a pattern,
-    so that a row written with zero codes and scales differs from a row left alone; a
-    second launch with only the V head of token 17 invalid must raise the flag by itself."""
+    token 17 head 0 a NaN in V only: as in the reference, which encodes K and V of a head
+    together, neither the K nor the V row of that head is written.  Token 25 head 3 has a
+    V value of 1e9, whose q8_0 block scale overflows fp16 (block 2, both rotations): blocks
+    0 and 1 of K and V are written, blocks 2 and 3 of neither (kv_q8_native.cuh:84-92).
+    The caches start filled with a pattern, so that a row written with zero codes and
+    scales differs from a row left alone; a second launch with only the V head of token
+    17 invalid must raise the flag by itself.  Every byte of both caches is compared."""
     print(f"[case] store nonfinite fmt={fmt} act={act}", flush=True)
     tokens, capacity = 40, 4096
     d0 = synth.chain_inputs(tokens, outliers=False, seed=91 + fmt)
@@ -408,6 +410,7 @@ def test_store_nonfinite_heads(oracle, fmt, act):
             k[3, 1, 5], v[3, 1, 77] = 0x7FC0, 0x7FC0
             k[10, 2, 0], v[10, 2, 127] = 0x7F80, 0xFF80
         v[17, 0, 64] = 0x7FC0
+        v[25, 3, 70] = 0x4E6E  # bf16(1e9)
         d["k"], d["v"] = k.view(d0["k"].dtype), v.view(d0["v"].dtype)
         _, wk, _ = _qk_oracle(oracle, d, tb, positions)
         width = 512 if fmt == abi.KV_Q8 else 544
@@ -431,13 +434,14 @@ def test_store_nonfinite_heads(oracle, fmt, act):
                             ops.positions_base(0), bad, v=conv(d["v"]), kv=kv)
         torch.cuda.synchronize()
         assert bad.item()
-        rows = np.arange(capacity) != 17
         assert np.array_equal(_np(vc, fmt), ev)
-        assert np.array_equal(_np(kc, fmt)[rows], ek[rows])
+        assert np.array_equal(_np(kc, fmt), ek)
+        # head 0 of token 17 (q8: codes 0-127; q8_0: scales d[0..3] and codes qs[0..127])
+        head0 = np.r_[0:128] if fmt == abi.KV_Q8 else np.r_[0:8, 32:160]
+        for c in (kc, vc):
+            assert np.all(_np(c, fmt)[17, head0] == kind(fill_code))
         if es is not None:
-            got = sc.cpu().numpy()
-            assert np.array_equal(got[..., 1], es[..., 1])
-            assert np.array_equal(got[rows, :, 0], es[rows, :, 0])
+            assert np.array_equal(sc.cpu().numpy(), es)
 
     run(True)
     run(False)
