@@ -309,6 +309,21 @@ int padra_DecodeAttentionFP8(void *stream, const void *q, const padra_KVCache *k
 /* Floats of scratch padra_DecodeAttention needs for a cache format (splits as passed,
  * 1..32); -1 if invalid. */
 long long padra_DecodeAttentionScratch(int format, int seqs, int q_heads, int splits);
+/* padra_DecodeAttentionNoAlloc: no counterpart in the reference.  For callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc): padra_DecodeAttention with the same kernels and results, whose
+ * workspace is a fixed device array of PADRA_DECODE_ATTENTION_STATIC_FLOATS floats
+ * (18 MiB: 64 sequences x 16 query heads x 32 splits fit) instead of a caller buffer.  It
+ * calls no allocator.  The array exists once per GPU and is held until the process ends;
+ * its address is looked up on the first call on each device.  A launch that needs more
+ * (padra_DecodeAttentionScratch) returns PADRA_INVALID_ARGUMENT with a message on stderr
+ * and launches nothing.  Every call on one GPU uses that GPU's one array: calls ordered
+ * on one stream are safe, calls that overlap on one GPU (several streams or threads)
+ * race. */
+#define PADRA_DECODE_ATTENTION_STATIC_FLOATS 4718592
+int padra_DecodeAttentionNoAlloc(void *stream, const void *q, const padra_KVCache *kv,
+                                 void *out, const padra_Positions *pos, int seqs, int q_heads,
+                                 int kv_heads, int local, int splits, int *bad, int act);
 /* padra_CheckFP8Paths: no counterpart in the reference.  Checks, over their whole domains,
  * the two identities padra_NormFP8's fast path relies on (the hardware E4M3 conversion, and
  * the reciprocal-plus-correction quotient) and writes the mismatch counts to counts[0..1]

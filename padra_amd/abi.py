@@ -64,6 +64,9 @@ _I = ctypes.c_int
 _F = ctypes.c_float
 
 # name -> argtypes (restype int unless listed otherwise)
+# Floats of padra_DecodeAttentionNoAlloc's fixed device workspace (padra_hip.h).
+DECODE_ATTENTION_STATIC_FLOATS = 4718592
+
 SIGNATURES = {
     "padra_ResidualPostNorm": [_P, _P, _P, _P, _P, _I, _I, _F, _I, _P, _P, _I],
     "padra_RopeTable": [_P, _I, _I, _F, _I, _F, _I],
@@ -87,6 +90,8 @@ SIGNATURES = {
     "padra_DecodeAttentionScratch": [_I, _I, _I, _I],
     "padra_DecodeAttention": [_P, _P, ctypes.POINTER(KVCache), _P, ctypes.POINTER(Positions), _I,
                               _I, _I, _I, _I, _P, ctypes.c_longlong, _P, _I],
+    "padra_DecodeAttentionNoAlloc": [_P, _P, ctypes.POINTER(KVCache), _P,
+                                     ctypes.POINTER(Positions), _I, _I, _I, _I, _I, _P, _I],
     "padra_DecodeAttentionFP8": [_P, _P, ctypes.POINTER(KVCache), _P, _P, _P,
                                  ctypes.POINTER(Positions), _I, _I, _I, _I, _I, _P,
                                  ctypes.c_longlong, _P, _I],

@@ -25,6 +25,8 @@
 #include <stdio.h>
 
 #include <algorithm>
+#include <atomic>
+#include <mutex>
 
 #include "common.h"
 #include "norm_fp8.h"
@@ -1024,6 +1026,14 @@ extern "C" long long padra_DecodeAttentionScratch(int format, int seqs, int q_he
 }
 
 namespace {
+// The reference's split counts: q8_0 16 (local) or 32; otherwise one per 32 keys of the
+// ring, at most 16 (local) or 32.
+int reference_splits(const padra_KVCache *kv, int local) {
+  if (kv->format == PADRA_KV_Q8_0)
+    return local ? 16 : 32;
+  return std::min((kv->cap + kKeys - 1) / kKeys, local ? 16 : 32);
+}
+
 // Both entry points: packed/scales non-null selects the merge with the FP8 encoding.
 int decode_attention(void *stream, const void *q, const padra_KVCache *kv, void *out,
                      uint8_t *packed, float *scales, const padra_Positions *pos, int seqs,
@@ -1049,8 +1059,8 @@ int decode_attention(void *stream, const void *q, const padra_KVCache *kv, void 
   const bool q8 = kv->format == PADRA_KV_Q8_0, q8s = kv->format == PADRA_KV_Q8;
   if (q8 && kv_heads * kD != 512)
     return PADRA_UNSUPPORTED; // the 544-byte q8_0 row of 4 KV heads
-  if (splits == 0) // the reference's counts
-    splits = q8 ? (local ? 16 : 32) : std::min((kv->cap + kKeys - 1) / kKeys, local ? 16 : 32);
+  if (splits == 0)
+    splits = reference_splits(kv, local);
   const long long need = padra_DecodeAttentionScratch(kv->format, seqs, q_heads, splits);
   if (scratch_floats < need)
     return PADRA_INVALID_ARGUMENT;
@@ -1155,4 +1165,67 @@ extern "C" int padra_DecodeAttentionFP8(void *stream, const void *q, const padra
     return PADRA_INVALID_ARGUMENT;
   return decode_attention(stream, q, kv, out, packed, scales, pos, seqs, q_heads, kv_heads,
                           local, splits, scratch, scratch_floats, bad, act);
+}
+
+// ---- the entry point that allocates nothing ---------------------------------------------
+//
+// padra_DecodeAttentionNoAlloc's workspace: a fixed array in device memory, one copy per
+// GPU the library runs on, held until the process ends.  Its name is a host-side
+// stand-in, not a device address: host code uses only the address hipGetSymbolAddress
+// returns for the current device (scratch_address below).
+static __device__ __align__(256) float scratch[PADRA_DECODE_ATTENTION_STATIC_FLOATS];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::atomic<float *> g_scratch_address[kMaxDevices];
+std::mutex g_scratch_mutex;
+
+// The array's device address on the current device, looked up on the first call there;
+// null when the lookup fails.
+float *scratch_address() {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return nullptr;
+  float *p = g_scratch_address[dev].load(std::memory_order_acquire);
+  if (p)
+    return p;
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  p = g_scratch_address[dev].load(std::memory_order_relaxed);
+  if (!p) {
+    void *address = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&address, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !address) {
+      fprintf(stderr, "padra: DecodeAttentionNoAlloc: workspace lookup failed: %s\n",
+              hipGetErrorString(e));
+      return nullptr;
+    }
+    p = static_cast<float *>(address);
+    g_scratch_address[dev].store(p, std::memory_order_release);
+  }
+  return p;
+}
+} // namespace
+
+extern "C" int padra_DecodeAttentionNoAlloc(void *stream, const void *q, const padra_KVCache *kv,
+                                            void *out, const padra_Positions *pos, int seqs,
+                                            int q_heads, int kv_heads, int local, int splits,
+                                            int *bad, int act) {
+  if (!kv || splits < 0 || splits > 32)
+    return PADRA_INVALID_ARGUMENT;
+  const long long need = padra_DecodeAttentionScratch(
+      kv->format, seqs, q_heads, splits ? splits : reference_splits(kv, local));
+  if (need < 0)
+    return PADRA_INVALID_ARGUMENT;
+  if (need > PADRA_DECODE_ATTENTION_STATIC_FLOATS) {
+    fprintf(stderr,
+            "padra: DecodeAttentionNoAlloc: %lld workspace floats needed (%d sequences, %d "
+            "query heads), the fixed workspace holds %d; use padra_DecodeAttention\n",
+            need, seqs, q_heads, PADRA_DECODE_ATTENTION_STATIC_FLOATS);
+    return PADRA_INVALID_ARGUMENT;
+  }
+  float *ws = scratch_address();
+  if (!ws)
+    return PADRA_INTERNAL;
+  return decode_attention(stream, q, kv, out, nullptr, nullptr, pos, seqs, q_heads, kv_heads,
+                          local, splits, ws, PADRA_DECODE_ATTENTION_STATIC_FLOATS, bad, act);
 }

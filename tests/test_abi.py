@@ -26,6 +26,12 @@ def test_library_exports_every_declaration():
     assert set(names) <= set(abi.SIGNATURES)
 
 
+def test_static_workspace_size_matches_header():
+    text = open(os.path.join(ROOT, "include", "padra_hip.h")).read()
+    m = re.search(r"#define PADRA_DECODE_ATTENTION_STATIC_FLOATS (\d+)", text)
+    assert m and int(m.group(1)) == abi.DECODE_ATTENTION_STATIC_FLOATS
+
+
 def test_version():
     assert b"gfx950" in abi.lib().padra_version()
 
@@ -150,6 +156,15 @@ def test_host_validation_newer_entry_points():
                                      2, 16, 4, 0, 0, _p(64), need, bad, 0) == abi.UNSUPPORTED
     assert lib.padra_DecodeAttention(None, _p(16), ctypes.byref(kv), _p(32), ctypes.byref(base),
                                      2, 16, 4, 0, 0, _p(64), need, bad, 0) == abi.INVALID_ARGUMENT
+    # the entry point without a workspace argument refuses launches its fixed array cannot
+    # hold (64 sequences x 64 query heads x 32 splits), before touching a device
+    assert lib.padra_DecodeAttentionScratch(abi.KV_BF16, 64, 64, 32) > \
+        abi.DECODE_ATTENTION_STATIC_FLOATS
+    assert lib.padra_DecodeAttentionNoAlloc(None, _p(16), ctypes.byref(kv), _p(32),
+                                            ctypes.byref(dec), 64, 64, 8, 0, 32, bad, 0) == \
+        abi.INVALID_ARGUMENT
+    assert lib.padra_DecodeAttentionNoAlloc(None, _p(16), None, _p(32), ctypes.byref(dec), 2,
+                                            16, 4, 0, 0, bad, 0) == abi.INVALID_ARGUMENT
     # the FP8 merge: both outputs required and aligned, at most 32 query heads, no q8_0
     fp8 = lib.padra_DecodeAttentionFP8
     assert fp8(None, _p(16), ctypes.byref(kv), _p(32), None, _p(96), ctypes.byref(dec), 2, 16,
