@@ -1,0 +1,215 @@
+"""GPU parity at the full sizes of BASELINE.json's configurations 0, 3 and 4, through the
+C-ABI, against the CPU oracle, bit for bit.
+
+- config 0: the fused chain (residual + RMSNorm with the 256-thread tree, Q/K norm + RoPE,
+  BF16 KV store) for one decode token at position 4097 of an 8192-row cache;
+- config 3: SwiGLU over 2048 tokens x top-8 = 16384 expert-permuted rows of width 1024
+  (several grid-stride iterations per thread), in place over gate;
+- config 4: the batched decode step of 64 sequences, vocabulary 131072, ragged positions
+  up to 131071, per-sequence caches of 131072 rows (row offsets above 4 GiB), both as one
+  fused launch and as gather then chain, in every KV format.  The caches are too large to
+  copy back whole: the written rows are gathered on the device and compared, and a count
+  of non-zero bytes over the whole cache shows that nothing else was written.
+"""
+import numpy as np
+import pytest
+import torch
+
+from padra_amd import abi, ops, synth
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module", autouse=True)
+def gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    abi.lib()
+    yield
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+
+
+def dev(a):
+    a = np.ascontiguousarray(a)
+    if a.dtype == np.uint16:
+        return torch.from_numpy(a.view(np.int16)).cuda()
+    return torch.from_numpy(a).cuda()
+
+
+def host16(t):
+    return t.cpu().numpy().view(np.uint16)
+
+
+def flag():
+    return torch.zeros(1, dtype=torch.int32, device="cuda")
+
+
+def _cache(fmt, rows):
+    if fmt == abi.KV_BF16:
+        mk = lambda: torch.zeros((rows, 512), dtype=torch.int16, device="cuda")
+        return mk(), mk(), None
+    if fmt == abi.KV_Q8:
+        mk = lambda: torch.zeros((rows, 512), dtype=torch.int8, device="cuda")
+        return mk(), mk(), torch.zeros((rows, 4, 2), dtype=torch.float32, device="cuda")
+    mk = lambda: torch.zeros((rows, 544), dtype=torch.uint8, device="cuda")
+    return mk(), mk(), None
+
+
+def _row_bytes(a):
+    """Host bytes of cache rows (any dtype) as uint8 [rows][bytes]."""
+    a = np.ascontiguousarray(a)
+    return a.view(np.uint8).reshape(a.shape[0], -1)
+
+
+def _expected_rows(oracle, fmt, wk, v):
+    """The K and V (and q8 scale) rows the reference writes for tokens whose rotated K is
+    wk and V is v, one row per token (each token encoded alone into a 1-row cache)."""
+    tokens = wk.shape[0]
+    rk, rv, rs = [], [], []
+    for t in range(tokens):
+        zero = np.zeros(1, np.int32)
+        if fmt == abi.KV_BF16:
+            kc, vc = np.zeros((1, 512), np.uint16), np.zeros((1, 512), np.uint16)
+            oracle.kv_store_bf16(wk[t:t + 1], v[t:t + 1], kc, vc, zero, 1, 0)
+            sc = None
+        elif fmt == abi.KV_Q8:
+            kc, vc = np.zeros((1, 512), np.int8), np.zeros((1, 512), np.int8)
+            sc = np.zeros((1, 4, 2), np.float32)
+            assert not oracle.kv_q8_encode(wk[t:t + 1], v[t:t + 1], kc, vc, sc, zero, 1, 0)
+        else:
+            kc, vc = np.zeros((1, 544), np.uint8), np.zeros((1, 544), np.uint8)
+            assert not oracle.kv_q8_0_encode(wk[t:t + 1], v[t:t + 1], kc, vc, zero, 1, 0,
+                                             rotate=fmt == abi.KV_Q8_0)
+            sc = None
+        rk.append(_row_bytes(kc)[0])
+        rv.append(_row_bytes(vc)[0])
+        if sc is not None:
+            rs.append(sc[0])
+    return np.stack(rk), np.stack(rv), (np.stack(rs) if rs else None)
+
+
+def test_config0_chain_position_4097(oracle):
+    """Config 0 as one fused launch: 1 token, DecodeState at position 4097, capacity 8192,
+    residual + RMSNorm in the decode kernel's 256-thread tree, then Q/K + BF16 store."""
+    print("[case] config0 chain at 4097", flush=True)
+    capacity, pos = 8192, 4097
+    d = synth.chain_inputs(1, outliers=False, seed=0)
+    tb = synth.bf16_bits(oracle.rope_table(capacity, 128, 1e6))
+    wx, wy, wst, wbad = oracle.residual_rmsnorm(d["x"], d["residual"], d["gamma"], threads=256)
+    wq, wk, _ = oracle.qk_norm_rope(d["q"], d["k"], d["qn"], d["kn"], tb,
+                                    np.array([pos], np.int32))
+    assert not wbad
+    x, r, g = dev(d["x"]), dev(d["residual"]), dev(d["gamma"])
+    y = torch.empty_like(x)
+    q, k = dev(d["q"]), dev(d["k"])
+    kc, vc, _ = _cache(abi.KV_BF16, capacity)
+    state = torch.tensor([[5, pos, capacity, 10, pos, 1024, 0, 0]], dtype=torch.int32,
+                         device="cuda")
+    st = torch.empty((1, 2), dtype=torch.float32, device="cuda")
+    bad = flag()
+    ops.ResidualNormQKRopeStore(x, r, y, g, q, k, dev(d["v"]), dev(d["qn"]), dev(d["kn"]),
+                                dev(tb), ops.positions_decode(state, maximum=capacity),
+                                ops.kv_cache(abi.KV_BF16, kc, vc, capacity), bad,
+                                tree=abi.TREE_256, statistics=st)
+    torch.cuda.synchronize()
+    assert bad.item() == 0
+    assert np.array_equal(host16(x), wx) and np.array_equal(host16(y), wy)
+    assert np.array_equal(st.cpu().numpy(), wst)
+    assert np.array_equal(host16(q), wq) and np.array_equal(host16(k), wk)
+    assert np.array_equal(host16(kc[pos]), wk.reshape(-1))
+    assert np.array_equal(host16(vc[pos]), d["v"].reshape(-1))
+    assert int((kc != 0).sum().item()) == int((kc[pos] != 0).sum().item())
+    assert int((vc != 0).sum().item()) == int((vc[pos] != 0).sum().item())
+
+
+@pytest.mark.parametrize("act", ["bf16", "f32"])
+def test_config3_swiglu_full(oracle, act):
+    """16384 expert-permuted rows x 1024, gate and up N(0, 2): every output bit against the
+    oracle, written in place over gate as the reference does (inference.cu:2554-2555)."""
+    print(f"[case] config3 swiglu full act={act}", flush=True)
+    d = synth.swiglu_inputs(tokens=2048, seed=3)
+    assert d["gate"].shape == (16384, 1024)
+    want, wbad = oracle.swiglu(d["gate"], d["up"])
+    assert not wbad
+    table = torch.empty(65536, dtype=torch.int16, device="cuda")
+    ops.SiluTableBuild(table)
+    if act == "bf16":
+        g, u = dev(d["gate"]), dev(d["up"])
+    else:
+        g = torch.from_numpy(synth.bf16_to_f32(d["gate"])).cuda()
+        u = torch.from_numpy(synth.bf16_to_f32(d["up"])).cuda()
+    bad = flag()
+    ops.SwiGLU(g, u, g, table, bad)
+    torch.cuda.synchronize()
+    assert bad.item() == 0
+    got = host16(g) if act == "bf16" else synth.bf16_bits(g.cpu().numpy())
+    if act == "f32":  # fp32 words holding BF16-exact values
+        assert np.array_equal(g.cpu().numpy(), synth.bf16_to_f32(want))
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("fmt", [abi.KV_BF16, abi.KV_Q8, abi.KV_Q8_0, abi.KV_Q8_0_NOROT])
+def test_config4_decode_step_full(oracle, fmt):
+    """64 sequences, embedding table 131072 x 2048 N(0, 0.02), Zipf(1.1) token ids,
+    positions U[0, 131071] (131071 and 0 included), per-sequence caches of 131072 rows
+    seq_stride 131072 apart: fused gather + chain, and padra_Embed then the chain, both
+    against the oracle."""
+    print(f"[case] config4 decode step full fmt={fmt}", flush=True)
+    seqs, vocab, hidden, capacity = 64, 131072, 2048, 131072
+    rng = np.random.default_rng(404)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(4)
+    emb = (torch.randn((vocab, hidden), generator=gen, device="cuda") * 0.02) \
+        .to(torch.bfloat16).view(torch.int16)
+    ids = synth.zipf_ids(seqs, vocab, 1.1, seed=4)
+    ids[2] = vocab - 1
+    positions = rng.integers(0, capacity, seqs).astype(np.int32)
+    positions[0], positions[1], positions[63] = capacity - 1, 0, capacity - 2
+    d = synth.chain_inputs(seqs, outliers=True, seed=44)
+    tb = synth.bf16_bits(oracle.rope_table(capacity, 128, 1e6))
+    states = np.zeros((seqs, 8), np.int32)
+    for s, p in enumerate(positions):
+        states[s] = [ids[s], p, capacity, 10, p, min(int(p), 1024), 0, 0]
+    xin = host16(emb[torch.from_numpy(ids).long().cuda()])
+    wx, wy, _, wbad = oracle.residual_rmsnorm(xin, d["residual"].reshape(seqs, hidden),
+                                              d["gamma"], threads=256)
+    wq, wk, _ = oracle.qk_norm_rope(d["q"], d["k"], d["qn"], d["kn"], tb, positions)
+    assert not wbad
+    ek, ev, es = _expected_rows(oracle, fmt, wk, d["v"])
+    kc, vc, sc = _cache(fmt, seqs * capacity)
+    rows = torch.from_numpy(np.arange(seqs) * capacity + positions).long().cuda()
+    table_dev, st = dev(tb), dev(states)
+    for fused in (True, False):
+        print(f"  fused={fused}", flush=True)
+        for c in (kc, vc, sc):
+            if c is not None:
+                c.zero_()
+        x = torch.from_numpy(d["x"].reshape(seqs, hidden).view(np.int16)).cuda()
+        r = torch.from_numpy(d["residual"].reshape(seqs, hidden).view(np.int16)).cuda()
+        y = torch.empty_like(x)
+        q, k = dev(d["q"]), dev(d["k"])
+        bad = flag()
+        pos = ops.positions_decode(st, maximum=capacity, vocab=vocab)
+        kv = ops.kv_cache(fmt, kc, vc, capacity, scales=sc, seq_stride=capacity)
+        args = (x, r, y, dev(d["gamma"]), q, k, dev(d["v"]), dev(d["qn"]), dev(d["kn"]),
+                table_dev, pos, kv, bad)
+        if fused:
+            ops.EmbedResidualNormQKRopeStore(emb, dev(ids), *args, tree=abi.TREE_256)
+        else:
+            ops.Embed(emb, x, bad, positions=pos)
+            ops.ResidualNormQKRopeStore(*args, tree=abi.TREE_256)
+        torch.cuda.synchronize()
+        assert bad.item() == 0
+        assert np.array_equal(host16(x), wx) and np.array_equal(host16(y), wy)
+        assert np.array_equal(host16(q), wq) and np.array_equal(host16(k), wk)
+        gk, gv = kc[rows].cpu().numpy(), vc[rows].cpu().numpy()
+        assert np.array_equal(_row_bytes(gk), ek) and np.array_equal(_row_bytes(gv), ev)
+        # nothing written outside the 64 rows
+        assert int((kc != 0).sum().item()) == int((kc[rows] != 0).sum().item())
+        assert int((vc != 0).sum().item()) == int((vc[rows] != 0).sum().item())
+        if sc is not None:
+            assert np.array_equal(sc[rows].cpu().numpy(), es)
+            assert int((sc != 0).sum().item()) == int((sc[rows] != 0).sum().item())
+    del kc, vc, sc, emb
+    torch.cuda.empty_cache()
