@@ -12,7 +12,9 @@ import subprocess
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB = os.path.join(HERE, "libpadra_oracle.so")
+# PADRA_ORACLE_LIB selects another build of the same source (the sanitizer build of
+# `make -C oracle asan`).
+LIB = os.environ.get("PADRA_ORACLE_LIB") or os.path.join(HERE, "libpadra_oracle.so")
 
 
 def build() -> str:

@@ -408,10 +408,18 @@ void po_rope_table(float *table, int positions, int head_dim, float theta, int y
 void po_qk_norm_rope_head(uint16_t *x, const uint16_t *weight, const uint16_t *table_row,
                           int head_dim, float eps, int *bad) {
   float v[1024], o[1024];
+  if (head_dim < 2 || head_dim > 1024 || head_dim % 2) { /* outside the local arrays */
+    set_bad(bad);
+    return;
+  }
   const int half = head_dim / 2;
   for (int i = 0; i < head_dim; ++i)
     v[i] = po_bf16_to_f32(x[i]);
+  /* v[0..head_dim) is written above; GCC cannot see that head_dim >= 2 holds here */
+#pragma GCC diagnostic push
+#pragma GCC diagnostic ignored "-Wmaybe-uninitialized"
   const float s = po_sumsq_tree(v, head_dim, 128);
+#pragma GCC diagnostic pop
   float var, inv;
   po_rms_inv(s, head_dim, eps, &var, &inv);
   for (int i = 0; i < head_dim; ++i)
