@@ -241,6 +241,9 @@ def cpu_baseline(host, seconds, threads):
         "value": rate(many),
         "unit": "GB/s",
         "cores": threads,
+        "host_cpus": os.cpu_count(),
+        "host_cpus_usable": len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else None,
+        "cpu_model": cpu_model(),
         "kind": "port",
         "sample": f"{reps} full 2048-token config-1 chunks (BF16 KV) on {threads} threads and "
                   f"{reps1} on one thread, about {seconds / 2:.0f} s each",
@@ -500,6 +503,18 @@ def bench_decode(torch, steps, seqs, vocab=131072, capacity=CAPACITY):
             "bytes_per_step": nbytes, "gbs": round(nbytes / (ms * 1e-3) / 1e9, 2)}
 
 
+def cpu_model() -> str:
+    """The host CPU's model name (lscpu's "Model name", from /proc/cpuinfo)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_threads() -> int:
     """Host threads for the CPU baseline: the box's CPU share for one GPU (16), or fewer
     where fewer cores exist."""
@@ -587,7 +602,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": traffic_from_profiles(formats[0]),
-                     "kernel": "k_chain<128,16,fmt,false>", "bytes_per_launch": head["bytes"]},
+                     "kernel": chain_kernel(formats[0]), "bytes_per_launch": head["bytes"]},
         "copy_ceiling_gbs": round(stream_gbs, 1),
         "copy_ceiling": {"kernel": "padra_StreamCopy", "bytes_per_launch": 2 * (head["bytes"] // 2 // 16 * 16),
                          "us_per_launch": round(stream_ms * 1e3, 3), "gbs": round(stream_gbs, 1),
@@ -599,7 +614,8 @@ def main():
                             round(float(np.percentile(r["spread"], q)) * 1e3, 3)
                             for q in (10, 50, 90)],
                         "bytes_per_launch": r["bytes"],
-                        "frac": round(r["gbs"] / HBM_PEAK_GBS, 4)} for f, r in results.items()},
+                        "frac": round(r["gbs"] / HBM_PEAK_GBS, 4),
+                        "traffic": traffic_from_profiles(f)} for f, r in results.items()},
     }
     if not args.no_configs:
         torch.cuda.empty_cache()
@@ -619,79 +635,123 @@ def main():
     print(json.dumps(line), flush=True)
 
 
-CHAIN_KERNEL = "k_chain<128, 16, 0, false>"  # config 1: tree 128, H 2048, BF16 KV, no gather
+FORMAT_CODES = {"bf16": 0, "q8": 1, "q8_0": 2, "q8_0_norot": 3}
+
+
+def chain_kernel(fmt: str) -> str:
+    """Kernel-trace name of the config-1 chain launch (tree 128, H 2048, no gather)."""
+    return f"k_chain<128, 16, {FORMAT_CODES[fmt]}, false>"
+
+
+def hbm_bytes(c: dict) -> dict:
+    """HBM bytes of one dispatch from the TCC-to-memory request counts.  Reads: on gfx950
+    every read request to memory that is not a 32-byte one moves a 128-byte line (reading
+    a 32 MiB buffer issues 262,144 of them and TCC_BUBBLE, the 128-byte request counter the
+    FETCH_SIZE formula relies on, stays 0, so FETCH_SIZE counts those lines as 64 bytes:
+    half the bytes).  Writes: 64-byte requests plus 32-byte ones (WRITE_SIZE's formula,
+    exact: a 32 MiB write issues 524,288 64-byte requests)."""
+    r, r32 = c["TCC_EA0_RDREQ_sum"], c["TCC_EA0_RDREQ_32B_sum"]
+    w, w64 = c["TCC_EA0_WRREQ_sum"], c["TCC_EA0_WRREQ_64B_sum"]
+    read = 128 * (r - r32) + 32 * r32
+    write = 64 * w64 + 32 * (w - w64)
+    return {"read": read, "write": write, "total": read + write}
+
+
+def _pmc(outdir: str, sub: str) -> dict:
+    """{short kernel name: {counter: median value per dispatch}} of one --pmc pass."""
+    import csv
+    import glob
+    import statistics
+    files = glob.glob(os.path.join(outdir, sub, "**", "*counter_collection.csv"), recursive=True)
+    vals: dict = {}
+    for path in files:
+        for r in csv.DictReader(open(path)):
+            name = r["Kernel_Name"].replace("void ", "").replace("(anonymous namespace)::", "")
+            name = name.split("(")[0]
+            vals.setdefault(name, {}).setdefault(r["Counter_Name"], []).append(
+                float(r["Counter_Value"]))
+    return {k: {c: statistics.median(v) for c, v in d.items()} for k, d in vals.items()}
 
 
 def summarize(outdir: str, command: str) -> None:
     """Digests rocprofv3 CSV output of this script into profiles/ (text only):
-    <outdir>/trace/bench_kernel_stats.csv (--kernel-trace --stats) and
-    <outdir>/fetch|write/bench_counter_collection.csv (--pmc FETCH_SIZE / WRITE_SIZE).
-    HBM traffic per launch = counter KiB x calibration, the calibration being the known
-    bytes moved by the plain copy kernel of the same run over its counter reading."""
+    <outdir>/trace (--kernel-trace --stats), <outdir>/rd (--pmc TCC_EA0_RDREQ_sum
+    TCC_EA0_RDREQ_32B_sum TCC_BUBBLE_sum), <outdir>/wr (--pmc TCC_EA0_WRREQ_sum
+    TCC_EA0_WRREQ_64B_sum) and <outdir>/sq (--pmc of the SQ wave and instruction counters
+    with GRBM_GUI_ACTIVE).  HBM traffic per launch comes from the request counts (hbm_bytes);
+    the streaming copy of known size is listed as the check of that arithmetic."""
     import csv
-    import statistics
+    import glob
     prof = os.path.join(ROOT, "profiles")
     os.makedirs(prof, exist_ok=True)
-    lines = ["# rocprofv3 summary: fused chain, config 1 (2048-token prefill chunk)", "",
-             "Command (from the repository root):", "", "```", command, "```", ""]
-    stats = os.path.join(outdir, "trace", "bench_kernel_stats.csv")
-    chain_ns = None
-    if os.path.exists(stats):
+    lines = ["# rocprofv3 summary: fused chain, config 1 (2048-token prefill chunk), every KV format",
+             "", "Command (from the repository root):", "", "```", command, "```", ""]
+    stats = glob.glob(os.path.join(outdir, "trace", "**", "*kernel_stats.csv"), recursive=True)
+    avg_ns = {}
+    if stats:
         lines += ["## Kernel trace (--kernel-trace --stats)", "",
                   "| kernel | calls | average us | min us | max us |", "|---|---:|---:|---:|---:|"]
-        for r in csv.DictReader(open(stats)):
-            name = r["Name"]
-            short = name.replace("void ", "").replace("(anonymous namespace)::", "").split("(")[0]
+        for r in csv.DictReader(open(stats[0])):
+            short = r["Name"].replace("void ", "").replace("(anonymous namespace)::", "").split("(")[0]
+            avg_ns[short] = float(r["AverageNs"])
             lines.append(f"| `{short[:70]}` | {r['Calls']} | {float(r['AverageNs'])/1e3:.2f} | "
                          f"{float(r['MinNs'])/1e3:.2f} | {float(r['MaxNs'])/1e3:.2f} |")
-            if CHAIN_KERNEL in name and chain_ns is None:
-                chain_ns = float(r["AverageNs"])
         lines.append("")
+    rd, wr, sq = _pmc(outdir, "rd"), _pmc(outdir, "wr"), _pmc(outdir, "sq")
     traffic = {}
-    for counter, sub in (("FETCH_SIZE", "fetch"), ("WRITE_SIZE", "write")):
-        path = os.path.join(outdir, sub, "bench_counter_collection.csv")
-        if not os.path.exists(path):
+    rows = []
+    kernels = [(f, chain_kernel(f), chain_bytes(f) * TOKENS) for f in FORMAT_CODES]
+    copy_name = next((k for k in rd if k.startswith("k_stream_copy")), None)
+    if copy_name:
+        kernels.append(("copy", copy_name, None))
+    for fmt, name, alg in kernels:
+        if name not in rd or name not in wr:
             continue
-        chain, copy = [], []
-        for r in csv.DictReader(open(path)):
-            if r["Counter_Name"] != counter:
-                continue
-            if CHAIN_KERNEL in r["Kernel_Name"]:
-                chain.append(float(r["Counter_Value"]))
-            elif "copyBuffer" in r["Kernel_Name"]:
-                copy.append(float(r["Counter_Value"]))
-        if chain and copy:
-            copy_bytes = COPY_BYTES // 2  # read (FETCH) or written (WRITE) per copy
-            factor = copy_bytes / (statistics.median(copy) * 1024)
-            traffic[counter] = {"chain_kib": statistics.median(chain), "copy_kib": statistics.median(copy),
-                                "calibration": factor,
-                                "chain_bytes": statistics.median(chain) * 1024 * factor}
-    if traffic:
-        lines += ["## HBM traffic per launch (--pmc, calibrated by the copy kernel)", "",
-                  "| counter | chain KiB | copy KiB (known %d B) | calibration | chain bytes |" % (COPY_BYTES // 2),
-                  "|---|---:|---:|---:|---:|"]
-        for c, t in traffic.items():
-            lines.append(f"| {c} | {t['chain_kib']:.0f} | {t['copy_kib']:.0f} | {t['calibration']:.3f} | "
-                         f"{t['chain_bytes']:.0f} |")
-        total = sum(t["chain_bytes"] for t in traffic.values())
-        alg = chain_bytes("bf16") * TOKENS
-        lines += ["", f"Total {total:.0f} B per launch against {alg} algorithmic bytes "
-                      f"({total / alg:.3f}x).", ""]
+        b = hbm_bytes({**rd[name], **wr[name]})
+        if fmt == "copy":
+            alg = b["write"] * 2  # the copy writes exactly what it reads
+        traffic[fmt] = {"kernel": name, "bytes_per_launch": int(b["total"]), "read": int(b["read"]),
+                        "write": int(b["write"]), "algorithmic_bytes": alg,
+                        "ratio": round(b["total"] / alg, 4),
+                        "counters": {**rd[name], **wr[name]}}
+        us = avg_ns.get(name, float("nan")) / 1e3
+        rows.append(f"| {fmt} | `{name}` | {b['read']:.0f} | {b['write']:.0f} | {b['total']:.0f} | "
+                    f"{alg} | {b['total'] / alg:.3f} | {us:.2f} | {alg / (us * 1e3):.0f} |")
+    if rows:
+        lines += ["## HBM traffic per launch (--pmc request counts, no calibration factor)", "",
+                  "Read bytes = 128 x (TCC_EA0_RDREQ_sum - TCC_EA0_RDREQ_32B_sum) + 32 x "
+                  "TCC_EA0_RDREQ_32B_sum; write bytes = 64 x TCC_EA0_WRREQ_64B_sum + 32 x the "
+                  "other write requests (see bench.hbm_bytes).  The copy's read bytes equal its "
+                  "written bytes: the check of the arithmetic.", "",
+                  "| format | kernel | read B | write B | traffic B | algorithmic B | traffic / alg | "
+                  "trace avg us | alg GB/s |", "|---|---|---:|---:|---:|---:|---:|---:|---:|"] + rows + [""]
         with open(os.path.join(prof, "chain_config1_traffic.json"), "w") as f:
-            json.dump({"bf16": {"bytes_per_launch": round(total), "counters": traffic,
-                                "algorithmic_bytes": alg}}, f, indent=1)
-    if chain_ns:
-        alg = chain_bytes("bf16") * TOKENS
-        lines += [f"Kernel-trace average {chain_ns/1e3:.2f} us per launch = "
-                  f"{alg / chain_ns:.1f} GB/s algorithmic.", ""]
-    with open(os.path.join(prof, "chain_config1_bf16.md"), "w") as f:
+            json.dump(traffic, f, indent=1)
+    sq_rows = []
+    for fmt, name, _ in kernels:
+        c = sq.get(name)
+        if not c or not c.get("SQ_WAVES"):
+            continue
+        waves = c["SQ_WAVES"]
+        sq_rows.append(f"| {fmt} | {waves:.0f} | {c.get('SQ_INSTS_VALU', 0) / waves:.0f} | "
+                       f"{c.get('SQ_INSTS_SALU', 0) / waves:.0f} | {c.get('SQ_INSTS_LDS', 0) / waves:.1f} | "
+                       f"{c.get('SQ_INSTS_VMEM_RD', 0) / waves:.1f} | {c.get('SQ_INSTS_VMEM_WR', 0) / waves:.1f} | "
+                       f"{c.get('SQ_INSTS_VALU', 0):.0f} | {c.get('SQ_WAVE_CYCLES', 0) / waves:.0f} | "
+                       f"{c.get('SQ_BUSY_CYCLES', 0):.0f} | {c.get('GRBM_GUI_ACTIVE', 0):.0f} |")
+    if sq_rows:
+        lines += ["## Wave and instruction counters (--pmc SQ_*, GRBM_GUI_ACTIVE)", "",
+                  "Per-wave figures are totals over the dispatch divided by SQ_WAVES.", "",
+                  "| format | waves | VALU / wave | SALU / wave | LDS / wave | VMEM rd / wave | "
+                  "VMEM wr / wave | VALU total | wave cycles / wave | SQ busy cycles | GRBM GUI active |",
+                  "|---|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|"] + sq_rows + [""]
+    with open(os.path.join(prof, "chain_config1.md"), "w") as f:
         f.write("\n".join(lines))
     print("\n".join(lines))
 
 
 def traffic_from_profiles(fmt):
-    """HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE (scaled by
-    the copy-kernel calibration), read from the committed profile summary if present."""
+    """HBM bytes per launch of the chain in `fmt`, from the rocprofv3 request counters
+    (hbm_bytes), read from the committed profile summary if present."""
     path = os.path.join(ROOT, "profiles", "chain_config1_traffic.json")
     if not os.path.exists(path):
         return None
