@@ -11,6 +11,8 @@
 
 #include "norm_fp8.h"
 #include "norm_rows.h"
+#include "norm_wg.h"
+#include "qk_head.h"
 #include "qk_quad.h"
 
 using namespace padra;
@@ -115,6 +117,57 @@ __global__ __launch_bounds__(64) void k_chain(NormArgs<uint16_t> n, QKArgs<uint1
     qk_heads_wave<uint16_t, FMT>(q, w, lds);
   }
 }
+
+// The fused chain for few tokens: a 256-lane workgroup per residual-norm row (norm_wg.h),
+// then four Q/K head vectors per workgroup, one wave each (qk_head.h).
+template <int VT, int J, int FMT, bool GATHER = false>
+__global__ __launch_bounds__(256) void k_chain_small(NormArgs<uint16_t> n, QKArgs<uint16_t> q,
+                                                     long long rows, long long head_waves) {
+  __shared__ float partials[8][2];
+  const long long b = blockIdx.x;
+  if (b < rows) { // workgroup-uniform
+    norm_row_wg<VT, J, GATHER>(n, (int)b, partials);
+    return;
+  }
+  const long long hv = (b - rows) * 4 + (threadIdx.x >> 6);
+  if (hv < head_waves)
+    qk_head_wave<uint16_t, FMT>(q, (unsigned)hv);
+}
+
+// The same with one wave per residual-norm row (norm_rows.h), for the 128-thread tree:
+// its 16 elements per lane at H = 2048 measured faster in one wave (16 / 64 / 128 tokens:
+// 3.4 / 3.7 / 4.0 us) than in a workgroup (4.1 / 4.1 / 4.5 us); the 256-thread decode tree
+// is the other way round (64-sequence decode step: 4.5 -> 3.5 us).
+template <int VT, int J, int FMT, bool GATHER = false>
+__global__ __launch_bounds__(64) void k_chain_heads(NormArgs<uint16_t> n, QKArgs<uint16_t> q,
+                                                    long long norm_waves, long long waves) {
+  const long long b = blockIdx.x;
+  if (b < norm_waves)
+    norm_row_wave<VT, J, uint16_t, true, false, GATHER>(n, (int)b, nullptr);
+  else if (b < waves)
+    qk_head_wave<uint16_t, FMT>(q, (unsigned)(b - norm_waves));
+}
+
+// Residual + RMSNorm, BF16 rows, one 256-lane workgroup per row (norm_wg.h).
+template <int VT, int J>
+__global__ __launch_bounds__(256) void k_norm_small(NormArgs<uint16_t> n) {
+  __shared__ float partials[8][2];
+  norm_row_wg<VT, J, false>(n, blockIdx.x, partials);
+}
+
+template <class T, int FMT> __global__ __launch_bounds__(64) void k_qk_heads(QKArgs<T> a) {
+  qk_head_wave<T, FMT>(a, blockIdx.x);
+}
+
+#ifndef PADRA_HEAD_WAVE_TOKENS
+#define PADRA_HEAD_WAVE_TOKENS 128
+#endif
+// Launches of at most this many tokens with no cache or a BF16 cache use one wave per Q/K
+// head vector (qk_head.h) and, in the fused chain, a workgroup per norm row (norm_wg.h);
+// larger ones the four-lanes-per-head waves (qk_quad.h) and a wave per row.  Measured on
+// MI355X (prefill chain, BF16 cache): per-head 3.4 / 3.7 / 4.0 / 5.2 us at 16 / 64 / 128 /
+// 256 tokens against 4.4 / 4.5 / 4.8 / 5.0 us.
+constexpr int kHeadWaveTokens = PADRA_HEAD_WAVE_TOKENS;
 
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
@@ -293,6 +346,12 @@ extern "C" int padra_ResidualPostNorm(void *stream, void *x, const void *residua
     a.rows = rows;
     a.eps = eps;
     return norm_shape(tree, hidden / tree, [&](auto vt, auto j) -> int {
+      if constexpr (std::is_same<T, uint16_t>::value && vt.value == 256) {
+        if (residual && rows <= kHeadWaveTokens) {
+          hipLaunchKernelGGL((k_norm_small<vt.value, j.value>), dim3(rows), dim3(256), 0, s, a);
+          return launched();
+        }
+      }
       if (residual) {
         hipLaunchKernelGGL((k_norm<vt.value, j.value, T, true>), dim3(grid), dim3(64), 0, s, a);
       } else {
@@ -390,6 +449,13 @@ extern "C" int padra_QKNormRopeStore(void *stream, void *q, void *k, const void 
     const QKArgs<T> a =
         make_qk<T>(q, k, v, qn, kn, table, table_rows, pos, tokens, q_heads, kv_heads, eps, kv, bad);
     return with_format(kv, [&](auto fmt) -> int {
+      if constexpr (fmt.value <= PADRA_KV_BF16) {
+        if (tokens <= kHeadWaveTokens) {
+          const long long grid = qk_head_waves<fmt.value>(tokens, q_heads, kv_heads);
+          hipLaunchKernelGGL((k_qk_heads<T, fmt.value>), dim3((unsigned)grid), dim3(64), 0, s, a);
+          return launched();
+        }
+      }
       const long long grid = qk_wave_count<fmt.value>(tokens, q_heads, kv_heads);
       hipLaunchKernelGGL((k_qk<T, fmt.value>), dim3((unsigned)grid), dim3(64), 0, s, a);
       return launched();
@@ -452,6 +518,34 @@ int chain(hipStream_t s, const uint16_t *gather, int vocab, const int32_t *ids, 
   if (!((tree == 128 && (j == 16 || j == 18)) || (tree == 256 && (j == 8 || j == 9))))
     return PADRA_UNSUPPORTED;
   return with_format(kv, [&](auto fmt) -> int {
+    if constexpr (fmt.value <= PADRA_KV_BF16) {
+      if (tokens <= kHeadWaveTokens) {
+        const long long heads = qk_head_waves<fmt.value>(tokens, q_heads, kv_heads);
+        if (tree == 256) {
+          const dim3 grid((unsigned)(tokens + (heads + 3) / 4)), block(256);
+          if (gather && j == 8)
+            hipLaunchKernelGGL((k_chain_small<256, 8, fmt.value, true>), grid, block, 0, s, n, a, (long long)tokens, heads);
+          else if (gather)
+            hipLaunchKernelGGL((k_chain_small<256, 9, fmt.value, true>), grid, block, 0, s, n, a, (long long)tokens, heads);
+          else if (j == 8)
+            hipLaunchKernelGGL((k_chain_small<256, 8, fmt.value>), grid, block, 0, s, n, a, (long long)tokens, heads);
+          else
+            hipLaunchKernelGGL((k_chain_small<256, 9, fmt.value>), grid, block, 0, s, n, a, (long long)tokens, heads);
+          return launched();
+        }
+        const long long waves = norm_waves + heads;
+        const dim3 grid((unsigned)waves), block(64);
+        if (gather && j == 16)
+          hipLaunchKernelGGL((k_chain_heads<128, 16, fmt.value, true>), grid, block, 0, s, n, a, norm_waves, waves);
+        else if (gather)
+          hipLaunchKernelGGL((k_chain_heads<128, 18, fmt.value, true>), grid, block, 0, s, n, a, norm_waves, waves);
+        else if (j == 16)
+          hipLaunchKernelGGL((k_chain_heads<128, 16, fmt.value>), grid, block, 0, s, n, a, norm_waves, waves);
+        else
+          hipLaunchKernelGGL((k_chain_heads<128, 18, fmt.value>), grid, block, 0, s, n, a, norm_waves, waves);
+        return launched();
+      }
+    }
     const long long waves = norm_waves + qk_wave_count<fmt.value>(tokens, q_heads, kv_heads);
     const dim3 grid((unsigned)waves), block(64);
     if (gather) {

@@ -320,9 +320,12 @@ FORMATS = [abi.KV_BF16, abi.KV_Q8, abi.KV_Q8_0, abi.KV_Q8_0_NOROT]
 
 
 @pytest.mark.parametrize("fmt", FORMATS)
-@pytest.mark.parametrize("tokens,base,cap", [(64, 0, 4096), (300, 1000, 4096), (1500, 100, 1024)])
+@pytest.mark.parametrize("tokens,base,cap", [(64, 0, 4096), (100, 5, 64), (300, 1000, 4096),
+                                             (1500, 100, 1024)])
 def test_qk_rope_store_prefill(oracle, fmt, tokens, base, cap):
     print(f"[case] store fmt={fmt} tokens={tokens} base={base} cap={cap}", flush=True)
+    if cap == 64 and fmt != abi.KV_BF16:
+        pytest.skip("a quantized ring is the capacity or the 1024-row local ring")
     d = synth.chain_inputs(tokens, outliers=True, seed=fmt * 7 + tokens)
     capacity = 4096
     first = 0 if cap == capacity else max(0, tokens - cap)
@@ -538,9 +541,12 @@ def test_invalid_prefill_state_writes_nothing(oracle):
 
 @pytest.mark.parametrize("fmt", FORMATS)
 @pytest.mark.parametrize("tree", [128, 256])
-def test_fused_chain_matches_oracle(oracle, fmt, tree):
-    print(f"[case] chain fmt={fmt} tree={tree}", flush=True)
-    tokens, capacity = 333, 4096
+@pytest.mark.parametrize("tokens", [333, 129, 128, 37])
+def test_fused_chain_matches_oracle(oracle, fmt, tree, tokens):
+    """Both launch shapes of the chain: up to 128 tokens (BF16 cache) a wave per Q/K head
+    and, with the 256-thread tree, a workgroup per norm row; above, four lanes per head."""
+    print(f"[case] chain fmt={fmt} tree={tree} tokens={tokens}", flush=True)
+    capacity = 4096
     d = synth.chain_inputs(tokens, outliers=True, seed=fmt + tree)
     tb = table_bits(oracle, capacity)
     positions = np.arange(tokens, dtype=np.int32) + 17
