@@ -549,6 +549,10 @@ def main():
     if len(sys.argv) > 2 and sys.argv[1] == "--summarize":
         summarize(sys.argv[2], " ".join(sys.argv[3:]) or "(see profiles/README)")
         return
+    if len(sys.argv) > 5 and sys.argv[1] == "--summarize-kernels":
+        # --summarize-kernels <outdir> <outfile> <title> <command> [name substrings...]
+        summarize_kernels(sys.argv[2], sys.argv[5], sys.argv[3], sys.argv[4], sys.argv[6:] or None)
+        return
     args = parse()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -745,6 +749,63 @@ def summarize(outdir: str, command: str) -> None:
                   "VMEM wr / wave | VALU total | wave cycles / wave | SQ busy cycles | GRBM GUI active |",
                   "|---|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|"] + sq_rows + [""]
     with open(os.path.join(prof, "chain_config1.md"), "w") as f:
+        f.write("\n".join(lines))
+    print("\n".join(lines))
+
+
+KERNEL_ROLES = {
+    "k_chain<128, 16, 0, false>": "config 1 chain, BF16 KV",
+    "k_chain<128, 16, 1, false>": "config 2 chain, q8 KV",
+    "k_chain<128, 16, 2, false>": "config 2 chain, q8_0 KV (rotated)",
+    "k_chain<128, 16, 3, false>": "config 2 chain, q8_0 KV (unrotated)",
+    "k_chain_small<256, 8, 0, true>": "config 4/0 decode step: gather + chain, one launch",
+    "k_chain_small<256, 8, 0, false>": "config 4/0 decode chain after a separate gather",
+    "k_embed": "embedding gather (separate launch)",
+    "k_swiglu": "config 3 SwiGLU",
+    "k_norm": "residual + RMSNorm (fp32 activations)",
+    "k_qk": "Q/K norm + RoPE + store (fp32 activations)",
+    "k_norm_fp8": "RMSNorm + FP8 E4M3",
+    "k_combine_norm": "expert combine + residual + RMSNorm + FP8",
+    "k_attn_mx": "decode attention split (BF16 / q8 cache)",
+    "k_attn_merge": "decode attention merge",
+    "k_q8_0_query": "decode attention, q8_0 query coding",
+    "k_q8_0_mx": "decode attention split (q8_0 cache)",
+    "k_q8_0_mx_merge": "decode attention merge (q8_0)",
+    "k_stream_copy": "streaming copy (practical ceiling)",
+}
+
+
+def summarize_kernels(outdir: str, command: str, outfile: str, title: str, only=None) -> None:
+    """Every kernel of a profiled run (torch's own set-up kernels left out): calls and
+    average / min / max duration from <outdir>/trace, and read / write HBM bytes per dispatch
+    (medians) from the request counters of <outdir>/rd and <outdir>/wr (hbm_bytes).
+    `only`: substrings of the kernel names to keep."""
+    import csv
+    import glob
+    stats = glob.glob(os.path.join(outdir, "trace", "**", "*kernel_stats.csv"), recursive=True)
+    rd, wr = _pmc(outdir, "rd"), _pmc(outdir, "wr")
+    lines = [f"# {title}", "", "Command (from the repository root):", "", "```", command, "```",
+             "", "Durations: averages over every dispatch of the run (graph replays, warm-up and "
+             "eager launches), so they sit a little above the bench's graph-timed figures.  "
+             "Bytes: HBM read and write bytes per dispatch from the TCC-to-memory request "
+             "counts (128 bytes per read request that is not a 32-byte one, 64 or 32 bytes per "
+             "write request; bench.hbm_bytes), medians over the dispatches.", "",
+             "| kernel | role | calls | average us | min us | max us | read B | write B |",
+             "|---|---|---:|---:|---:|---:|---:|---:|"]
+    rows = []
+    for r in csv.DictReader(open(stats[0])):
+        short = r["Name"].replace("void ", "").replace("(anonymous namespace)::", "").split("(")[0]
+        if short.startswith(("at::", "__amd_rocclr")) or (only and not any(o in short for o in only)):
+            continue
+        role = KERNEL_ROLES.get(short) or next((v for k, v in KERNEL_ROLES.items()
+                                                if short.split("<")[0] == k), "")
+        b = hbm_bytes({**rd[short], **wr[short]}) if short in rd and short in wr else None
+        rows.append((float(r["AverageNs"]), f"| `{short[:60]}` | {role} | {r['Calls']} | "
+                     f"{float(r['AverageNs'])/1e3:.2f} | {float(r['MinNs'])/1e3:.2f} | "
+                     f"{float(r['MaxNs'])/1e3:.2f} | "
+                     + (f"{b['read']:,.0f} | {b['write']:,.0f} |" if b else "— | — |")))
+    lines += [r for _, r in sorted(rows, key=lambda t: -t[0])] + [""]
+    with open(os.path.join(ROOT, "profiles", outfile), "w") as f:
         f.write("\n".join(lines))
     print("\n".join(lines))
 
