@@ -129,7 +129,7 @@ def time_graph(torch, sets, steps, warmup, replays=None):
     return ms
 
 
-def warm_graph(torch, graph, seconds=0.03, most=50):
+def warm_graph(torch, graph, seconds=0.2, most=400):
     """Untimed replays of the captured graph for about `seconds` (at most `most` replays)
     before the timed one: on a fresh process the GPU clocks are still ramping during the
     first milliseconds of work (measured: the first 32-launch replay runs 4% slower than
