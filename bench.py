@@ -640,6 +640,7 @@ def main():
 
 
 FORMAT_CODES = {"bf16": 0, "q8": 1, "q8_0": 2, "q8_0_norot": 3}
+SHADER_ENGINES, SIMDS = 32, 1024  # MI355X (rocminfo: 32 shader engines, 256 CUs x 4 SIMDs)
 
 
 def chain_kernel(fmt: str) -> str:
@@ -742,12 +743,29 @@ def summarize(outdir: str, command: str) -> None:
                        f"{c.get('SQ_INSTS_VMEM_RD', 0) / waves:.1f} | {c.get('SQ_INSTS_VMEM_WR', 0) / waves:.1f} | "
                        f"{c.get('SQ_INSTS_VALU', 0):.0f} | {c.get('SQ_WAVE_CYCLES', 0) / waves:.0f} | "
                        f"{c.get('SQ_BUSY_CYCLES', 0):.0f} | {c.get('GRBM_GUI_ACTIVE', 0):.0f} |")
+    derived = []
+    for fmt, name, _ in kernels:
+        c = sq.get(name)
+        us = avg_ns.get(name, 0.0) / 1e3
+        if not c or not c.get("SQ_BUSY_CYCLES") or not us:
+            continue
+        ghz = c["SQ_BUSY_CYCLES"] / SHADER_ENGINES / (us * 1e3)
+        valu_us = c.get("SQ_INSTS_VALU", 0) * 4 / SIMDS / (ghz * 1e3)
+        derived.append(f"| {fmt} | {us:.2f} | {ghz:.2f} | {valu_us:.2f} | {valu_us / us:.2f} |")
     if sq_rows:
         lines += ["## Wave and instruction counters (--pmc SQ_*, GRBM_GUI_ACTIVE)", "",
                   "Per-wave figures are totals over the dispatch divided by SQ_WAVES.", "",
                   "| format | waves | VALU / wave | SALU / wave | LDS / wave | VMEM rd / wave | "
                   "VMEM wr / wave | VALU total | wave cycles / wave | SQ busy cycles | GRBM GUI active |",
                   "|---|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|"] + sq_rows + [""]
+    if derived:
+        lines += ["## Derived: clock and VALU issue time", "",
+                  f"Clock = SQ_BUSY_CYCLES / {SHADER_ENGINES} shader engines (rocminfo) / the "
+                  "kernel-trace average.  VALU issue time = SQ_INSTS_VALU x 4 cycles (a wave64 "
+                  f"VALU instruction on a 16-lane SIMD) / {SIMDS} SIMDs / clock: the time the "
+                  "arithmetic alone occupies the SIMDs, against the kernel's duration.", "",
+                  "| format | trace avg us | clock GHz | VALU issue us | VALU issue / duration |",
+                  "|---|---:|---:|---:|---:|"] + derived + [""]
     with open(os.path.join(prof, "chain_config1.md"), "w") as f:
         f.write("\n".join(lines))
     print("\n".join(lines))
