@@ -299,8 +299,9 @@ def bench_swiglu(torch, steps, sets=4):
 
 def bench_f32_layer(torch, steps, sets=8):
     """The config-1 chunk in the reference's own activation form (fp32 buffers holding
-    BF16-exact values, PADRA_ACT_F32), launched as the reference launches it: the residual
-    + RMSNorm, then the Q/K norm + RoPE + BF16 KV store.  Each launch is timed alone."""
+    BF16-exact values, PADRA_ACT_F32): launched as the reference launches it (the residual
+    + RMSNorm, then the Q/K norm + RoPE + BF16 KV store, each timed alone), and as one
+    fused launch."""
     from padra_amd import abi, ops, synth
     host = synth.chain_inputs(TOKENS, HIDDEN, HQ, HKV, D, outliers=True, seed=0)
     f32 = lambda a: torch.from_numpy(synth.bf16_to_f32(a)).cuda()
@@ -319,13 +320,19 @@ def bench_f32_layer(torch, steps, sets=8):
     qk_ms = graph_time(torch, lambda i: ops.QKNormRopeStore(
         bufs[i % sets][3], bufs[i % sets][4], qn, kn, table, ops.positions_base(0), bad,
         v=bufs[i % sets][5], kv=bufs[i % sets][6]), steps)
+    fused_ms = graph_time(torch, lambda i: ops.ResidualNormQKRopeStore(
+        *bufs[i % sets][:3], g, *bufs[i % sets][3:6], qn, kn, table, ops.positions_base(0),
+        bufs[i % sets][6], bad), steps)
     if bad.item():
         raise SystemExit("device error flag set in the fp32-activation benchmark")
     norm_bytes = TOKENS * HIDDEN * 4 * 4
     qk_bytes = TOKENS * (((HQ + 2 * HKV) + (HQ + HKV)) * D * 4 + 2 * HKV * D * 2 + 2 * D)
     rate = lambda b, ms: round(b / (ms * 1e-3) / 1e9, 2)
     return {"workload": "config1 chunk with fp32 activations: residual+RMSNorm, then "
-                        "QK-norm+RoPE+BF16 KV store (two launches)",
+                        "QK-norm+RoPE+BF16 KV store (two launches, and fused in one)",
+            "fused_us": round(fused_ms * 1e3, 3),
+            "fused_gbs": rate(norm_bytes + qk_bytes, fused_ms),
+            "fused_frac": round((norm_bytes + qk_bytes) / (fused_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
             "norm_us": round(norm_ms * 1e3, 3), "norm_bytes": norm_bytes,
             "norm_gbs": rate(norm_bytes, norm_ms),
             "qk_us": round(qk_ms * 1e3, 3), "qk_bytes": qk_bytes, "qk_gbs": rate(qk_bytes, qk_ms),

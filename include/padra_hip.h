@@ -169,8 +169,10 @@ int padra_QKNormRopeStore(void *stream, void *q, void *k, const void *v, const u
 /* ---- fused per-token chain ----------------------------------------------------------
  * One launch of padra_ResidualPostNorm over `tokens` rows and padra_QKNormRopeStore over
  * the same tokens (the two have no data dependence; exact-fusions-v1 runs them as
- * separate kernels).  Arguments mean what they mean there; results are bit-identical to
- * the two calls. */
+ * separate kernels: the prefill Add + Norm, inference.cu:475-481, 188-214, and
+ * QKNormRopeStoreControlled, qk_rope_store_exact.cuh:4-49).  Arguments mean what they mean
+ * there, act included (x, residual, normalized, q, k, v all of that type); results are
+ * bit-identical to the two calls. */
 int padra_ResidualNormQKRopeStore(void *stream, void *x, const void *residual,
                                   void *normalized, const uint16_t *gamma, int hidden,
                                   int tree, float *statistics, void *q, void *k,
@@ -178,7 +180,7 @@ int padra_ResidualNormQKRopeStore(void *stream, void *x, const void *residual,
                                   const uint16_t *table, int table_rows,
                                   const padra_Positions *pos, int tokens, int q_heads,
                                   int kv_heads, int head_dim, float eps,
-                                  const padra_KVCache *kv, int *bad);
+                                  const padra_KVCache *kv, int *bad, int act);
 /* padra_EmbedResidualNormQKRopeStore: padra_Embed (BF16 output into x, same positions)
  * followed by padra_ResidualNormQKRopeStore, in one launch: the norm rows read row t of x
  * from embed[token_t] instead of from x.  The layer-0 decode step, EmbedControlled

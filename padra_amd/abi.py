@@ -74,7 +74,7 @@ SIGNATURES = {
                               _I, _I, _F, ctypes.POINTER(KVCache), _P, _I],
     "padra_ResidualNormQKRopeStore": [_P, _P, _P, _P, _P, _I, _I, _P, _P, _P, _P, _P, _P, _P, _I,
                                       ctypes.POINTER(Positions), _I, _I, _I, _I, _F,
-                                      ctypes.POINTER(KVCache), _P],
+                                      ctypes.POINTER(KVCache), _P, _I],
     "padra_EmbedResidualNormQKRopeStore": [_P, _P, _I, _P, _P, _P, _P, _P, _I, _I, _P, _P, _P,
                                            _P, _P, _P, _P, _I, ctypes.POINTER(Positions), _I,
                                            _I, _I, _I, _F, ctypes.POINTER(KVCache), _P],

@@ -97,13 +97,14 @@ template <int J, class T> __global__ __launch_bounds__(64) void k_norm_fp8(NormF
 // tensors alone, and the VALU-heavier Q/K waves follow as norm waves retire.  Putting the
 // Q/K waves first measured 15% slower.
 // GATHER: the norm rows read their x from the embedding table (the fused decode step).
-template <int VT, int J, int FMT, bool GATHER = false>
-__global__ __launch_bounds__(64) void k_chain(NormArgs<uint16_t> n, QKArgs<uint16_t> q,
-                                              long long norm_waves, long long waves) {
-  __shared__ uint4 lds[quad_image_slots_fmt<uint16_t, FMT>()];
+// T: the activation type (BF16, or fp32 words holding BF16-exact values).
+template <int VT, int J, int FMT, bool GATHER = false, class T = uint16_t>
+__global__ __launch_bounds__(64) void k_chain(NormArgs<T> n, QKArgs<T> q, long long norm_waves,
+                                              long long waves) {
+  __shared__ uint4 lds[quad_image_slots_fmt<T, FMT>()];
   const long long b = blockIdx.x;
   if (b < norm_waves)
-    norm_row_wave<VT, J, uint16_t, true, false, GATHER>(n, (int)b, nullptr);
+    norm_row_wave<VT, J, T, true, false, GATHER>(n, (int)b, nullptr);
   else if (b < waves) {
     // Quantized caches: the K waves (K norm + RoPE, then the K and V encodings: the
     // heaviest waves) are dispatched before the Q waves instead of last, so they do not
@@ -114,7 +115,7 @@ __global__ __launch_bounds__(64) void k_chain(NormArgs<uint16_t> n, QKArgs<uint1
       if (w >= waves - norm_waves)
         w -= waves - norm_waves;
     }
-    qk_heads_wave<uint16_t, FMT>(q, w, lds);
+    qk_heads_wave<T, FMT>(q, w, lds);
   }
 }
 
@@ -573,12 +574,66 @@ int chain(hipStream_t s, const uint16_t *gather, int vocab, const int32_t *ids, 
 
 } // namespace
 
+namespace {
+// The fused chain on fp32 activations (the reference's buffers): norm-row waves, then the
+// four-lanes-per-head Q/K waves, at every token count.
+int chain_f32(hipStream_t s, void *x, const void *residual, void *normalized,
+              const uint16_t *gamma, int hidden, int tree, float *statistics, void *q, void *k,
+              const void *v, const uint16_t *qn, const uint16_t *kn, const uint16_t *table,
+              int table_rows, const padra_Positions *pos, int tokens, int q_heads, int kv_heads,
+              int head_dim, float eps, const padra_KVCache *kv, int *bad) {
+  int st = check_norm(x, normalized, gamma, tokens, hidden, eps, tree, bad, PADRA_ACT_F32);
+  if (st)
+    return st;
+  if (!residual || !aligned16(residual) || residual == x)
+    return PADRA_INVALID_ARGUMENT;
+  st = check_qk(q, k, v, qn, kn, table, table_rows, pos, tokens, q_heads, kv_heads, head_dim, eps,
+                kv, bad, PADRA_ACT_F32);
+  if (st)
+    return st;
+  NormArgs<float> n;
+  n.x = static_cast<float *>(x);
+  n.residual = static_cast<const float *>(residual);
+  n.y = static_cast<float *>(normalized);
+  n.gamma = gamma;
+  n.stats = statistics;
+  n.bad = bad;
+  n.rows = tokens;
+  n.eps = eps;
+  const QKArgs<float> a = make_qk<float>(q, k, v, qn, kn, table, table_rows, pos, tokens,
+                                         q_heads, kv_heads, eps, kv, bad);
+  const int j = hidden / tree;
+  if (!((tree == 128 && (j == 16 || j == 18)) || (tree == 256 && (j == 8 || j == 9))))
+    return PADRA_UNSUPPORTED;
+  const long long norm_waves = tokens;
+  return with_format(kv, [&](auto fmt) -> int {
+    const long long waves = norm_waves + qk_wave_count<fmt.value>(tokens, q_heads, kv_heads);
+    const dim3 grid((unsigned)waves), block(64);
+    if (tree == 128 && j == 16)
+      hipLaunchKernelGGL((k_chain<128, 16, fmt.value, false, float>), grid, block, 0, s, n, a, norm_waves, waves);
+    else if (tree == 128)
+      hipLaunchKernelGGL((k_chain<128, 18, fmt.value, false, float>), grid, block, 0, s, n, a, norm_waves, waves);
+    else if (j == 8)
+      hipLaunchKernelGGL((k_chain<256, 8, fmt.value, false, float>), grid, block, 0, s, n, a, norm_waves, waves);
+    else
+      hipLaunchKernelGGL((k_chain<256, 9, fmt.value, false, float>), grid, block, 0, s, n, a, norm_waves, waves);
+    return launched();
+  });
+}
+} // namespace
+
 extern "C" int padra_ResidualNormQKRopeStore(
     void *stream, void *x, const void *residual, void *normalized, const uint16_t *gamma,
     int hidden, int tree, float *statistics, void *q, void *k, const void *v,
     const uint16_t *qn, const uint16_t *kn, const uint16_t *table, int table_rows,
     const padra_Positions *pos, int tokens, int q_heads, int kv_heads, int head_dim, float eps,
-    const padra_KVCache *kv, int *bad) {
+    const padra_KVCache *kv, int *bad, int act) {
+  if (act == PADRA_ACT_F32)
+    return chain_f32(static_cast<hipStream_t>(stream), x, residual, normalized, gamma, hidden,
+                     tree, statistics, q, k, v, qn, kn, table, table_rows, pos, tokens, q_heads,
+                     kv_heads, head_dim, eps, kv, bad);
+  if (act != PADRA_ACT_BF16)
+    return PADRA_INVALID_ARGUMENT;
   return chain(static_cast<hipStream_t>(stream), nullptr, 0, nullptr, x, residual, normalized,
                gamma, hidden, tree, statistics, q, k, v, qn, kn, table, table_rows, pos, tokens,
                q_heads, kv_heads, head_dim, eps, kv, bad);

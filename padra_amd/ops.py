@@ -174,7 +174,8 @@ def QKNormRopeStore(q, k, qn, kn, table, positions: abi.Positions, bad, eps=1e-6
 def ResidualNormQKRopeStore(x, residual, normalized, gamma, q, k, v, qn, kn, table,
                             positions: abi.Positions, kv: abi.KVCache | None, bad, eps=1e-6,
                             tree=abi.TREE_128, statistics=None):
-    """ResidualPostNorm and QKNormRopeStore over the same tokens in one launch."""
+    """ResidualPostNorm and QKNormRopeStore over the same tokens in one launch (BF16 or
+    fp32 activations, by x's dtype)."""
     _need_cuda(x, residual, normalized, gamma, q, k, v, qn, kn, table, bad, statistics)
     tokens, q_heads, kv_heads, head_dim = _shape_qk(q, k)
     if x.shape[0] != tokens:
@@ -182,7 +183,8 @@ def ResidualNormQKRopeStore(x, residual, normalized, gamma, q, k, v, qn, kn, tab
     abi.call("padra_ResidualNormQKRopeStore", _stream(x), _p(x), _p(residual), _p(normalized),
              _p(gamma), x.shape[-1], int(tree), _p(statistics), _p(q), _p(k), _p(v), _p(qn),
              _p(kn), _p(table), table.shape[0], ctypes.byref(positions), tokens, q_heads,
-             kv_heads, head_dim, float(eps), None if kv is None else ctypes.byref(kv), _p(bad))
+             kv_heads, head_dim, float(eps), None if kv is None else ctypes.byref(kv), _p(bad),
+             _act(x))
 
 
 def EmbedResidualNormQKRopeStore(embed, ids, x, residual, normalized, gamma, q, k, v, qn, kn,

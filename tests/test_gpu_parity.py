@@ -573,6 +573,42 @@ def test_fused_chain_matches_oracle(oracle, fmt, tree, tokens):
         assert np.array_equal(sc.cpu().numpy(), es)
 
 
+@pytest.mark.parametrize("fmt", FORMATS)
+@pytest.mark.parametrize("tree,tokens", [(128, 300), (256, 64)])
+def test_fused_chain_f32_activations(oracle, fmt, tree, tokens):
+    """The fused chain on fp32 activations holding BF16-exact values (the reference's
+    buffers): every output equal to the oracle's, as floats."""
+    print(f"[case] chain f32 fmt={fmt} tree={tree} tokens={tokens}", flush=True)
+    capacity = 4096
+    d = synth.chain_inputs(tokens, outliers=True, seed=300 + fmt + tree)
+    tb = table_bits(oracle, capacity)
+    positions = np.arange(tokens, dtype=np.int32) + 9
+    wx, wy, wst, _ = oracle.residual_rmsnorm(d["x"], d["residual"], d["gamma"], threads=tree)
+    wq, wk, _ = _qk_oracle(oracle, d, tb, positions)
+    ek, ev, es = _expected_cache(oracle, fmt, wk, d["v"], positions, capacity, 0)
+    f32 = lambda a: torch.from_numpy(synth.bf16_to_f32(a)).cuda()
+    x, r, q, k = f32(d["x"]), f32(d["residual"]), f32(d["q"]), f32(d["k"])
+    y = torch.empty_like(x)
+    st = torch.empty((tokens, 2), dtype=torch.float32, device="cuda")
+    kc, vc, sc = _alloc_cache(fmt, capacity)
+    bad = flag()
+    ops.ResidualNormQKRopeStore(x, r, y, dev(d["gamma"]), q, k, f32(d["v"]), dev(d["qn"]),
+                                dev(d["kn"]), dev(tb), ops.positions_base(9),
+                                ops.kv_cache(fmt, kc, vc, capacity, scales=sc), bad, tree=tree,
+                                statistics=st)
+    torch.cuda.synchronize()
+    assert not bad.item()
+    as_f32 = lambda t: t.cpu().numpy()
+    assert np.array_equal(as_f32(x), synth.bf16_to_f32(wx))
+    assert np.array_equal(as_f32(y), synth.bf16_to_f32(wy))
+    assert np.array_equal(st.cpu().numpy(), wst)
+    assert np.array_equal(as_f32(q), synth.bf16_to_f32(wq))
+    assert np.array_equal(as_f32(k), synth.bf16_to_f32(wk))
+    assert np.array_equal(_np(kc, fmt), ek) and np.array_equal(_np(vc, fmt), ev)
+    if es is not None:
+        assert np.array_equal(sc.cpu().numpy(), es)
+
+
 def test_config1_full_chunk(oracle):
     """Config 1 at full size: 2048-token prefill chunk, BF16 KV, cap 131072, outliers."""
     print("[case] config1 full", flush=True)
