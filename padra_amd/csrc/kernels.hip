@@ -208,6 +208,25 @@ template <class F> int norm_shape(int tree, int j, F &&f) {
 }
 #undef PADRA_NORM_J
 
+// The (tree, hidden/tree) pairs of the fused chain: H = 2048 and 2304 in either tree.
+template <class F> int chain_shape(int tree, int j, F &&f) {
+  using std::integral_constant;
+  if (tree == 128 && j == 16)
+    return f(integral_constant<int, 128>{}, integral_constant<int, 16>{});
+  if (tree == 128 && j == 18)
+    return f(integral_constant<int, 128>{}, integral_constant<int, 18>{});
+  if (tree == 256 && j == 8)
+    return f(integral_constant<int, 256>{}, integral_constant<int, 8>{});
+  if (tree == 256 && j == 9)
+    return f(integral_constant<int, 256>{}, integral_constant<int, 9>{});
+  return PADRA_UNSUPPORTED;
+}
+
+// A runtime flag as a compile-time one.
+template <class F> int with_flag(bool b, F &&f) {
+  return b ? f(std::true_type{}) : f(std::false_type{});
+}
+
 int check_norm(const void *x, const void *normalized, const uint16_t *gamma, int rows,
                int hidden, float eps, int tree, int *bad, int act) {
   if (!x || !normalized || !gamma || !bad || x == normalized || rows < 1 || hidden < 1 ||
@@ -515,60 +534,33 @@ int chain(hipStream_t s, const uint16_t *gather, int vocab, const int32_t *ids, 
   const QKArgs<uint16_t> a = make_qk<uint16_t>(q, k, v, qn, kn, table, table_rows, pos, tokens,
                                                q_heads, kv_heads, eps, kv, bad);
   const long long norm_waves = (tokens + rows_per_wave(tree) - 1) / rows_per_wave(tree);
-  const int j = hidden / tree;
-  if (!((tree == 128 && (j == 16 || j == 18)) || (tree == 256 && (j == 8 || j == 9))))
-    return PADRA_UNSUPPORTED;
-  return with_format(kv, [&](auto fmt) -> int {
-    if constexpr (fmt.value <= PADRA_KV_BF16) {
-      if (tokens <= kHeadWaveTokens) {
-        const long long heads = qk_head_waves<fmt.value>(tokens, q_heads, kv_heads);
-        if (tree == 256) {
-          const dim3 grid((unsigned)(tokens + (heads + 3) / 4)), block(256);
-          if (gather && j == 8)
-            hipLaunchKernelGGL((k_chain_small<256, 8, fmt.value, true>), grid, block, 0, s, n, a, (long long)tokens, heads);
-          else if (gather)
-            hipLaunchKernelGGL((k_chain_small<256, 9, fmt.value, true>), grid, block, 0, s, n, a, (long long)tokens, heads);
-          else if (j == 8)
-            hipLaunchKernelGGL((k_chain_small<256, 8, fmt.value>), grid, block, 0, s, n, a, (long long)tokens, heads);
-          else
-            hipLaunchKernelGGL((k_chain_small<256, 9, fmt.value>), grid, block, 0, s, n, a, (long long)tokens, heads);
-          return launched();
+  return chain_shape(tree, hidden / tree, [&](auto vt, auto j) -> int {
+    return with_flag(gather != nullptr, [&](auto g) -> int {
+      return with_format(kv, [&](auto fmt) -> int {
+        constexpr int VT = vt.value, J = j.value, FMT = fmt.value;
+        constexpr bool G = g.value;
+        if constexpr (FMT <= PADRA_KV_BF16) {
+          if (tokens <= kHeadWaveTokens) {
+            const long long heads = qk_head_waves<FMT>(tokens, q_heads, kv_heads);
+            if constexpr (VT == 256) {
+              // One workgroup per norm row, then one per four head vectors.
+              const dim3 grid((unsigned)(tokens + (heads + 3) / 4)), block(256);
+              hipLaunchKernelGGL((k_chain_small<VT, J, FMT, G>), grid, block, 0, s, n, a,
+                                 (long long)tokens, heads);
+            } else {
+              const long long waves = norm_waves + heads;
+              hipLaunchKernelGGL((k_chain_heads<VT, J, FMT, G>), dim3((unsigned)waves),
+                                 dim3(64), 0, s, n, a, norm_waves, waves);
+            }
+            return launched();
+          }
         }
-        const long long waves = norm_waves + heads;
-        const dim3 grid((unsigned)waves), block(64);
-        if (gather && j == 16)
-          hipLaunchKernelGGL((k_chain_heads<128, 16, fmt.value, true>), grid, block, 0, s, n, a, norm_waves, waves);
-        else if (gather)
-          hipLaunchKernelGGL((k_chain_heads<128, 18, fmt.value, true>), grid, block, 0, s, n, a, norm_waves, waves);
-        else if (j == 16)
-          hipLaunchKernelGGL((k_chain_heads<128, 16, fmt.value>), grid, block, 0, s, n, a, norm_waves, waves);
-        else
-          hipLaunchKernelGGL((k_chain_heads<128, 18, fmt.value>), grid, block, 0, s, n, a, norm_waves, waves);
+        const long long waves = norm_waves + qk_wave_count<FMT>(tokens, q_heads, kv_heads);
+        hipLaunchKernelGGL((k_chain<VT, J, FMT, G>), dim3((unsigned)waves), dim3(64), 0, s, n,
+                           a, norm_waves, waves);
         return launched();
-      }
-    }
-    const long long waves = norm_waves + qk_wave_count<fmt.value>(tokens, q_heads, kv_heads);
-    const dim3 grid((unsigned)waves), block(64);
-    if (gather) {
-      if (tree == 128 && j == 16)
-        hipLaunchKernelGGL((k_chain<128, 16, fmt.value, true>), grid, block, 0, s, n, a, norm_waves, waves);
-      else if (tree == 128)
-        hipLaunchKernelGGL((k_chain<128, 18, fmt.value, true>), grid, block, 0, s, n, a, norm_waves, waves);
-      else if (j == 8)
-        hipLaunchKernelGGL((k_chain<256, 8, fmt.value, true>), grid, block, 0, s, n, a, norm_waves, waves);
-      else
-        hipLaunchKernelGGL((k_chain<256, 9, fmt.value, true>), grid, block, 0, s, n, a, norm_waves, waves);
-    } else {
-      if (tree == 128 && j == 16)
-        hipLaunchKernelGGL((k_chain<128, 16, fmt.value>), grid, block, 0, s, n, a, norm_waves, waves);
-      else if (tree == 128)
-        hipLaunchKernelGGL((k_chain<128, 18, fmt.value>), grid, block, 0, s, n, a, norm_waves, waves);
-      else if (j == 8)
-        hipLaunchKernelGGL((k_chain<256, 8, fmt.value>), grid, block, 0, s, n, a, norm_waves, waves);
-      else
-        hipLaunchKernelGGL((k_chain<256, 9, fmt.value>), grid, block, 0, s, n, a, norm_waves, waves);
-    }
-    return launched();
+      });
+    });
   });
 }
 
@@ -602,22 +594,14 @@ int chain_f32(hipStream_t s, void *x, const void *residual, void *normalized,
   n.eps = eps;
   const QKArgs<float> a = make_qk<float>(q, k, v, qn, kn, table, table_rows, pos, tokens,
                                          q_heads, kv_heads, eps, kv, bad);
-  const int j = hidden / tree;
-  if (!((tree == 128 && (j == 16 || j == 18)) || (tree == 256 && (j == 8 || j == 9))))
-    return PADRA_UNSUPPORTED;
   const long long norm_waves = tokens;
-  return with_format(kv, [&](auto fmt) -> int {
-    const long long waves = norm_waves + qk_wave_count<fmt.value>(tokens, q_heads, kv_heads);
-    const dim3 grid((unsigned)waves), block(64);
-    if (tree == 128 && j == 16)
-      hipLaunchKernelGGL((k_chain<128, 16, fmt.value, false, float>), grid, block, 0, s, n, a, norm_waves, waves);
-    else if (tree == 128)
-      hipLaunchKernelGGL((k_chain<128, 18, fmt.value, false, float>), grid, block, 0, s, n, a, norm_waves, waves);
-    else if (j == 8)
-      hipLaunchKernelGGL((k_chain<256, 8, fmt.value, false, float>), grid, block, 0, s, n, a, norm_waves, waves);
-    else
-      hipLaunchKernelGGL((k_chain<256, 9, fmt.value, false, float>), grid, block, 0, s, n, a, norm_waves, waves);
-    return launched();
+  return chain_shape(tree, hidden / tree, [&](auto vt, auto j) -> int {
+    return with_format(kv, [&](auto fmt) -> int {
+      const long long waves = norm_waves + qk_wave_count<fmt.value>(tokens, q_heads, kv_heads);
+      hipLaunchKernelGGL((k_chain<vt.value, j.value, fmt.value, false, float>),
+                         dim3((unsigned)waves), dim3(64), 0, s, n, a, norm_waves, waves);
+      return launched();
+    });
   });
 }
 } // namespace
