@@ -27,6 +27,7 @@
 #include <algorithm>
 #include <atomic>
 #include <mutex>
+#include <type_traits>
 
 #include "common.h"
 #include "norm_fp8.h"
@@ -36,6 +37,9 @@ using namespace padra;
 namespace {
 
 constexpr int kD = 128, kKeys = 32;
+// Launches of up to this many sequences on a global cache order their split waves by
+// window length (the ranking reads seqs^2 control records).
+constexpr int kOrderMaxSeqs = 512;
 constexpr float kScoreScale = .08838834764831845f;
 
 int launched(const char *what) {
@@ -62,6 +66,9 @@ struct AttnArgs {
   int8_t *qcodes;
   float *qscale;
   const float *kvscales; // q8 caches: (k, v) scale pair per row and KV head
+  // The split kernels' sequence for grid slot z (longest window first), or null for
+  // slot z = sequence z.
+  int *order;
 };
 
 // The sequence's admission and key window (Admitted, attention_gqa8_fragment_validation.cuh:
@@ -74,6 +81,31 @@ __device__ __forceinline__ bool attn_window(const AttnArgs &a, int seq, int &n, 
   first = st.position + 1 - n;
   return ok;
 }
+
+// Sequence `seq`'s place in the split kernels' dispatch order, written by a 64-lane block:
+// windows by decreasing length (a sequence that is not admitted counts as 0 keys), ties
+// by sequence index.  The split kernels give grid slot z to order[z], so the longest
+// windows start first and the shortest fill the end of the launch; every output is the
+// same as in sequence order.
+__device__ __forceinline__ void attn_rank(const AttnArgs &a, int seq) {
+  int n, first;
+  const int mine = attn_window(a, seq, n, first) ? n : 0;
+  int before = 0;
+  for (int j = threadIdx.x; j < a.seqs; j += 64) {
+    const int other = attn_window(a, j, n, first) ? n : 0;
+    before += other > mine || (other == mine && j < seq);
+  }
+#pragma unroll
+  for (int d = 32; d >= 1; d /= 2)
+    before += __shfl_xor(before, d, 64);
+  if (threadIdx.x == 0)
+    a.order[before] = seq;
+}
+__device__ __forceinline__ int attn_seq(const AttnArgs &a) {
+  return a.order ? a.order[blockIdx.z] : (int)blockIdx.z;
+}
+
+__global__ __launch_bounds__(64) void k_attn_order(AttnArgs a) { attn_rank(a, blockIdx.x); }
 
 __device__ __forceinline__ float xor_max32(float v) {
 #pragma unroll
@@ -125,30 +157,29 @@ __device__ __forceinline__ bool q8_scale_fast(float scale) {
   return scale > 0.f && 127.f * scale < 0x1.ffp127f;
 }
 
-// Nonzero in bit 7 of a byte when the word holds a 0x80 byte (code -128): the zero-byte
-// test of x = w ^ 0x80808080, (x - 0x01010101) & ~x & 0x80808080, where the bits 7 of ~x
-// are those of w.  Accumulated over words; the caller masks with 0x80808080.
-__device__ __forceinline__ uint32_t q8_minus128(uint32_t w) {
-  return ((w ^ 0x80808080u) + 0xfefefeffu) & w;
-}
-
-// The 16 values code * scale of a code chunk (kv_q8::Decode), accumulating the -128 test
-// and whether the scale passes q8_scale_fast.  Keys past the window decode zero codes with
-// a unit scale, as the reference stages them.
+// The 16 values code * scale of a code chunk (kv_q8::Decode), with the least code seen
+// (as a float; -128 is the code the reference rejects) and whether the scale passes
+// q8_scale_fast.  Keys past the window decode zero codes with a unit scale, as the
+// reference stages them.  Each code is one v_cvt_f32_i32 with a sign-extended byte select.
 __device__ __forceinline__ void q8_values16(uint4 c, float scale, bool inside, float (&f)[16],
-                                            uint32_t &m128, bool &slow) {
+                                            float &least, bool &slow) {
   if (!inside) {
     c = make_uint4(0, 0, 0, 0);
     scale = 1.f;
   }
   const uint32_t w[4] = {c.x, c.y, c.z, c.w};
+  float code[16];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int b = 0; b < 4; ++b)
-      f[4 * i + b] = (float)(int8_t)((w[i] >> (8 * b)) & 0xffu) * scale;
-    m128 |= q8_minus128(w[i]);
-  }
+      code[4 * i + b] = (float)(int8_t)((w[i] >> (8 * b)) & 0xffu);
+#pragma unroll
+  for (int i = 0; i < 16; i += 2)
+    least = fminf(least, fminf(code[i], code[i + 1]));
+#pragma unroll
+  for (int i = 0; i < 16; ++i)
+    f[i] = code[i] * scale;
   slow = slow || !q8_scale_fast(scale);
 }
 
@@ -188,7 +219,7 @@ __global__ __launch_bounds__(64) void k_attn_mx(AttnArgs a) {
   __shared__ __align__(16) uint32_t ks[kKeys][KW];
   // (V[4j][d], V[4j+1][d]), (V[4j+2][d], V[4j+3][d]) at slot vq_slot(d)
   __shared__ __align__(16) uint2 vq[kKeys / 4][VW];
-  const int split = blockIdx.x, kv = blockIdx.y, seq = blockIdx.z, lane = threadIdx.x;
+  const int split = blockIdx.x, kv = blockIdx.y, seq = attn_seq(a), lane = threadIdx.x;
   const int col = lane & 15, grp = lane >> 4;
   int n, first;
   if (!attn_window(a, seq, n, first)) {
@@ -251,7 +282,39 @@ __global__ __launch_bounds__(64) void k_attn_mx(AttnArgs a) {
   auto vkey = [&](int m) {
     return Q8 ? 4 * (lane >> 3) + m : 16 * (m >> 2) + 4 * grp + (m & 3);
   };
+  // A tile whose 32 keys are inside the window and do not wrap is 32 consecutive cache
+  // rows from `base`: load m of a lane is then the tile's first row, plus this lane's
+  // offset for m = 0 (bytes), plus a per-m step that is the same for every lane.
+  //  q8 K: key lane / 8 + 8 m; V: key 4 (lane / 8) + m.  BF16 K: key lane / 16 + 4 m;
+  //  V: key 4 grp + 16 (m / 4) + m % 4.
+  constexpr int ES = Q8 ? 1 : 2; // bytes per cache element
+  const size_t row_bytes = (size_t)features * ES;
+  const uint32_t koff = (uint32_t)(Q8 ? (lane >> 3) * row_bytes + 16 * (lane & 7)
+                                      : (lane >> 4) * row_bytes + 16 * (lane & 15));
+  const uint32_t voff = (uint32_t)(Q8 ? 4 * (lane >> 3) * row_bytes + 16 * (lane & 7)
+                                      : 4 * grp * row_bytes + 16 * col);
+  const uint32_t kso = (uint32_t)((lane >> 3) * a.hkv * 8), vso = 4 * kso + 4;
+  auto kstep = [&](int m) { return (size_t)(Q8 ? 8 * m : 4 * m) * row_bytes; };
+  auto vstep = [&](int m) { return (size_t)(Q8 ? m : 16 * (m >> 2) + (m & 3)) * row_bytes; };
+  const char *kbytes = Q8 ? reinterpret_cast<const char *>(k8) : reinterpret_cast<const char *>(kc);
+  const char *vbytes = Q8 ? reinterpret_cast<const char *>(v8) : reinterpret_cast<const char *>(vc);
+  const char *sbytes = reinterpret_cast<const char *>(sc);
   auto load_tile = [&](int tile, uint4 (&kw)[8], uint4 (&vw)[8]) {
+    const int base = (first + tile * kKeys) % a.cap;
+    if (tile * kKeys + kKeys <= n && base + kKeys <= a.cap) { // block-uniform
+      const char *kt = kbytes + (size_t)base * row_bytes, *vt = vbytes + (size_t)base * row_bytes;
+      const char *st = sbytes + (size_t)base * a.hkv * 8;
+#pragma unroll
+      for (int m = 0; m < CH; ++m) {
+        kw[m] = ld_nt(reinterpret_cast<const uint4 *>(kt + kstep(m) + koff));
+        vw[m] = ld_nt(reinterpret_cast<const uint4 *>(vt + vstep(m) + voff));
+        if constexpr (Q8) {
+          ksc[m] = *reinterpret_cast<const float *>(st + (size_t)8 * m * a.hkv * 8 + kso);
+          vsc[m] = *reinterpret_cast<const float *>(st + (size_t)m * a.hkv * 8 + vso);
+        }
+      }
+      return;
+    }
 #pragma unroll
     for (int m = 0; m < CH; ++m) {
       const int c = lane + 64 * m;
@@ -279,25 +342,33 @@ __global__ __launch_bounds__(64) void k_attn_mx(AttnArgs a) {
     const int left = n - tile * kKeys; // keys of this tile inside the window (may be >= 32)
     // Stage K rows and V key groups as BF16.
     if constexpr (Q8) {
-      uint32_t m128 = 0;
+      float least = 0.f;
       bool slow = false;
-#pragma unroll
-      for (int m = 0; m < CH; ++m) {
-        const int c = lane + 64 * m, key = c >> 3, part = c & 7;
-        float f[16];
-        q8_values16(kw[m], ksc[m], key < left, f, m128, slow);
-        uint32_t w[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e)
-          w[e] = pack2(f[2 * e], f[2 * e + 1]);
-        *reinterpret_cast<uint4 *>(&ks[key][part * 8]) = make_uint4(w[0], w[1], w[2], w[3]);
-        *reinterpret_cast<uint4 *>(&ks[key][part * 8 + 4]) = make_uint4(w[4], w[5], w[6], w[7]);
-      }
       float fv[4][16];
+      // K rows into LDS and the V values; `whole`: every key of the tile is in the window
+      // (all but a window's last tile), so nothing is masked.
+      auto decode = [&](auto whole) {
 #pragma unroll
-      for (int m = 0; m < 4; ++m)
-        q8_values16(vw[m], vsc[m], vkey(m) < left, fv[m], m128, slow);
-      fine = fine && (m128 & 0x80808080u) == 0;
+        for (int m = 0; m < CH; ++m) {
+          const int c = lane + 64 * m, key = c >> 3, part = c & 7;
+          float f[16];
+          q8_values16(kw[m], ksc[m], whole.value || key < left, f, least, slow);
+          uint32_t w[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            w[e] = pack2(f[2 * e], f[2 * e + 1]);
+          *reinterpret_cast<uint4 *>(&ks[key][part * 8]) = make_uint4(w[0], w[1], w[2], w[3]);
+          *reinterpret_cast<uint4 *>(&ks[key][part * 8 + 4]) = make_uint4(w[4], w[5], w[6], w[7]);
+        }
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+          q8_values16(vw[m], vsc[m], whole.value || vkey(m) < left, fv[m], least, slow);
+      };
+      if (left >= kKeys) // block-uniform
+        decode(std::true_type{});
+      else
+        decode(std::false_type{});
+      fine = fine && least > -128.f;
       if (__ballot(slow) != 0) { // rare: huge or invalid scales
 #pragma unroll
         for (int m = 0; m < CH; ++m) {
@@ -566,6 +637,8 @@ constexpr int kQ8Tile = 128, kRowBytes = 544;
 
 template <class T> __global__ __launch_bounds__(64) void k_q8_0_query(AttnArgs a) {
   const int head = blockIdx.x, seq = blockIdx.y, lane = threadIdx.x;
+  if (a.order && head == 0) // the split kernel's dispatch order, one sequence per block
+    attn_rank(a, seq);
   const size_t base = ((size_t)seq * a.hq + head) * kD;
   float x0 = act_value<T>(a.q, base + lane), x1 = act_value<T>(a.q, base + 64 + lane);
   if (__ballot(!isfinite(x0) || !isfinite(x1)) != 0) {
@@ -670,7 +743,7 @@ template <int G> __global__ __launch_bounds__(256) void k_q8_0_mx(AttnArgs a) {
   __shared__ float ksc_all[4][32][4];    // K block scales by key
   __shared__ float vsc_all[4][4][32];    // V block scales by block
   __shared__ float ps_all[4][8][36];     // probabilities by head (rows padded)
-  const int split = blockIdx.x, seq = blockIdx.z, tid = threadIdx.x, kv = tid >> 6;
+  const int split = blockIdx.x, seq = attn_seq(a), tid = threadIdx.x, kv = tid >> 6;
   const int lane = tid & 63, col = lane & 15, grp = lane >> 4;
   auto &kq = kq_all[kv].r;
   auto &vq = vq_all[kv].r;
@@ -1022,7 +1095,9 @@ extern "C" long long padra_DecodeAttentionScratch(int format, int seqs, int q_he
   // partial outputs and log-sum-exps per split, rounded up to 16 bytes
   const long long base = ((long long)seqs * splits * q_heads * (kD + 1) + 3) & ~3ll;
   // q8_0: the coded query (128 bytes) and its 4 block scales per head, after the lse
-  return format == PADRA_KV_Q8_0 ? base + (long long)seqs * q_heads * (kD / 4 + 4) : base;
+  const long long query = format == PADRA_KV_Q8_0 ? (long long)seqs * q_heads * (kD / 4 + 4) : 0;
+  // then the split kernels' dispatch order, one int per sequence, rounded up to 16 bytes
+  return base + query + ((seqs + 3) & ~3ll);
 }
 
 namespace {
@@ -1078,6 +1153,11 @@ int decode_attention(void *stream, const void *q, const padra_KVCache *kv, void 
   a.lse = scratch + entries * kD;
   a.qcodes = reinterpret_cast<int8_t *>(scratch + qbase);
   a.qscale = scratch + qbase + (long long)seqs * q_heads * (kD / 4);
+  // Longest windows first when the lengths can differ much: several sequences on a
+  // global cache (a local ring's windows are at most 1024 keys).
+  const long long obase = qbase + (q8 ? (long long)seqs * q_heads * (kD / 4 + 4) : 0);
+  a.order = seqs >= 2 && seqs <= kOrderMaxSeqs && !local ? reinterpret_cast<int *>(scratch + obase)
+                                                         : nullptr;
   a.decode = pos->decode;
   a.seqs = seqs;
   a.hq = q_heads;
@@ -1097,6 +1177,8 @@ int decode_attention(void *stream, const void *q, const padra_KVCache *kv, void 
     return PADRA_UNSUPPORTED;
   auto launch = [&](auto tag) -> int {
     using T = decltype(tag);
+    if (a.order && !q8) // (the q8_0 query kernel ranks the sequences itself)
+      hipLaunchKernelGGL(k_attn_order, dim3(seqs), dim3(64), 0, s, a);
     if (q8) {
       hipLaunchKernelGGL((k_q8_0_query<T>), merge_grid, dim3(64), 0, s, a);
       switch (group) {

@@ -134,14 +134,16 @@ def test_host_validation_newer_entry_points():
     kv = abi.KVCache(format=abi.KV_BF16, k=16, v=32, scales=None, cap=4096, first=0,
                      seq_stride=4096)
     need = lib.padra_DecodeAttentionScratch(abi.KV_BF16, 2, 16, 32)
-    assert need == 2 * 32 * 16 * 129
+    assert need == 2 * 32 * 16 * 129 + 4  # partials and lse, then the dispatch order
     assert lib.padra_DecodeAttentionScratch(abi.KV_Q8_0, 2, 16, 32) == need + 2 * 16 * 36
     assert lib.padra_DecodeAttentionScratch(abi.KV_BF16, 2, 16, 33) == -1
     assert lib.padra_DecodeAttentionScratch(abi.KV_Q8, 2, 16, 32) == need
     assert lib.padra_DecodeAttentionScratch(abi.KV_Q8_0_NOROT, 2, 16, 32) == -1
-    # the lse ends on a 16-byte boundary before the q8_0 query region
-    assert lib.padra_DecodeAttentionScratch(abi.KV_BF16, 1, 1, 1) == 132
-    assert lib.padra_DecodeAttentionScratch(abi.KV_Q8_0, 1, 1, 1) == 132 + 36
+    # the lse ends on a 16-byte boundary before the q8_0 query region; the dispatch order
+    # (one int per sequence) is last, rounded up to 16 bytes
+    assert lib.padra_DecodeAttentionScratch(abi.KV_BF16, 1, 1, 1) == 132 + 4
+    assert lib.padra_DecodeAttentionScratch(abi.KV_Q8_0, 1, 1, 1) == 132 + 36 + 4
+    assert lib.padra_DecodeAttentionScratch(abi.KV_BF16, 5, 1, 1) == 5 * 129 + 3 + 8
     assert lib.padra_DecodeAttention(None, _p(16), ctypes.byref(kv), _p(32), ctypes.byref(dec), 2,
                                      16, 4, 0, 0, _p(64), need - 1, bad, 0) == abi.INVALID_ARGUMENT
     assert lib.padra_DecodeAttention(None, _p(16), ctypes.byref(kv), _p(32), ctypes.byref(dec), 2,

@@ -627,7 +627,22 @@ def test_decode_attention_q8(oracle, hq, local):
         assert not wbad
         close, d = _attn_close(got[s], want)
         assert close.all(), (s, int(d.max()))
-    # a -128 code inside the window raises the flag
+    # a -128 code inside the window raises the flag: in the window's first tile (whole,
+    # for a window of 32 keys or more) and at the current position
+    if not local and positions[1] >= 64:
+        codes_k[1, 0, 5] = -128
+        kv1 = ops.kv_cache(abi.KV_Q8, torch.from_numpy(codes_k.reshape(seqs * cap, -1)).cuda(),
+                           torch.from_numpy(codes_v.reshape(seqs * cap, -1)).cuda(), cap,
+                           scales=torch.from_numpy(scales.reshape(seqs * cap, hkv, 2)).cuda(),
+                           seq_stride=cap)
+        bad.zero_()
+        ops.DecodeAttention(dev(q), kv1, out,
+                            ops.positions_decode(torch.from_numpy(states).cuda(),
+                                                 maximum=capacity), bad, kv_heads=hkv)
+        torch.cuda.synchronize()
+        assert bad.item() == 1
+        codes_k[1, 0, 5] = 0
+        bad.zero_()
     codes_k[1, positions[1] % cap, 5] = -128
     kv2 = ops.kv_cache(abi.KV_Q8, torch.from_numpy(codes_k.reshape(seqs * cap, -1)).cuda(),
                        torch.from_numpy(codes_v.reshape(seqs * cap, -1)).cuda(), cap,
@@ -638,6 +653,56 @@ def test_decode_attention_q8(oracle, hq, local):
                         bad, kv_heads=hkv, local=local)
     torch.cuda.synchronize()
     assert bad.item() == 1
+
+
+@pytest.mark.parametrize("fmt", [abi.KV_BF16, abi.KV_Q8, abi.KV_Q8_0])
+def test_decode_attention_dispatch_order(fmt):
+    """Several sequences on a global cache run their split waves longest window first;
+    every output equals the same sequence decoded alone (one sequence, sequence order),
+    bit for bit.  Windows of 1, 6, 101, 2048 and twice 3001 keys (a tie) plus a sequence
+    at the last row."""
+    print(f"[case] decode attention dispatch order fmt={fmt}", flush=True)
+    seqs, hq, hkv, cap = 7, 16, 4, 4096
+    rng = np.random.default_rng(150 + fmt)
+    positions = np.array([5, 3000, 100, 3000, 0, 2047, cap - 1], np.int32)
+    q = synth.bf16_bits((rng.standard_normal((seqs, hq, 128)) * 2).astype(np.float32))
+    if fmt == abi.KV_BF16:
+        kc = synth.bf16_bits(rng.standard_normal((seqs * cap, hkv * 128)).astype(np.float32))
+        vc = synth.bf16_bits(rng.standard_normal((seqs * cap, hkv * 128)).astype(np.float32))
+        kc, vc, sc = kc.view(np.int16), vc.view(np.int16), None
+    elif fmt == abi.KV_Q8:
+        kc = rng.integers(-127, 128, (seqs * cap, hkv * 128)).astype(np.int8)
+        vc = rng.integers(-127, 128, (seqs * cap, hkv * 128)).astype(np.int8)
+        sc = rng.uniform(0.005, 0.02, (seqs * cap, hkv, 2)).astype(np.float32)
+    else:
+        kc = rng.integers(-127, 128, (seqs * cap, 544)).astype(np.int8)
+        vc = rng.integers(-127, 128, (seqs * cap, 544)).astype(np.int8)
+        kc[:, :32].view(np.int16)[:] = 0x2400  # block scales 1/64 (fp16)
+        vc[:, :32].view(np.int16)[:] = 0x2400
+        sc = None
+    states = np.zeros((seqs, 8), np.int32)
+    for i, p in enumerate(positions):
+        states[i] = [5, p, cap, 10, p, min(p, 1024), 0, 0]
+    kd, vd = torch.from_numpy(kc).cuda(), torch.from_numpy(vc).cuda()
+    sd = torch.from_numpy(sc).cuda() if sc is not None else None
+    qd = dev(q)
+    out = torch.empty((seqs, hq, 128), dtype=torch.int16, device="cuda")
+    bad = flag()
+    ops.DecodeAttention(qd, ops.kv_cache(fmt, kd, vd, cap, scales=sd, seq_stride=cap), out,
+                        ops.positions_decode(torch.from_numpy(states).cuda(), maximum=cap),
+                        bad, kv_heads=hkv)
+    torch.cuda.synchronize()
+    assert bad.item() == 0
+    for i in range(seqs):
+        one = torch.empty((1, hq, 128), dtype=torch.int16, device="cuda")
+        rows = slice(i * cap, (i + 1) * cap)
+        kv = ops.kv_cache(fmt, kd[rows], vd[rows], cap, scales=sd[rows] if sd is not None else None)
+        ops.DecodeAttention(qd[i:i + 1], kv, one,
+                            ops.positions_decode(torch.from_numpy(states[i:i + 1]).cuda(),
+                                                 maximum=cap), bad, kv_heads=hkv)
+        torch.cuda.synchronize()
+        assert bad.item() == 0
+        assert torch.equal(one[0], out[i]), i
 
 
 @pytest.mark.parametrize("fmt", [abi.KV_BF16, abi.KV_Q8])
