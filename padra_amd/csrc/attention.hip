@@ -175,8 +175,8 @@ __device__ __forceinline__ void q8_values16(uint4 c, float scale, bool inside, f
     for (int b = 0; b < 4; ++b)
       code[4 * i + b] = (float)(int8_t)((w[i] >> (8 * b)) & 0xffu);
 #pragma unroll
-  for (int i = 0; i < 16; i += 2)
-    least = fminf(least, fminf(code[i], code[i + 1]));
+  for (int i = 0; i < 16; ++i) // min(min(least, a), b): one v_min3_f32 per pair
+    least = fminf(least, code[i]);
 #pragma unroll
   for (int i = 0; i < 16; ++i)
     f[i] = code[i] * scale;
@@ -344,30 +344,22 @@ __global__ __launch_bounds__(64) void k_attn_mx(AttnArgs a) {
     if constexpr (Q8) {
       float least = 0.f;
       bool slow = false;
+#pragma unroll
+      for (int m = 0; m < CH; ++m) {
+        const int c = lane + 64 * m, key = c >> 3, part = c & 7;
+        float f[16];
+        q8_values16(kw[m], ksc[m], key < left, f, least, slow);
+        uint32_t w[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          w[e] = pack2(f[2 * e], f[2 * e + 1]);
+        *reinterpret_cast<uint4 *>(&ks[key][part * 8]) = make_uint4(w[0], w[1], w[2], w[3]);
+        *reinterpret_cast<uint4 *>(&ks[key][part * 8 + 4]) = make_uint4(w[4], w[5], w[6], w[7]);
+      }
       float fv[4][16];
-      // K rows into LDS and the V values; `whole`: every key of the tile is in the window
-      // (all but a window's last tile), so nothing is masked.
-      auto decode = [&](auto whole) {
 #pragma unroll
-        for (int m = 0; m < CH; ++m) {
-          const int c = lane + 64 * m, key = c >> 3, part = c & 7;
-          float f[16];
-          q8_values16(kw[m], ksc[m], whole.value || key < left, f, least, slow);
-          uint32_t w[8];
-#pragma unroll
-          for (int e = 0; e < 8; ++e)
-            w[e] = pack2(f[2 * e], f[2 * e + 1]);
-          *reinterpret_cast<uint4 *>(&ks[key][part * 8]) = make_uint4(w[0], w[1], w[2], w[3]);
-          *reinterpret_cast<uint4 *>(&ks[key][part * 8 + 4]) = make_uint4(w[4], w[5], w[6], w[7]);
-        }
-#pragma unroll
-        for (int m = 0; m < 4; ++m)
-          q8_values16(vw[m], vsc[m], whole.value || vkey(m) < left, fv[m], least, slow);
-      };
-      if (left >= kKeys) // block-uniform
-        decode(std::true_type{});
-      else
-        decode(std::false_type{});
+      for (int m = 0; m < 4; ++m)
+        q8_values16(vw[m], vsc[m], vkey(m) < left, fv[m], least, slow);
       fine = fine && least > -128.f;
       if (__ballot(slow) != 0) { // rare: huge or invalid scales
 #pragma unroll
@@ -386,13 +378,18 @@ __global__ __launch_bounds__(64) void k_attn_mx(AttnArgs a) {
             make_uint4(pack2(fv[0][e], fv[1][e]), pack2(fv[2][e], fv[3][e]),
                        pack2(fv[0][e + 1], fv[1][e + 1]), pack2(fv[2][e + 1], fv[3][e + 1]));
     } else {
+      if (left < kKeys) { // block-uniform: the window's last tile
+#pragma unroll
+        for (int m = 0; m < 8; ++m) {
+          if (((lane + 64 * m) >> 4) >= left)
+            kw[m] = make_uint4(0, 0, 0, 0);
+          if (vkey(m) >= left)
+            vw[m] = make_uint4(0, 0, 0, 0);
+        }
+      }
 #pragma unroll
       for (int m = 0; m < 8; ++m) {
         const int c = lane + 64 * m;
-        if ((c >> 4) >= left)
-          kw[m] = make_uint4(0, 0, 0, 0);
-        if (vkey(m) >= left)
-          vw[m] = make_uint4(0, 0, 0, 0);
         *reinterpret_cast<uint4 *>(&ks[c >> 4][(c & 15) * 4]) = kw[m];
       }
 #pragma unroll
@@ -799,8 +796,26 @@ template <int G> __global__ __launch_bounds__(256) void k_q8_0_mx(AttnArgs a) {
   };
   uint4 kw[4], vw[4], hw = make_uint4(0, 0, 0, 0);
   const int hrow = (tid >> 1) & 31;
+  // A slice whose 32 rows are inside the window and consecutive in the cache: load m is
+  // the slice's first row plus a per-thread offset plus a step common to all threads
+  // (K: 8 m rows, V: m rows).
+  const uint32_t koff = (uint32_t)((tid >> 5) * kRowBytes + dbytes + 16 * (tid & 31));
+  const uint32_t voff = (uint32_t)(4 * (tid >> 5) * kRowBytes + dbytes + 16 * (tid & 31));
+  const uint32_t hoff = (uint32_t)(hrow * kRowBytes + 16 * (tid & 1));
   auto load_slice = [&](int tile, int s) {
     const int o0 = tile * kQ8Tile + 32 * s;
+    const int r0 = a.local ? (first + o0) & 1023 : first + o0;
+    if (o0 + 32 <= n && (!a.local || r0 + 32 <= 1024)) { // block-uniform
+      const uint8_t *kt = krows + (size_t)r0 * kRowBytes, *vt = vrows + (size_t)r0 * kRowBytes;
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        kw[m] = ld_nt(reinterpret_cast<const uint4 *>(kt + (size_t)(8 * m) * kRowBytes + koff));
+        vw[m] = ld_nt(reinterpret_cast<const uint4 *>(vt + (size_t)m * kRowBytes + voff));
+      }
+      if (tid < 128)
+        hw = *reinterpret_cast<const uint4 *>((tid < 64 ? kt : vt) + hoff);
+      return;
+    }
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
       const int c = tid + 256 * m;
@@ -878,7 +893,8 @@ template <int G> __global__ __launch_bounds__(256) void k_q8_0_mx(AttnArgs a) {
             d[b] = inside ? f16_bits((b & 1) ? word >> 16 : word & 0xffffu) : 0.f;
           }
           if (tid < 64) {
-            *reinterpret_cast<float4 *>(&ksc_all[hd][hrow][0]) = make_float4(d[0], d[1], d[2], d[3]);
+            *reinterpret_cast<float4 *>(&ksc_all[hd][hrow][0]) =
+                make_float4(d[0], d[1], d[2], d[3]);
           } else {
 #pragma unroll
             for (int b = 0; b < 4; ++b)
