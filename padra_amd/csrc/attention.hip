@@ -857,15 +857,17 @@ template <int G> __global__ __launch_bounds__(256) void k_q8_0_mx(AttnArgs a) {
 #pragma unroll
       for (int m = 0; m < 4; ++m) {
         const int c = tid + 256 * m;
-        const uint4 w = o0 + (c >> 5) < n ? kw[m] : make_uint4(0, 0, 0, 0);
+        // keys past the window stage zero codes (a mask, not a branch per key)
+        const uint32_t keep = o0 + (c >> 5) < n ? ~0u : 0u;
+        const uint4 w = make_uint4(kw[m].x & keep, kw[m].y & keep, kw[m].z & keep, kw[m].w & keep);
         *reinterpret_cast<uint4 *>(&kq_all[(c >> 3) & 3].r[c >> 5][4 * (c & 7)]) = w;
       }
       {
         float f[4][16];
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
-          const uint4 c = o0 + 4 * (tid >> 5) + m < n ? vw[m] : make_uint4(0, 0, 0, 0);
-          const uint32_t w[4] = {c.x, c.y, c.z, c.w};
+          const uint32_t keep = o0 + 4 * (tid >> 5) + m < n ? ~0u : 0u;
+          const uint32_t w[4] = {vw[m].x & keep, vw[m].y & keep, vw[m].z & keep, vw[m].w & keep};
 #pragma unroll
           for (int i = 0; i < 4; ++i)
 #pragma unroll
