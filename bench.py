@@ -639,6 +639,16 @@ def main():
                            "attention": bench_attention(torch, 10),
                            "attention_q8_0": bench_attention(torch, 10, fmt="q8_0"),
                            "attention_q8": bench_attention(torch, 10, fmt="q8")}
+        # The streaming copy of each memory-bound kernel's own byte count, timed the same
+        # way: how far a launch of that size is from the copy, apart from the HBM peak.
+        for key in ("config3", "norm_fp8", "combine_norm", "config1_f32_activations"):
+            entry = line["configs"][key]
+            nbytes = entry.get("bytes_per_launch") or (entry["norm_bytes"] + entry["qk_bytes"])
+            gbs, ms = stream_copy_ceiling(torch, nbytes, steps=100)
+            entry["copy_us"] = round(ms * 1e3, 3)
+            entry["frac_of_copy"] = round(entry["gbs"] / gbs, 4)
+            if "fused_gbs" in entry:
+                entry["fused_frac_of_copy"] = round(entry["fused_gbs"] / gbs, 4)
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(host, args.cpu_seconds, cpu_threads())
         if not args.no_configs:

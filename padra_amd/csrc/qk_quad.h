@@ -331,23 +331,44 @@ __device__ __forceinline__ void qk_heads_wave_quad(const QKArgs<T> &a, long long
   const int hh = live ? (int)(idx - (unsigned)t * heads) : 0;
   const PosState ps = fetch_state(a.pos, t);
 
+  // A block of 16 live heads of one role (every block when the head counts divide into
+  // blocks) is 16 consecutive head vectors: its pieces are 64 m + lane 16-byte units from
+  // the block's first vector, with no per-piece head lookup.
+  const unsigned h0 = slot_head(0u);
+  const bool whole = slot_head(15u) == h0 + 15u &&
+                     (h0 + 15u < nq || (h0 >= nq && h0 + 15u < nq + nk)); // wave-uniform
+  const uint4 *block = reinterpret_cast<const uint4 *>(head_src(a, whole ? h0 : 0u, nq, nk));
+  const uint4 *vblock = reinterpret_cast<const uint4 *>(a.v + (size_t)(whole && h0 >= nq ? h0 - nq : 0u) * D);
+
   // 1. PL coalesced loads per lane (clamped, unconditional), for the LDS image.
   uint4 in[PL];
+  if (whole) {
 #pragma unroll
-  for (int m = 0; m < PL; ++m) {
-    const int c = 64 * m + lane;
-    const unsigned hc = min(slot_head((unsigned)(c / CH)), total - 1u);
-    in[m] = ld_nt(reinterpret_cast<const uint4 *>(head_src(a, hc, nq, nk)) + (c % CH));
+    for (int m = 0; m < PL; ++m)
+      in[m] = ld_nt(block + 64 * m + lane);
+  } else {
+#pragma unroll
+    for (int m = 0; m < PL; ++m) {
+      const int c = 64 * m + lane;
+      const unsigned hc = min(slot_head((unsigned)(c / CH)), total - 1u);
+      in[m] = ld_nt(reinterpret_cast<const uint4 *>(head_src(a, hc, nq, nk)) + (c % CH));
+    }
   }
   // The V heads of a K wave (quantized cache), the same pieces of a.v.
   uint4 inv_[FMT > PADRA_KV_BF16 ? PL : 1];
   if constexpr (FMT > PADRA_KV_BF16) {
     if (kv_wave) {
+      if (whole) {
 #pragma unroll
-      for (int m = 0; m < PL; ++m) {
-        const int c = 64 * m + lane;
-        const unsigned hc = min(slot_head((unsigned)(c / CH)), nq + nk - 1u) - nq;
-        inv_[m] = ld_nt(reinterpret_cast<const uint4 *>(a.v + (size_t)hc * D) + (c % CH));
+        for (int m = 0; m < PL; ++m)
+          inv_[m] = ld_nt(vblock + 64 * m + lane);
+      } else {
+#pragma unroll
+        for (int m = 0; m < PL; ++m) {
+          const int c = 64 * m + lane;
+          const unsigned hc = min(slot_head((unsigned)(c / CH)), nq + nk - 1u) - nq;
+          inv_[m] = ld_nt(reinterpret_cast<const uint4 *>(a.v + (size_t)hc * D) + (c % CH));
+        }
       }
     }
   }
@@ -508,6 +529,11 @@ __device__ __forceinline__ void qk_heads_wave_quad(const QKArgs<T> &a, long long
 #pragma unroll
     for (int m = 0; m < PL; ++m) {
       const int c = 64 * m + lane, j = c / CH, ci = c % CH;
+      if (whole) {
+        if (head_live[j])
+          st_nt(const_cast<uint4 *>(block) + c, stage[quad_piece_slot<T>(4 * j + ci / PL, ci % PL)]);
+        continue;
+      }
       const unsigned hc = slot_head((unsigned)j);
       if (!head_live[j] || hc >= nq + nk)
         continue;
@@ -532,10 +558,19 @@ __device__ __forceinline__ void qk_heads_wave_quad(const QKArgs<T> &a, long long
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
       const int c = 64 * m + lane, j = c >> 4, ci = c & 15;
-      const unsigned hc = slot_head((unsigned)j);
       if (!head_live[j])
         continue; // past the end, or a head that writes nothing
       const uint4 d = stage[quad_slot(4 * j + (ci >> 2), ci & 3)];
+      if (whole) { // Q or K heads of one block
+        st_nt(const_cast<uint4 *>(block) + c, d);
+        if constexpr (FMT == PADRA_KV_BF16) {
+          const long long r = head_row[j];
+          if (r >= 0)
+            st_nt(reinterpret_cast<uint4 *>(static_cast<uint16_t *>(a.kc) + r) + ci, d);
+        }
+        continue;
+      }
+      const unsigned hc = slot_head((unsigned)j);
       if constexpr (FMT == PADRA_KV_BF16) {
         const long long r = head_row[j];
         if (hc >= nq + nk) { // V head: cache only
