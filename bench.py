@@ -662,7 +662,7 @@ SHADER_ENGINES, SIMDS = 32, 1024  # MI355X (rocminfo: 32 shader engines, 256 CUs
 
 def chain_kernel(fmt: str) -> str:
     """Kernel-trace name of the config-1 chain launch (tree 128, H 2048, no gather)."""
-    return f"k_chain<128, 16, {FORMAT_CODES[fmt]}, false>"
+    return f"k_chain<128, 16, {FORMAT_CODES[fmt]}, false, unsigned short>"
 
 
 def hbm_bytes(c: dict) -> dict:
@@ -789,10 +789,12 @@ def summarize(outdir: str, command: str) -> None:
 
 
 KERNEL_ROLES = {
-    "k_chain<128, 16, 0, false>": "config 1 chain, BF16 KV",
-    "k_chain<128, 16, 1, false>": "config 2 chain, q8 KV",
-    "k_chain<128, 16, 2, false>": "config 2 chain, q8_0 KV (rotated)",
-    "k_chain<128, 16, 3, false>": "config 2 chain, q8_0 KV (unrotated)",
+    "k_attn_order": "decode attention: windows ranked longest first (dispatch order)",
+    "k_chain<128, 16, 0, false, unsigned short>": "config 1 chain, BF16 KV",
+    "k_chain<128, 16, 1, false, unsigned short>": "config 2 chain, q8 KV",
+    "k_chain<128, 16, 2, false, unsigned short>": "config 2 chain, q8_0 KV (rotated)",
+    "k_chain<128, 16, 3, false, unsigned short>": "config 2 chain, q8_0 KV (unrotated)",
+    "k_chain<128, 16, 0, false, float>": "config 1 chain on fp32 activations, one launch",
     "k_chain_small<256, 8, 0, true>": "config 4/0 decode step: gather + chain, one launch",
     "k_chain_small<256, 8, 0, false>": "config 4/0 decode chain after a separate gather",
     "k_embed": "embedding gather (separate launch)",
@@ -806,7 +808,7 @@ KERNEL_ROLES = {
     "k_q8_0_query": "decode attention, q8_0 query coding",
     "k_q8_0_mx": "decode attention split (q8_0 cache)",
     "k_q8_0_mx_merge": "decode attention merge (q8_0)",
-    "k_stream_copy": "streaming copy (practical ceiling)",
+    "k_stream_copy": "streaming copy: the ceilings at each leg's byte count (mixed sizes)",
 }
 
 
