@@ -655,16 +655,27 @@ def test_decode_attention_q8(oracle, hq, local):
     assert bad.item() == 1
 
 
-@pytest.mark.parametrize("fmt", [abi.KV_BF16, abi.KV_Q8, abi.KV_Q8_0])
-def test_decode_attention_dispatch_order(fmt):
-    """Several sequences on a global cache run their split waves longest window first;
-    every output equals the same sequence decoded alone (one sequence, sequence order),
-    bit for bit.  Windows of 1, 6, 101, 2048 and twice 3001 keys (a tie) plus a sequence
-    at the last row."""
-    print(f"[case] decode attention dispatch order fmt={fmt}", flush=True)
-    seqs, hq, hkv, cap = 7, 16, 4, 4096
-    rng = np.random.default_rng(150 + fmt)
-    positions = np.array([5, 3000, 100, 3000, 0, 2047, cap - 1], np.int32)
+@pytest.mark.parametrize("fmt,seqs", [(abi.KV_BF16, 7), (abi.KV_Q8, 7), (abi.KV_Q8_0, 7),
+                                      (abi.KV_BF16, 512), (abi.KV_BF16, 513),
+                                      (abi.KV_Q8_0, 513)])
+def test_decode_attention_dispatch_order(fmt, seqs):
+    """Several sequences on a global cache run their split waves longest window first (up
+    to 512 sequences; more run in sequence order); every output equals the same sequence
+    decoded alone, bit for bit.  7 sequences: windows of 1, 6, 101, 2048 and twice 3001
+    keys (a tie) plus one at the last row of 4096; 512 and 513: random windows of a
+    64-row cache, every sequence with position 10 (ties), each sixteenth checked alone."""
+    print(f"[case] decode attention dispatch order fmt={fmt} seqs={seqs}", flush=True)
+    hq, hkv = 16, 4
+    rng = np.random.default_rng(150 + fmt + seqs)
+    if seqs == 7:
+        cap = 4096
+        positions = np.array([5, 3000, 100, 3000, 0, 2047, cap - 1], np.int32)
+        check = range(seqs)
+    else:
+        cap = 64
+        positions = rng.integers(0, cap, seqs).astype(np.int32)
+        positions[::5] = 10
+        check = range(0, seqs, 16)
     q = synth.bf16_bits((rng.standard_normal((seqs, hq, 128)) * 2).astype(np.float32))
     if fmt == abi.KV_BF16:
         kc = synth.bf16_bits(rng.standard_normal((seqs * cap, hkv * 128)).astype(np.float32))
@@ -693,10 +704,11 @@ def test_decode_attention_dispatch_order(fmt):
                         bad, kv_heads=hkv)
     torch.cuda.synchronize()
     assert bad.item() == 0
-    for i in range(seqs):
+    for i in check:
         one = torch.empty((1, hq, 128), dtype=torch.int16, device="cuda")
         rows = slice(i * cap, (i + 1) * cap)
-        kv = ops.kv_cache(fmt, kd[rows], vd[rows], cap, scales=sd[rows] if sd is not None else None)
+        kv = ops.kv_cache(fmt, kd[rows], vd[rows], cap,
+                          scales=sd[rows] if sd is not None else None)
         ops.DecodeAttention(qd[i:i + 1], kv, one,
                             ops.positions_decode(torch.from_numpy(states[i:i + 1]).cuda(),
                                                  maximum=cap), bad, kv_heads=hkv)
