@@ -7,8 +7,8 @@
   codes follow mellum16::KVCacheFormat's order (kv_cache_layout.h:6);
 - runs mellum16::KVCacheLayout::Make for every format at 1, 1024, 8192 and 131072 rows and
   compares it with padra_amd.ops.kv_cache_layout, which the tests and the bench use;
-- compiles the calls shown in INTEGRATION.md section 1 with -fsyntax-only against
-  include/padra_hip.h.
+- compiles the C++ calls of the repository's integration guide (its section 1) with
+  -fsyntax-only against include/padra_hip.h.
 
 The reference headers are read where they lie under /root/reference (nothing is copied
 into the repository); DecodeState lives in a CUDA header, so its struct definition is
@@ -137,8 +137,8 @@ def _integration_blocks():
     return re.findall(r"```cpp\n(.*?)```", sec, re.S)
 
 
-# Declarations of the names INTEGRATION.md's snippets use, with the types the reference's
-# runtime gives them (fp32 activation buffers, BF16 weights and tables, device states).
+# Declarations of the names the integration guide's snippets use, with the types the
+# reference's runtime gives them (fp32 activation buffers, BF16 weights and tables, device states).
 SNIPPET_PRELUDE = r'''
 #include <algorithm>
 #include <cstdint>
