@@ -905,11 +905,12 @@ template <int G> __global__ __launch_bounds__(256) void k_q8_0_mx(AttnArgs a) {
         }
       }
       __syncthreads();
-      // The next slice's loads are in flight during this slice's arithmetic (the last one
-      // reloads the first slice, keeping the loads unconditional).
+      // The next slice's loads are in flight during this slice's arithmetic: the next tile
+      // of this stream, or the next stream's first slice.  After the last slice the loads
+      // stay unconditional and repeat the slice just read, which L2 still holds.
       {
-        const bool last_tile = it + 1 == slices;
-        load_slice(last_tile ? begin : tile + 1, last_tile ? (s + 1) & 3 : s);
+        const bool last_tile = it + 1 == slices, last = last_tile && s == kStreams - 1;
+        load_slice(last ? tile : (last_tile ? begin : tile + 1), last_tile && !last ? s + 1 : s);
       }
 
       // Scores: head 4 j + grp, key 16 k + col.
