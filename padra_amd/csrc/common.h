@@ -172,10 +172,11 @@ __device__ __forceinline__ void raise_bad(int *bad) {
     atomicExch(bad, 1);
 }
 
+// The codes below are returned as the clamped int (its low byte is the int8 code).
+
 // q8 code (kv_q8.cuh:12-14): RNE of the correctly rounded quotient, clamped to +-127.
 __device__ __forceinline__ uint32_t q8_code(float value, float scale) {
-  const int c = max(-127, min(127, (int)rintf(value / scale)));
-  return (uint32_t)(c & 0xff);
+  return (uint32_t)max(-127, min(127, (int)rintf(value / scale)));
 }
 // The same code through the head's cached reciprocal: q = v * inverse, r = q * scale - v
 // (one fused multiply-add), q - r * inverse, then RNE and the clamp; three instructions
@@ -188,8 +189,7 @@ __device__ __forceinline__ uint32_t q8_code(float value, float scale) {
 __device__ __forceinline__ uint32_t q8_code_fast(float value, float scale, float inverse) {
   const float q = value * inverse;
   const float r = __builtin_fmaf(q, scale, -value);
-  const int c = max(-127, min(127, (int)rintf(__builtin_fmaf(-r, inverse, q))));
-  return (uint32_t)(c & 0xff);
+  return (uint32_t)max(-127, min(127, (int)rintf(__builtin_fmaf(-r, inverse, q))));
 }
 __device__ __forceinline__ bool q8_fast_ok(float scale) { return scale >= 0x1p-100f; }
 // q8_0 code (kv_q8_native.cuh:46-48): roundf (half away from zero) of v * inverse.
@@ -199,8 +199,15 @@ __device__ __forceinline__ bool q8_fast_ok(float scale) { return scale >= 0x1p-1
 // them): three instructions instead of roundf's seven.
 __device__ __forceinline__ uint32_t q8_0_code(float value, float inverse) {
   const float v = value * inverse;
-  const int c = max(-127, min(127, (int)(v + __builtin_copysignf(0.49999997f, v))));
-  return (uint32_t)(c & 0xff);
+  return (uint32_t)max(-127, min(127, (int)(v + __builtin_copysignf(0.49999997f, v))));
+}
+// Four codes (the low bytes of c0..c3) as one word, c0 in the lowest byte: three byte
+// permutes instead of a mask, a shift and an or per code.
+__device__ __forceinline__ uint32_t pack_codes4(uint32_t c0, uint32_t c1, uint32_t c2,
+                                                uint32_t c3) {
+  const uint32_t lo = __builtin_amdgcn_perm(c1, c0, 0x0c0c0400u); // c0, c1, 0, 0
+  const uint32_t hi = __builtin_amdgcn_perm(c3, c2, 0x0c0c0400u); // c2, c3, 0, 0
+  return __builtin_amdgcn_perm(hi, lo, 0x05040100u);             // c0, c1, c2, c3
 }
 // A 32-byte control record read as eight words issued together: the checks below then
 // work on registers, instead of one dependent load per field under short-circuit tests.

@@ -141,12 +141,11 @@ __device__ __forceinline__ void encode_head_q(const A &a, float (&xa)[32], float
     uint32_t w0[8], w1[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      w0[i] = w1[i] = 0u;
-#pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        w0[i] |= (fast ? q8_code_fast(xa[4 * i + b], scale, inverse) : q8_code(xa[4 * i + b], scale)) << (8 * b);
-        w1[i] |= (fast ? q8_code_fast(xb[4 * i + b], scale, inverse) : q8_code(xb[4 * i + b], scale)) << (8 * b);
-      }
+      auto code = [&](float x) { return fast ? q8_code_fast(x, scale, inverse) : q8_code(x, scale); };
+      w0[i] = pack_codes4(code(xa[4 * i]), code(xa[4 * i + 1]), code(xa[4 * i + 2]),
+                          code(xa[4 * i + 3]));
+      w1[i] = pack_codes4(code(xb[4 * i]), code(xb[4 * i + 1]), code(xb[4 * i + 2]),
+                          code(xb[4 * i + 3]));
     }
     store_codes32(codes + 32 * half, w0);
     store_codes32(codes + 64 + 32 * half, w1);
@@ -199,12 +198,10 @@ __device__ __forceinline__ void encode_head_q(const A &a, float (&xa)[32], float
     uint32_t w0[8], w1[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      w0[i] = w1[i] = 0u;
-#pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        w0[i] |= q8_0_code(xa[4 * i + b], ai) << (8 * b);
-        w1[i] |= q8_0_code(xb[4 * i + b], bi) << (8 * b);
-      }
+      w0[i] = pack_codes4(q8_0_code(xa[4 * i], ai), q8_0_code(xa[4 * i + 1], ai),
+                          q8_0_code(xa[4 * i + 2], ai), q8_0_code(xa[4 * i + 3], ai));
+      w1[i] = pack_codes4(q8_0_code(xb[4 * i], bi), q8_0_code(xb[4 * i + 1], bi),
+                          q8_0_code(xb[4 * i + 2], bi), q8_0_code(xb[4 * i + 3], bi));
     }
     const uint16_t a16 = __half_as_ushort(ah), b16 = __half_as_ushort(bh);
     if (stop == 4) {

@@ -132,20 +132,16 @@ __device__ __forceinline__ QuadCodes quad_codes(float (&x)[32], int g) {
     r.scale = scale;
     if (q8_fast_ok(scale)) { // quad-uniform
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        r.cw[i] = 0u;
-#pragma unroll
-        for (int b = 0; b < 4; ++b)
-          r.cw[i] |= q8_code_fast(x[4 * i + b], scale, inverse) << (8 * b);
-      }
+      for (int i = 0; i < 8; ++i)
+        r.cw[i] = pack_codes4(q8_code_fast(x[4 * i], scale, inverse),
+                              q8_code_fast(x[4 * i + 1], scale, inverse),
+                              q8_code_fast(x[4 * i + 2], scale, inverse),
+                              q8_code_fast(x[4 * i + 3], scale, inverse));
     } else {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        r.cw[i] = 0u;
-#pragma unroll
-        for (int b = 0; b < 4; ++b)
-          r.cw[i] |= q8_code(x[4 * i + b], scale) << (8 * b);
-      }
+      for (int i = 0; i < 8; ++i)
+        r.cw[i] = pack_codes4(q8_code(x[4 * i], scale), q8_code(x[4 * i + 1], scale),
+                              q8_code(x[4 * i + 2], scale), q8_code(x[4 * i + 3], scale));
     }
   } else {
     if constexpr (FMT == PADRA_KV_Q8_0) {
@@ -174,12 +170,9 @@ __device__ __forceinline__ QuadCodes quad_codes(float (&x)[32], int g) {
     r.d = __half_as_ushort(dh);
     const float inverse = ad == 0.f ? 0.f : 1.f / ad;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      r.cw[i] = 0u;
-#pragma unroll
-      for (int b = 0; b < 4; ++b)
-        r.cw[i] |= q8_0_code(x[4 * i + b], inverse) << (8 * b);
-    }
+    for (int i = 0; i < 8; ++i)
+      r.cw[i] = pack_codes4(q8_0_code(x[4 * i], inverse), q8_0_code(x[4 * i + 1], inverse),
+                            q8_0_code(x[4 * i + 2], inverse), q8_0_code(x[4 * i + 3], inverse));
   }
   return r;
 }
