@@ -49,16 +49,13 @@ __device__ __forceinline__ void combine8(const T *x, const T *down, size_t exper
 #pragma unroll
   for (int k = 0; k < 8; ++k)
     c[k] = 0.f;
+  // B() of one value is one conversion whose result is already the float; rounding a pair
+  // with one conversion would need two unpacks to continue.
 #pragma unroll
-  for (int e = 0; e < kExperts; ++e) {
+  for (int e = 0; e < kExperts; ++e)
 #pragma unroll
-    for (int k = 0; k < 8; k += 2) {
-      const uint32_t p = pack2(d[e][k] * wt[e], d[e][k + 1] * wt[e]);
-      const uint32_t q = pack2(c[k] + lo16(p), c[k + 1] + hi16(p));
-      c[k] = lo16(q);
-      c[k + 1] = hi16(q);
-    }
-  }
+    for (int k = 0; k < 8; ++k)
+      c[k] = B(c[k] + B(d[e][k] * wt[e]));
   uint32_t bad_bits = 0;
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
