@@ -6,6 +6,8 @@ import torch
 
 from padra_amd import abi, ops, synth
 
+from attn_tolerance import attn_close as _attn_close
+
 pytestmark = pytest.mark.gpu
 
 
@@ -457,25 +459,6 @@ def test_kv_checkpoint_capture(oracle, fmt):
 
 
 # ---- decode attention --------------------------------------------------------------------
-
-def _attn_close(got_bits, want_bits):
-    """Per element: within 1 BF16 ulp of the oracle, or within 2^-12 of the head's largest
-    |output|.  The second bound covers near-cancelling sums, where a BF16 probability that
-    rounds the other way (the score's fp32 sum order differs) moves the output by a
-    fraction of one term, not of the small result."""
-    d = _ulp_diff(got_bits, want_bits)
-    g, w = synth.bf16_to_f32(got_bits), synth.bf16_to_f32(want_bits)
-    head_max = np.abs(w).max(axis=-1, keepdims=True)
-    return (d <= 1) | (np.abs(g - w) <= 2.0**-12 * head_max), d
-
-
-def _ulp_diff(got_bits, want_bits):
-    """Distance in BF16 ulps (ordered bit patterns, both signs)."""
-    def ordered(b):
-        b = b.astype(np.int32)
-        return np.where(b & 0x8000, 0x8000 - (b & 0x7FFF), 0x8000 + b)
-    return np.abs(ordered(got_bits) - ordered(want_bits))
-
 
 @pytest.mark.parametrize("hq,local,splits", [(16, False, 0), (32, False, 0), (16, True, 0),
                                              (16, False, 5), (4, False, 0), (8, True, 0)])

@@ -9,7 +9,10 @@ C-ABI, against the CPU oracle, bit for bit.
   up to 131071, per-sequence caches of 131072 rows (row offsets above 4 GiB), both as one
   fused launch and as gather then chain, in every KV format.  The caches are too large to
   copy back whole: the written rows are gathered on the device and compared, and a count
-  of non-zero bytes over the whole cache shows that nothing else was written.
+  of non-zero bytes over the whole cache shows that nothing else was written;
+- config 4's consumer: decode attention over those 64 full-size caches in every cache
+  format, sampled sequences (the longest window of all 131072 rows among them) against the
+  oracle within the attention tolerance.
 """
 import numpy as np
 import pytest
@@ -212,4 +215,80 @@ def test_config4_decode_step_full(oracle, fmt):
             assert np.array_equal(sc[rows].cpu().numpy(), es)
             assert int((sc != 0).sum().item()) == int((sc[rows] != 0).sum().item())
     del kc, vc, sc, emb
+    torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("fmt", [abi.KV_BF16, abi.KV_Q8, abi.KV_Q8_0])
+def test_config4_attention_full(oracle, fmt):
+    """Decode attention at config 4's scale: 64 sequences, per-sequence caches of 131072
+    rows (seq_stride 131072, byte offsets past 4 GiB), ragged positions including 131071
+    (a window of every row) and 0, in one launch (the split waves ordered by window
+    length); four sequences checked against the oracle within the attention tolerance
+    (tests/attn_tolerance.py), the others only for a raised flag."""
+    from attn_tolerance import attn_close
+    print(f"[case] config4 attention full fmt={fmt}", flush=True)
+    seqs, hq, hkv, cap = 64, 16, 4, 131072
+    rng = np.random.default_rng(410 + fmt)
+    positions = rng.integers(0, cap, seqs).astype(np.int32)
+    positions[0], positions[1], positions[40] = cap - 1, 0, 70000
+    sample = (0, 1, 17, 40)
+    q = synth.bf16_bits((rng.standard_normal((seqs, hq, 128)) * 2).astype(np.float32))
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(41 + fmt)
+    rows = seqs * cap
+    if fmt == abi.KV_BF16:
+        mk = lambda: torch.randn((rows, hkv * 128), generator=gen, device="cuda") \
+            .to(torch.bfloat16).view(torch.int16)
+        kc, vc, sc = mk(), mk(), None
+    elif fmt == abi.KV_Q8:
+        mk = lambda: torch.randint(-127, 128, (rows, hkv * 128), generator=gen, device="cuda",
+                                   dtype=torch.int8)
+        kc, vc = mk(), mk()
+        sc = torch.rand((rows, hkv, 2), generator=gen, device="cuda") * 0.015 + 0.005
+    else:
+        def mk():
+            r = torch.randint(-127, 128, (rows, 544), generator=gen, device="cuda",
+                              dtype=torch.int8)
+            # block scales: positive normal fp16 values between 2^-8 and 2^-5
+            r[:, :32].view(torch.int16).copy_(torch.randint(
+                0x1C00, 0x2800, (rows, 16), generator=gen, device="cuda", dtype=torch.int16))
+            return r
+        kc, vc, sc = mk(), mk(), None
+    states = np.zeros((seqs, 8), np.int32)
+    for s, p in enumerate(positions):
+        states[s] = [5, p, cap, 10, p, min(int(p), 1024), 0, 0]
+    out = torch.empty((seqs, hq, 128), dtype=torch.int16, device="cuda")
+    bad = flag()
+    ops.DecodeAttention(dev(q), ops.kv_cache(fmt, kc, vc, cap, scales=sc, seq_stride=cap), out,
+                        ops.positions_decode(dev(states), maximum=cap), bad, kv_heads=hkv)
+    torch.cuda.synchronize()
+    assert bad.item() == 0
+    got = host16(out)
+    for s in sample:
+        window = slice(s * cap, s * cap + int(positions[s]) + 1)  # rows 0..position
+        if fmt == abi.KV_Q8_0:
+            rk = np.zeros((cap, 544), np.uint8)
+            rv = np.zeros((cap, 544), np.uint8)
+            n = int(positions[s]) + 1
+            rk[:n] = kc[window].cpu().numpy().view(np.uint8)
+            rv[:n] = vc[window].cpu().numpy().view(np.uint8)
+            want, _, wbad = oracle.decode_attention_q8_0(q[s], rk, rv, positions[s])
+        else:
+            n = int(positions[s]) + 1
+            dk = np.zeros((cap, hkv * 128), np.uint16)
+            dv = np.zeros((cap, hkv * 128), np.uint16)
+            if fmt == abi.KV_BF16:
+                dk[:n] = kc[window].cpu().numpy().view(np.uint16)
+                dv[:n] = vc[window].cpu().numpy().view(np.uint16)
+            else:  # kv_q8::Decode: bf16(code * scale) per (row, head)
+                scl = sc[window].cpu().numpy()
+                ck = kc[window].cpu().numpy().reshape(n, hkv, 128).astype(np.float32)
+                cv = vc[window].cpu().numpy().reshape(n, hkv, 128).astype(np.float32)
+                dk[:n] = synth.bf16_bits(ck * scl[:, :, 0:1]).reshape(n, -1)
+                dv[:n] = synth.bf16_bits(cv * scl[:, :, 1:2]).reshape(n, -1)
+            want, _, wbad = oracle.decode_attention(q[s], dk, dv, positions[s])
+        assert not wbad
+        close, d = attn_close(got[s], want)
+        assert close.all(), (s, int(d.max()))
+    del kc, vc, sc
     torch.cuda.empty_cache()
