@@ -366,11 +366,12 @@ def test_combine(oracle, residual, act):
     assert bool(bad.item()) == want_bad
 
 
-@pytest.mark.parametrize("hidden", [2048, 2304])
+@pytest.mark.parametrize("hidden,rows", [(2048, 67), (2304, 67), (2048, 2048)])
 @pytest.mark.parametrize("fp8", [True, False])
-def test_combine_norm(oracle, hidden, fp8):
-    print(f"[case] combine norm hidden={hidden} fp8={fp8}", flush=True)
-    rows = 67
+def test_combine_norm(oracle, hidden, rows, fp8):
+    """Combine + RMSNorm (+ FP8) against the oracle bit for bit; 2048 x 2048 is the size the
+    bench times."""
+    print(f"[case] combine norm hidden={hidden} rows={rows} fp8={fp8}", flush=True)
     d, down, w = _combine_inputs(rows, hidden, 32 + hidden)
     want_x, want_y, want_p, want_s, want_st, want_bad = oracle.combine_norm(
         d["x"], down, w, d["gamma"], fp8=fp8)

@@ -124,8 +124,8 @@ def test_residual_norm_nonfinite_sets_bad():
 
 # ---- RMSNorm + FP8 E4M3 row encoding ---------------------------------------------------------
 
-@pytest.mark.parametrize("hidden", [2048, 2304])
-@pytest.mark.parametrize("rows", [1, 37, 512])
+@pytest.mark.parametrize("hidden,rows", [(2048, 1), (2048, 37), (2048, 512), (2048, 2048),
+                                         (2304, 1), (2304, 37), (2304, 512)])
 @pytest.mark.parametrize("act", ["bf16", "f32"])
 def test_norm_fp8(oracle, hidden, rows, act):
     print(f"[case] norm fp8 hidden={hidden} rows={rows} act={act}", flush=True)
