@@ -366,6 +366,96 @@ def bench_norm_fp8(torch, steps, sets=8):
             "frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
 
 
+def bench_kv_neighbours(torch, steps=100, sets=4):
+    """The cache writers and readers next to the chain, on the config-1/2 chunk (2048
+    tokens, 4 KV heads of 128): the store-only encode of a chunk buffer (padra_KVStore,
+    cap = 2048), its commit into a 131072-row ring (padra_KVCommit), the q8_0 decode of a
+    1024-row local ring's prefix (padra_KvQ8_0DequantizePrefix), the in-place K rotation
+    of the chunk's K rows (padra_RotateRows) and the 1024-row local-ring snapshot
+    (padra_KVCheckpointCapture).  Bytes: what each reads and writes once."""
+    from padra_amd import abi, ops, synth
+    T, F = TOKENS, HKV * D
+    host = synth.chain_inputs(T, HIDDEN, HQ, HKV, D, outliers=True, seed=0)
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).cuda()
+    bad = torch.zeros(1, dtype=torch.int32, device="cuda")
+    k, v = dev(host["k"]), dev(host["v"])
+    row_bytes = {abi.KV_BF16: 2 * F, abi.KV_Q8: F, abi.KV_Q8_0: ops.q8_0_row_bytes(F)}
+
+    def planes(fmt, rows):
+        if fmt == abi.KV_BF16:
+            return (torch.zeros((rows, F), dtype=torch.int16, device="cuda"),
+                    torch.zeros((rows, F), dtype=torch.int16, device="cuda"), None)
+        if fmt == abi.KV_Q8:
+            return (torch.zeros((rows, F), dtype=torch.int8, device="cuda"),
+                    torch.zeros((rows, F), dtype=torch.int8, device="cuda"),
+                    torch.zeros((rows, HKV, 2), dtype=torch.float32, device="cuda"))
+        rb = row_bytes[fmt]
+        return (torch.zeros((rows, rb), dtype=torch.uint8, device="cuda"),
+                torch.zeros((rows, rb), dtype=torch.uint8, device="cuda"), None)
+
+    def entry(name, ms, nbytes):
+        return name, {"us_per_launch": round(ms * 1e3, 3), "bytes_per_launch": nbytes,
+                      "gbs": round(nbytes / (ms * 1e-3) / 1e9, 2),
+                      "frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+
+    out = {}
+    names = {abi.KV_BF16: "bf16", abi.KV_Q8: "q8", abi.KV_Q8_0: "q8_0"}
+    state = torch.tensor([0, 0, T, CAPACITY, 0, 1, 1, 1], dtype=torch.int32, device="cuda")
+    for fmt in (abi.KV_BF16, abi.KV_Q8, abi.KV_Q8_0):
+        scale_bytes = T * HKV * 8 if fmt == abi.KV_Q8 else 0
+        chunks = [planes(fmt, T) for _ in range(sets)]
+        rings = [planes(fmt, CAPACITY) for _ in range(sets)]
+        ms = graph_time(torch, lambda i: ops.KVStore(
+            k, v, ops.positions_base(0),
+            ops.kv_cache(fmt, *chunks[i % sets][:2], T, scales=chunks[i % sets][2]), bad), steps)
+        name, e = entry(f"store_{names[fmt]}", ms, 2 * T * F * 2 + 2 * T * row_bytes[fmt] + scale_bytes)
+        out[name] = e
+        ms = graph_time(torch, lambda i: ops.KVCommit(
+            ops.kv_cache(fmt, *chunks[i % sets][:2], T, scales=chunks[i % sets][2]),
+            ops.kv_cache(fmt, *rings[i % sets][:2], CAPACITY, scales=rings[i % sets][2]),
+            ops.positions_prefill(state, maximum=CAPACITY), T, HKV, bad), steps)
+        name, e = entry(f"commit_{names[fmt]}", ms, 2 * (2 * T * row_bytes[fmt] + scale_bytes))
+        out[name] = e
+        del rings
+    # q8_0 prefix decode of a 1024-row local ring whose chunk starts at base 4096
+    ring_state = torch.tensor([4096, 4096, T, CAPACITY, 4096, 1, 1, 1], dtype=torch.int32,
+                              device="cuda")
+    rk, rv, _ = planes(abi.KV_Q8_0, 1024)
+    rk.view(torch.int16)[:, :16].fill_(0x2400)
+    rv.view(torch.int16)[:, :16].fill_(0x2400)
+    ok = torch.empty((1024, F), dtype=torch.int16, device="cuda")
+    ov = torch.empty_like(ok)
+    ms = graph_time(torch, lambda i: ops.KvQ8_0DequantizePrefix(
+        rk, rv, ok, ov, ops.positions_prefill(ring_state, maximum=CAPACITY), T, bad), steps)
+    name, e = entry("q8_0_dequantize_prefix_1024", ms,
+                    2 * 1024 * row_bytes[abi.KV_Q8_0] + 2 * 1024 * F * 2)
+    out[name] = e
+    kr = [dev(host["k"]) for _ in range(sets)]
+    ms = graph_time(torch, lambda i: ops.RotateRows(kr[i % sets], bad), steps)
+    name, e = entry("rotate_rows_k", ms, 2 * T * F * 2)
+    out[name] = e
+    # snapshot of a 1024-row BF16 local ring before the chunk at base 700, anchor 1250
+    snap_state = torch.tensor([700, 700, 600, CAPACITY, 700, 1, 1, 1], dtype=torch.int32,
+                              device="cuda")
+    old, cur, sv = planes(abi.KV_BF16, 1024), planes(abi.KV_BF16, 600), planes(abi.KV_BF16, 1024)
+    ms = graph_time(torch, lambda i: ops.KVCheckpointCapture(
+        ops.kv_cache(abi.KV_BF16, old[0], old[1], 1024), ops.kv_cache(abi.KV_BF16, cur[0], cur[1], 600),
+        ops.kv_cache(abi.KV_BF16, sv[0], sv[1], 1024),
+        ops.positions_prefill(snap_state, maximum=CAPACITY), 600, 1250, bad), steps)
+    name, e = entry("checkpoint_capture_bf16_1024", ms, 2 * 2 * 1024 * F * 2)
+    out[name] = e
+    torch.cuda.synchronize()
+    if bad.item():
+        raise SystemExit("device error flag set in the cache neighbour benchmarks")
+    for name, e in out.items():
+        gbs, cms = stream_copy_ceiling(torch, e["bytes_per_launch"], steps=steps)
+        e["copy_us"] = round(cms * 1e3, 3)
+        e["frac_of_copy"] = round(e["gbs"] / gbs, 4)
+    return {"workload": "cache neighbours of the 2048-token chunk: store-only encode, commit "
+                        "into a 131072-row ring, q8_0 prefix decode, K rotation, local-ring "
+                        "snapshot", **out}
+
+
 def bench_combine_norm(torch, steps, sets=8):
     """The step after the expert down projection over the config-1 chunk: the ordered BF16
     combine of 8 expert rows into the residual, the RMSNorm and its FP8 encoding; 2048 rows
@@ -638,7 +728,8 @@ def main():
                            "combine_norm": bench_combine_norm(torch, 100),
                            "attention": bench_attention(torch, 10),
                            "attention_q8_0": bench_attention(torch, 10, fmt="q8_0"),
-                           "attention_q8": bench_attention(torch, 10, fmt="q8")}
+                           "attention_q8": bench_attention(torch, 10, fmt="q8"),
+                           "kv_neighbours": bench_kv_neighbours(torch)}
         # The streaming copy of each memory-bound kernel's own byte count, timed the same
         # way: how far a launch of that size is from the copy, apart from the HBM peak.
         for key in ("config3", "norm_fp8", "combine_norm", "config1_f32_activations"):

@@ -6,7 +6,7 @@
 #include <algorithm>
 #include <type_traits>
 
-#include "qk_heads.h"
+#include "qk_quad.h"
 
 using namespace padra;
 
@@ -56,54 +56,157 @@ int check_positions(const padra_Positions *pos, int tokens) {
 
 // ---- store / encode of K and V rows ----------------------------------------------------
 //
-// A wave covers 16 (token, KV head) pairs, two lanes per head vector (the lane-pair
-// layout of the quantizers): lanes 0-31 the K vectors, lanes 32-63 the V vectors of the
-// same pairs, so the encoder sees both halves of a head (lane ^ 32).  BF16 rows are a
-// plain copy.
-template <class T, int FMT>
-__global__ __launch_bounds__(64) void k_kv_store(QKArgs<T> a) {
+// A wave covers 8 (token, KV head) pairs, four lanes per head vector (lane g of a quad:
+// features 32g .. 32g+31, one q8_0 block): lanes 0-31 hold the K vectors, lanes 32-63 the
+// V vectors of the same pairs, so that the pair's K and V quads (lane ^ 32) can decide
+// together what is written, as the reference's one warp per (token, head) does.  Both
+// halves run one instruction stream: the q8_0 rotation's K-only stage (feature bit 6) takes
+// its partner through a DPP move that is enabled in the K rows of the wave only (V lanes
+// read 0), with the per-lane sign and scale making it the identity plus the 1/8 scale for
+// V.  BF16 rows are a plain copy.
+// `write` (equal in the K and V quads of a pair): false for a pair that writes nothing,
+// whose lanes still take part in the exchanges (with zeros in x).
+template <int FMT, class A>
+__device__ __forceinline__ void encode_quad_rt(const A &a, float (&x)[32], long long slot,
+                                               int h, int g, bool isv, bool write) {
   constexpr int D = 128;
-  const int lane = threadIdx.x & 63, half = lane & 1;
-  const unsigned nk = (unsigned)a.tokens * (unsigned)a.hkv;
-  const unsigned idx = blockIdx.x * 16u + (unsigned)((lane >> 1) & 15);
-  if (idx >= nk)
-    return; // both halves of the pair
-  const bool isv = lane >= 32;
-  const int t = (int)(idx / (unsigned)a.hkv), h = (int)(idx % (unsigned)a.hkv);
-  const T *src = (isv ? a.v : a.k) + (size_t)idx * D;
-  const PosState ps = fetch_state(a.pos, t);
-  Act32<T> xa, xb;
-  xa.load(src + 32 * half);
-  xb.load(src + 64 + 32 * half);
-  bool ok;
-  const int pos = resolve_position(a.pos, ps, t, a.cap, a.first, FMT > PADRA_KV_BF16, ok);
-  if (!ok || pos < 0) {
-    if (half == 0)
+  const int features = a.hkv * D;
+  bool invalid = false;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) {
+    invalid |= !isfinite(x[i]);
+    if constexpr (FMT == PADRA_KV_Q8) // q8 also rejects values that are not BF16-exact
+      invalid |= (__float_as_uint(x[i]) & 0xffffu) != 0;
+  }
+  // an invalid K or V vector: neither is written (every lane runs the exchanges)
+  uint32_t bad_any = invalid ? 1u : 0u;
+  bad_any |= quad_xor1(bad_any);
+  bad_any |= quad_xor2(bad_any);
+  bad_any |= (uint32_t)__shfl_xor((int)bad_any, 32, 64);
+  if (bad_any) {
+    if (write && g == 0 && !isv)
       raise_bad(a.bad);
     return;
   }
-  if (t < a.first)
-    return;
-  const long long seq = a.pos.mode == PADRA_POS_DECODE ? t : 0;
-  const long long slot = seq * a.seq_stride + pos % a.cap;
-  if constexpr (FMT == PADRA_KV_BF16) {
-    uint16_t *dst = static_cast<uint16_t *>(isv ? a.vc : a.kc) + slot * (a.hkv * D) + h * D;
-    uint32_t pa[16], pb[16];
+  if constexpr (FMT == PADRA_KV_Q8) {
+    // kv_q8::Encode (kv_q8.cuh:56-73): scale = amax/127 (1 for an all-zero head), codes
+    // RNE(x / scale) clamped to +-127; the (k, v) scale pair as one 8-byte store.
+    float m = 0.f;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      pa[i] = pack2(xa.get(2 * i), xa.get(2 * i + 1));
-      pb[i] = pack2(xb.get(2 * i), xb.get(2 * i + 1));
+    for (int i = 0; i < 32; ++i)
+      m = fmaxf(m, fabsf(x[i]));
+    m = fmaxf(m, fquad_xor1(m));
+    m = fmaxf(m, fquad_xor2(m));
+    const float scale = m == 0.f ? 1.f : m / 127.f, inverse = 1.f / scale;
+    const bool fast = q8_fast_ok(scale); // quad-uniform
+    uint32_t w[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      auto code = [&](float v) { return fast ? q8_code_fast(v, scale, inverse) : q8_code(v, scale); };
+      w[i] = pack_codes4(code(x[4 * i]), code(x[4 * i + 1]), code(x[4 * i + 2]),
+                         code(x[4 * i + 3]));
     }
-    store32_bf16(dst + 32 * half, pa);
-    store32_bf16(dst + 64 + 32 * half, pb);
+    const float vscale = __shfl_xor(scale, 32, 64);
+    if (!write)
+      return;
+    store_codes32(static_cast<int8_t *>(isv ? a.vc : a.kc) + slot * features + h * D + 32 * g, w);
+    if (g == 0 && !isv)
+      reinterpret_cast<float2 *>(a.scales)[slot * a.hkv + h] = make_float2(scale, vscale);
   } else {
-    float fa[32], fb[32];
+    if constexpr (FMT == PADRA_KV_Q8_0) {
+      // q8_native::Rotate (kv_q8_native.cuh:22-45): feature bits 0-4 in the lane, bit 5
+      // across lanes g ^ 1, bit 6 (K only) across lanes g ^ 2, then the scale.
+      hadamard32(x);
+      hadamard_quad<1>(x, g);
+      const float sgn = isv || !(g & 2) ? 1.f : -1.f;
+      const float sc = isv ? .125f : .08838834764831845f;
 #pragma unroll
-    for (int i = 0; i < 32; ++i) {
-      fa[i] = xa.get(i);
-      fb[i] = xb.get(i);
+      for (int f = 0; f < 32; ++f) {
+        // lane g ^ 2's value in the K rows (rows 0 and 1 of the wave), 0 in the V rows
+        const float other = __int_as_float(__builtin_amdgcn_update_dpp(
+            0, __float_as_int(x[f]), 0x4e /* quad_perm [2,3,0,1] */, 0x3, 0xf, false));
+        x[f] = __builtin_fmaf(sgn, x[f], other) * sc;
+      }
     }
-    encode_head_q<FMT>(a, fa, fb, slot, h, half, isv);
+    // Block g (kv_q8_native.cuh:84-99): d = half(amax/127), codes roundf(x * (1/d_fp32)).
+    float am = 0.f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i)
+      am = fmaxf(am, fabsf(x[i]));
+    const float ad = am / 127.f;
+    const __half dh = __float2half(ad);
+    const bool fail = !isfinite(am) || !isfinite(__half2float(dh));
+    // A failing block stops the reference at that block, in K and V together.
+    uint32_t stop = fail ? (uint32_t)g : 4u;
+    stop = min(stop, quad_xor1(stop));
+    stop = min(stop, quad_xor2(stop));
+    stop = min(stop, (uint32_t)__shfl_xor((int)stop, 32, 64));
+    if (!write)
+      return;
+    if (stop < 4u && g == 0 && !isv)
+      raise_bad(a.bad);
+    if ((uint32_t)g >= stop)
+      return;
+    const float inverse = ad == 0.f ? 0.f : 1.f / ad;
+    uint32_t w[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      w[i] = pack_codes4(q8_0_code(x[4 * i], inverse), q8_0_code(x[4 * i + 1], inverse),
+                         q8_0_code(x[4 * i + 2], inverse), q8_0_code(x[4 * i + 3], inverse));
+    const int row_bytes = ((2 * (features / 32) + features) + 15) / 16 * 16;
+    uint8_t *row = static_cast<uint8_t *>(isv ? a.vc : a.kc) + slot * row_bytes;
+    reinterpret_cast<uint16_t *>(row)[h * 4 + g] = __half_as_ushort(dh);
+    store_codes32(reinterpret_cast<int8_t *>(row + 2 * (features / 32) + h * D + 32 * g), w);
+  }
+}
+
+template <class T, int FMT>
+__global__ __launch_bounds__(64) void k_kv_store(QKArgs<T> a) {
+  constexpr int D = 128;
+  const int lane = threadIdx.x & 63, g = lane & 3;
+  const bool isv = lane >= 32;
+  const unsigned nk = (unsigned)a.tokens * (unsigned)a.hkv;
+  const unsigned idx = blockIdx.x * 8u + (unsigned)((lane >> 2) & 7);
+  if (blockIdx.x * 8u >= nk)
+    return; // wave-uniform
+  // Pairs past the end run on the last pair's data (the exchanges need every lane) and
+  // write nothing.
+  const bool live = idx < nk; // quad-uniform, and equal in the K and V quads of a pair
+  const unsigned ci = live ? idx : nk - 1u;
+  const int t = (int)(ci / (unsigned)a.hkv), h = (int)(ci % (unsigned)a.hkv);
+  const PosState ps = fetch_state(a.pos, t);
+  Act32<T> xv;
+  xv.load((isv ? a.v : a.k) + (size_t)ci * D + 32 * g);
+  bool ok;
+  const int pos = resolve_position(a.pos, ps, t, a.cap, a.first, FMT > PADRA_KV_BF16, ok);
+  const bool write = live && ok && pos >= 0 && t >= a.first; // pair-uniform
+  if (live && !(ok && pos >= 0) && g == 0 && !isv)
+    raise_bad(a.bad);
+  const long long seq = a.pos.mode == PADRA_POS_DECODE ? t : 0;
+  const long long slot = seq * a.seq_stride + (write ? pos % a.cap : 0);
+  if constexpr (FMT == PADRA_KV_BF16) {
+    if (!write)
+      return;
+    uint32_t w[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      w[i] = pack2(xv.get(2 * i), xv.get(2 * i + 1));
+    store32_bf16(static_cast<uint16_t *>(isv ? a.vc : a.kc) + slot * (a.hkv * D) + h * D + 32 * g,
+                 w);
+  } else {
+    float x[32];
+#pragma unroll
+    for (int i = 0; i < 32; ++i)
+      x[i] = xv.get(i);
+    // Quads that write nothing still take part in the exchanges with zeros.
+    if (!write) {
+#pragma unroll
+      for (int i = 0; i < 32; ++i)
+        x[i] = 0.f;
+    }
+    if (__ballot(write) == 0)
+      return; // wave-uniform
+    encode_quad_rt<FMT>(a, x, slot, h, g, isv, write);
   }
 }
 
@@ -339,7 +442,7 @@ extern "C" int padra_KVStore(void *stream, const void *k, const void *v,
       (pos->mode != PADRA_POS_DECODE && tokens - kv->first > kv->cap))
     return PADRA_INVALID_ARGUMENT;
   const hipStream_t s = static_cast<hipStream_t>(stream);
-  const long long grid = ((long long)tokens * kv_heads + 15) / 16;
+  const long long grid = ((long long)tokens * kv_heads + 7) / 8;
   auto launch = [&](auto tag) -> int {
     using T = decltype(tag);
     QKArgs<T> a{};
