@@ -305,54 +305,48 @@ __global__ __launch_bounds__(256) void k_q8_0_dequant(const uint8_t *rk, const u
 //
 // q8_native::RotateRows (kv_q8_native.cuh:391-412): each 128-wide row rotated with the K
 // transform (VALUE false) or the two 64-point V transforms (VALUE true), output B(x).
+// Four lanes per row (lane g: features 32g .. 32g+31), 16 rows per wave.
 template <class T, bool VALUE>
 __global__ __launch_bounds__(64) void k_rotate_rows(T *data, long long rows, int *bad) {
   constexpr int D = 128;
-  const int lane = threadIdx.x & 63, half = lane & 1;
-  const long long r = blockIdx.x * 32ll + (lane >> 1);
-  if (r >= rows)
-    return;
-  T *p = data + r * D;
-  Act32<T> xa, xb;
-  xa.load(p + 32 * half);
-  xb.load(p + 64 + 32 * half);
-  float a[32], b[32];
+  const int lane = threadIdx.x & 63, g = lane & 3;
+  const long long r = blockIdx.x * 16ll + (lane >> 2);
+  if (blockIdx.x * 16ll >= rows)
+    return; // wave-uniform
+  // rows past the end rotate the last row's values (the exchanges need every lane) and
+  // store nothing
+  const bool live = r < rows;
+  T *p = data + (live ? r : rows - 1) * D + 32 * g;
+  Act32<T> xv;
+  xv.load(p);
+  float x[32];
 #pragma unroll
-  for (int i = 0; i < 32; ++i) {
-    a[i] = xa.get(i);
-    b[i] = xb.get(i);
-  }
-  hadamard32(a);
-  hadamard32(b);
-  hadamard_cross(a, half);
-  hadamard_cross(b, half);
+  for (int i = 0; i < 32; ++i)
+    x[i] = xv.get(i);
+  hadamard32(x);        // feature bits 0..4
+  hadamard_quad<1>(x, g); // bit 5
   if constexpr (!VALUE) {
+    hadamard_quad<2>(x, g); // bit 6
 #pragma unroll
-    for (int i = 0; i < 32; ++i) {
-      const float lower = a[i], upper = b[i];
-      a[i] = (lower + upper) * .08838834764831845f;
-      b[i] = (lower - upper) * .08838834764831845f;
-    }
+    for (int i = 0; i < 32; ++i)
+      x[i] *= .08838834764831845f;
   } else {
 #pragma unroll
-    for (int i = 0; i < 32; ++i) {
-      a[i] = a[i] * .125f;
-      b[i] = b[i] * .125f;
-    }
+    for (int i = 0; i < 32; ++i)
+      x[i] *= .125f;
   }
   bool fine = true;
-  uint32_t wa[16], wb[16];
+  uint32_t w[16];
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
-    fine = fine && isfinite(a[2 * i]) && isfinite(a[2 * i + 1]) && isfinite(b[2 * i]) &&
-           isfinite(b[2 * i + 1]);
-    wa[i] = pack2(a[2 * i], a[2 * i + 1]);
-    wb[i] = pack2(b[2 * i], b[2 * i + 1]);
+    fine = fine && isfinite(x[2 * i]) && isfinite(x[2 * i + 1]);
+    w[i] = pack2(x[2 * i], x[2 * i + 1]);
   }
+  if (!live)
+    return;
   if (!fine)
     raise_bad(bad);
-  store32<T>(p + 32 * half, wa);
-  store32<T>(p + 64 + 32 * half, wb);
+  store32<T>(p, w);
 }
 
 template <class F> int with_kv_format(int fmt, F &&f) {
@@ -566,7 +560,7 @@ extern "C" int padra_RotateRows(void *stream, void *data, long long rows, int va
   if (!data || !bad || rows < 1 || !aligned16(data) ||
       (act != PADRA_ACT_BF16 && act != PADRA_ACT_F32))
     return PADRA_INVALID_ARGUMENT;
-  const unsigned grid = (unsigned)((rows + 31) / 32);
+  const unsigned grid = (unsigned)((rows + 15) / 16);
   const hipStream_t s = static_cast<hipStream_t>(stream);
   if (act == PADRA_ACT_BF16) {
     if (value)
