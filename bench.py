@@ -880,6 +880,14 @@ def summarize(outdir: str, command: str) -> None:
 
 
 KERNEL_ROLES = {
+    "k_kv_store<unsigned short, 0>": "store-only BF16 cache rows (KVStore)",
+    "k_kv_store<unsigned short, 1>": "store-only q8 encode (KVStore)",
+    "k_kv_store<unsigned short, 2>": "store-only q8_0 encode, rotated (KVStore)",
+    "k_kv_commit": "encoded chunk rows into the ring (KVCommit)",
+    "k_q8_0_dequant<unsigned short>": "q8_0 rows to BF16 (KvQ8_0DequantizePrefix / Dequantize)",
+    "k_rotate_rows<unsigned short, false>": "K-transform rotation of 128-wide rows (RotateRows)",
+    "k_kv_checkpoint": "1024-row local-ring snapshot (KVCheckpointCapture)",
+    "k_silu_table": "SiLU table build (once)",
     "k_attn_order": "decode attention: windows ranked longest first (dispatch order)",
     "k_chain<128, 16, 0, false, unsigned short>": "config 1 chain, BF16 KV",
     "k_chain<128, 16, 1, false, unsigned short>": "config 2 chain, q8 KV",
