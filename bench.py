@@ -551,10 +551,11 @@ def bench_attention(torch, steps, seqs=64, capacity=CAPACITY, fill_seed=0, fmt="
             "frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
 
 
-def bench_decode(torch, steps, seqs, vocab=131072, capacity=CAPACITY):
+def bench_decode(torch, steps, seqs, vocab=131072, capacity=CAPACITY, fmt="bf16"):
     """Config 4 (seqs=64) and the GPU side of config 0 (seqs=1): embedding gather, then the
-    fused residual-norm (256-thread decode tree) + Q/K norm + RoPE + BF16 KV store at each
-    sequence's own position (DecodeState per sequence, per-sequence caches)."""
+    fused residual-norm (256-thread decode tree) + Q/K norm + RoPE + KV store (BF16, or the
+    q8 / q8_0 formats with fmt) at each sequence's own position (DecodeState per sequence,
+    per-sequence caches)."""
     from padra_amd import abi, ops, synth
     rng = np.random.default_rng(0)
     gen = torch.Generator(device="cuda").manual_seed(0)
@@ -569,15 +570,20 @@ def bench_decode(torch, steps, seqs, vocab=131072, capacity=CAPACITY):
         states[i] = [ids[i], p, capacity, 1 << 20, p, min(int(p), 1024), 0, 0]
     st = torch.from_numpy(states).cuda()
     rope = torch.from_numpy(ops.RopeTable(capacity, D, 1e6).view(torch.int16).numpy()).cuda()
-    kc = torch.empty((seqs * capacity, HKV * D), dtype=torch.int16, device="cuda")
-    vc = torch.empty_like(kc)
+    code = {"bf16": abi.KV_BF16, "q8": abi.KV_Q8, "q8_0": abi.KV_Q8_0}[fmt]
+    width = {"bf16": HKV * D, "q8": HKV * D, "q8_0": ops.q8_0_row_bytes(HKV * D)}[fmt]
+    dtype = torch.int16 if fmt == "bf16" else torch.uint8
+    kc = torch.zeros((seqs * capacity, width), dtype=dtype, device="cuda")
+    vc = torch.zeros_like(kc)
+    sc = torch.zeros((seqs * capacity, HKV, 2), dtype=torch.float32, device="cuda") \
+        if fmt == "q8" else None
     x = torch.empty((seqs, HIDDEN), dtype=torch.int16, device="cuda")
     r, y = dev(host["residual"]), torch.empty_like(x)
     q, k, v = dev(host["q"]), dev(host["k"]), dev(host["v"])
     g, qn, kn = dev(host["gamma"]), dev(host["qn"]), dev(host["kn"])
     bad = torch.zeros(1, dtype=torch.int32, device="cuda")
     pos = ops.positions_decode(st, maximum=capacity, vocab=vocab)
-    kv = ops.kv_cache(abi.KV_BF16, kc, vc, capacity, seq_stride=capacity)
+    kv = ops.kv_cache(code, kc, vc, capacity, scales=sc, seq_stride=capacity)
     tbl = table.view(torch.int16)
 
     def step(i):
@@ -591,9 +597,10 @@ def bench_decode(torch, steps, seqs, vocab=131072, capacity=CAPACITY):
     fused_ms = graph_time(torch, fused_step, steps)
     if bad.item():
         raise SystemExit("device error flag set in the decode benchmark")
-    nbytes = seqs * (2 * 2 * HIDDEN + chain_bytes("bf16"))
+    nbytes = seqs * (2 * 2 * HIDDEN + chain_bytes(fmt))
     return {"workload": f"{'config4' if seqs > 1 else 'config0'}: decode step of {seqs} "
-                        "sequence(s): gather + fused chain (256-thread tree), ragged positions",
+                        f"sequence(s): gather + fused chain (256-thread tree), ragged positions, "
+                        f"{fmt} KV",
             "us_per_step": round(ms * 1e3, 3), "tokens_per_s": round(seqs / (ms * 1e-3), 1),
             "fused_us_per_step": round(fused_ms * 1e3, 3),
             "fused_tokens_per_s": round(seqs / (fused_ms * 1e-3), 1),
@@ -723,6 +730,8 @@ def main():
         line["configs"] = {"config3": bench_swiglu(torch, 50),
                            "config4": bench_decode(torch, 100, 64),
                            "config0_gpu": bench_decode(torch, 200, 1, capacity=8192),
+                           "config4_q8": bench_decode(torch, 100, 64, fmt="q8"),
+                           "config4_q8_0": bench_decode(torch, 100, 64, fmt="q8_0"),
                            "config1_f32_activations": bench_f32_layer(torch, 200),
                            "norm_fp8": bench_norm_fp8(torch, 200),
                            "combine_norm": bench_combine_norm(torch, 100),

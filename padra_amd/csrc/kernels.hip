@@ -469,12 +469,10 @@ extern "C" int padra_QKNormRopeStore(void *stream, void *q, void *k, const void 
     const QKArgs<T> a =
         make_qk<T>(q, k, v, qn, kn, table, table_rows, pos, tokens, q_heads, kv_heads, eps, kv, bad);
     return with_format(kv, [&](auto fmt) -> int {
-      if constexpr (fmt.value <= PADRA_KV_BF16) {
-        if (tokens <= kHeadWaveTokens) {
-          const long long grid = qk_head_waves<fmt.value>(tokens, q_heads, kv_heads);
-          hipLaunchKernelGGL((k_qk_heads<T, fmt.value>), dim3((unsigned)grid), dim3(64), 0, s, a);
-          return launched();
-        }
+      if (tokens <= kHeadWaveTokens) {
+        const long long grid = qk_head_waves<fmt.value>(tokens, q_heads, kv_heads);
+        hipLaunchKernelGGL((k_qk_heads<T, fmt.value>), dim3((unsigned)grid), dim3(64), 0, s, a);
+        return launched();
       }
       const long long grid = qk_wave_count<fmt.value>(tokens, q_heads, kv_heads);
       hipLaunchKernelGGL((k_qk<T, fmt.value>), dim3((unsigned)grid), dim3(64), 0, s, a);
@@ -539,21 +537,19 @@ int chain(hipStream_t s, const uint16_t *gather, int vocab, const int32_t *ids, 
       return with_format(kv, [&](auto fmt) -> int {
         constexpr int VT = vt.value, J = j.value, FMT = fmt.value;
         constexpr bool G = g.value;
-        if constexpr (FMT <= PADRA_KV_BF16) {
-          if (tokens <= kHeadWaveTokens) {
-            const long long heads = qk_head_waves<FMT>(tokens, q_heads, kv_heads);
-            if constexpr (VT == 256) {
-              // One workgroup per norm row, then one per four head vectors.
-              const dim3 grid((unsigned)(tokens + (heads + 3) / 4)), block(256);
-              hipLaunchKernelGGL((k_chain_small<VT, J, FMT, G>), grid, block, 0, s, n, a,
-                                 (long long)tokens, heads);
-            } else {
-              const long long waves = norm_waves + heads;
-              hipLaunchKernelGGL((k_chain_heads<VT, J, FMT, G>), dim3((unsigned)waves),
-                                 dim3(64), 0, s, n, a, norm_waves, waves);
-            }
-            return launched();
+        if (tokens <= kHeadWaveTokens) {
+          const long long heads = qk_head_waves<FMT>(tokens, q_heads, kv_heads);
+          if constexpr (VT == 256) {
+            // One workgroup per norm row, then one per four head vectors.
+            const dim3 grid((unsigned)(tokens + (heads + 3) / 4)), block(256);
+            hipLaunchKernelGGL((k_chain_small<VT, J, FMT, G>), grid, block, 0, s, n, a,
+                               (long long)tokens, heads);
+          } else {
+            const long long waves = norm_waves + heads;
+            hipLaunchKernelGGL((k_chain_heads<VT, J, FMT, G>), dim3((unsigned)waves),
+                               dim3(64), 0, s, n, a, norm_waves, waves);
           }
+          return launched();
         }
         const long long waves = norm_waves + qk_wave_count<FMT>(tokens, q_heads, kv_heads);
         hipLaunchKernelGGL((k_chain<VT, J, FMT, G>), dim3((unsigned)waves), dim3(64), 0, s, n,
