@@ -161,14 +161,26 @@ template <class T, int FMT> __global__ __launch_bounds__(64) void k_qk_heads(QKA
 }
 
 #ifndef PADRA_HEAD_WAVE_TOKENS
-#define PADRA_HEAD_WAVE_TOKENS 128
+#define PADRA_HEAD_WAVE_TOKENS 192
 #endif
-// Launches of at most this many tokens with no cache or a BF16 cache use one wave per Q/K
-// head vector (qk_head.h) and, in the fused chain, a workgroup per norm row (norm_wg.h);
-// larger ones the four-lanes-per-head waves (qk_quad.h) and a wave per row.  Measured on
-// MI355X (prefill chain, BF16 cache): per-head 3.4 / 3.7 / 4.0 / 5.2 us at 16 / 64 / 128 /
-// 256 tokens against 4.4 / 4.5 / 4.8 / 5.0 us.
-constexpr int kHeadWaveTokens = PADRA_HEAD_WAVE_TOKENS;
+#ifndef PADRA_HEAD_WAVE_TOKENS_Q
+#define PADRA_HEAD_WAVE_TOKENS_Q 320
+#endif
+// Launches of at most this many tokens use one wave per Q/K head vector (qk_head.h; with
+// a quantized cache one wave per K head that also encodes the pair) and, in the fused
+// chain, a workgroup (256-thread tree) or a wave (128) per norm row; larger ones the
+// four-lanes-per-head waves (qk_quad.h) and a wave per row.  Measured on MI355X (prefill
+// chain, 128-thread tree), per-head against quad:
+//   BF16 cache: 3.0 / 3.2 / 3.8 / 4.5 / 5.2 / 6.7 us at 16 / 64 / 128 / 192 / 256 / 384
+//   tokens against 4.3 / 4.4 / 4.9 / 5.0 / 5.2 / 5.3 us;
+//   q8: 3.6 / 3.9 / 4.4 / 4.7 / 6.1 / 7.6 us against 6.6 / 6.9 / 7.2 / 7.3 / 7.4 / 7.5 us;
+//   q8_0: 3.6 / 4.3 / 4.9 / 5.2 / 6.6 / 8.3 us against 7.1 / 7.3 / 7.6 / 7.7 / 7.9 / 8.1 us.
+template <int FMT> constexpr int head_wave_tokens() {
+  return FMT > PADRA_KV_BF16 ? PADRA_HEAD_WAVE_TOKENS_Q : PADRA_HEAD_WAVE_TOKENS;
+}
+// The standalone residual-norm with the 256-thread tree takes a workgroup per row up to
+// this many rows.
+constexpr int kNormWgRows = 128;
 
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
@@ -367,7 +379,7 @@ extern "C" int padra_ResidualPostNorm(void *stream, void *x, const void *residua
     a.eps = eps;
     return norm_shape(tree, hidden / tree, [&](auto vt, auto j) -> int {
       if constexpr (std::is_same<T, uint16_t>::value && vt.value == 256) {
-        if (residual && rows <= kHeadWaveTokens) {
+        if (residual && rows <= kNormWgRows) {
           hipLaunchKernelGGL((k_norm_small<vt.value, j.value>), dim3(rows), dim3(256), 0, s, a);
           return launched();
         }
@@ -469,7 +481,7 @@ extern "C" int padra_QKNormRopeStore(void *stream, void *q, void *k, const void 
     const QKArgs<T> a =
         make_qk<T>(q, k, v, qn, kn, table, table_rows, pos, tokens, q_heads, kv_heads, eps, kv, bad);
     return with_format(kv, [&](auto fmt) -> int {
-      if (tokens <= kHeadWaveTokens) {
+      if (tokens <= head_wave_tokens<fmt.value>()) {
         const long long grid = qk_head_waves<fmt.value>(tokens, q_heads, kv_heads);
         hipLaunchKernelGGL((k_qk_heads<T, fmt.value>), dim3((unsigned)grid), dim3(64), 0, s, a);
         return launched();
@@ -537,7 +549,7 @@ int chain(hipStream_t s, const uint16_t *gather, int vocab, const int32_t *ids, 
       return with_format(kv, [&](auto fmt) -> int {
         constexpr int VT = vt.value, J = j.value, FMT = fmt.value;
         constexpr bool G = g.value;
-        if (tokens <= kHeadWaveTokens) {
+        if (tokens <= head_wave_tokens<FMT>()) {
           const long long heads = qk_head_waves<FMT>(tokens, q_heads, kv_heads);
           if constexpr (VT == 256) {
             // One workgroup per norm row, then one per four head vectors.

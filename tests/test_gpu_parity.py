@@ -541,10 +541,12 @@ def test_invalid_prefill_state_writes_nothing(oracle):
 
 @pytest.mark.parametrize("fmt", FORMATS)
 @pytest.mark.parametrize("tree", [128, 256])
-@pytest.mark.parametrize("tokens", [333, 129, 128, 37])
+@pytest.mark.parametrize("tokens", [333, 321, 193, 192, 37])
 def test_fused_chain_matches_oracle(oracle, fmt, tree, tokens):
-    """Both launch shapes of the chain: up to 128 tokens (BF16 cache) a wave per Q/K head
-    and, with the 256-thread tree, a workgroup per norm row; above, four lanes per head."""
+    """Both launch shapes of the chain on each side of their thresholds: up to 192 tokens
+    (BF16 cache) or 320 (quantized caches) a wave per Q/K head, which with a quantized
+    cache also encodes the K/V pair, and with the 256-thread tree a workgroup per norm
+    row; above, four lanes per head."""
     print(f"[case] chain fmt={fmt} tree={tree} tokens={tokens}", flush=True)
     capacity = 4096
     d = synth.chain_inputs(tokens, outliers=True, seed=fmt + tree)
