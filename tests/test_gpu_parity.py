@@ -537,6 +537,31 @@ def test_invalid_prefill_state_writes_nothing(oracle):
         assert np.array_equal(host16(q), d["q"]) and not kc.any().item(), field
 
 
+@pytest.mark.parametrize("fmt", [abi.KV_Q8, abi.KV_Q8_0])
+@pytest.mark.parametrize("tokens", [8, 400])
+def test_quantized_ring_rule_writes_nothing(oracle, fmt, tokens):
+    """A quantized cache binding whose capacity is neither the state's capacity nor the
+    1024-row local ring (kv_q8.cuh:36-38): every token fails, so the flag is raised and no
+    Q, K or cache byte is written, in the per-head launch (8 tokens) and the quad launch
+    (400 tokens) alike."""
+    print(f"[case] quantized ring rule fmt={fmt} tokens={tokens}", flush=True)
+    d = synth.chain_inputs(tokens, seed=19)
+    tb = table_bits(oracle, 4096)
+    q, k = dev(d["q"]), dev(d["k"])
+    kc, vc, sc = _alloc_cache(fmt, 512)
+    state = _prefill_state(0, tokens, 4096)
+    bad = flag()
+    ops.QKNormRopeStore(q, k, dev(d["qn"]), dev(d["kn"]), dev(tb),
+                        ops.positions_prefill(state, maximum=4096), bad, v=dev(d["v"]),
+                        kv=ops.kv_cache(fmt, kc, vc, 512, scales=sc))
+    torch.cuda.synchronize()
+    assert bad.item() == 1
+    assert np.array_equal(host16(q), d["q"]) and np.array_equal(host16(k), d["k"])
+    assert not kc.any().item() and not vc.any().item()
+    if sc is not None:
+        assert not sc.any().item()
+
+
 # ---- fused chain -----------------------------------------------------------------------------
 
 @pytest.mark.parametrize("fmt", FORMATS)
