@@ -95,9 +95,7 @@ __device__ __forceinline__ void attn_rank(const AttnArgs &a, int seq) {
     const int other = attn_window(a, j, n, first) ? n : 0;
     before += other > mine || (other == mine && j < seq);
   }
-#pragma unroll
-  for (int d = 32; d >= 1; d /= 2)
-    before += __shfl_xor(before, d, 64);
+  before = xor_reduce<32>(before, [](int x, int y) { return x + y; });
   if (threadIdx.x == 0)
     a.order[before] = seq;
 }
@@ -107,17 +105,26 @@ __device__ __forceinline__ int attn_seq(const AttnArgs &a) {
 
 __global__ __launch_bounds__(64) void k_attn_order(AttnArgs a) { attn_rank(a, blockIdx.x); }
 
+// Hadamard stages on lane bits 0..5, bit 0 first, of two values per lane.
+__device__ __forceinline__ void hadamard64_pair(float &x0, float &x1, int lane) {
+  x0 = hadamard_lane<1>(x0, lane);
+  x1 = hadamard_lane<1>(x1, lane);
+  x0 = hadamard_lane<2>(x0, lane);
+  x1 = hadamard_lane<2>(x1, lane);
+  x0 = hadamard_lane<4>(x0, lane);
+  x1 = hadamard_lane<4>(x1, lane);
+  x0 = hadamard_lane<8>(x0, lane);
+  x1 = hadamard_lane<8>(x1, lane);
+  x0 = hadamard_lane<16>(x0, lane);
+  x1 = hadamard_lane<16>(x1, lane);
+  x0 = hadamard_lane<32>(x0, lane);
+  x1 = hadamard_lane<32>(x1, lane);
+}
 __device__ __forceinline__ float xor_max32(float v) {
-#pragma unroll
-  for (int d = 16; d >= 1; d /= 2)
-    v = fmaxf(v, __shfl_xor(v, d, 64));
-  return v;
+  return xor_reduce<16>(v, [](float x, float y) { return fmaxf(x, y); });
 }
 __device__ __forceinline__ float xor_sum32(float v) {
-#pragma unroll
-  for (int d = 16; d >= 1; d /= 2)
-    v = v + __shfl_xor(v, d, 64);
-  return v;
+  return xor_reduce<16>(v, [](float x, float y) { return x + y; });
 }
 
 template <class T> __device__ __forceinline__ float act_value(const void *p, size_t i) {
@@ -435,8 +442,8 @@ __global__ __launch_bounds__(64) void k_attn_mx(AttnArgs a) {
         sv[4 * h + i] = v;
         tmax = fmaxf(tmax, v);
       }
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+    tmax = fmaxf(tmax, lane_xor<16>(tmax));
+    tmax = fmaxf(tmax, lane_xor<32>(tmax));
     const float next = fmaxf(maximum, tmax);
     const float alpha = isfinite(maximum) ? __expf(maximum - next) : 0.f;
     float p[8], total = 0.f;
@@ -445,8 +452,8 @@ __global__ __launch_bounds__(64) void k_attn_mx(AttnArgs a) {
       p[k] = isfinite(sv[k]) ? __expf(sv[k] - next) : 0.f;
       total += p[k];
     }
-    total += __shfl_xor(total, 16, 64);
-    total += __shfl_xor(total, 32, 64);
+    total += lane_xor<16>(total);
+    total += lane_xor<32>(total);
     den = __builtin_fmaf(den, alpha, total);
     maximum = next;
     const uint4 pa = make_uint4(pack2(p[0], p[1]), pack2(p[2], p[3]), pack2(p[4], p[5]),
@@ -588,9 +595,7 @@ __global__ __launch_bounds__(256) void k_attn_merge_fp8(AttnArgs a, uint8_t *pac
       *reinterpret_cast<float2 *>(static_cast<float *>(a.out) + o) =
           make_float2(lo16(word), hi16(word));
   }
-#pragma unroll
-  for (int d = 32; d >= 1; d /= 2)
-    amax = fmaxf(amax, __shfl_xor(amax, d, 64));
+  amax = xor_reduce<32>(amax, [](float x, float y) { return fmaxf(x, y); });
   if (lane == 0)
     maxima[wave] = amax;
   const bool row_fine = !__syncthreads_or(!fine);
@@ -644,20 +649,12 @@ template <class T> __global__ __launch_bounds__(64) void k_q8_0_query(AttnArgs a
     return;
   }
   // features lane and lane + 64: stages on bits 0..5 across lanes, bit 6 in the lane
-#pragma unroll
-  for (int bit = 1; bit < 64; bit *= 2) {
-    const float o0 = __shfl_xor(x0, bit, 64), o1 = __shfl_xor(x1, bit, 64);
-    x0 = (lane & bit) ? o0 - x0 : x0 + o0;
-    x1 = (lane & bit) ? o1 - x1 : x1 + o1;
-  }
+  hadamard64_pair(x0, x1, lane);
   const float y0 = (x0 + x1) * .08838834764831845f, y1 = (x0 - x1) * .08838834764831845f;
   // blocks lane / 32 (feature lane) and 2 + lane / 32 (feature lane + 64)
   float m0 = fabsf(y0), m1 = fabsf(y1);
-#pragma unroll
-  for (int d = 16; d >= 1; d /= 2) {
-    m0 = fmaxf(m0, __shfl_xor(m0, d, 64));
-    m1 = fmaxf(m1, __shfl_xor(m1, d, 64));
-  }
+  m0 = xor_max32(m0);
+  m1 = xor_max32(m1);
   const float d0 = m0 / 127.f, d1 = m1 / 127.f;
   if (__ballot(!isfinite(d0) || !isfinite(d1)) != 0) {
     if (lane == 0)
@@ -1066,14 +1063,10 @@ template <class T> __global__ __launch_bounds__(64) void k_q8_0_mx_merge(AttnArg
   const size_t base = (size_t)seq * a.splits;
   const float v = l32 < active ? a.lse[(base + l32) * a.hq + head] : -INFINITY;
   float mxv = v;
-#pragma unroll
-  for (int d = 16; d >= 1; d /= 2)
-    mxv = fmaxf(mxv, __shfl_xor(mxv, d, 32));
+  mxv = xor_max32(mxv);
   const float p = isfinite(v) ? expf(v - mxv) : 0.f;
   float den = p;
-#pragma unroll
-  for (int d = 16; d >= 1; d /= 2)
-    den = den + __shfl_xor(den, d, 32);
+  den = xor_sum32(den);
   const float weight = p / den;
   float x0 = 0.f, x1 = 0.f;
   for (int sp = 0; sp < active; ++sp) {
@@ -1083,12 +1076,7 @@ template <class T> __global__ __launch_bounds__(64) void k_q8_0_mx_merge(AttnArg
     x1 = __builtin_fmaf(w, src[64 + lane], x1);
   }
   // back from the V rotation: two 64-point transforms (features lane and lane + 64)
-#pragma unroll
-  for (int bit = 1; bit < 64; bit *= 2) {
-    const float o0 = __shfl_xor(x0, bit, 64), o1 = __shfl_xor(x1, bit, 64);
-    x0 = (lane & bit) ? o0 - x0 : x0 + o0;
-    x1 = (lane & bit) ? o1 - x1 : x1 + o1;
-  }
+  hadamard64_pair(x0, x1, lane);
   x0 *= .125f;
   x1 *= .125f;
   const uint32_t word = pack2(x0, x1); // lo: feature lane, hi: feature lane + 64

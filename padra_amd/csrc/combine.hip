@@ -165,9 +165,7 @@ __global__ __launch_bounds__(64) void k_quantize_fp8(const T *x, uint8_t *packed
       amax = fmaxf(amax, fabsf(v[i]));
     }
   }
-#pragma unroll
-  for (int d = 32; d >= 1; d /= 2)
-    amax = fmaxf(amax, __shfl_xor(amax, d, 64));
+  amax = xor_reduce<32>(amax, [](float x, float y) { return fmaxf(x, y); });
   const bool row_fine = __ballot(!fine) == 0, row_bf16 = __ballot(!exact) == 0;
   if (!row_fine && lane == 0)
     raise_bad(bad);

@@ -64,8 +64,61 @@ __device__ __forceinline__ void fold(float s2, float e2, float &s, float &e) {
   s = next;
 }
 
-__device__ __forceinline__ float shfl_down(float v, int d) { return __shfl_down(v, d, 64); }
-__device__ __forceinline__ float shfl_xor(float v, int m) { return __shfl_xor(v, m, 64); }
+// Value of lane (lane ^ M) for M a power of two below 64, through VALU exchanges instead
+// of an LDS round trip (ds_bpermute): DPP quad permutes for 1 and 2; for 4 the half-row
+// mirror (lane i of 8 reads 7 - i) then the quad reversal (i reads i ^ 3),
+// 7 - (i ^ 3) = i ^ 4; for 8 a row rotation by 8.  For 16, v_permlane16_swap of the value
+// with itself swaps rows 1 and 3 of the first operand with rows 0 and 2 of the second, so
+// the first result holds row r - 1 in the odd rows and the second row r + 1 in the even
+// ones; for 32, v_permlane32_swap does the same with the 32-lane halves.  The values are
+// those of __shfl_xor(v, M): only the route differs.
+template <int M> __device__ __forceinline__ uint32_t lane_xor_u(uint32_t v) {
+  static_assert(M >= 1 && M <= 32 && (M & (M - 1)) == 0, "lane xor of a power of two below 64");
+  const int i = (int)v;
+  if constexpr (M == 1) {
+    return (uint32_t)__builtin_amdgcn_mov_dpp(i, 0xb1 /* quad_perm [1,0,3,2] */, 0xf, 0xf, true);
+  } else if constexpr (M == 2) {
+    return (uint32_t)__builtin_amdgcn_mov_dpp(i, 0x4e /* quad_perm [2,3,0,1] */, 0xf, 0xf, true);
+  } else if constexpr (M == 4) {
+    return (uint32_t)__builtin_amdgcn_mov_dpp(
+        __builtin_amdgcn_mov_dpp(i, 0x141 /* row_half_mirror */, 0xf, 0xf, true),
+        0x1b /* quad_perm [3,2,1,0] */, 0xf, 0xf, true);
+  } else if constexpr (M == 8) {
+    return (uint32_t)__builtin_amdgcn_mov_dpp(i, 0x128 /* row_ror:8 */, 0xf, 0xf, true);
+  } else if constexpr (M == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(i, i, false, false);
+    return (uint32_t)((threadIdx.x & 16) ? r[0] : r[1]);
+  } else {
+    const auto r = __builtin_amdgcn_permlane32_swap(i, i, false, false);
+    return (uint32_t)((threadIdx.x & 32) ? r[0] : r[1]);
+  }
+}
+template <int M> __device__ __forceinline__ float lane_xor(float v) {
+  return __uint_as_float(lane_xor_u<M>(__float_as_uint(v)));
+}
+template <int M> __device__ __forceinline__ int lane_xor(int v) {
+  return (int)lane_xor_u<M>((uint32_t)v);
+}
+template <int M> __device__ __forceinline__ uint32_t lane_xor(uint32_t v) {
+  return lane_xor_u<M>(v);
+}
+// Lane 0's value, as a wave-uniform scalar.
+__device__ __forceinline__ float lane0(float v) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+}
+// The butterfly v = op(v, lane ^ d) for d = TOP, TOP / 2, ..., 1, in that order (the
+// order of a shuffle-xor reduction loop from TOP down).
+template <int TOP, class V, class Op> __device__ __forceinline__ V xor_reduce(V v, Op op) {
+  if constexpr (TOP >= 1)
+    return xor_reduce<TOP / 2>(op(v, lane_xor<TOP>(v)), op);
+  else
+    return v;
+}
+// One Hadamard stage on lane bit log2(M): lower' = lower + upper, upper' = lower - upper.
+template <int M> __device__ __forceinline__ float hadamard_lane(float v, int lane) {
+  const float o = lane_xor<M>(v);
+  return (lane & M) ? o - v : v + o;
+}
 
 // Streaming (non-temporal) global accesses for data each launch touches once: the
 // activations, the KV rows.  On gfx950 these bypass the normal cache allocation policy;

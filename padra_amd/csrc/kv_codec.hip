@@ -82,7 +82,7 @@ __device__ __forceinline__ void encode_quad_rt(const A &a, float (&x)[32], long 
   uint32_t bad_any = invalid ? 1u : 0u;
   bad_any |= quad_xor1(bad_any);
   bad_any |= quad_xor2(bad_any);
-  bad_any |= (uint32_t)__shfl_xor((int)bad_any, 32, 64);
+  bad_any |= lane_xor<32>(bad_any);
   if (bad_any) {
     if (write && g == 0 && !isv)
       raise_bad(a.bad);
@@ -106,7 +106,7 @@ __device__ __forceinline__ void encode_quad_rt(const A &a, float (&x)[32], long 
       w[i] = pack_codes4(code(x[4 * i]), code(x[4 * i + 1]), code(x[4 * i + 2]),
                          code(x[4 * i + 3]));
     }
-    const float vscale = __shfl_xor(scale, 32, 64);
+    const float vscale = lane_xor<32>(scale);
     if (!write)
       return;
     store_codes32(static_cast<int8_t *>(isv ? a.vc : a.kc) + slot * features + h * D + 32 * g, w);
@@ -140,7 +140,7 @@ __device__ __forceinline__ void encode_quad_rt(const A &a, float (&x)[32], long 
     uint32_t stop = fail ? (uint32_t)g : 4u;
     stop = min(stop, quad_xor1(stop));
     stop = min(stop, quad_xor2(stop));
-    stop = min(stop, (uint32_t)__shfl_xor((int)stop, 32, 64));
+    stop = min(stop, lane_xor<32>(stop));
     if (!write)
       return;
     if (stop < 4u && g == 0 && !isv)

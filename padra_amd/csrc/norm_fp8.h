@@ -121,7 +121,7 @@ __device__ __forceinline__ void norm_fp8_finish(const NormFP8Args<T> &a, int row
   warp_tree<K>(s, e);
   float S = s[0], E = e[0];
   partials_tree<VT / 32, 32 / K>(S, E);
-  const float total = __shfl(S + E, 0, 64);
+  const float total = lane0(S + E);
   const float variance = total / (float)H;
   const float inv = 1.f / sqrtf(variance + a.eps);
   if (a.stats && row == 0 && lane == 0) {
@@ -142,9 +142,7 @@ __device__ __forceinline__ void norm_fp8_finish(const NormFP8Args<T> &a, int row
     Lanes<T, K>::template store<WT>(a.y + off + VT * j, &yw[j]);
   }
   uint32_t mag = max((uint32_t)mag2.x, (uint32_t)mag2.y);
-#pragma unroll
-  for (int d = 32; d >= 1; d /= 2)
-    mag = max(mag, (uint32_t)__shfl_xor((int)mag, d, 64));
+  mag = xor_reduce<32>(mag, [](uint32_t x, uint32_t y) { return max(x, y); });
   // Every y finite <=> the largest magnitude is below the BF16 infinity (wave-uniform).
   const bool row_fine = mag < 0x7f80u;
   if (!row_fine && lane == 0)
@@ -159,9 +157,7 @@ __device__ __forceinline__ void norm_fp8_finish(const NormFP8Args<T> &a, int row
         mag = max(mag, lo > 0x7f80u ? 0u : lo);
         mag = max(mag, hi > 0x7f80u ? 0u : hi);
       }
-#pragma unroll
-      for (int d = 32; d >= 1; d /= 2)
-        mag = max(mag, (uint32_t)__shfl_xor((int)mag, d, 64));
+      mag = xor_reduce<32>(mag, [](uint32_t x, uint32_t y) { return max(x, y); });
     }
     const float amax = __uint_as_float(mag << 16);
     const float scale = amax == 0.f ? 1.f : amax / 448.f;

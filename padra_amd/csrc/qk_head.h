@@ -21,27 +21,12 @@
 
 namespace padra {
 
-// Value of lane (lane ^ 16): v_permlane16_swap of the value with itself swaps rows 1 and
-// 3 of the first operand with rows 0 and 2 of the second, so the first result holds row
-// r - 1 in the odd rows, the second row r + 1 in the even ones.
-__device__ __forceinline__ float lane_xor16(float v) {
-  const int i = __float_as_int(v);
-  const auto r = __builtin_amdgcn_permlane16_swap(i, i, false, false);
-  return __int_as_float((threadIdx.x & 16) ? (int)r[0] : (int)r[1]);
-}
-// Value of lane (lane ^ 32), through v_permlane32_swap (the 32-lane halves).
-__device__ __forceinline__ float lane_xor32(float v) {
-  const int i = __float_as_int(v);
-  const auto r = __builtin_amdgcn_permlane32_swap(i, i, false, false);
-  return __int_as_float((threadIdx.x & 32) ? (int)r[0] : (int)r[1]);
-}
-
 // One 32-thread warp tree on the partial (s, e) of every lane: after it, lane 32h of each
 // half holds its warp's (sum, error).  Lanes whose partner lies outside the warp read
 // values the tree never consumes.
 __device__ __forceinline__ void warp_tree_lanes(float &s, float &e) {
   {
-    const float s2 = lane_xor16(s), e2 = lane_xor16(e);
+    const float s2 = lane_xor<16>(s), e2 = lane_xor<16>(e);
     fold(s2, e2, s, e);
   }
   {
@@ -62,34 +47,6 @@ __device__ __forceinline__ void warp_tree_lanes(float &s, float &e) {
   }
 }
 
-// Value of lane (lane ^ M) for M a power of two below 64, all VALU exchanges: DPP quad
-// permutes for 1 and 2; for 4 the half-row mirror (lane i of 8 reads 7 - i) then the quad
-// reversal (i reads i ^ 3), 7 - (i ^ 3) = i ^ 4; for 8 a row rotation by 8; for 16 and 32
-// the permlane swaps.
-template <int M> __device__ __forceinline__ float lane_xor(float v) {
-  const int i = __float_as_int(v);
-  if constexpr (M == 1)
-    return __int_as_float(__builtin_amdgcn_mov_dpp(i, 0xb1 /* quad_perm [1,0,3,2] */, 0xf, 0xf, true));
-  else if constexpr (M == 2)
-    return __int_as_float(__builtin_amdgcn_mov_dpp(i, 0x4e /* quad_perm [2,3,0,1] */, 0xf, 0xf, true));
-  else if constexpr (M == 4)
-    return __int_as_float(__builtin_amdgcn_mov_dpp(
-        __builtin_amdgcn_mov_dpp(i, 0x141 /* row_half_mirror */, 0xf, 0xf, true),
-        0x1b /* quad_perm [3,2,1,0] */, 0xf, 0xf, true));
-  else if constexpr (M == 8)
-    return __int_as_float(__builtin_amdgcn_mov_dpp(i, 0x128 /* row_ror:8 */, 0xf, 0xf, true));
-  else if constexpr (M == 16)
-    return lane_xor16(v);
-  else
-    return lane_xor32(v);
-}
-
-// One Hadamard stage on feature bit log2(M), the feature's bit being the lane's:
-// lower' = lower + upper, upper' = lower - upper (kv_q8_native.cuh:24-31).
-template <int M> __device__ __forceinline__ float hadamard_lane(float v, int lane) {
-  const float o = lane_xor<M>(v);
-  return (lane & M) ? o - v : v + o;
-}
 // The stages on feature bits 0..5 (bit 0 first) of the N values of a lane.
 template <int N> __device__ __forceinline__ void hadamard64_lanes(float (&x)[N], int lane) {
 #pragma unroll
@@ -113,14 +70,7 @@ template <int N> __device__ __forceinline__ void hadamard64_lanes(float (&x)[N],
 }
 // Maximum over the 32-lane half (S = 16) or over the wave (S = 32).
 template <int S> __device__ __forceinline__ float lanes_max(float m) {
-  m = fmaxf(m, lane_xor<1>(m));
-  m = fmaxf(m, lane_xor<2>(m));
-  m = fmaxf(m, lane_xor<4>(m));
-  m = fmaxf(m, lane_xor<8>(m));
-  m = fmaxf(m, lane_xor<16>(m));
-  if constexpr (S == 32)
-    m = fmaxf(m, lane_xor<32>(m));
-  return m;
+  return xor_reduce<S>(m, [](float x, float y) { return fmaxf(x, y); });
 }
 
 // The quantized codes of one head vector held by a wave, lane l holding features l and
@@ -213,7 +163,7 @@ __device__ __forceinline__ void store_pair_lanes(const A &a, const LaneCodes &k,
     // First failing block (4 = none): block `half` in the first registers, half + 2 in
     // the second.
     const int mine = (k.fail0 || v.fail0) ? half : ((k.fail1 || v.fail1) ? half + 2 : 4);
-    const int stop = min(mine, (int)__float_as_uint(lane_xor32(__uint_as_float((uint32_t)mine))));
+    const int stop = min(mine, lane_xor<32>(mine));
     if (stop < 4 && lane == 0)
       raise_bad(a.bad);
     const int row_bytes = ((2 * (features / 32) + features) + 15) / 16 * 16;

@@ -1,7 +1,6 @@
-// Helpers of the per-head Q/K RMSNorm + NeoX RoPE + KV-cache store: the in-lane warp
-// tree, the Hadamard stages, and the lane-pair K/V encoders of the store-only kernel
-// (padra_KVStore), which holds a head in two lanes.  The Q/K kernels themselves hold a
-// head in four lanes (qk_quad.h).
+// Helpers of the Q/K RMSNorm + NeoX RoPE + KV-cache store kernels (qk_quad.h, qk_head.h)
+// and the store-only kernels (kv_codec.hip): the argument block, the in-lane warp tree,
+// the in-lane Hadamard stages, and packed activation and code stores.
 //
 // Reference: QKNormRopeStoreControlled (qk_rope_store_exact.cuh:4-49), QKNormRope
 // (qknorm_rope.cuh:4-50), QKNormRopePair64 (qknorm_rope_pair64.cuh:3-83).  The reference
@@ -81,150 +80,9 @@ __device__ __forceinline__ void hadamard32(float (&x)[32]) {
         x[f | bit] = lower - upper;
       }
 }
-// Stage on feature bit 5 (features f and f + 32 live in the two lanes of the pair).
-__device__ __forceinline__ void hadamard_cross(float (&x)[32], int half) {
-#pragma unroll
-  for (int f = 0; f < 32; ++f) {
-    const float other = shfl_xor(x[f], 1);
-    x[f] = half ? other - x[f] : x[f] + other;
-  }
-}
-
 __device__ __forceinline__ void store_codes32(int8_t *p, const uint32_t (&w)[8]) {
   st_nt(reinterpret_cast<uint4 *>(p), make_uint4(w[0], w[1], w[2], w[3]));
   st_nt(reinterpret_cast<uint4 *>(p) + 1, make_uint4(w[4], w[5], w[6], w[7]));
-}
-
-// Q8 / Q8_0 encoding of one head vector of the K cache (ISV false: the rotated K row)
-// or the V cache (ISV true), held by the two lanes of a pair: this lane has features
-// 32*half + i in xa and 64 + 32*half + i in xb.  Writes codes and scales to row `slot`.
-// The pair at lane ^ 32 holds the same head's other vector and is active with this one.
-// As in the reference's one warp per (token, head) (kv_q8.cuh:41-73,
-// kv_q8_native.cuh:70-100), an invalid K or V vector (non-finite, or for q8 not
-// BF16-exact) raises the flag and writes neither, and a q8_0 block that fails in K or in
-// V ends the writes of both.
-template <int FMT, class A>
-__device__ __forceinline__ void encode_head_q(const A &a, float (&xa)[32], float (&xb)[32],
-                                              long long slot, int h, int half, bool isv) {
-  constexpr int D = 128;
-  const int features = a.hkv * D;
-  bool invalid = false;
-#pragma unroll
-  for (int i = 0; i < 32; ++i) {
-    invalid |= !isfinite(xa[i]) || !isfinite(xb[i]);
-    if constexpr (FMT == PADRA_KV_Q8) // q8 also rejects values that are not BF16-exact
-      invalid |= (__float_as_uint(xa[i]) & 0xffffu) != 0 || (__float_as_uint(xb[i]) & 0xffffu) != 0;
-  }
-  // Both exchanges run in every lane (a lane that skipped one would leave its value
-  // unreadable to the partner).
-  const int pair_bad = __shfl_xor((int)invalid, 1, 64);
-  invalid = invalid || pair_bad != 0;
-  const int other_bad = __shfl_xor((int)invalid, 32, 64);
-  invalid = invalid || other_bad != 0;
-  if (invalid) {
-    if (half == 0)
-      raise_bad(a.bad);
-    return;
-  }
-  if constexpr (FMT == PADRA_KV_Q8) {
-    // kv_q8::Encode (kv_q8.cuh:56-73): scale = amax/127 (1 for an all-zero head), codes
-    // RNE(x / scale) clamped to +-127.
-    float m = 0.f;
-#pragma unroll
-    for (int i = 0; i < 32; ++i)
-      m = fmaxf(m, fmaxf(fabsf(xa[i]), fabsf(xb[i])));
-    m = fmaxf(m, shfl_xor(m, 1));
-    const float scale = m == 0.f ? 1.f : m / 127.f;
-    int8_t *codes = static_cast<int8_t *>(isv ? a.vc : a.kc) + slot * features + h * D;
-    const float inverse = 1.f / scale;
-    const bool fast = q8_fast_ok(scale); // pair-uniform
-    uint32_t w0[8], w1[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      auto code = [&](float x) { return fast ? q8_code_fast(x, scale, inverse) : q8_code(x, scale); };
-      w0[i] = pack_codes4(code(xa[4 * i]), code(xa[4 * i + 1]), code(xa[4 * i + 2]),
-                          code(xa[4 * i + 3]));
-      w1[i] = pack_codes4(code(xb[4 * i]), code(xb[4 * i + 1]), code(xb[4 * i + 2]),
-                          code(xb[4 * i + 3]));
-    }
-    store_codes32(codes + 32 * half, w0);
-    store_codes32(codes + 64 + 32 * half, w1);
-    if (half == 0)
-      reinterpret_cast<float *>(a.scales)[(slot * a.hkv + h) * 2 + (isv ? 1 : 0)] = scale;
-  } else {
-    if constexpr (FMT == PADRA_KV_Q8_0) {
-      // q8_native::Rotate (kv_q8_native.cuh:22-45): stages on feature bits 0..4 in lane,
-      // bit 5 across the pair, and for K bit 6 between the lane's two groups.
-      hadamard32(xa);
-      hadamard32(xb);
-      hadamard_cross(xa, half);
-      hadamard_cross(xb, half);
-      // K: the stage on feature bit 6 (xa with xb) and the 1/sqrt(128) scale; V: the 1/8
-      // scale.  Lanes of both halves run this loop with per-lane operands: for V,
-      // lower + 0 and lower - 0 leave each value (a zero's sign aside, which no code or
-      // scale sees).
-      const float sc = isv ? .125f : .08838834764831845f;
-#pragma unroll
-      for (int i = 0; i < 32; ++i) {
-        const float lower = xa[i], upper = isv ? 0.f : xb[i];
-        xa[i] = (lower + upper) * sc;
-        xb[i] = (isv ? xb[i] : lower - upper) * sc;
-      }
-    }
-    // Blocks (kv_q8_native.cuh:84-99): this lane holds block `half` (xa) and block
-    // `half + 2` (xb); d = half(amax/127), codes roundf(x * (1/d_fp32)).
-    float am = 0.f, bm = 0.f;
-#pragma unroll
-    for (int i = 0; i < 32; ++i) {
-      am = fmaxf(am, fabsf(xa[i]));
-      bm = fmaxf(bm, fabsf(xb[i]));
-    }
-    const float ad = am / 127.f, bd = bm / 127.f;
-    const __half ah = __float2half(ad), bh = __float2half(bd);
-    // A failing block stops the reference at that block: blocks before the first failing
-    // one are written, later ones are not.
-    const bool fa = !isfinite(am) || !isfinite(__half2float(ah));
-    const bool fb = !isfinite(bm) || !isfinite(__half2float(bh));
-    const int mine = fa ? half : (fb ? half + 2 : 4);
-    int stop = min(mine, __shfl_xor(mine, 1, 64)); // first failing block, 4 = none
-    stop = min(stop, __shfl_xor(stop, 32, 64));      // of K and V together
-    if (stop < 4 && half == 0)
-      raise_bad(a.bad);
-    const int row_bytes = ((2 * (features / 32) + features) + 15) / 16 * 16;
-    uint8_t *row = static_cast<uint8_t *>(isv ? a.vc : a.kc) + slot * row_bytes;
-    int8_t *qs = reinterpret_cast<int8_t *>(row + 2 * (features / 32) + h * D);
-    uint16_t *d = reinterpret_cast<uint16_t *>(row) + h * 4;
-    const float ai = ad == 0.f ? 0.f : 1.f / ad, bi = bd == 0.f ? 0.f : 1.f / bd;
-    uint32_t w0[8], w1[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      w0[i] = pack_codes4(q8_0_code(xa[4 * i], ai), q8_0_code(xa[4 * i + 1], ai),
-                          q8_0_code(xa[4 * i + 2], ai), q8_0_code(xa[4 * i + 3], ai));
-      w1[i] = pack_codes4(q8_0_code(xb[4 * i], bi), q8_0_code(xb[4 * i + 1], bi),
-                          q8_0_code(xb[4 * i + 2], bi), q8_0_code(xb[4 * i + 3], bi));
-    }
-    const uint16_t a16 = __half_as_ushort(ah), b16 = __half_as_ushort(bh);
-    if (stop == 4) {
-      // The head's four block scales go out as one 8-byte store from lane 0 of the pair:
-      // d[0] = block 0 (lane 0, a), d[1] = block 1 (lane 1, a), d[2], d[3] the b blocks.
-      const uint32_t mine_d = (uint32_t)a16 | ((uint32_t)b16 << 16);
-      const uint32_t other = __shfl_xor(mine_d, 1, 64);
-      if (half == 0)
-        *reinterpret_cast<uint2 *>(d) = make_uint2((mine_d & 0xffffu) | (other << 16),
-                                                   (mine_d >> 16) | (other & 0xffff0000u));
-      store_codes32(qs + 32 * half, w0);
-      store_codes32(qs + 64 + 32 * half, w1);
-    } else {
-      if (half < stop) {
-        d[half] = a16;
-        store_codes32(qs + 32 * half, w0);
-      }
-      if (half + 2 < stop) {
-        d[half + 2] = b16;
-        store_codes32(qs + 64 + 32 * half, w1);
-      }
-    }
-  }
 }
 
 // 32 consecutive activations of one lane, kept packed: 4 x 16 B of BF16 or 8 x 16 B of
