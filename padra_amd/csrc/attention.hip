@@ -1020,7 +1020,10 @@ template <int G> __global__ __launch_bounds__(256) void k_q8_0_mx(AttnArgs a) {
         for (int u = 0; u < 2; ++u)
 #pragma unroll
           for (int v = 0; v < 2; ++v) {
-            const float x = (grp >> 1) ? o[4 * u + 2 + v][i] : o[4 * u + v][i];
+            // both values first: a conditional over the two array elements would select
+            // an address and index the accumulators at run time
+            const float xa = o[4 * u + v][i], xb = o[4 * u + 2 + v][i];
+            const float x = (grp >> 1) ? xb : xa;
             cs[2 * u + v][i] = __builtin_fmaf(cs[2 * u + v][i], wa, wb * (x / d));
           }
         cm[i] = m2;
