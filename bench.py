@@ -593,8 +593,18 @@ def bench_decode(torch, steps, seqs, vocab=131072, capacity=CAPACITY, fmt="bf16"
     def fused_step(i):
         ops.EmbedResidualNormQKRopeStore(tbl, None, x, r, y, g, q, k, v, qn, kn, rope, pos, kv,
                                          bad, tree=256)
+    # The chain alone on the reference's own activation form (fp32 buffers holding
+    # BF16-exact values), at the same positions into the same caches.
+    f32 = lambda a: torch.from_numpy(synth.bf16_to_f32(a)).cuda()
+    x32, r32, q32, k32, v32 = (f32(host[n]) for n in ("x", "residual", "q", "k", "v"))
+    y32 = torch.empty_like(x32)
+
+    def f32_step(i):
+        ops.ResidualNormQKRopeStore(x32, r32, y32, g, q32, k32, v32, qn, kn, rope, pos, kv, bad,
+                                    tree=256)
     ms = graph_time(torch, step, steps)
     fused_ms = graph_time(torch, fused_step, steps)
+    f32_ms = graph_time(torch, f32_step, steps)
     if bad.item():
         raise SystemExit("device error flag set in the decode benchmark")
     nbytes = seqs * (2 * 2 * HIDDEN + chain_bytes(fmt))
@@ -604,6 +614,7 @@ def bench_decode(torch, steps, seqs, vocab=131072, capacity=CAPACITY, fmt="bf16"
             "us_per_step": round(ms * 1e3, 3), "tokens_per_s": round(seqs / (ms * 1e-3), 1),
             "fused_us_per_step": round(fused_ms * 1e3, 3),
             "fused_tokens_per_s": round(seqs / (fused_ms * 1e-3), 1),
+            "f32_chain_us_per_step": round(f32_ms * 1e3, 3),
             "bytes_per_step": nbytes, "gbs": round(nbytes / (ms * 1e-3) / 1e9, 2)}
 
 

@@ -139,14 +139,15 @@ __global__ __launch_bounds__(256) void k_chain_small(NormArgs<uint16_t> n, QKArg
 // its 16 elements per lane at H = 2048 measured faster in one wave (16 / 64 / 128 tokens:
 // 3.4 / 3.7 / 4.0 us) than in a workgroup (4.1 / 4.1 / 4.5 us); the 256-thread decode tree
 // is the other way round (64-sequence decode step: 4.5 -> 3.5 us).
-template <int VT, int J, int FMT, bool GATHER = false>
-__global__ __launch_bounds__(64) void k_chain_heads(NormArgs<uint16_t> n, QKArgs<uint16_t> q,
+// T: the activation type; fp32 activations take this kernel with either tree.
+template <int VT, int J, int FMT, bool GATHER = false, class T = uint16_t>
+__global__ __launch_bounds__(64) void k_chain_heads(NormArgs<T> n, QKArgs<T> q,
                                                     long long norm_waves, long long waves) {
   const long long b = blockIdx.x;
   if (b < norm_waves)
-    norm_row_wave<VT, J, uint16_t, true, false, GATHER>(n, (int)b, nullptr);
+    norm_row_wave<VT, J, T, true, false, GATHER>(n, (int)b, nullptr);
   else if (b < waves)
-    qk_head_wave<uint16_t, FMT>(q, (unsigned)(b - norm_waves));
+    qk_head_wave<T, FMT>(q, (unsigned)(b - norm_waves));
 }
 
 // Residual + RMSNorm, BF16 rows, one 256-lane workgroup per row (norm_wg.h).
@@ -175,8 +176,16 @@ template <class T, int FMT> __global__ __launch_bounds__(64) void k_qk_heads(QKA
 //   tokens against 4.3 / 4.4 / 4.9 / 5.0 / 5.2 / 5.3 us;
 //   q8: 3.6 / 3.9 / 4.4 / 4.7 / 6.1 / 7.6 us against 6.6 / 6.9 / 7.2 / 7.3 / 7.4 / 7.5 us;
 //   q8_0: 3.6 / 4.3 / 4.9 / 5.2 / 6.6 / 8.3 us against 7.1 / 7.3 / 7.6 / 7.7 / 7.9 / 8.1 us.
-template <int FMT> constexpr int head_wave_tokens() {
-  return FMT > PADRA_KV_BF16 ? PADRA_HEAD_WAVE_TOKENS_Q : PADRA_HEAD_WAVE_TOKENS;
+// fp32 activations (fused chain, 64 tokens): BF16 cache 4.0 against 5.8 us, q8 4.1 against
+// 8.9, q8_0 4.2 against 8.1; with a BF16 cache per-head stays ahead up to 384 tokens (7.3
+// against 7.6 us), quad from 512 (8.9 against 8.2).
+#ifndef PADRA_HEAD_WAVE_TOKENS_F32
+#define PADRA_HEAD_WAVE_TOKENS_F32 384
+#endif
+template <int FMT, class T = uint16_t> constexpr int head_wave_tokens() {
+  if (FMT > PADRA_KV_BF16)
+    return PADRA_HEAD_WAVE_TOKENS_Q;
+  return std::is_same<T, float>::value ? PADRA_HEAD_WAVE_TOKENS_F32 : PADRA_HEAD_WAVE_TOKENS;
 }
 // The standalone residual-norm with the 256-thread tree takes a workgroup per row up to
 // this many rows.
@@ -481,7 +490,7 @@ extern "C" int padra_QKNormRopeStore(void *stream, void *q, void *k, const void 
     const QKArgs<T> a =
         make_qk<T>(q, k, v, qn, kn, table, table_rows, pos, tokens, q_heads, kv_heads, eps, kv, bad);
     return with_format(kv, [&](auto fmt) -> int {
-      if (tokens <= head_wave_tokens<fmt.value>()) {
+      if (tokens <= head_wave_tokens<fmt.value, T>()) {
         const long long grid = qk_head_waves<fmt.value>(tokens, q_heads, kv_heads);
         hipLaunchKernelGGL((k_qk_heads<T, fmt.value>), dim3((unsigned)grid), dim3(64), 0, s, a);
         return launched();
@@ -576,7 +585,7 @@ int chain(hipStream_t s, const uint16_t *gather, int vocab, const int32_t *ids, 
 
 namespace {
 // The fused chain on fp32 activations (the reference's buffers): norm-row waves, then the
-// four-lanes-per-head Q/K waves, at every token count.
+// Q/K waves, one per head vector up to head_wave_tokens, else four lanes per head.
 int chain_f32(hipStream_t s, void *x, const void *residual, void *normalized,
               const uint16_t *gamma, int hidden, int tree, float *statistics, void *q, void *k,
               const void *v, const uint16_t *qn, const uint16_t *kn, const uint16_t *table,
@@ -605,6 +614,12 @@ int chain_f32(hipStream_t s, void *x, const void *residual, void *normalized,
   const long long norm_waves = tokens;
   return chain_shape(tree, hidden / tree, [&](auto vt, auto j) -> int {
     return with_format(kv, [&](auto fmt) -> int {
+      if (tokens <= head_wave_tokens<fmt.value, float>()) {
+        const long long waves = norm_waves + qk_head_waves<fmt.value>(tokens, q_heads, kv_heads);
+        hipLaunchKernelGGL((k_chain_heads<vt.value, j.value, fmt.value, false, float>),
+                           dim3((unsigned)waves), dim3(64), 0, s, n, a, norm_waves, waves);
+        return launched();
+      }
       const long long waves = norm_waves + qk_wave_count<fmt.value>(tokens, q_heads, kv_heads);
       hipLaunchKernelGGL((k_chain<vt.value, j.value, fmt.value, false, float>),
                          dim3((unsigned)waves), dim3(64), 0, s, n, a, norm_waves, waves);

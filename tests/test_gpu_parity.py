@@ -483,9 +483,21 @@ def test_qk_rope_store_f32_activations(oracle, fmt, tokens, base, cap):
 
 
 @pytest.mark.parametrize("fmt", FORMATS)
-def test_qk_rope_store_decode_batch(oracle, fmt):
-    """Ragged positions, one token per sequence, per-sequence caches (seq_stride rows)."""
-    print(f"[case] decode batch fmt={fmt}", flush=True)
+@pytest.mark.parametrize("act", ["bf16", "f32"])
+def test_qk_rope_store_decode_batch(oracle, fmt, act):
+    """Ragged positions, one token per sequence, per-sequence caches (seq_stride rows), on
+    BF16 activations and on fp32 activations holding BF16-exact values (whose outputs must
+    stay BF16-exact)."""
+    print(f"[case] decode batch fmt={fmt} act={act}", flush=True)
+    if act == "f32":
+        conv = lambda a: torch.from_numpy(synth.bf16_to_f32(a)).cuda()
+
+        def back(t):
+            w = t.cpu().numpy().view(np.uint32)
+            assert not (w & 0xFFFF).any()
+            return (w >> 16).astype(np.uint16)
+    else:
+        conv, back = dev, host16
     seqs, cap, capacity = 16, 256, 256
     rng = np.random.default_rng(fmt)
     positions = rng.integers(0, capacity, seqs).astype(np.int32)
@@ -497,15 +509,15 @@ def test_qk_rope_store_decode_batch(oracle, fmt):
     states[3, 7] = 1  # stopped: this sequence must write nothing and raise the flag
     wq, wk, _ = _qk_oracle(oracle, d, tb, positions)
     kc, vc, sc = _alloc_cache(fmt, seqs * cap)
-    q, k = dev(d["q"]), dev(d["k"])
+    q, k = conv(d["q"]), conv(d["k"])
     bad = flag()
     kv = ops.kv_cache(fmt, kc, vc, cap, scales=sc, seq_stride=cap)
     ops.QKNormRopeStore(q, k, dev(d["qn"]), dev(d["kn"]), dev(tb),
                         ops.positions_decode(torch.from_numpy(states).cuda(), maximum=capacity),
-                        bad, v=dev(d["v"]), kv=kv)
+                        bad, v=conv(d["v"]), kv=kv)
     torch.cuda.synchronize()
     assert bad.item() == 1
-    gq, gk = host16(q).copy(), host16(k).copy()
+    gq, gk = back(q).copy(), back(k).copy()
     assert np.array_equal(gq[3], d["q"][3]) and np.array_equal(gk[3], d["k"][3])
     keep = [s for s in range(seqs) if s != 3]
     assert np.array_equal(gq[keep], wq[keep]) and np.array_equal(gk[keep], wk[keep])
@@ -601,10 +613,12 @@ def test_fused_chain_matches_oracle(oracle, fmt, tree, tokens):
 
 
 @pytest.mark.parametrize("fmt", FORMATS)
-@pytest.mark.parametrize("tree,tokens", [(128, 300), (256, 64)])
+@pytest.mark.parametrize("tree,tokens", [(128, 300), (256, 64), (128, 385), (256, 384)])
 def test_fused_chain_f32_activations(oracle, fmt, tree, tokens):
     """The fused chain on fp32 activations holding BF16-exact values (the reference's
-    buffers): every output equal to the oracle's, as floats."""
+    buffers): every output equal to the oracle's, as floats, on both launch shapes (a wave
+    per head vector up to 384 tokens with a BF16 cache and 320 with a quantized one, four
+    lanes per head above)."""
     print(f"[case] chain f32 fmt={fmt} tree={tree} tokens={tokens}", flush=True)
     capacity = 4096
     d = synth.chain_inputs(tokens, outliers=True, seed=300 + fmt + tree)
