@@ -166,14 +166,11 @@ __device__ __forceinline__ bool q8_scale_fast(float scale) {
 
 // The 16 values code * scale of a code chunk (kv_q8::Decode), with the least code seen
 // (as a float; -128 is the code the reference rejects) and whether the scale passes
-// q8_scale_fast.  Keys past the window decode zero codes with a unit scale, as the
-// reference stages them.  Each code is one v_cvt_f32_i32 with a sign-extended byte select.
-__device__ __forceinline__ void q8_values16(uint4 c, float scale, bool inside, float (&f)[16],
-                                            float &least, bool &slow) {
-  if (!inside) {
-    c = make_uint4(0, 0, 0, 0);
-    scale = 1.f;
-  }
+// q8_scale_fast.  The caller gives keys past the window zero codes and a unit scale, as
+// the reference stages them.  Each code is one v_cvt_f32_i32 with a sign-extended byte
+// select.
+__device__ __forceinline__ void q8_values16(uint4 c, float scale, float (&f)[16], float &least,
+                                            bool &slow) {
   const uint32_t w[4] = {c.x, c.y, c.z, c.w};
   float code[16];
 #pragma unroll
@@ -349,13 +346,29 @@ __global__ __launch_bounds__(64) void k_attn_mx(AttnArgs a) {
     const int left = n - tile * kKeys; // keys of this tile inside the window (may be >= 32)
     // Stage K rows and V key groups as BF16.
     if constexpr (Q8) {
+      if (left < kKeys) { // block-uniform: the window's last tile
+#pragma unroll
+        for (int m = 0; m < CH; ++m) {
+          if (((lane + 64 * m) >> 3) >= left) {
+            kw[m] = make_uint4(0, 0, 0, 0);
+            ksc[m] = 1.f;
+          }
+        }
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          if (vkey(m) >= left) {
+            vw[m] = make_uint4(0, 0, 0, 0);
+            vsc[m] = 1.f;
+          }
+        }
+      }
       float least = 0.f;
       bool slow = false;
 #pragma unroll
       for (int m = 0; m < CH; ++m) {
         const int c = lane + 64 * m, key = c >> 3, part = c & 7;
         float f[16];
-        q8_values16(kw[m], ksc[m], key < left, f, least, slow);
+        q8_values16(kw[m], ksc[m], f, least, slow);
         uint32_t w[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e)
@@ -366,7 +379,7 @@ __global__ __launch_bounds__(64) void k_attn_mx(AttnArgs a) {
       float fv[4][16];
 #pragma unroll
       for (int m = 0; m < 4; ++m)
-        q8_values16(vw[m], vsc[m], vkey(m) < left, fv[m], least, slow);
+        q8_values16(vw[m], vsc[m], fv[m], least, slow);
       fine = fine && least > -128.f;
       if (__ballot(slow) != 0) { // rare: huge or invalid scales
 #pragma unroll
@@ -850,21 +863,27 @@ template <int G> __global__ __launch_bounds__(256) void k_q8_0_mx(AttnArgs a) {
       o[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     for (int it = 0; it < slices; ++it) {
       const int tile = begin + it, o0 = tile * kQ8Tile + 32 * s;
-      // Stage the slice.
+      // Stage the slice.  Keys past the window stage zero codes: only a slice that crosses
+      // the window's end (block-uniform test) zeroes them, with a mask per key.
+      if (o0 + 32 > n) {
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          const uint32_t kkeep = o0 + ((tid + 256 * m) >> 5) < n ? ~0u : 0u;
+          const uint32_t vkeep = o0 + 4 * (tid >> 5) + m < n ? ~0u : 0u;
+          kw[m] = make_uint4(kw[m].x & kkeep, kw[m].y & kkeep, kw[m].z & kkeep, kw[m].w & kkeep);
+          vw[m] = make_uint4(vw[m].x & vkeep, vw[m].y & vkeep, vw[m].z & vkeep, vw[m].w & vkeep);
+        }
+      }
 #pragma unroll
       for (int m = 0; m < 4; ++m) {
         const int c = tid + 256 * m;
-        // keys past the window stage zero codes (a mask, not a branch per key)
-        const uint32_t keep = o0 + (c >> 5) < n ? ~0u : 0u;
-        const uint4 w = make_uint4(kw[m].x & keep, kw[m].y & keep, kw[m].z & keep, kw[m].w & keep);
-        *reinterpret_cast<uint4 *>(&kq_all[(c >> 3) & 3].r[c >> 5][4 * (c & 7)]) = w;
+        *reinterpret_cast<uint4 *>(&kq_all[(c >> 3) & 3].r[c >> 5][4 * (c & 7)]) = kw[m];
       }
       {
         float f[4][16];
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
-          const uint32_t keep = o0 + 4 * (tid >> 5) + m < n ? ~0u : 0u;
-          const uint32_t w[4] = {vw[m].x & keep, vw[m].y & keep, vw[m].z & keep, vw[m].w & keep};
+          const uint32_t w[4] = {vw[m].x, vw[m].y, vw[m].z, vw[m].w};
 #pragma unroll
           for (int i = 0; i < 4; ++i)
 #pragma unroll
