@@ -225,24 +225,29 @@ __device__ __forceinline__ void raise_bad(int *bad) {
     atomicExch(bad, 1);
 }
 
-// The codes below are returned as the clamped int (its low byte is the int8 code).
+// The codes below are returned as a word whose low byte is the int8 code (two's
+// complement); callers use that byte only.
 
 // q8 code (kv_q8.cuh:12-14): RNE of the correctly rounded quotient, clamped to +-127.
 __device__ __forceinline__ uint32_t q8_code(float value, float scale) {
   return (uint32_t)max(-127, min(127, (int)rintf(value / scale)));
 }
 // The same code through the head's cached reciprocal: q = v * inverse, r = q * scale - v
-// (one fused multiply-add), q - r * inverse, then RNE and the clamp; three instructions
-// where the correctly rounded division takes ten.  For every BF16 value v with |v| <= amax,
-// amax a BF16 maximum whose scale = amax / 127 is at least 2^-100 (q8_fast_ok: then r,
-// whose size is about 2^-24 |v|, loses at most 2^-150 to the subnormal range, which moves
-// q - r * inverse by at most 2^-43), its code equals q8_code's: padra_CheckQ8Path compares
-// the two on every such (amax, v) pair on the device.  With smaller scales the two differ
-// (a scale of 2^-125 puts an exact 63.5 quotient at 63.499996).
+// (one fused multiply-add), q - r * inverse; three instructions where the correctly
+// rounded division takes ten.  RNE then takes one addition: with |q| < 2^22, the float sum
+// q + 1.5 * 2^23 lies in [2^23, 2^24), where the spacing is 1, so it is rounded to
+// 1.5 * 2^23 + RNE(q) (1.5 * 2^23 is even, so ties go as RNE(q)'s), whose low byte is
+// RNE(q) mod 256.  Here |v| <= amax and scale = RN(amax / 127), so |q| is within a few
+// ulps of 127 at most and needs no clamp.  For every BF16 value v with |v| <= amax, amax a
+// BF16 maximum whose scale = amax / 127 is at least 2^-100 (q8_fast_ok: then r, whose size
+// is about 2^-24 |v|, loses at most 2^-150 to the subnormal range, which moves
+// q - r * inverse by at most 2^-43), its code byte equals q8_code's: padra_CheckQ8Path
+// compares the two on every such (amax, v) pair on the device.  With smaller scales the
+// two differ (a scale of 2^-125 puts an exact 63.5 quotient at 63.499996).
 __device__ __forceinline__ uint32_t q8_code_fast(float value, float scale, float inverse) {
   const float q = value * inverse;
   const float r = __builtin_fmaf(q, scale, -value);
-  return (uint32_t)max(-127, min(127, (int)rintf(__builtin_fmaf(-r, inverse, q))));
+  return __float_as_uint(__builtin_fmaf(-r, inverse, q) + 12582912.f);
 }
 __device__ __forceinline__ bool q8_fast_ok(float scale) { return scale >= 0x1p-100f; }
 // q8_0 code (kv_q8_native.cuh:46-48): roundf (half away from zero) of v * inverse.

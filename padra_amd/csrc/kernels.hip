@@ -435,7 +435,7 @@ extern "C" int padra_NormFP8(void *stream, const void *x, void *normalized,
 
 // Device self-check of q8_code_fast: for every positive finite BF16 maximum amax whose
 // scale amax / 127 passes q8_fast_ok (scale >= 2^-100), and every BF16 v with
-// |v| <= amax (both signs), the code through the reciprocal equals the code of the correctly rounded quotient
+// |v| <= amax (both signs), the code byte through the reciprocal equals the code of the correctly rounded quotient
 // (2.1e9 pairs).  Mismatches are added to counts[0].
 __global__ __launch_bounds__(256) void k_check_q8(unsigned long long *counts) {
   const uint32_t mb = blockIdx.x + 1; // BF16 bits of the maximum, 0x0001 .. 0x7f7f
@@ -448,7 +448,7 @@ __global__ __launch_bounds__(256) void k_check_q8(unsigned long long *counts) {
 #pragma unroll
     for (int sg = 0; sg < 2; ++sg) {
       const float v = __uint_as_float((vb << 16) | (sg ? 0x80000000u : 0u));
-      bad += q8_code_fast(v, scale, inverse) != q8_code(v, scale);
+      bad += ((q8_code_fast(v, scale, inverse) ^ q8_code(v, scale)) & 0xffu) != 0;
     }
   }
   if (bad)
