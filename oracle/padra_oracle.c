@@ -551,11 +551,20 @@ int po_q8_0_row_bytes(int features) {
 
 /* q8_native::Code (kv_q8_native.cuh:46-48): roundf (half away from zero) of v * (1/ad). */
 static int8_t q8_0_code(float value, float inverse) {
-  int c = (int)roundf(value * inverse);
-  if (c > 127)
+  /* The reference's (int) of the rounded float is CUDA's saturating conversion (NaN to 0,
+   * out-of-range values to the int limits), then the clamp to +-127; C leaves the
+   * conversion of infinities and NaN undefined, so those cases are written out.  An
+   * infinite product comes from a block whose 1/ad overflows (ad subnormal). */
+  const float r = roundf(value * inverse);
+  int c;
+  if (r != r)
+    c = 0;
+  else if (r >= 127.f)
     c = 127;
-  if (c < -127)
+  else if (r <= -127.f)
     c = -127;
+  else
+    c = (int)r;
   return (int8_t)c;
 }
 

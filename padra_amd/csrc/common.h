@@ -259,6 +259,14 @@ __device__ __forceinline__ uint32_t q8_0_code(float value, float inverse) {
   const float v = value * inverse;
   return (uint32_t)max(-127, min(127, (int)(v + __builtin_copysignf(0.49999997f, v))));
 }
+// The same without the clamp, for a value of a block whose inverse = 1 / (amax / 127) is
+// finite: |value| <= amax puts |v| within a few ulps of 127, so the sum stays below 128
+// and the truncation gives at most 127.  (An infinite inverse, amax below about 2^-121,
+// needs the clamp.)
+__device__ __forceinline__ uint32_t q8_0_code_in_range(float value, float inverse) {
+  const float v = value * inverse;
+  return (uint32_t)(int)(v + __builtin_copysignf(0.49999997f, v));
+}
 // Four codes (the low bytes of c0..c3) as one word, c0 in the lowest byte: three byte
 // permutes instead of a mask, a shift and an or per code.
 __device__ __forceinline__ uint32_t pack_codes4(uint32_t c0, uint32_t c1, uint32_t c2,

@@ -149,10 +149,7 @@ __device__ __forceinline__ void encode_quad_rt(const A &a, float (&x)[32], long 
       return;
     const float inverse = ad == 0.f ? 0.f : 1.f / ad;
     uint32_t w[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-      w[i] = pack_codes4(q8_0_code(x[4 * i], inverse), q8_0_code(x[4 * i + 1], inverse),
-                         q8_0_code(x[4 * i + 2], inverse), q8_0_code(x[4 * i + 3], inverse));
+    q8_0_codes32(x, inverse, w);
     const int row_bytes = ((2 * (features / 32) + features) + 15) / 16 * 16;
     uint8_t *row = static_cast<uint8_t *>(isv ? a.vc : a.kc) + slot * row_bytes;
     reinterpret_cast<uint16_t *>(row)[h * 4 + g] = __half_as_ushort(dh);

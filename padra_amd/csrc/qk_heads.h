@@ -80,6 +80,25 @@ __device__ __forceinline__ void hadamard32(float (&x)[32]) {
         x[f | bit] = lower - upper;
       }
 }
+// The q8_0 codes of a lane's 32-value block, packed four to a word: without the clamp
+// when every active lane of the wave has a finite inverse (wave-uniform test).
+__device__ __forceinline__ void q8_0_codes32(const float (&x)[32], float inverse,
+                                             uint32_t (&w)[8]) {
+  if (__ballot(!isfinite(inverse)) == 0) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      w[i] = pack_codes4(q8_0_code_in_range(x[4 * i], inverse),
+                         q8_0_code_in_range(x[4 * i + 1], inverse),
+                         q8_0_code_in_range(x[4 * i + 2], inverse),
+                         q8_0_code_in_range(x[4 * i + 3], inverse));
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      w[i] = pack_codes4(q8_0_code(x[4 * i], inverse), q8_0_code(x[4 * i + 1], inverse),
+                         q8_0_code(x[4 * i + 2], inverse), q8_0_code(x[4 * i + 3], inverse));
+  }
+}
+
 __device__ __forceinline__ void store_codes32(int8_t *p, const uint32_t (&w)[8]) {
   st_nt(reinterpret_cast<uint4 *>(p), make_uint4(w[0], w[1], w[2], w[3]));
   st_nt(reinterpret_cast<uint4 *>(p) + 1, make_uint4(w[4], w[5], w[6], w[7]));

@@ -169,10 +169,7 @@ __device__ __forceinline__ QuadCodes quad_codes(float (&x)[32], int g) {
     r.fail = !isfinite(am) || !isfinite(__half2float(dh));
     r.d = __half_as_ushort(dh);
     const float inverse = ad == 0.f ? 0.f : 1.f / ad;
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-      r.cw[i] = pack_codes4(q8_0_code(x[4 * i], inverse), q8_0_code(x[4 * i + 1], inverse),
-                            q8_0_code(x[4 * i + 2], inverse), q8_0_code(x[4 * i + 3], inverse));
+    q8_0_codes32(x, inverse, r.cw);
   }
   return r;
 }

@@ -361,8 +361,10 @@ def test_store_extreme_value_scales(oracle, fmt):
     v = d["v"].view(np.uint16).reshape(tokens, -1).astype(np.uint32) << 16
     vf = v.view(np.float32).copy()
     # q8_0 scales are fp16 (amax / 127 must stay finite there), q8 scales fp32
+    # q8_0 also takes subnormal V heads (1e-39): their block's 1 / ad overflows to
+    # infinity, the one case whose codes need the clamp
     factors = np.array([1e-36, 3e-33, 1e-30, 1.0, 1e30, 1e36] if fmt == abi.KV_Q8 else
-                       [1e-36, 1e-20, 1e-6, 1.0, 1e3, 1e5], np.float32)
+                       [1e-36, 1e-20, 1e-6, 1.0, 1e3, 1e5, 1e-39, 1.0], np.float32)
     vf *= factors[np.arange(tokens) % len(factors)][:, None]
     d["v"] = synth.bf16_bits(vf).reshape(d["v"].shape)
     tb = table_bits(oracle, capacity)
