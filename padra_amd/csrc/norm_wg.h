@@ -27,6 +27,11 @@ __device__ __forceinline__ void norm_row_wg(const NormArgs<uint16_t> &a, int row
   const size_t off = (size_t)row * H + (act ? t : 0);
   float v[J];
   float s = 0.f, e = 0.f;
+  // The norm weights first: independent of the row, they are in flight during the tree.
+  uint16_t gw[J];
+#pragma unroll
+  for (int j = 0; j < J; ++j)
+    gw[j] = a.gamma[(act ? t : 0) + VT * j];
   if (act) {
     uint16_t rr[J], xx[J];
 #pragma unroll
@@ -86,7 +91,7 @@ __device__ __forceinline__ void norm_row_wg(const NormArgs<uint16_t> &a, int row
   bool fine = isfinite(total);
 #pragma unroll
   for (int j = 0; j < J; ++j) {
-    const float g = __uint_as_float((uint32_t)a.gamma[t + VT * j] << 16);
+    const float g = __uint_as_float((uint32_t)gw[j] << 16);
     const float y = B(v[j] * inv) * g;
     if constexpr (CHECK_Y)
       fine = fine && bf16_finite_after_round(y);

@@ -253,6 +253,9 @@ __device__ __forceinline__ void qk_head_wave_plain(const QKArgs<T> &a, unsigned 
   const PosState ps = fetch_state(a.pos, t);
   const T *src = head_src(a, hv, nq, nk);
   const float x0 = head_load(src + lane), x1 = head_load(src + 64 + lane);
+  // The norm weights before the position check, so that they are in flight with the data.
+  const uint16_t *w = (role == 1 ? a.kn : a.qn);
+  const float w0 = head_load(w + lane), w1 = head_load(w + 64 + lane);
   bool ok = false;
   const int pos = resolve_position(a.pos, ps, t, FMT >= 0 ? a.cap : 0, a.first,
                                    FMT > PADRA_KV_BF16, ok);
@@ -274,8 +277,6 @@ __device__ __forceinline__ void qk_head_wave_plain(const QKArgs<T> &a, unsigned 
     }
     return;
   }
-  const uint16_t *w = (role == 1 ? a.kn : a.qn);
-  const float w0 = head_load(w + lane), w1 = head_load(w + 64 + lane);
   const uint16_t *trow = a.table + (size_t)pos * D;
   const float c = head_load(trow + lane), sn = head_load(trow + 64 + lane);
   float lo, hi;
@@ -306,6 +307,7 @@ __device__ __forceinline__ void qk_pair_wave(const QKArgs<T> &a, unsigned kidx) 
   const T *src = a.k + (size_t)kidx * D, *vsrc = a.v + (size_t)kidx * D;
   const float x0 = head_load(src + lane), x1 = head_load(src + 64 + lane);
   const float v0 = head_load(vsrc + lane), v1 = head_load(vsrc + 64 + lane);
+  const float w0 = head_load(a.kn + lane), w1 = head_load(a.kn + 64 + lane);
   bool ok = false;
   const int pos = resolve_position(a.pos, ps, t, a.cap, a.first, true, ok);
   ok = ok && pos >= 0 && pos < a.table_rows;
@@ -314,7 +316,6 @@ __device__ __forceinline__ void qk_pair_wave(const QKArgs<T> &a, unsigned kidx) 
       raise_bad(a.bad);
     return; // wave-uniform
   }
-  const float w0 = head_load(a.kn + lane), w1 = head_load(a.kn + 64 + lane);
   const uint16_t *trow = a.table + (size_t)pos * D;
   const float c = head_load(trow + lane), sn = head_load(trow + 64 + lane);
   const LaneCodes cv = lane_codes<FMT, true>(v0, v1, lane);
