@@ -114,10 +114,12 @@ template <int TOP, class V, class Op> __device__ __forceinline__ V xor_reduce(V 
   else
     return v;
 }
-// One Hadamard stage on lane bit log2(M): lower' = lower + upper, upper' = lower - upper.
+// One Hadamard stage on lane bit log2(M): lower' = lower + upper, upper' = lower - upper,
+// as one fused multiply-add with the lane's sign (+-1 products are exact, so the sum is
+// rounded once, as the add or subtract is).
 template <int M> __device__ __forceinline__ float hadamard_lane(float v, int lane) {
   const float o = lane_xor<M>(v);
-  return (lane & M) ? o - v : v + o;
+  return __builtin_fmaf((lane & M) ? -1.f : 1.f, v, o);
 }
 
 // Streaming (non-temporal) global accesses for data each launch touches once: the
