@@ -362,21 +362,24 @@ __device__ __forceinline__ void qk_heads_wave_quad(const QKArgs<T> &a, long long
       }
     }
   }
-  // 2. The head's position (its control record was requested first), then the weight and
-  // table loads, so that they are in flight with the data loads.
+  // 2. The norm weights of the group (independent of the position), the head's position
+  // (its control record was requested first), then the table loads, so that they are in
+  // flight with the data loads.
+  const uint16_t *wsrc = (role == 1 ? a.kn : a.qn) + 32 * g;
+  Bf8 w8[4], c8[4], s8[4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m)
+    w8[m].load(wsrc + 8 * m);
   bool ok = false;
   int pos = resolve_position(a.pos, ps, t, FMT >= 0 ? a.cap : 0, a.first, FMT > PADRA_KV_BF16,
                              ok);
   ok = ok && live && pos >= 0 && pos < a.table_rows;
   if (live && !ok && g == 0)
     raise_bad(a.bad);
-  // Norm weights of the group and the table entries of its pair index (f mod 64).
-  const uint16_t *wsrc = (role == 1 ? a.kn : a.qn) + 32 * g;
+  // The table entries of the group's pair index (f mod 64).
   const uint16_t *row = a.table + (size_t)(ok ? pos : 0) * D + 32 * (g & 1);
-  Bf8 w8[4], c8[4], s8[4];
 #pragma unroll
   for (int m = 0; m < 4; ++m) {
-    w8[m].load(wsrc + 8 * m);
     c8[m].load(row + 8 * m);
     s8[m].load(row + 64 + 8 * m);
   }
