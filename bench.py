@@ -916,6 +916,9 @@ KERNEL_ROLES = {
     "k_chain<128, 16, 0, false, float>": "config 1 chain on fp32 activations, one launch",
     "k_chain_small<256, 8, 0, true>": "config 4/0 decode step: gather + chain, one launch",
     "k_chain_small<256, 8, 0, false>": "config 4/0 decode chain after a separate gather",
+    "k_chain_heads<256, 8, 0, false, float>": "config 4/0 decode chain on fp32 activations, BF16 KV",
+    "k_chain_heads<256, 8, 1, false, float>": "config 4 decode chain on fp32 activations, q8 KV",
+    "k_chain_heads<256, 8, 2, false, float>": "config 4 decode chain on fp32 activations, q8_0 KV",
     "k_chain_small<256, 8, 1, true>": "config 4 decode step, q8 KV: gather + chain (pair waves)",
     "k_chain_small<256, 8, 1, false>": "config 4 decode chain, q8 KV, after a separate gather",
     "k_chain_small<256, 8, 2, true>": "config 4 decode step, q8_0 KV: gather + chain (pair waves)",
