@@ -584,8 +584,9 @@ int chain(hipStream_t s, const uint16_t *gather, int vocab, const int32_t *ids, 
 } // namespace
 
 namespace {
-// The fused chain on fp32 activations (the reference's buffers): norm-row waves, then the
-// Q/K waves, one per head vector up to head_wave_tokens, else four lanes per head.
+// The chain on fp32 activations (the reference's buffers): up to head_wave_tokens one
+// launch of norm-row waves and per-head Q/K waves; above, the residual-norm launch, then
+// the four-lanes-per-head Q/K launch.
 int chain_f32(hipStream_t s, void *x, const void *residual, void *normalized,
               const uint16_t *gamma, int hidden, int tree, float *statistics, void *q, void *k,
               const void *v, const uint16_t *qn, const uint16_t *kn, const uint16_t *table,
@@ -620,9 +621,18 @@ int chain_f32(hipStream_t s, void *x, const void *residual, void *normalized,
                            dim3((unsigned)waves), dim3(64), 0, s, n, a, norm_waves, waves);
         return launched();
       }
-      const long long waves = norm_waves + qk_wave_count<fmt.value>(tokens, q_heads, kv_heads);
-      hipLaunchKernelGGL((k_chain<vt.value, j.value, fmt.value, false, float>),
-                         dim3((unsigned)waves), dim3(64), 0, s, n, a, norm_waves, waves);
+      // Larger launches run the two halves as two kernels on the stream: one kernel would
+      // give its norm rows the Q/K waves' registers (142 VGPRs, 3 waves per SIMD, against
+      // 89 and 5 for the norm rows alone); config 1: 22.1 us in one kernel, 11.4 + 9.8 us
+      // as two.
+      hipLaunchKernelGGL((k_norm<vt.value, j.value, float, true>), dim3((unsigned)norm_waves),
+                         dim3(64), 0, s, n);
+      const int st2 = launched();
+      if (st2)
+        return st2;
+      hipLaunchKernelGGL((k_qk<float, fmt.value>),
+                         dim3((unsigned)qk_wave_count<fmt.value>(tokens, q_heads, kv_heads)),
+                         dim3(64), 0, s, a);
       return launched();
     });
   });

@@ -615,12 +615,13 @@ def test_fused_chain_matches_oracle(oracle, fmt, tree, tokens):
 
 
 @pytest.mark.parametrize("fmt", FORMATS)
-@pytest.mark.parametrize("tree,tokens", [(128, 300), (256, 64), (128, 385), (256, 384)])
+@pytest.mark.parametrize("tree,tokens", [(128, 300), (256, 64), (128, 385), (256, 384),
+                                         (256, 700)])
 def test_fused_chain_f32_activations(oracle, fmt, tree, tokens):
     """The fused chain on fp32 activations holding BF16-exact values (the reference's
-    buffers): every output equal to the oracle's, as floats, on both launch shapes (a wave
-    per head vector up to 384 tokens with a BF16 cache and 320 with a quantized one, four
-    lanes per head above)."""
+    buffers): every output equal to the oracle's, as floats, on both launch shapes (one
+    launch with a wave per head vector up to 384 tokens with a BF16 cache and 320 with a
+    quantized one; above, the norm launch and the four-lanes-per-head Q/K launch)."""
     print(f"[case] chain f32 fmt={fmt} tree={tree} tokens={tokens}", flush=True)
     capacity = 4096
     d = synth.chain_inputs(tokens, outliers=True, seed=300 + fmt + tree)
