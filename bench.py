@@ -300,8 +300,8 @@ def bench_swiglu(torch, steps, sets=4):
 def bench_f32_layer(torch, steps, sets=8):
     """The config-1 chunk in the reference's own activation form (fp32 buffers holding
     BF16-exact values, PADRA_ACT_F32): launched as the reference launches it (the residual
-    + RMSNorm, then the Q/K norm + RoPE + BF16 KV store, each timed alone), and as one
-    fused launch."""
+    + RMSNorm, then the Q/K norm + RoPE + BF16 KV store, each timed alone), and through
+    the one chain entry point (padra_ResidualNormQKRopeStore)."""
     from padra_amd import abi, ops, synth
     host = synth.chain_inputs(TOKENS, HIDDEN, HQ, HKV, D, outliers=True, seed=0)
     f32 = lambda a: torch.from_numpy(synth.bf16_to_f32(a)).cuda()
@@ -329,7 +329,8 @@ def bench_f32_layer(torch, steps, sets=8):
     qk_bytes = TOKENS * (((HQ + 2 * HKV) + (HQ + HKV)) * D * 4 + 2 * HKV * D * 2 + 2 * D)
     rate = lambda b, ms: round(b / (ms * 1e-3) / 1e9, 2)
     return {"workload": "config1 chunk with fp32 activations: residual+RMSNorm, then "
-                        "QK-norm+RoPE+BF16 KV store (two launches, and fused in one)",
+                        "QK-norm+RoPE+BF16 KV store (two entry points, and the one chain "
+                        "entry point)",
             "fused_us": round(fused_ms * 1e3, 3),
             "fused_gbs": rate(norm_bytes + qk_bytes, fused_ms),
             "fused_frac": round((norm_bytes + qk_bytes) / (fused_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
@@ -913,7 +914,6 @@ KERNEL_ROLES = {
     "k_chain<128, 16, 1, false, unsigned short>": "config 2 chain, q8 KV",
     "k_chain<128, 16, 2, false, unsigned short>": "config 2 chain, q8_0 KV (rotated)",
     "k_chain<128, 16, 3, false, unsigned short>": "config 2 chain, q8_0 KV (unrotated)",
-    "k_chain<128, 16, 0, false, float>": "config 1 chain on fp32 activations, one launch",
     "k_chain_small<256, 8, 0, true>": "config 4/0 decode step: gather + chain, one launch",
     "k_chain_small<256, 8, 0, false>": "config 4/0 decode chain after a separate gather",
     "k_chain_heads<256, 8, 0, false, float>": "config 4/0 decode chain on fp32 activations, BF16 KV",
