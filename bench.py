@@ -661,6 +661,91 @@ def cpu_decode_token(seconds=2.0):
     return {"us_per_token": round(el / reps * 1e6, 3), "tokens_per_s": round(reps / el, 1),
             "cores": 1, "kind": "port"}
 
+def _cpu_repeat(work, pieces, threads, seconds):
+    """Runs work(i) for i in range(pieces) on `threads` threads (ctypes releases the GIL in
+    each oracle call), repeated until `seconds` have elapsed; returns (s per pass, passes)."""
+    from concurrent.futures import ThreadPoolExecutor
+    reps, t0 = 0, time.perf_counter()
+    with ThreadPoolExecutor(threads) as pool:
+        while True:
+            list(pool.map(work, range(pieces)))
+            reps += 1
+            el = time.perf_counter() - t0
+            if el >= seconds:
+                return el / reps, reps
+
+
+def cpu_configs(host, threads, seconds=2.0):
+    """The oracle on the host for configs 2-4, each a bounded sample of about `seconds` on
+    `threads` threads (work split into contiguous slices): the config-2 chunk with q8 and
+    rotated q8_0 caches, the config-3 SwiGLU (16384 rows of 1024), and the config-4 decode
+    step (64 sequences: gather from a 4096-row slice of the embedding table, ids mod 4096,
+    then the 256-thread-tree chain at ragged positions into a 131072-row cache)."""
+    from oracle import oracle
+    from padra_amd import synth
+    oracle.lib()
+    out = {}
+    table = synth.bf16_bits(oracle.rope_table(TOKENS, D, 1e6))
+    bounds = np.linspace(0, TOKENS, threads + 1).astype(int)
+    for fmt in ("q8", "q8_0"):
+        if fmt == "q8":
+            ck, cv = np.zeros((TOKENS, HKV * D), np.int8), np.zeros((TOKENS, HKV * D), np.int8)
+            sc = np.zeros((TOKENS, HKV, 2), np.float32)
+        else:
+            ck, cv = np.zeros((TOKENS, 544), np.uint8), np.zeros((TOKENS, 544), np.uint8)
+
+        def piece(i, fmt=fmt, ck=ck, cv=cv):
+            lo, hi = bounds[i], bounds[i + 1]
+            pos = np.arange(lo, hi, dtype=np.int32)
+            oracle.residual_rmsnorm(host["x"][lo:hi], host["residual"][lo:hi], host["gamma"],
+                                    1e-6, 128)
+            _, k, _ = oracle.qk_norm_rope(host["q"][lo:hi], host["k"][lo:hi], host["qn"],
+                                          host["kn"], table, pos)
+            if fmt == "q8":
+                oracle.kv_q8_encode(k, host["v"][lo:hi], ck, cv, sc, pos, TOKENS)
+            else:
+                oracle.kv_q8_0_encode(k, host["v"][lo:hi], ck, cv, pos, TOKENS)
+        per, reps = _cpu_repeat(piece, threads, threads, seconds)
+        out[f"config2_{fmt}"] = {"us_per_chunk": round(per * 1e6, 1),
+                                 "tokens_per_s": round(TOKENS / per, 1),
+                                 "gbs": round(chain_bytes(fmt) * TOKENS / per / 1e9, 3),
+                                 "cores": threads, "kind": "port",
+                                 "sample": f"{reps} full 2048-token chunks"}
+    d = synth.swiglu_inputs(tokens=2048, top_k=8, width=1024, experts=64, sigma=2.0, seed=0)
+    rows = d["gate"].shape[0]
+    sb = np.linspace(0, rows, threads + 1).astype(int)
+    per, reps = _cpu_repeat(lambda i: oracle.swiglu(d["gate"][sb[i]:sb[i + 1]],
+                                                    d["up"][sb[i]:sb[i + 1]]),
+                            threads, threads, seconds)
+    out["config3"] = {"us_per_launch": round(per * 1e6, 1),
+                      "rows_per_s": round(rows / per, 1),
+                      "gbs": round(6 * rows * 1024 / per / 1e9, 3), "cores": threads,
+                      "kind": "port", "sample": f"{reps} passes over {rows} rows"}
+    seqs, vocab_slice, cap = 64, 4096, CAPACITY
+    emb = synth.chain_inputs(vocab_slice, HIDDEN, HQ, HKV, D, outliers=False, seed=1)["x"]
+    dec = synth.chain_inputs(seqs, HIDDEN, HQ, HKV, D, outliers=False, seed=0)
+    ids = synth.zipf_ids(seqs, 131072, s=1.1, seed=0) % vocab_slice
+    positions = np.random.default_rng(0).integers(0, cap, seqs).astype(np.int32)
+    dtable = synth.bf16_bits(oracle.rope_table(cap, D, 1e6))
+    kc = np.zeros((cap, HKV * D), np.uint16)
+    vc = np.zeros_like(kc)
+    db = np.linspace(0, seqs, threads + 1).astype(int)
+
+    def step(i):
+        lo, hi = db[i], db[i + 1]
+        if hi <= lo:
+            return
+        x, _ = oracle.embed(emb, ids[lo:hi].astype(np.int32))
+        oracle.residual_rmsnorm(x, dec["residual"][lo:hi], dec["gamma"], 1e-6, 256)
+        _, k, _ = oracle.qk_norm_rope(dec["q"][lo:hi], dec["k"][lo:hi], dec["qn"], dec["kn"],
+                                      dtable, positions[lo:hi])
+        oracle.kv_store_bf16(k, dec["v"][lo:hi], kc, vc, positions[lo:hi], cap)
+    per, reps = _cpu_repeat(step, threads, threads, seconds)
+    out["config4"] = {"us_per_step": round(per * 1e6, 1), "tokens_per_s": round(seqs / per, 1),
+                      "cores": threads, "kind": "port", "sample": f"{reps} steps of {seqs} sequences"}
+    return out
+
+
 def main():
     if len(sys.argv) > 2 and sys.argv[1] == "--summarize":
         summarize(sys.argv[2], " ".join(sys.argv[3:]) or "(see profiles/README)")
@@ -765,6 +850,7 @@ def main():
         line["cpu_baseline"] = cpu_baseline(host, args.cpu_seconds, cpu_threads())
         if not args.no_configs:
             line["configs"]["config0_cpu"] = cpu_decode_token()
+            line["configs"]["cpu_configs"] = cpu_configs(host, cpu_threads())
     print(json.dumps(line), flush=True)
 
 
