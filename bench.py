@@ -358,13 +358,21 @@ def bench_norm_fp8(torch, steps, sets=8):
     ms = graph_time(torch, lambda i: ops.NormFP8(bufs[i % sets][0], bufs[i % sets][1], g,
                                                  bufs[i % sets][2], bufs[i % sets][3], bad),
                     steps)
+    # The same RMSNorm without the encoding (padra_ResidualPostNorm with no residual, the
+    # reference's Norm): reads x, writes normalized.
+    norm_ms = graph_time(torch, lambda i: ops.ResidualPostNorm(bufs[i % sets][0], None,
+                                                               bufs[i % sets][1], g, bad), steps)
     if bad.item():
         raise SystemExit("device error flag set in the FP8 norm benchmark")
     nbytes = TOKENS * (HIDDEN * (2 + 2 + 1) + 4)
+    norm_bytes = TOKENS * HIDDEN * 2 * 2
     return {"workload": "RMSNorm + FP8 E4M3 row encoding, 2048 rows x 2048 (BF16 in/out)",
             "us_per_launch": round(ms * 1e3, 3), "bytes_per_launch": nbytes,
             "gbs": round(nbytes / (ms * 1e-3) / 1e9, 2),
-            "frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+            "frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "norm_only": {"us_per_launch": round(norm_ms * 1e3, 3), "bytes_per_launch": norm_bytes,
+                          "gbs": round(norm_bytes / (norm_ms * 1e-3) / 1e9, 2),
+                          "frac": round(norm_bytes / (norm_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}}
 
 
 def bench_kv_neighbours(torch, steps=100, sets=4):
@@ -838,8 +846,11 @@ def main():
                            "kv_neighbours": bench_kv_neighbours(torch)}
         # The streaming copy of each memory-bound kernel's own byte count, timed the same
         # way: how far a launch of that size is from the copy, apart from the HBM peak.
-        for key in ("config3", "norm_fp8", "combine_norm", "config1_f32_activations"):
-            entry = line["configs"][key]
+        for key in ("config3", "norm_fp8", "norm_fp8.norm_only", "combine_norm",
+                    "config1_f32_activations"):
+            entry = line["configs"]
+            for part in key.split("."):
+                entry = entry[part]
             nbytes = entry.get("bytes_per_launch") or (entry["norm_bytes"] + entry["qk_bytes"])
             gbs, ms = stream_copy_ceiling(torch, nbytes, steps=100)
             entry["copy_us"] = round(ms * 1e3, 3)
