@@ -1022,7 +1022,9 @@ KERNEL_ROLES = {
     "k_chain_small<256, 8, 2, false>": "config 4 decode chain, q8_0 KV, after a separate gather",
     "k_embed": "embedding gather (separate launch)",
     "k_swiglu": "config 3 SwiGLU",
-    "k_norm": "residual + RMSNorm (fp32 activations)",
+    "k_norm<128, 16, float, true>": "residual + RMSNorm (fp32 activations)",
+    "k_norm<128, 16, unsigned short, false>": "RMSNorm alone (no residual; BF16)",
+    "k_norm": "residual + RMSNorm",
     "k_qk": "Q/K norm + RoPE + store (fp32 activations)",
     "k_norm_fp8": "RMSNorm + FP8 E4M3",
     "k_combine_norm": "expert combine + residual + RMSNorm + FP8",
