@@ -77,8 +77,7 @@ template <int S> __device__ __forceinline__ float lanes_max(float m) {
 // l + 64 in x0 and x1: computed, not stored (kv_q8.cuh:56-73, kv_q8_native.cuh:76-100).
 //  - `bad`: a non-finite value (q8: or a value that is not BF16-exact) in this lane.
 //  - q8: scale = amax/127 over the head (1 for a zero head), codes RNE(x / scale) clamped
-//    to +-127: the reciprocal form where q8_fast_ok admits it, else the division, chosen
-//    per lane (two values a lane: cheaper than a branch).
+//    to +-127: the reciprocal form where q8_fast_ok admits it, else the division.
 //  - q8_0: the rotation for the rotated format (K: stages on feature bits 0..6, scale
 //    1/sqrt(128); V: bits 0..5, scale 1/8), then blocks of 32 features: x0 is in block
 //    l / 32, x1 in block 2 + l / 32, so a block is a 32-lane half of one register;
@@ -102,10 +101,14 @@ __device__ __forceinline__ LaneCodes lane_codes(float x0, float x1, int lane) {
   if constexpr (FMT == PADRA_KV_Q8) {
     const float m = lanes_max<32>(fmaxf(fabsf(x0), fabsf(x1)));
     const float scale = m == 0.f ? 1.f : m / 127.f, inverse = 1.f / scale;
-    const bool fast = q8_fast_ok(scale);
     r.scale = scale;
-    r.c0 = fast ? q8_code_fast(x0, scale, inverse) : q8_code(x0, scale);
-    r.c1 = fast ? q8_code_fast(x1, scale, inverse) : q8_code(x1, scale);
+    if (q8_fast_ok(scale)) { // wave-uniform: the divisions stay off the common path
+      r.c0 = q8_code_fast(x0, scale, inverse);
+      r.c1 = q8_code_fast(x1, scale, inverse);
+    } else {
+      r.c0 = q8_code(x0, scale);
+      r.c1 = q8_code(x1, scale);
+    }
   } else {
     if constexpr (FMT == PADRA_KV_Q8_0) {
       float x[2] = {x0, x1};
