@@ -718,11 +718,13 @@ def test_config2_full_chunk(oracle, fmt):
 
 @pytest.mark.parametrize("fmt", FORMATS)
 @pytest.mark.parametrize("tree", [128, 256])
-def test_reference_geometry_chain(oracle, fmt, tree):
+@pytest.mark.parametrize("tokens", [97, 400])
+def test_reference_geometry_chain(oracle, fmt, tree, tokens):
     """The reference model's own shapes: hidden 2304, 32 Q heads, 4 KV heads
-    (inference.cu:184-186, qk_rope_store_exact.cuh:23-26), ragged token count."""
-    print(f"[case] reference geometry fmt={fmt} tree={tree}", flush=True)
-    tokens, capacity, hidden, hq = 97, 2048, 2304, 32
+    (inference.cu:184-186, qk_rope_store_exact.cuh:23-26), ragged token counts on each
+    launch shape (97: a wave per head vector; 400: four lanes per head)."""
+    print(f"[case] reference geometry fmt={fmt} tree={tree} tokens={tokens}", flush=True)
+    capacity, hidden, hq = 2048, 2304, 32
     d = synth.chain_inputs(tokens, hidden=hidden, q_heads=hq, outliers=True, seed=70 + fmt)
     tb = table_bits(oracle, capacity, theta=5e5)
     positions = np.arange(tokens, dtype=np.int32) + 1000
