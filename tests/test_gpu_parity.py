@@ -352,13 +352,15 @@ def test_qk_rope_store_prefill(oracle, fmt, tokens, base, cap):
 
 
 @pytest.mark.parametrize("fmt", [abi.KV_Q8, abi.KV_Q8_0, abi.KV_Q8_0_NOROT])
-def test_store_extreme_value_scales(oracle, fmt):
+@pytest.mark.parametrize("tokens", [48, 400])
+def test_store_extreme_value_scales(oracle, fmt, tokens):
     """V heads of tiny and huge magnitude (q8: scales below 2^-100, where the store takes
     the division instead of the reciprocal form, and near the top of the fp32 range; q8_0:
     fp16 block scales from subnormal to near their top), bit-exact against the oracle's
-    codes and scales."""
-    print(f"[case] store extreme scales fmt={fmt}", flush=True)
-    tokens, capacity = 48, 4096
+    codes and scales, in both launch shapes (48 tokens: a wave per (token, KV head) pair;
+    400: four lanes per head)."""
+    print(f"[case] store extreme scales fmt={fmt} tokens={tokens}", flush=True)
+    capacity = 4096
     d = synth.chain_inputs(tokens, outliers=False, seed=77 + fmt)
     v = d["v"].view(np.uint16).reshape(tokens, -1).astype(np.uint32) << 16
     vf = v.view(np.float32).copy()
@@ -391,7 +393,8 @@ def test_store_extreme_value_scales(oracle, fmt):
 
 @pytest.mark.parametrize("act", ["bf16", "f32"])
 @pytest.mark.parametrize("fmt", [abi.KV_Q8, abi.KV_Q8_0, abi.KV_Q8_0_NOROT])
-def test_store_nonfinite_heads(oracle, fmt, act):
+@pytest.mark.parametrize("tokens", [40, 400])
+def test_store_nonfinite_heads(oracle, fmt, act, tokens):
     """Non-finite K and V heads in the quantized stores (kv_q8.cuh:49-54,
     kv_q8_native.cuh:70-79): the flag is raised and the head's codes and scales are not
     written.  Token 3 head 1 has a NaN in K and V, token 10 head 2 infinities in both,
@@ -401,9 +404,11 @@ def test_store_nonfinite_heads(oracle, fmt, act):
     0 and 1 of K and V are written, blocks 2 and 3 of neither (kv_q8_native.cuh:84-92).
     The caches start filled with a pattern, so that a row written with zero codes and
     scales differs from a row left alone; a second launch with only the V head of token
-    17 invalid must raise the flag by itself.  Every byte of both caches is compared."""
-    print(f"[case] store nonfinite fmt={fmt} act={act}", flush=True)
-    tokens, capacity = 40, 4096
+    17 invalid must raise the flag by itself.  Every byte of both caches is compared, in
+    both launch shapes (40 tokens: a wave per (token, KV head) pair; 400: four lanes per
+    head)."""
+    print(f"[case] store nonfinite fmt={fmt} act={act} tokens={tokens}", flush=True)
+    capacity = 4096
     d0 = synth.chain_inputs(tokens, outliers=False, seed=91 + fmt)
     tb = table_bits(oracle, capacity)
     positions = np.arange(tokens, dtype=np.int32)
@@ -488,11 +493,13 @@ def test_qk_rope_store_f32_activations(oracle, fmt, tokens, base, cap):
 
 @pytest.mark.parametrize("fmt", FORMATS)
 @pytest.mark.parametrize("act", ["bf16", "f32"])
-def test_qk_rope_store_decode_batch(oracle, fmt, act):
+@pytest.mark.parametrize("seqs", [16, 400])
+def test_qk_rope_store_decode_batch(oracle, fmt, act, seqs):
     """Ragged positions, one token per sequence, per-sequence caches (seq_stride rows), on
     BF16 activations and on fp32 activations holding BF16-exact values (whose outputs must
-    stay BF16-exact)."""
-    print(f"[case] decode batch fmt={fmt} act={act}", flush=True)
+    stay BF16-exact), with 16 sequences (a wave per head vector) and 400 (four lanes per
+    head)."""
+    print(f"[case] decode batch fmt={fmt} act={act} seqs={seqs}", flush=True)
     if act == "f32":
         conv = lambda a: torch.from_numpy(synth.bf16_to_f32(a)).cuda()
 
@@ -502,7 +509,7 @@ def test_qk_rope_store_decode_batch(oracle, fmt, act):
             return (w >> 16).astype(np.uint16)
     else:
         conv, back = dev, host16
-    seqs, cap, capacity = 16, 256, 256
+    cap, capacity = 256, 256
     rng = np.random.default_rng(fmt)
     positions = rng.integers(0, capacity, seqs).astype(np.int32)
     d = synth.chain_inputs(seqs, outliers=True, seed=40 + fmt)
@@ -526,6 +533,7 @@ def test_qk_rope_store_decode_batch(oracle, fmt, act):
     keep = [s for s in range(seqs) if s != 3]
     assert np.array_equal(gq[keep], wq[keep]) and np.array_equal(gk[keep], wk[keep])
     kca, vca = _np(kc, fmt).reshape(seqs, cap, -1), _np(vc, fmt).reshape(seqs, cap, -1)
+    sca = None if sc is None else sc.cpu().numpy().reshape(seqs, cap, 4, 2)
     for s in range(seqs):
         ek, ev, es = _expected_cache(oracle, fmt, wk[s:s + 1], d["v"][s:s + 1],
                                      positions[s:s + 1], cap, 0)
@@ -534,7 +542,7 @@ def test_qk_rope_store_decode_batch(oracle, fmt, act):
             continue
         assert np.array_equal(kca[s], ek) and np.array_equal(vca[s], ev)
         if es is not None:
-            assert np.array_equal(sc.cpu().numpy().reshape(seqs, cap, 4, 2)[s], es)
+            assert np.array_equal(sca[s], es)
 
 
 def test_invalid_prefill_state_writes_nothing(oracle):
