@@ -59,9 +59,12 @@ def parse():
 
 
 class ChainSet:
-    """One independent buffer set of the config-1 workload."""
+    """One independent buffer set of the config-1 workload (`tokens` rows of host's)."""
 
-    def __init__(self, torch, host, table, fmt):
+    def __init__(self, torch, host, table, fmt, tokens=TOKENS, base_positions=False):
+        if tokens != len(host["x"]):
+            host = {k: (v[:tokens] if k in ("x", "residual", "q", "k", "v") else v)
+                    for k, v in host.items()}
         from padra_amd import abi, ops
         dev = lambda a: torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).cuda()
         self.x, self.r = dev(host["x"]), dev(host["residual"])
@@ -83,10 +86,11 @@ class ChainSet:
             self.kc = torch.empty((CAPACITY, 544), dtype=torch.uint8, device="cuda")
             self.vc = torch.empty_like(self.kc)
             self.sc = None
-        self.state = torch.tensor([0, 0, TOKENS, CAPACITY, 0, 1, 1, 1], dtype=torch.int32,
+        self.state = torch.tensor([0, 0, tokens, CAPACITY, 0, 1, 1, 1], dtype=torch.int32,
                                   device="cuda")
         self.bad = torch.zeros(1, dtype=torch.int32, device="cuda")
-        self.pos = ops.positions_prefill(self.state, maximum=CAPACITY)
+        self.pos = ops.positions_base(0) if base_positions else \
+            ops.positions_prefill(self.state, maximum=CAPACITY)
         self.kv = ops.kv_cache(code, self.kc, self.vc, CAPACITY, scales=self.sc)
         self.ops = ops
 
@@ -339,6 +343,33 @@ def bench_f32_layer(torch, steps, sets=8):
             "qk_us": round(qk_ms * 1e3, 3), "qk_bytes": qk_bytes, "qk_gbs": rate(qk_bytes, qk_ms),
             "gbs": rate(norm_bytes + qk_bytes, norm_ms + qk_ms),
             "frac": round((norm_bytes + qk_bytes) / ((norm_ms + qk_ms) * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+
+
+def bench_chain_sizes(torch, sizes=(2048, 4096, 8192, 16384), steps=50, sets=4):
+    """The BF16 chain at several token counts, each beside a streaming copy of the same bytes
+    timed the same way: how much of a launch is its fixed cost and how fast the chain
+    streams once the launch is large.  Host-known positions (PADRA_POS_BASE) at every
+    size, since a prefill chunk holds at most 2048 tokens."""
+    from padra_amd import ops, synth
+    host = synth.chain_inputs(max(sizes), HIDDEN, HQ, HKV, D, outliers=True, seed=0)
+    table = torch.from_numpy(ops.RopeTable(max(sizes), D, 1e6).view(torch.int16).numpy()).cuda()
+    out = {}
+    for t in sizes:
+        chain_sets = [ChainSet(torch, host, table, "bf16", tokens=t, base_positions=True)
+                      for _ in range(sets)]
+        ms = time_graph(torch, chain_sets, steps, 5)
+        if any(int(c.bad.item()) for c in chain_sets):
+            raise SystemExit(f"device error flag set in the chain at {t} tokens")
+        del chain_sets
+        torch.cuda.empty_cache()
+        nbytes = chain_bytes("bf16") * t
+        _, copy_ms = stream_copy_ceiling(torch, nbytes, steps=steps, sets=sets)
+        out[str(t)] = {"us_per_launch": round(ms * 1e3, 3), "bytes_per_launch": nbytes,
+                       "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                       "frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                       "copy_us": round(copy_ms * 1e3, 3),
+                       "frac_of_copy": round(copy_ms / ms, 4)}
+    return out
 
 
 def bench_norm_fp8(torch, steps, sets=8):
@@ -843,7 +874,8 @@ def main():
                            "attention": bench_attention(torch, 10),
                            "attention_q8_0": bench_attention(torch, 10, fmt="q8_0"),
                            "attention_q8": bench_attention(torch, 10, fmt="q8"),
-                           "kv_neighbours": bench_kv_neighbours(torch)}
+                           "kv_neighbours": bench_kv_neighbours(torch),
+                           "config1_chunk_sizes": bench_chain_sizes(torch)}
         # The streaming copy of each memory-bound kernel's own byte count, timed the same
         # way: how far a launch of that size is from the copy, apart from the HBM peak.
         for key in ("config3", "norm_fp8", "norm_fp8.norm_only", "combine_norm",
