@@ -8,7 +8,9 @@ import ctypes
 import os
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-library_path = os.path.join(_HERE, "libpadra_hip.so")
+# PADRA_HIP_LIB selects another build of the same library (the host-sanitizer build of
+# padra_amd/build.py --asan); it must exist like the default one.
+library_path = os.environ.get("PADRA_HIP_LIB") or os.path.join(_HERE, "libpadra_hip.so")
 
 # Status codes (mellum16::StatusCode numbering, include/mellum16/status.h:11-21).
 OK, INVALID_ARGUMENT, UNSUPPORTED, INTERNAL = 0, 1, 5, 8

@@ -25,16 +25,32 @@ def hipcc() -> str:
     return os.path.join(rocm, "bin", "hipcc")
 
 
-def command(out: str = OUT) -> list[str]:
+# The host-sanitizer build: the library's host code (argument checks, launch set-up, the
+# RoPE table builder) under AddressSanitizer and UndefinedBehaviorSanitizer; device code
+# is compiled as usual (no GPU sanitizer).  The CPU tests run against it with the clang
+# ASan runtime preloaded (python is not instrumented):
+#   python -m padra_amd.build --asan
+#   PADRA_HIP_LIB=padra_amd/_asan/libpadra_hip.so ASAN_OPTIONS=detect_leaks=0 \
+#     LD_PRELOAD=$(hipcc -print-file-name=libclang_rt.asan-x86_64.so) \
+#     python -m pytest tests/test_abi.py -m "not gpu"
+ASAN_OUT = os.path.join(HERE, "_asan", "libpadra_hip.so")
+ASAN_FLAGS = ["-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fsanitize=undefined",
+              "-Xarch_host", "-fno-sanitize-recover=undefined", "-shared-libasan", "-g"]
+
+
+def command(out: str = OUT, asan: bool = False) -> list[str]:
     return [hipcc(), "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",
             "-ffp-contract=off", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-            "-mllvm", "-amdgpu-mfma-vgpr-form",
-            "-Wall", "-I", os.path.join(ROOT, "include"), "-o", out] + \
+            "-mllvm", "-amdgpu-mfma-vgpr-form"] + (ASAN_FLAGS if asan else []) + \
+           ["-Wall", "-I", os.path.join(ROOT, "include"), "-o", out] + \
            [os.path.join(HERE, s) for s in SOURCES]
 
 
-def build(out: str = OUT, verbose: bool = False) -> str:
-    cmd = command(out)
+def build(out: str = OUT, verbose: bool = False, asan: bool = False) -> str:
+    if asan:
+        out = ASAN_OUT
+        os.makedirs(os.path.dirname(out), exist_ok=True)
+    cmd = command(out, asan)
     res = subprocess.run(cmd, capture_output=True, text=True)
     noise = ("packed-fp32-ops", "warning: argument unused")
     msgs = [l for l in (res.stdout + res.stderr).splitlines() if l and not any(n in l for n in noise)]
@@ -46,4 +62,4 @@ def build(out: str = OUT, verbose: bool = False) -> str:
 
 
 if __name__ == "__main__":
-    print(build(verbose=True))
+    print(build(verbose=True, asan="--asan" in sys.argv[1:]))
