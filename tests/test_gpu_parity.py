@@ -762,13 +762,15 @@ def test_reference_geometry_chain(oracle, fmt, tree, tokens):
 
 # ---- graph capture ----------------------------------------------------------------------------
 
-def test_decode_chain_graph_replays(oracle):
-    """The decode step (residual norm, 256-thread tree, + Q/K norm/RoPE + BF16 store at each
-    sequence's DecodeState position) captured once into a graph and replayed at new
-    positions: positions are read on the device, so each replay must match the oracle at
-    the positions the state held when it ran.  Eager work and synchronizations run between
-    the replays (state updates, input resets)."""
-    print("[case] decode chain graph replays", flush=True)
+@pytest.mark.parametrize("fmt", [abi.KV_BF16, abi.KV_Q8, abi.KV_Q8_0])
+def test_decode_chain_graph_replays(oracle, fmt):
+    """The decode step (residual norm, 256-thread tree, + Q/K norm/RoPE + KV store at each
+    sequence's DecodeState position; BF16, or a quantized cache through the per-pair
+    encoder) captured once into a graph and replayed at new positions: positions are read
+    on the device, so each replay must match the oracle at the positions the state held
+    when it ran.  Eager work and synchronizations run between the replays (state updates,
+    input and cache resets)."""
+    print(f"[case] decode chain graph replays fmt={fmt}", flush=True)
     seqs, capacity = 8, 512
     d = synth.chain_inputs(seqs, outliers=True, seed=81)
     tb = table_bits(oracle, capacity)
@@ -777,12 +779,11 @@ def test_decode_chain_graph_replays(oracle):
     r, g, v = dev(d["residual"]), dev(d["gamma"]), dev(d["v"])
     qn, kn, table = dev(d["qn"]), dev(d["kn"]), dev(tb)
     y = torch.empty_like(x)
-    kc = torch.zeros((seqs * capacity, 512), dtype=torch.int16, device="cuda")
-    vc = torch.zeros_like(kc)
+    kc, vc, sc = _alloc_cache(fmt, seqs * capacity)
     states = torch.zeros((seqs, 8), dtype=torch.int32, device="cuda")
     bad = flag()
     pos = ops.positions_decode(states, maximum=capacity)
-    kv = ops.kv_cache(abi.KV_BF16, kc, vc, capacity, seq_stride=capacity)
+    kv = ops.kv_cache(fmt, kc, vc, capacity, scales=sc, seq_stride=capacity)
 
     def set_positions(p):
         host = np.zeros((seqs, 8), np.int32)
@@ -808,6 +809,8 @@ def test_decode_chain_graph_replays(oracle):
         set_positions(p)
         x.copy_(x0), q.copy_(q0), k.copy_(k0)
         kc.zero_(), vc.zero_()
+        if sc is not None:
+            sc.zero_()
         torch.cuda.synchronize()
         graph.replay()
         torch.cuda.synchronize()
@@ -815,9 +818,12 @@ def test_decode_chain_graph_replays(oracle):
         wq, wk, _ = _qk_oracle(oracle, d, tb, p)
         assert np.array_equal(host16(x), wx) and np.array_equal(host16(y), wy), replay
         assert np.array_equal(host16(q), wq) and np.array_equal(host16(k), wk), replay
-        kca = host16(kc).reshape(seqs, capacity, 512)
-        vca = host16(vc).reshape(seqs, capacity, 512)
+        kca = _np(kc, fmt).reshape(seqs, capacity, -1)
+        vca = _np(vc, fmt).reshape(seqs, capacity, -1)
+        sca = None if sc is None else sc.cpu().numpy().reshape(seqs, capacity, 4, 2)
         for s in range(seqs):
-            assert np.array_equal(kca[s, p[s]], wk[s].reshape(-1)), (replay, s)
-            assert np.array_equal(vca[s, p[s]], d["v"][s].reshape(-1)), (replay, s)
-            assert np.count_nonzero(kca[s].any(axis=1)) == 1, (replay, s)
+            ek, ev, es = _expected_cache(oracle, fmt, wk[s:s + 1], d["v"][s:s + 1],
+                                         p[s:s + 1], capacity, 0)
+            assert np.array_equal(kca[s], ek) and np.array_equal(vca[s], ev), (replay, s)
+            if es is not None:
+                assert np.array_equal(sca[s], es), (replay, s)
