@@ -529,11 +529,16 @@ def bench_combine_norm(torch, steps, sets=8):
             "frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
 
 
-def bench_attention(torch, steps, seqs=64, capacity=CAPACITY, fill_seed=0, fmt="bf16"):
+def bench_attention(torch, steps, seqs=64, capacity=CAPACITY, fill_seed=0, fmt="bf16",
+                    local=False, splits=0):
     """Decode attention over BF16 caches (the consumer of the stored rows), one step of
     `seqs` sequences at ragged positions U[0, capacity) with per-sequence caches of
-    `capacity` rows: the split-K pass and the per-head merge.  Bytes: every key and value
-    row of the window (4 KV heads x 256 B each) plus q and the output."""
+    `capacity` rows: the split-K pass and the per-head merge.  With `local`, each
+    sequence's cache is the 1024-row local ring and the window its last 1024 keys (a local
+    layer).  `splits` as padra_DecodeAttention takes it (0: the reference's count, -1: the
+    MI355X-tuned count); a non-zero value also times the reference's count for comparison.
+    Bytes: every key and value row of the window (4 KV heads x 256 B each) plus q and the
+    output."""
     from padra_amd import abi, ops, synth
     rng = np.random.default_rng(fill_seed)
     positions = rng.integers(0, capacity, seqs).astype(np.int32)
@@ -542,27 +547,28 @@ def bench_attention(torch, steps, seqs=64, capacity=CAPACITY, fill_seed=0, fmt="
         states[i] = [1, p, capacity, 1 << 20, p, min(int(p), 1024), 0, 0]
     st = torch.from_numpy(states).cuda()
     gen = torch.Generator(device="cuda").manual_seed(fill_seed)
+    rows_per_seq = 1024 if local else capacity
     if fmt == "q8_0":
         # valid rows: random codes, block scales 1/64 (fp16 0x2400)
         def rows():
-            r = torch.randint(-127, 128, (seqs * capacity, 544), generator=gen, device="cuda",
-                              dtype=torch.int8)
+            r = torch.randint(-127, 128, (seqs * rows_per_seq, 544), generator=gen,
+                              device="cuda", dtype=torch.int8)
             r[:, :32].view(torch.int16).fill_(0x2400)
             return r
         kc, vc = rows(), rows()
         row_bytes = 544
         scales = None
     elif fmt == "q8":
-        kc = torch.randint(-127, 128, (seqs * capacity, HKV * D), generator=gen, device="cuda",
-                           dtype=torch.int8)
-        vc = torch.randint(-127, 128, (seqs * capacity, HKV * D), generator=gen, device="cuda",
-                           dtype=torch.int8)
-        scales = torch.full((seqs * capacity, HKV, 2), 1.0 / 64, device="cuda")
+        kc = torch.randint(-127, 128, (seqs * rows_per_seq, HKV * D), generator=gen,
+                           device="cuda", dtype=torch.int8)
+        vc = torch.randint(-127, 128, (seqs * rows_per_seq, HKV * D), generator=gen,
+                           device="cuda", dtype=torch.int8)
+        scales = torch.full((seqs * rows_per_seq, HKV, 2), 1.0 / 64, device="cuda")
         row_bytes = HKV * D
     else:
-        kc = (torch.randn((seqs * capacity, HKV * D), generator=gen, device="cuda")).to(
+        kc = (torch.randn((seqs * rows_per_seq, HKV * D), generator=gen, device="cuda")).to(
             torch.bfloat16).view(torch.int16)
-        vc = (torch.randn((seqs * capacity, HKV * D), generator=gen, device="cuda")).to(
+        vc = (torch.randn((seqs * rows_per_seq, HKV * D), generator=gen, device="cuda")).to(
             torch.bfloat16).view(torch.int16)
         row_bytes = HKV * D * 2
         scales = None
@@ -571,24 +577,34 @@ def bench_attention(torch, steps, seqs=64, capacity=CAPACITY, fill_seed=0, fmt="
     out = torch.empty_like(q)
     bad = torch.zeros(1, dtype=torch.int32, device="cuda")
     code = {"bf16": abi.KV_BF16, "q8": abi.KV_Q8, "q8_0": abi.KV_Q8_0}[fmt]
-    kv = ops.kv_cache(code, kc, vc, capacity, scales=scales, seq_stride=capacity)
+    kv = ops.kv_cache(code, kc, vc, rows_per_seq, scales=scales, seq_stride=rows_per_seq)
     pos = ops.positions_decode(st, maximum=capacity)
-    scratch = ops.DecodeAttention(q, kv, out, pos, bad)  # allocates the scratch once
-    ms = graph_time(torch, lambda i: ops.DecodeAttention(q, kv, out, pos, bad, scratch=scratch),
-                    steps)
+    used = abi.lib().padra_DecodeAttentionSplits(ctypes.byref(kv), seqs, HKV, int(local), splits)
+
+    def timed(s):
+        scratch = ops.DecodeAttention(q, kv, out, pos, bad, local=local, splits=s)  # allocates
+        return graph_time(torch, lambda i: ops.DecodeAttention(q, kv, out, pos, bad,
+                                                               local=local, splits=s,
+                                                               scratch=scratch), steps)
+    ms = timed(splits)
+    ms_reference = timed(0) if splits else None
     if bad.item():
         raise SystemExit("device error flag set in the decode attention benchmark")
     # every K and V row of the window (a q8_0 row holds all 4 KV heads: each KV head's
     # split reads its 128 codes and 8 scale bytes of it), plus q and the output
     per_row = {"bf16": HKV * D * 2, "q8": HKV * (D + 4), "q8_0": HKV * (D + 8)}[fmt]
-    nbytes = int((positions.astype(np.int64) + 1).sum()) * per_row * 2 + 2 * q.numel() * 2
+    window = np.minimum(positions.astype(np.int64) + 1, 1024 if local else capacity)
+    nbytes = int(window.sum()) * per_row * 2 + 2 * q.numel() * 2
     del kc, vc, scales
     torch.cuda.empty_cache()
     return {"workload": f"decode attention, {seqs} sequences at ragged positions < {capacity}, "
-                        f"{fmt} caches (split-K + merge)",
-            "us_per_step": round(ms * 1e3, 3), "bytes_per_step": nbytes,
+                        f"{fmt} caches{', 1024-row local rings' if local else ''} "
+                        "(split-K + merge)",
+            "splits": used, "us_per_step": round(ms * 1e3, 3), "bytes_per_step": nbytes,
             "gbs": round(nbytes / (ms * 1e-3) / 1e9, 2),
-            "frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+            "frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            **({"reference_splits_us_per_step": round(ms_reference * 1e3, 3)}
+               if ms_reference else {})}
 
 
 def bench_decode(torch, steps, seqs, vocab=131072, capacity=CAPACITY, fmt="bf16"):
@@ -874,6 +890,11 @@ def main():
                            "attention": bench_attention(torch, 10),
                            "attention_q8_0": bench_attention(torch, 10, fmt="q8_0"),
                            "attention_q8": bench_attention(torch, 10, fmt="q8"),
+                           "attention_local": bench_attention(torch, 10, local=True, splits=-1),
+                           "attention_local_q8": bench_attention(torch, 10, fmt="q8",
+                                                                 local=True, splits=-1),
+                           "attention_local_q8_0": bench_attention(torch, 10, fmt="q8_0",
+                                                                   local=True, splits=-1),
                            "kv_neighbours": bench_kv_neighbours(torch),
                            "config1_chunk_sizes": bench_chain_sizes(torch)}
         # The streaming copy of each memory-bound kernel's own byte count, timed the same

@@ -288,8 +288,12 @@ int padra_CombineNorm(void *stream, void *x, const void *down, const float *weig
  * sequence, seq_stride rows apart); pos: PADRA_POS_DECODE states.  local != 0: a local
  * ring (BF16: cap = min(1024, capacity)), else cap must equal capacity.  splits: 1..32
  * split-K partitions, 0 for the reference's count (BF16: min(ceil(cap/32), local ? 16 : 32);
- * q8_0: local ? 16 : 32).  scratch: device fp32 workspace of
- * padra_DecodeAttentionScratch(kv->format, seqs, q_heads, splits) floats.  A sequence whose
+ * q8_0: local ? 16 : 32), -1 for the count tuned on MI355X (padra_DecodeAttentionSplits;
+ * the same as 0 for global windows, fewer splits for a local ring with many sequences).
+ * A count other than the reference's changes only the order in which the split partials
+ * are merged.  scratch: device fp32 workspace of
+ * padra_DecodeAttentionScratch(kv->format, seqs, q_heads, padra_DecodeAttentionSplits(...))
+ * floats.  A sequence whose
  * state is not admitted raises *bad and writes nothing; non-finite queries, scores or
  * outputs raise *bad.  Results match the reference within the tolerance its tensor-core
  * accumulation order (BF16) and CUDA expf/logf leave. */
@@ -308,9 +312,14 @@ int padra_DecodeAttentionFP8(void *stream, const void *q, const padra_KVCache *k
                              uint8_t *packed, float *scales, const padra_Positions *pos,
                              int seqs, int q_heads, int kv_heads, int local, int splits,
                              float *scratch, long long scratch_floats, int *bad, int act);
-/* Floats of scratch padra_DecodeAttention needs for a cache format (splits as passed,
+/* Floats of scratch padra_DecodeAttention needs for a cache format (splits as resolved,
  * 1..32); -1 if invalid. */
 long long padra_DecodeAttentionScratch(int format, int seqs, int q_heads, int splits);
+/* The split count padra_DecodeAttention runs for these arguments (splits 1..32 as given,
+ * 0: the reference's, -1: the MI355X-tuned count); -1 if invalid.  No counterpart in the
+ * reference, whose kernels fix their count: callers size the scratch with it. */
+int padra_DecodeAttentionSplits(const padra_KVCache *kv, int seqs, int kv_heads, int local,
+                                int splits);
 /* padra_DecodeAttentionNoAlloc: no counterpart in the reference.  For callers that cannot
  * allocate device memory (code under HIP graph capture, tight serving loops, harnesses
  * that forbid hipMalloc): padra_DecodeAttention with the same kernels and results, whose

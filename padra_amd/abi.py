@@ -90,6 +90,7 @@ SIGNATURES = {
     "padra_CheckFP8Paths": [_P, _P],
     "padra_CheckQ8Path": [_P, _P],
     "padra_DecodeAttentionScratch": [_I, _I, _I, _I],
+    "padra_DecodeAttentionSplits": [ctypes.POINTER(KVCache), _I, _I, _I, _I],
     "padra_DecodeAttention": [_P, _P, ctypes.POINTER(KVCache), _P, ctypes.POINTER(Positions), _I,
                               _I, _I, _I, _I, _P, ctypes.c_longlong, _P, _I],
     "padra_DecodeAttentionNoAlloc": [_P, _P, ctypes.POINTER(KVCache), _P,

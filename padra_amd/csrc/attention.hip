@@ -1138,6 +1138,32 @@ int reference_splits(const padra_KVCache *kv, int local) {
   return std::min((kv->cap + kKeys - 1) / kKeys, local ? 16 : 32);
 }
 
+// The split count for splits = -1, from a sweep on MI355X (64-sequence decode step):
+// global windows keep the reference's count (within 1.5% of the best of 8-32); a local
+// ring's 1024-key windows want about 1,024 resident waves for BF16 and q8_0 and 2,048 for
+// q8 (1 / 8 / 64 sequences, BF16: 16 / 16 / 4 splits best; q8: 32 / 32 / 8; q8_0:
+// 16 / 16 / 4; at 64 sequences 29.4 / 23.7 / 30.2 us against 40.8 / 31.8 / 49.9 us with the
+// reference's 16).
+int tuned_splits(const padra_KVCache *kv, int local, int seqs, int kv_heads) {
+  if (!local)
+    return reference_splits(kv, local);
+  const int per_seq = std::max(1, seqs);
+  if (kv->format == PADRA_KV_Q8_0)
+    return std::clamp(256 / per_seq, 4, 16); // one 4-wave workgroup per (split, sequence)
+  const int waves = kv->format == PADRA_KV_Q8 ? 2048 : 1024;
+  const int cap_splits = std::min((kv->cap + kKeys - 1) / kKeys, kv->format == PADRA_KV_Q8 ? 32 : 16);
+  return std::clamp(waves / (per_seq * std::max(1, kv_heads)), std::min(2, cap_splits), cap_splits);
+}
+
+// splits as passed (1..32), 0: the reference's count, -1: the tuned count; 0 if invalid.
+int resolve_splits(const padra_KVCache *kv, int local, int seqs, int kv_heads, int splits) {
+  if (splits == 0)
+    return reference_splits(kv, local);
+  if (splits == -1)
+    return tuned_splits(kv, local, seqs, kv_heads);
+  return splits >= 1 && splits <= 32 ? splits : 0;
+}
+
 // Both entry points: packed/scales non-null selects the merge with the FP8 encoding.
 int decode_attention(void *stream, const void *q, const padra_KVCache *kv, void *out,
                      uint8_t *packed, float *scales, const padra_Positions *pos, int seqs,
@@ -1148,7 +1174,7 @@ int decode_attention(void *stream, const void *q, const padra_KVCache *kv, void 
       kv->cap > 131072 || pos->mode != PADRA_POS_DECODE || !pos->decode || pos->maximum < 1 ||
       pos->maximum > 131072 || pos->vocab < 1 || (seqs > 1 && kv->seq_stride < kv->cap) ||
       (act != PADRA_ACT_BF16 && act != PADRA_ACT_F32) || !aligned16(kv->k) ||
-      !aligned16(kv->v) || !aligned16(scratch) || splits < 0 || splits > 32)
+      !aligned16(kv->v) || !aligned16(scratch) || splits < -1 || splits > 32)
     return PADRA_INVALID_ARGUMENT;
   if (kv->format != PADRA_KV_BF16 && kv->format != PADRA_KV_Q8 && kv->format != PADRA_KV_Q8_0)
     return PADRA_UNSUPPORTED;
@@ -1163,8 +1189,7 @@ int decode_attention(void *stream, const void *q, const padra_KVCache *kv, void 
   const bool q8 = kv->format == PADRA_KV_Q8_0, q8s = kv->format == PADRA_KV_Q8;
   if (q8 && kv_heads * kD != 512)
     return PADRA_UNSUPPORTED; // the 544-byte q8_0 row of 4 KV heads
-  if (splits == 0)
-    splits = reference_splits(kv, local);
+  splits = resolve_splits(kv, local, seqs, kv_heads, splits);
   const long long need = padra_DecodeAttentionScratch(kv->format, seqs, q_heads, splits);
   if (scratch_floats < need)
     return PADRA_INVALID_ARGUMENT;
@@ -1258,6 +1283,15 @@ int decode_attention(void *stream, const void *q, const padra_KVCache *kv, void 
 }
 } // namespace
 
+extern "C" int padra_DecodeAttentionSplits(const padra_KVCache *kv, int seqs, int kv_heads,
+                                           int local, int splits) {
+  if (!kv || seqs < 1 || kv_heads < 1 || kv->cap < 1 || splits < -1 || splits > 32 ||
+      (kv->format != PADRA_KV_BF16 && kv->format != PADRA_KV_Q8 && kv->format != PADRA_KV_Q8_0))
+    return -1;
+  return resolve_splits(kv, local, seqs, kv_heads, splits);
+}
+
+
 extern "C" int padra_DecodeAttention(void *stream, const void *q, const padra_KVCache *kv,
                                      void *out, const padra_Positions *pos, int seqs,
                                      int q_heads, int kv_heads, int local, int splits,
@@ -1321,10 +1355,10 @@ extern "C" int padra_DecodeAttentionNoAlloc(void *stream, const void *q, const p
                                             void *out, const padra_Positions *pos, int seqs,
                                             int q_heads, int kv_heads, int local, int splits,
                                             int *bad, int act) {
-  if (!kv || splits < 0 || splits > 32)
+  if (!kv || splits < -1 || splits > 32)
     return PADRA_INVALID_ARGUMENT;
-  const long long need = padra_DecodeAttentionScratch(
-      kv->format, seqs, q_heads, splits ? splits : reference_splits(kv, local));
+  splits = resolve_splits(kv, local, seqs, kv_heads, splits);
+  const long long need = padra_DecodeAttentionScratch(kv->format, seqs, q_heads, splits);
   if (need < 0)
     return PADRA_INVALID_ARGUMENT;
   if (need > PADRA_DECODE_ATTENTION_STATIC_FLOATS) {

@@ -247,15 +247,17 @@ def DecodeAttention(q, kv: abi.KVCache, out, positions: abi.Positions, bad, kv_h
     """Decode attention over a BF16 or q8_0 cache for q [seqs][q_heads][128]
     (SplitBF16 + per-head Merge, attention_gqa8_fragment_validation.cuh:79-214,
     attention_perhead_exact.cuh:7-38; q8_native EncodeQuery/Split/Merge,
-    kv_q8_native.cuh:103-363).  Allocates the fp32 scratch when none is given.  With packed
+    kv_q8_native.cuh:103-363).  splits: 0 runs the reference's split count, -1 the MI355X-tuned
+    count (fewer splits for a local ring with many sequences), 1..32 as given; anything else
+    raises ValueError.  Allocates the fp32 scratch when none is given.  With packed
     ([seqs][q_heads * 128] uint8) and scales ([seqs] fp32), the merge also writes each
     output row's E4M3 encoding (MergeQuantize, attention_merge_quantize_wide_exact.cuh:9-66)."""
     _need_cuda(q, out, bad, scratch)
     seqs, q_heads = q.shape[0], q.shape[1]
-    if kv.format == abi.KV_Q8_0:
-        used = splits or (16 if local else 32)
-    else:
-        used = splits or min((kv.cap + 31) // 32, 16 if local else 32)
+    used = abi.lib().padra_DecodeAttentionSplits(ctypes.byref(kv), seqs, int(kv_heads),
+                                                 int(bool(local)), int(splits))
+    if used < 1:
+        raise ValueError("invalid decode attention arguments")
     need = abi.lib().padra_DecodeAttentionScratch(kv.format, seqs, q_heads, used)
     if scratch is None:
         scratch = torch.empty(need, dtype=torch.float32, device=q.device)

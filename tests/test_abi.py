@@ -194,3 +194,31 @@ def test_host_validation_newer_entry_points():
         None, bad) == abi.INVALID_ARGUMENT
     assert lib.padra_StreamCopy(None, _p(16), _p(32), 24) == abi.INVALID_ARGUMENT
     assert lib.padra_StreamCopy(None, _p(16), _p(40), 32) == abi.INVALID_ARGUMENT
+
+
+def test_decode_attention_split_counts():
+    """padra_DecodeAttentionSplits: 0 gives the reference's count, -1 the tuned count for a
+    local ring (a global window keeps the reference's), 1..32 as given, anything else -1."""
+    lib = abi.lib()
+
+    def splits(fmt, cap, seqs, local, s, kv_heads=4):
+        kv = abi.KVCache(fmt, None, None, None, cap, 0, 0)
+        return lib.padra_DecodeAttentionSplits(ctypes.byref(kv), seqs, kv_heads, local, s)
+
+    bf16, q8, q8_0 = abi.KV_BF16, abi.KV_Q8, abi.KV_Q8_0
+    # reference counts: min(ceil(cap / 32), 16 local / 32 global); q8_0 always 16 / 32
+    assert splits(bf16, 4096, 64, 1, 0) == 16 and splits(bf16, 4096, 64, 0, 0) == 32
+    assert splits(bf16, 100, 64, 0, 0) == 4 and splits(q8_0, 100, 64, 0, 0) == 32
+    assert splits(q8_0, 4096, 1, 1, 0) == 16
+    # tuned, local: ~1,024 resident waves (BF16, q8_0 by sequences alone), ~2,048 for q8
+    assert [splits(bf16, 4096, n, 1, -1) for n in (1, 8, 40, 64, 512)] == [16, 16, 6, 4, 2]
+    assert [splits(q8, 4096, n, 1, -1) for n in (1, 8, 40, 64, 512)] == [32, 32, 12, 8, 2]
+    assert [splits(q8_0, 4096, n, 1, -1) for n in (1, 8, 40, 64, 512)] == [16, 16, 6, 4, 4]
+    assert splits(bf16, 100, 1, 1, -1) == 4 and splits(bf16, 64, 64, 1, -1) == 2
+    assert splits(bf16, 4096, 64, 1, -1, kv_heads=1) == 16
+    # tuned, global: the reference's count
+    for fmt in (bf16, q8, q8_0):
+        assert splits(fmt, 4096, 64, 0, -1) == splits(fmt, 4096, 64, 0, 0)
+    # explicit counts pass through; out of range is invalid
+    assert splits(bf16, 4096, 64, 1, 7) == 7 and splits(q8, 4096, 64, 0, 32) == 32
+    assert splits(bf16, 4096, 64, 1, 33) == -1 and splits(bf16, 4096, 64, 1, -2) == -1

@@ -1,5 +1,7 @@
 """GPU parity of the KV store/commit/decode, row rotation, SwiGLU and embedding gather
 kernels against the CPU oracle, through the C-ABI.  Exact equality throughout."""
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -530,6 +532,76 @@ def test_decode_attention_f32_and_invalid(oracle):
     for s in range(2):
         want, _, _ = oracle.decode_attention(q[s], kc[s], vc[s], positions[s])
         assert _attn_close(synth.bf16_bits(got[s]), want)[0].all()
+
+
+
+@pytest.mark.parametrize("fmt", [abi.KV_BF16, abi.KV_Q8, abi.KV_Q8_0])
+def test_decode_attention_tuned_splits(oracle, fmt):
+    """splits = -1 on a local ring of 40 sequences runs the MI355X count (6 / 12 / 6 splits
+    for BF16 / q8 / q8_0, against the reference's 16): the result is the oracle's at that
+    count, within the _attn_close tolerance."""
+    seqs, hq, hkv, capacity, cap = 40, 16, 4, 4096, 1024
+    kv_probe = abi.KVCache(fmt, None, None, None, cap, 0, 0)
+    used = abi.lib().padra_DecodeAttentionSplits(ctypes.byref(kv_probe), seqs, hkv, 1, -1)
+    print(f"[case] decode attention tuned splits fmt={fmt} -> {used}", flush=True)
+    assert used == (12 if fmt == abi.KV_Q8 else 6)
+    rng = np.random.default_rng(150 + fmt)
+    positions = rng.integers(0, capacity, seqs).astype(np.int32)
+    positions[0], positions[1], positions[2] = 0, 33, 1023
+    q = synth.bf16_bits((rng.standard_normal((seqs, hq, 128)) * 2).astype(np.float32))
+    states = np.zeros((seqs, 8), np.int32)
+    for s, p in enumerate(positions):
+        states[s] = [5, p, capacity, 10, p, min(p, 1024), 0, 0]
+    if fmt == abi.KV_Q8_0:
+        rk = np.zeros((seqs, cap, 544), np.uint8)
+        rv = np.zeros((seqs, cap, 544), np.uint8)
+        for s in range(seqs):
+            d = synth.chain_inputs(cap, outliers=True, seed=300 + s)
+            oracle.kv_q8_0_encode(d["k"], d["v"], rk[s], rv[s], np.arange(cap, dtype=np.int32),
+                                  cap)
+        kv = ops.kv_cache(fmt, dev(rk.reshape(seqs * cap, 544)), dev(rv.reshape(seqs * cap, 544)),
+                          cap, seq_stride=cap)
+    elif fmt == abi.KV_Q8:
+        codes_k = rng.integers(-127, 128, (seqs, cap, hkv * 128)).astype(np.int8)
+        codes_v = rng.integers(-127, 128, (seqs, cap, hkv * 128)).astype(np.int8)
+        scales = rng.uniform(0.005, 0.02, (seqs, cap, hkv, 2)).astype(np.float32)
+        kc = synth.bf16_bits(codes_k.reshape(seqs, cap, hkv, 128).astype(np.float32) *
+                             scales[..., 0:1]).reshape(seqs, cap, -1)
+        vc = synth.bf16_bits(codes_v.reshape(seqs, cap, hkv, 128).astype(np.float32) *
+                             scales[..., 1:2]).reshape(seqs, cap, -1)
+        kv = ops.kv_cache(fmt, torch.from_numpy(codes_k.reshape(seqs * cap, -1)).cuda(),
+                          torch.from_numpy(codes_v.reshape(seqs * cap, -1)).cuda(), cap,
+                          scales=torch.from_numpy(scales.reshape(seqs * cap, hkv, 2)).cuda(),
+                          seq_stride=cap)
+    else:
+        kc = synth.bf16_bits(rng.standard_normal((seqs, cap, hkv * 128)).astype(np.float32))
+        vc = synth.bf16_bits(rng.standard_normal((seqs, cap, hkv * 128)).astype(np.float32))
+        kv = ops.kv_cache(fmt, dev(kc.reshape(seqs * cap, -1)), dev(vc.reshape(seqs * cap, -1)),
+                          cap, seq_stride=cap)
+    out = torch.empty((seqs, hq, 128), dtype=torch.int16, device="cuda")
+    bad = flag()
+    ops.DecodeAttention(dev(q), kv, out, ops.positions_decode(torch.from_numpy(states).cuda(),
+                                                              maximum=capacity),
+                        bad, kv_heads=hkv, local=True, splits=-1)
+    torch.cuda.synchronize()
+    assert bad.item() == 0
+    got = host16(out)
+    worst = 0
+    for s in range(seqs):
+        if fmt == abi.KV_Q8_0:
+            want, wsplits, wbad = oracle.decode_attention_q8_0(q[s], rk[s], rv[s], positions[s],
+                                                               local=True, splits=used)
+        else:
+            want, wsplits, wbad = oracle.decode_attention(q[s], kc[s], vc[s], positions[s],
+                                                          local=True, splits=used)
+        # the splits the oracle ran: the count, capped by the window's tiles (32 keys; 128
+        # for q8_0)
+        tile = 128 if fmt == abi.KV_Q8_0 else 32
+        assert not wbad and wsplits == min(used, (min(positions[s] + 1, cap) + tile - 1) // tile)
+        close, d = _attn_close(got[s], want)
+        worst = max(worst, int(d.max()))
+        assert close.all(), (s, int(d.max()))
+    print(f"  max BF16 ulp difference {worst}", flush=True)
 
 
 @pytest.mark.parametrize("hq,local", [(16, False), (32, False), (16, True), (4, False),
