@@ -116,16 +116,21 @@ __device__ __forceinline__ void encode_quad_rt(const A &a, float (&x)[32], long 
     if constexpr (FMT == PADRA_KV_Q8_0) {
       // q8_native::Rotate (kv_q8_native.cuh:22-45): feature bits 0-4 in the lane, bit 5
       // across lanes g ^ 1, bit 6 (K only) across lanes g ^ 2, then the scale.
+      // Both quad stages in the signed form (hadamard_quad_signed): the value held is the
+      // rotated one times -1 per stage taken on an upper lane, and that sign rides in the
+      // scale multiply (codes do not see the sign of a zero).
       hadamard32(x);
-      hadamard_quad<1>(x, g);
-      const float sgn = isv || !(g & 2) ? 1.f : -1.f;
-      const float sc = isv ? .125f : .08838834764831845f;
+      hadamard_quad_signed<1>(x, g);
+      const bool neg2 = !isv && (g & 2);
+      const float sgn = neg2 ? -1.f : 1.f;
+      const float sc = ((g & 1) != neg2) ? (isv ? -.125f : -.08838834764831845f)
+                                         : (isv ? .125f : .08838834764831845f);
 #pragma unroll
       for (int f = 0; f < 32; ++f) {
         // lane g ^ 2's value in the K rows (rows 0 and 1 of the wave), 0 in the V rows
         const float other = __int_as_float(__builtin_amdgcn_update_dpp(
             0, __float_as_int(x[f]), 0x4e /* quad_perm [2,3,0,1] */, 0x3, 0xf, false));
-        x[f] = __builtin_fmaf(sgn, x[f], other) * sc;
+        x[f] = __builtin_fmaf(other, sgn, x[f]) * sc;
       }
     }
     // Block g (kv_q8_native.cuh:84-99): d = half(amax/127), codes roundf(x * (1/d_fp32)).

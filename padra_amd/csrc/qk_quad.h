@@ -91,6 +91,49 @@ __device__ __forceinline__ void v_rows_copy16(const A &a, unsigned block0, unsig
 // (D = 1: feature bit 5, D = 2: bit 6); the lower lane keeps lower + upper, the upper lane
 // lower - upper.  Both are one fused multiply-add other + s * x with s = +-1: s * x is
 // exact, so it rounds once, as the sum or difference does.
+// Signed form, for values that only feed q8_0 codes: x + s * partner with s = -1 on the
+// upper lane, one fused multiply-add whose partner operand is read across lanes inside the
+// instruction (no separate lane move).  The upper lane then holds upper - lower, the exact
+// negation of the rounded lower - upper (round-to-nearest-even is symmetric), so the true
+// value is sign_quad * x with sign_quad = -1 on upper lanes; the caller folds the product
+// of the stages' signs into its scale multiply.  Only the sign of a zero result can differ
+// from hadamard_quad's, and codes (|x| maximum, rounded magnitudes) do not see it.
+// The compiler does not fold a lane move into v_fmac_f32, so each half of the values is
+// one asm block of sixteen v_fmac_f32_dpp.  The s_nop 1 at its head gives the two wait
+// states a DPP read needs after a VALU write of its source; inside the block every
+// instruction reads a register no earlier instruction of the block wrote; the s_nop 1 at
+// its tail covers a DPP read of the block's last results that follows it (the hazard
+// recognizer does not see the block's writes as VALU writes).
+#define PADRA_FMAC_DPP(i, perm) \
+  "v_fmac_f32_dpp %" #i ", %" #i ", %16 quad_perm:" perm " row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+#define PADRA_FMAC_DPP16(perm)                                                            \
+  "s_nop 1\n" PADRA_FMAC_DPP(0, perm) PADRA_FMAC_DPP(1, perm) PADRA_FMAC_DPP(2, perm)     \
+      PADRA_FMAC_DPP(3, perm) PADRA_FMAC_DPP(4, perm) PADRA_FMAC_DPP(5, perm)             \
+          PADRA_FMAC_DPP(6, perm) PADRA_FMAC_DPP(7, perm) PADRA_FMAC_DPP(8, perm)         \
+              PADRA_FMAC_DPP(9, perm) PADRA_FMAC_DPP(10, perm) PADRA_FMAC_DPP(11, perm)   \
+                  PADRA_FMAC_DPP(12, perm) PADRA_FMAC_DPP(13, perm)                       \
+                      PADRA_FMAC_DPP(14, perm) PADRA_FMAC_DPP(15, perm) "s_nop 1\n"
+template <int D> __device__ __forceinline__ void hadamard_quad_signed(float (&x)[32], int g) {
+  const float sgn = (g & D) ? -1.f : 1.f;
+#pragma unroll
+  for (int h = 0; h < 32; h += 16) {
+    float *y = x + h;
+    if constexpr (D == 1)
+      asm volatile(PADRA_FMAC_DPP16("[1,0,3,2]")
+                   : "+v"(y[0]), "+v"(y[1]), "+v"(y[2]), "+v"(y[3]), "+v"(y[4]), "+v"(y[5]),
+                     "+v"(y[6]), "+v"(y[7]), "+v"(y[8]), "+v"(y[9]), "+v"(y[10]), "+v"(y[11]),
+                     "+v"(y[12]), "+v"(y[13]), "+v"(y[14]), "+v"(y[15])
+                   : "v"(sgn));
+    else
+      asm volatile(PADRA_FMAC_DPP16("[2,3,0,1]")
+                   : "+v"(y[0]), "+v"(y[1]), "+v"(y[2]), "+v"(y[3]), "+v"(y[4]), "+v"(y[5]),
+                     "+v"(y[6]), "+v"(y[7]), "+v"(y[8]), "+v"(y[9]), "+v"(y[10]), "+v"(y[11]),
+                     "+v"(y[12]), "+v"(y[13]), "+v"(y[14]), "+v"(y[15])
+                   : "v"(sgn));
+  }
+}
+#undef PADRA_FMAC_DPP16
+#undef PADRA_FMAC_DPP
 template <int D> __device__ __forceinline__ void hadamard_quad(float (&x)[32], int g) {
   const float sgn = (g & D) ? -1.f : 1.f;
 #pragma unroll
@@ -145,20 +188,16 @@ __device__ __forceinline__ QuadCodes quad_codes(float (&x)[32], int g) {
     }
   } else {
     if constexpr (FMT == PADRA_KV_Q8_0) {
+      // the stages' signs (lane bit 0 for bit 5, lane bit 1 for bit 6) ride in the scale
       hadamard32(x);
-      hadamard_quad<1>(x, g);
-      if constexpr (!ISV) {
-        const float sgn = (g & 2) ? -1.f : 1.f;
+      hadamard_quad_signed<1>(x, g);
+      if constexpr (!ISV)
+        hadamard_quad_signed<2>(x, g);
+      const float sc = ((g ^ (ISV ? 0 : g >> 1)) & 1) ? -(ISV ? .125f : .08838834764831845f)
+                                                      : (ISV ? .125f : .08838834764831845f);
 #pragma unroll
-        for (int f = 0; f < 32; ++f) {
-          const float other = __uint_as_float(quad_xor2(__float_as_uint(x[f])));
-          x[f] = __builtin_fmaf(sgn, x[f], other) * .08838834764831845f;
-        }
-      } else {
-#pragma unroll
-        for (int f = 0; f < 32; ++f)
-          x[f] = x[f] * .125f;
-      }
+      for (int f = 0; f < 32; ++f)
+        x[f] = x[f] * sc;
     }
     float am = 0.f;
 #pragma unroll
