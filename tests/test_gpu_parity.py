@@ -827,3 +827,68 @@ def test_decode_chain_graph_replays(oracle, fmt):
             assert np.array_equal(kca[s], ek) and np.array_equal(vca[s], ev), (replay, s)
             if es is not None:
                 assert np.array_equal(sca[s], es), (replay, s)
+
+
+def _cancelling_heads(rng, tokens):
+    """[tokens][4][128] floats whose rotation cancels: pattern (t * 4 + h) % 5 is
+    0: features 32-63 equal 0-31 and 96-127 equal 64-95 (the bit-5 stage's differences
+    are exact zeros), 1: every feature equal (every output but the first is zero),
+    2: features 64-127 equal 0-63 (the K bit-6 stage's differences), 3: features 32-63
+    the negation of 0-31 and 96-127 of 64-95 (zero sums), 4: unstructured."""
+    x = rng.standard_normal((tokens, 4, 128)).astype(np.float32)
+    kind = (np.arange(tokens)[:, None] * 4 + np.arange(4)[None, :]) % 5
+    for t in range(tokens):
+        for h in range(4):
+            r = x[t, h]
+            if kind[t, h] == 0:
+                r[32:64], r[96:128] = r[0:32], r[64:96]
+            elif kind[t, h] == 1:
+                r[:] = r[0]
+            elif kind[t, h] == 2:
+                r[64:] = r[:64]
+            elif kind[t, h] == 3:
+                r[32:64], r[96:128] = -r[0:32], -r[64:96]
+    return synth.bf16_bits(x)
+
+
+@pytest.mark.parametrize("fmt", [abi.KV_Q8_0, abi.KV_Q8_0_NOROT])
+@pytest.mark.parametrize("path", ["store", "chain"])
+@pytest.mark.parametrize("tokens", [40, 400])
+def test_q8_0_cancelling_heads(oracle, fmt, path, tokens):
+    """K and V heads whose rotation stages produce exact zeros (equal or opposite halves):
+    the cross-lane stages hold the upper lane's value negated and fold the signs into the
+    scale multiply, so a zero there is -0 before the codes; the codes and scales must
+    still equal the oracle's byte for byte.  Both the store-only encoder and the fused
+    Q/K store (there the table is cos 1, sin 0 and the K norm weight 1, so K keeps its
+    structure through the norm and RoPE), in both launch shapes."""
+    print(f"[case] q8_0 cancelling heads fmt={fmt} path={path} tokens={tokens}", flush=True)
+    capacity = 4096
+    rng = np.random.default_rng(1234 + tokens)
+    d = synth.chain_inputs(tokens, outliers=False, seed=5 + tokens)
+    d["k"] = _cancelling_heads(rng, tokens).reshape(d["k"].shape)
+    d["v"] = _cancelling_heads(rng, tokens).reshape(d["v"].shape)
+    positions = np.arange(tokens, dtype=np.int32)
+    kc, vc, _ = _alloc_cache(fmt, capacity)
+    bad = flag()
+    kv = ops.kv_cache(fmt, kc, vc, capacity)
+    if path == "store":
+        wk = d["k"]
+        ops.KVStore(dev(d["k"]), dev(d["v"]), ops.positions_base(0), kv, bad)
+    else:
+        d["kn"] = np.full_like(d["kn"], 0x3F80)
+        tb = np.zeros((capacity, 128), np.uint16)
+        tb[:, :64] = 0x3F80
+        wq, wk, _ = _qk_oracle(oracle, d, tb, positions)
+        q, k = dev(d["q"]), dev(d["k"])
+        ops.QKNormRopeStore(q, k, dev(d["qn"]), dev(d["kn"]), dev(tb), ops.positions_base(0),
+                            bad, v=dev(d["v"]), kv=kv)
+    torch.cuda.synchronize()
+    assert not bad.item()
+    ek, ev, _ = _expected_cache(oracle, fmt, wk, d["v"], positions, capacity, 0)
+    if fmt == abi.KV_Q8_0:
+        # the structure reaches the codes: most rotated codes of patterns 0-3 are zero
+        assert (ek[:tokens, 32:] == 0).mean() > 0.3 and (ev[:tokens, 32:] == 0).mean() > 0.3
+    if path == "chain":
+        assert np.array_equal(host16(q), wq) and np.array_equal(host16(k), wk)
+    assert np.array_equal(_np(kc, fmt), ek)
+    assert np.array_equal(_np(vc, fmt), ev)
