@@ -102,6 +102,11 @@ template <int M> __device__ __forceinline__ int lane_xor(int v) {
 template <int M> __device__ __forceinline__ uint32_t lane_xor(uint32_t v) {
   return lane_xor_u<M>(v);
 }
+template <int M> __device__ __forceinline__ double lane_xor(double v) {
+  const uint64_t b = (uint64_t)__double_as_longlong(v);
+  const uint64_t lo = lane_xor_u<M>((uint32_t)b), hi = lane_xor_u<M>((uint32_t)(b >> 32));
+  return __longlong_as_double((long long)((hi << 32) | lo));
+}
 // Lane 0's value, as a wave-uniform scalar.
 __device__ __forceinline__ float lane0(float v) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
@@ -114,12 +119,82 @@ template <int TOP, class V, class Op> __device__ __forceinline__ V xor_reduce(V 
   else
     return v;
 }
+// ---------------------------------------------------------------------------------------
+// Sum of squares without the reference's order, rounded to the reference's result when
+// that result is certain.
+//
+// The reference sums the fp32 squares p_i >= 0 of a row (or head) with Accumulate
+// (inference.cu:103-109) over a fixed tree: each thread folds its m squares in order,
+// then ten shuffle-down levels (a warp's five, then five over the warp partials), two
+// Accumulate steps per level, and it returns RN32(s + e) (inference.cu:134).  In every
+// Accumulate step the new sum is RN(sum + value) and its rounding error is recovered
+// exactly (Fast2Sum with the larger magnitude first); only `error = RN(error +
+// residual)` rounds.  So s + e = S - sum_k delta_k exactly, S = sum p_i, where delta_k is
+// the rounding error of the k-th error update, |delta_k| <= u |e_k|, u = 2^-24.
+// Bound, for S < 2^126 (no partial overflows):
+//  - every residual is at most u |next| of its step; along the tree that feeds the
+//    result the steps' |next| add up to at most (m + 20) S (1 + 2^-20): each thread's
+//    m partial sums are below its share of S, and each of the ten levels adds two steps
+//    per receiving lane whose sums are disjoint parts of S;
+//  - a residual enters at most D = m + 20 error updates on its way to the result (the
+//    thread's m, then two per level), so sum_k |e_k| <= D (1 + 2^-20) sum |residual|;
+//  - hence |s + e - S| <= 1.003 (m + 20)^2 u^2 S.
+// The fp64 sum S64 of the same p_i (each exact in fp64), in any order whose longest
+// chain of additions is `depth`, is within 1.001 depth 2^-53 S of S.  If RN32 maps both
+// ends of [S64 (1 - c), S64 (1 + c)] to the same float f, with c above the sum of both
+// bounds (and the rounding of the two ends), then S and s + e lie inside that interval,
+// and RN32 being monotone, the reference's RN32(s + e) = f.
+// Squares of BF16 values are exact in fp32 except below 2^-126, where RN32 moves each by at
+// most 2^-150; with S >= 2^-60 that is under 2^-77 S for any row here, inside the 2^-51
+// slack of the margin.
+// Otherwise (a result near an fp32 rounding midpoint, about 2 c / 2^-23.5 of rows, or S
+// outside [2^-60, 2^126), or a non-finite square) the caller replays the reference tree.
+// m: squares per reference thread; depth: the fp64 summation's longest chain.
+__host__ __device__ constexpr double sumsq_margin(int m, int depth) {
+  return 1.01 * (1.003 * (m + 20.0) * (m + 20.0) * 0x1p-48 + 1.001 * depth * 0x1p-53) +
+         0x1p-51;
+}
+// RN32 of an fp64 sum of squares when it is certain to equal the reference's compensated
+// result (`out`), else false.  A NaN or infinite s fails the tests.
+__device__ __forceinline__ bool certified_sum(double s, double margin, float &out) {
+  const float lo = (float)__builtin_fma(-margin, s, s);
+  const float hi = (float)__builtin_fma(margin, s, s);
+  out = hi;
+  return (lo == hi) & (s >= 0x1p-60) & (s < 0x1p126);
+}
+// acc + v^2 in fp64 for a BF16-exact v (v^2 has at most 16 significant bits: exact).
+__device__ __forceinline__ double sq64(float v, double acc) {
+  return __builtin_fma((double)v, (double)v, acc);
+}
+// acc + RN32(v * v) in fp64, for any fp32 v (the reference's __fmul_rn square).
+__device__ __forceinline__ double sq64_rn(float v, double acc) { return acc + (double)(v * v); }
+// The wave's total of an fp64 value, in every lane (xor butterfly: each level adds the
+// same two values in every lane, so all lanes end equal).
+__device__ __forceinline__ double wave_sum64(double v) {
+  return xor_reduce<32>(v, [](double a, double b) { return a + b; });
+}
+
 // One Hadamard stage on lane bit log2(M): lower' = lower + upper, upper' = lower - upper,
 // as one fused multiply-add with the lane's sign (+-1 products are exact, so the sum is
 // rounded once, as the add or subtract is).
 template <int M> __device__ __forceinline__ float hadamard_lane(float v, int lane) {
   const float o = lane_xor<M>(v);
   return __builtin_fmaf((lane & M) ? -1.f : 1.f, v, o);
+}
+
+// An empty use of v at this point of the program: its load is issued before here and is
+// not sunk past a later branch.
+__device__ __forceinline__ void pin(const uint4 &v) {
+  asm volatile("" : : "v"(v.x), "v"(v.y), "v"(v.z), "v"(v.w));
+}
+__device__ __forceinline__ void pin(uint32_t v) { asm volatile("" : : "v"(v)); }
+// A point that the compiler moves no instruction across: memory accesses written before it
+// stay before (the clobber), and the machine scheduler moves nothing over it (a
+// sched_barrier with an empty mask), so loads written before it are issued before any
+// instruction written after it.
+__device__ __forceinline__ void issue_point() {
+  asm volatile("" : : : "memory");
+  __builtin_amdgcn_sched_barrier(0);
 }
 
 // Streaming (non-temporal) global accesses for data each launch touches once: the

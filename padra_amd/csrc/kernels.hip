@@ -19,10 +19,14 @@ using namespace padra;
 
 namespace {
 
+// BF16 rows: the 16-byte layout and the order-free sum of squares; fp32 rows: the
+// ownership layout and the reference tree (the order-free sum measured slower there:
+// 11.28 -> 11.95 us at 2048 x 2048).
 template <int VT, int J, class T, bool RES>
 __global__ __launch_bounds__(64) void k_norm(NormArgs<T> a) {
   __shared__ uint4 lds[VT * J / 8];
-  norm_row_wave<VT, J, T, RES>(a, blockIdx.x, lds);
+  constexpr bool BF = std::is_same<T, uint16_t>::value;
+  norm_row_wave<VT, J, T, RES, BF, false, BF>(a, blockIdx.x, lds);
 }
 
 template <class T, int FMT> __global__ __launch_bounds__(64) void k_qk(QKArgs<T> a) {
@@ -101,10 +105,17 @@ template <int J, class T> __global__ __launch_bounds__(64) void k_norm_fp8(NormF
 template <int VT, int J, int FMT, bool GATHER = false, class T = uint16_t>
 __global__ __launch_bounds__(64) void k_chain(NormArgs<T> n, QKArgs<T> q, long long norm_waves,
                                               long long waves) {
-  __shared__ uint4 lds[quad_image_slots_fmt<T, FMT>()];
+  // The order-free sums of squares (sumsq_margin, common.h) with a BF16 or no cache; the
+  // reference trees alone with a quantized cache or fp32 activations, where the order-free
+  // form measured slower (rotated q8_0: 13.56 -> 14.59 us, q8: 13.10 -> 13.86 us).
+  constexpr bool FAST = FMT <= PADRA_KV_BF16 && std::is_same<T, uint16_t>::value;
+  // the Q/K waves' image, or a BF16 row of the norm waves (the rare ordered-sum replay)
+  constexpr int SLOTS = quad_image_slots_fmt<T, FMT>() > VT * J / 8 ? quad_image_slots_fmt<T, FMT>()
+                                                                    : VT * J / 8;
+  __shared__ uint4 lds[SLOTS];
   const long long b = blockIdx.x;
   if (b < norm_waves)
-    norm_row_wave<VT, J, T, true, false, GATHER>(n, (int)b, nullptr);
+    norm_row_wave<VT, J, T, true, FAST && !GATHER, GATHER, FAST>(n, (int)b, lds);
   else if (b < waves) {
     // Quantized caches: the K waves (K norm + RoPE, then the K and V encodings: the
     // heaviest waves) are dispatched before the Q waves instead of last, so they do not
@@ -124,7 +135,7 @@ __global__ __launch_bounds__(64) void k_chain(NormArgs<T> n, QKArgs<T> q, long l
 template <int VT, int J, int FMT, bool GATHER = false>
 __global__ __launch_bounds__(256) void k_chain_small(NormArgs<uint16_t> n, QKArgs<uint16_t> q,
                                                      long long rows, long long head_waves) {
-  __shared__ float partials[8][2];
+  __shared__ __attribute__((aligned(16))) float partials[8][2];
   const long long b = blockIdx.x;
   if (b < rows) { // workgroup-uniform
     norm_row_wg<VT, J, GATHER>(n, (int)b, partials);
@@ -153,7 +164,7 @@ __global__ __launch_bounds__(64) void k_chain_heads(NormArgs<T> n, QKArgs<T> q,
 // Residual + RMSNorm, BF16 rows, one 256-lane workgroup per row (norm_wg.h).
 template <int VT, int J>
 __global__ __launch_bounds__(256) void k_norm_small(NormArgs<uint16_t> n) {
-  __shared__ float partials[8][2];
+  __shared__ __attribute__((aligned(16))) float partials[8][2];
   norm_row_wg<VT, J, false>(n, blockIdx.x, partials);
 }
 
@@ -552,7 +563,6 @@ int chain(hipStream_t s, const uint16_t *gather, int vocab, const int32_t *ids, 
   }
   const QKArgs<uint16_t> a = make_qk<uint16_t>(q, k, v, qn, kn, table, table_rows, pos, tokens,
                                                q_heads, kv_heads, eps, kv, bad);
-  const long long norm_waves = (tokens + rows_per_wave(tree) - 1) / rows_per_wave(tree);
   return chain_shape(tree, hidden / tree, [&](auto vt, auto j) -> int {
     return with_flag(gather != nullptr, [&](auto g) -> int {
       return with_format(kv, [&](auto fmt) -> int {
@@ -566,12 +576,13 @@ int chain(hipStream_t s, const uint16_t *gather, int vocab, const int32_t *ids, 
             hipLaunchKernelGGL((k_chain_small<VT, J, FMT, G>), grid, block, 0, s, n, a,
                                (long long)tokens, heads);
           } else {
-            const long long waves = norm_waves + heads;
+            const long long norm_waves = tokens, waves = norm_waves + heads;
             hipLaunchKernelGGL((k_chain_heads<VT, J, FMT, G>), dim3((unsigned)waves),
                                dim3(64), 0, s, n, a, norm_waves, waves);
           }
           return launched();
         }
+        const long long norm_waves = tokens;
         const long long waves = norm_waves + qk_wave_count<FMT>(tokens, q_heads, kv_heads);
         hipLaunchKernelGGL((k_chain<VT, J, FMT, G>), dim3((unsigned)waves), dim3(64), 0, s, n,
                            a, norm_waves, waves);

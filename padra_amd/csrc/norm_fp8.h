@@ -111,17 +111,31 @@ __device__ __forceinline__ void norm_fp8_finish(const NormFP8Args<T> &a, int row
   constexpr int VT = 128, K = 2, H = VT * J;
   const int lane = threadIdx.x & 63;
   const size_t off = (size_t)row * H + K * lane;
-  float s[K] = {0.f, 0.f}, e[K] = {0.f, 0.f};
+  // The order-free sum (sumsq_margin, common.h), or (rarely; wave-uniform) the tree.
+  double acc[4] = {0.0, 0.0, 0.0, 0.0}; // independent fp64 chains
 #pragma unroll
   for (int j = 0; j < J; ++j) {
-    const float v0 = lo16(vp[j]), v1 = hi16(vp[j]);
-    acc_pos(v0 * v0, s[0], e[0]);
-    acc_pos(v1 * v1, s[1], e[1]);
+    acc[2 * (j & 1)] = sq64(lo16(vp[j]), acc[2 * (j & 1)]);
+    acc[2 * (j & 1) + 1] = sq64(hi16(vp[j]), acc[2 * (j & 1) + 1]);
   }
-  warp_tree<K>(s, e);
-  float S = s[0], E = e[0];
-  partials_tree<VT / 32, 32 / K>(S, E);
-  const float total = lane0(S + E);
+  const double lane_sum = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+#pragma unroll
+  for (int j = 0; j < J; ++j)
+    pin(gr[j].w[0]); // the gamma loads stay ahead of the rarely taken branch below
+  float total;
+  if (!certified_sum(wave_sum64(lane_sum), sumsq_margin(J, 2 * J + 6), total)) {
+    float s[K] = {0.f, 0.f}, e[K] = {0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      const float v0 = lo16(vp[j]), v1 = hi16(vp[j]);
+      acc_pos(v0 * v0, s[0], e[0]);
+      acc_pos(v1 * v1, s[1], e[1]);
+    }
+    warp_tree<K>(s, e);
+    float S = s[0], E = e[0];
+    partials_tree<VT / 32, 32 / K>(S, E);
+    total = lane0(S + E);
+  }
   const float variance = total / (float)H;
   const float inv = 1.f / sqrtf(variance + a.eps);
   if (a.stats && row == 0 && lane == 0) {

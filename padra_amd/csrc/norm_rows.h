@@ -1,5 +1,8 @@
 // Residual-add + RMSNorm over hidden rows: one 64-lane wavefront per row.
 //
+// The sum of squares: where a kernel takes the order-free fp64 sum (sumsq_margin,
+// common.h), the tree below is its rarely taken fallback; elsewhere it is the sum.
+//
 // Reference: Add + Norm (inference.cu:475-481, 188-214) for VT = 128 and
 // ResidualPostNormWideExact (residual_norm_wide_exact.cuh:6-80) for VT = 256.  The
 // reference block has VT threads; thread t owns elements t, t+VT, t+2VT, ... and sums
@@ -196,15 +199,11 @@ __device__ __forceinline__ void norm_load_gamma(const uint16_t *gamma,
     gr[j].template load<false>(gamma + K * (threadIdx.x & 63) + VT * j);
 }
 
-// Everything after the loads: v = B(x + r), the reference reduction tree, the outputs.
-template <int VT, int J, class T, bool RES>
-__device__ __forceinline__ void norm_compute(const NormArgs<T> &a, int row,
-                                             const RowIn<VT, J, T> &in,
-                                             const Lanes<uint16_t, VT / 64> (&gr)[J]) {
-  constexpr int K = VT / 64, H = VT * J, LPW = 32 / K, WARPS = VT / 32;
-  const int lane = threadIdx.x & 63;
-  const size_t off = (size_t)row * H + K * lane;
-  uint32_t vp[J][K / 2];
+// The reference's per-thread compensated sums over packed v words (lane l: threads
+// K l .. K l + K - 1, words vp[j][w]) and its tree: the row's total in every lane.
+template <int VT, int J>
+__device__ __forceinline__ float ordered_total(const uint32_t (&vp)[J][VT / 128]) {
+  constexpr int K = VT / 64, LPW = 32 / K, WARPS = VT / 32;
   float s[K], e[K];
 #pragma unroll
   for (int k = 0; k < K; ++k) {
@@ -215,26 +214,95 @@ __device__ __forceinline__ void norm_compute(const NormArgs<T> &a, int row,
   for (int j = 0; j < J; ++j) {
 #pragma unroll
     for (int w = 0; w < K / 2; ++w) {
-      const float a0 = RES ? in.x[j].get(2 * w) + in.r[j].get(2 * w) : in.x[j].get(2 * w);
-      const float a1 =
-          RES ? in.x[j].get(2 * w + 1) + in.r[j].get(2 * w + 1) : in.x[j].get(2 * w + 1);
-      vp[j][w] = pack2(a0, a1);
       const float v0 = lo16(vp[j][w]), v1 = hi16(vp[j][w]);
       acc_pos(v0 * v0, s[2 * w], e[2 * w]);
       acc_pos(v1 * v1, s[2 * w + 1], e[2 * w + 1]);
     }
-  }
-  if constexpr (RES) {
-#pragma unroll
-    for (int j = 0; j < J; ++j)
-      Lanes<T, K>::store(a.x + off + VT * j, vp[j]);
   }
   warp_tree<K>(s, e);
   float S = s[0], E = e[0];
   partials_tree<WARPS, LPW>(S, E);
   // lane 0's total through ds_bpermute: a v_readlane here measured 0.8% slower on the
   // quantized chunk chains (13.76 -> 13.89 us, q8_0)
-  const float total = __shfl(S + E, 0, 64);
+  return __shfl(S + E, 0, 64);
+}
+
+// Everything after the loads: v = B(x + r), the sum of squares, the outputs.  FAST: the
+// order-free fp64 sum (sumsq_margin, common.h) with the reference tree as its rarely
+// taken fallback; otherwise the reference tree alone.  The fast form is slower in the
+// quantized-cache chain and on fp32 rows (both lose a wave of occupancy or its memory
+// schedule to it), so those keep the tree.
+template <int VT, int J, class T, bool RES, bool FAST = true>
+__device__ __forceinline__ void norm_compute(const NormArgs<T> &a, int row,
+                                             const RowIn<VT, J, T> &in,
+                                             const Lanes<uint16_t, VT / 64> (&gr)[J]) {
+  constexpr int K = VT / 64, H = VT * J, LPW = 32 / K, WARPS = VT / 32;
+  const int lane = threadIdx.x & 63;
+  const size_t off = (size_t)row * H + K * lane;
+  uint32_t vp[J][K / 2];
+  float total;
+  if constexpr (FAST) {
+    double acc[4] = {0.0, 0.0, 0.0, 0.0}; // independent fp64 chains
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+#pragma unroll
+      for (int w = 0; w < K / 2; ++w) {
+        const float a0 = RES ? in.x[j].get(2 * w) + in.r[j].get(2 * w) : in.x[j].get(2 * w);
+        const float a1 =
+            RES ? in.x[j].get(2 * w + 1) + in.r[j].get(2 * w + 1) : in.x[j].get(2 * w + 1);
+        vp[j][w] = pack2(a0, a1);
+        const int c = (2 * (j * (K / 2) + w)) & 3;
+        acc[c] = sq64(lo16(vp[j][w]), acc[c]);
+        acc[c + 1] = sq64(hi16(vp[j][w]), acc[c + 1]);
+      }
+    }
+    if constexpr (RES) {
+#pragma unroll
+      for (int j = 0; j < J; ++j)
+        Lanes<T, K>::store(a.x + off + VT * j, vp[j]);
+    }
+    // keep the gamma loads ahead of the rarely taken branch below (see norm_row_wave_wide)
+#pragma unroll
+    for (int j = 0; j < J; ++j)
+#pragma unroll
+      for (int w = 0; w < K / 2; ++w)
+        pin(gr[j].w[w]);
+    const double lane_sum = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+    if (!certified_sum(wave_sum64(lane_sum), sumsq_margin(J, J * K + 6), total))
+      total = ordered_total<VT, J>(vp); // rare, wave-uniform
+  } else {
+    // The tree alone, its per-thread sums interleaved with v (this order schedules best).
+    float s[K], e[K];
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      s[k] = 0.f;
+      e[k] = 0.f;
+    }
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+#pragma unroll
+      for (int w = 0; w < K / 2; ++w) {
+        const float a0 = RES ? in.x[j].get(2 * w) + in.r[j].get(2 * w) : in.x[j].get(2 * w);
+        const float a1 =
+            RES ? in.x[j].get(2 * w + 1) + in.r[j].get(2 * w + 1) : in.x[j].get(2 * w + 1);
+        vp[j][w] = pack2(a0, a1);
+        const float v0 = lo16(vp[j][w]), v1 = hi16(vp[j][w]);
+        acc_pos(v0 * v0, s[2 * w], e[2 * w]);
+        acc_pos(v1 * v1, s[2 * w + 1], e[2 * w + 1]);
+      }
+    }
+    if constexpr (RES) {
+#pragma unroll
+      for (int j = 0; j < J; ++j)
+        Lanes<T, K>::store(a.x + off + VT * j, vp[j]);
+    }
+    warp_tree<K>(s, e);
+    float S = s[0], E = e[0];
+    partials_tree<WARPS, LPW>(S, E);
+    // lane 0's total through ds_bpermute: a v_readlane here measured 0.8% slower on the
+    // quantized chunk chains (13.76 -> 13.89 us, q8_0)
+    total = __shfl(S + E, 0, 64);
+  }
   const float variance = total / (float)H;
   const float inv = 1.f / sqrtf(variance + a.eps);
   if (a.stats && lane == 0) {
@@ -266,10 +334,11 @@ __device__ __forceinline__ void norm_compute(const NormArgs<T> &a, int row,
 
 // BF16 rows with 16-byte accesses.  Piece c of lane L is elements 512c + 8L .. 512c + 8L + 7
 // of x, the residual, gamma and the outputs: every load and store of the row is a 1 KB
-// coalesced instruction (4 per tensor at H = 2048, instead of 16 of 4 or 8 bytes).  Only
-// the sum of squares needs the reference's thread ownership (thread t: elements t + VT j,
-// summed in j order): v = B(x + r) crosses LDS once, packed, and each lane reads back the
-// words of its K threads.  The outputs are elementwise and stay in the piece layout.
+// coalesced instruction (4 per tensor at H = 2048, instead of 16 of 4 or 8 bytes).  The
+// sum of squares is the order-free fp64 sum (sumsq_margin, common.h), so it needs no
+// thread ownership; only its rare fallback, the reference's per-thread sums (thread t:
+// elements t + VT j, summed in j order) and tree, sends v = B(x + r) across LDS once so
+// that each lane can read the words of its K threads.
 template <int VT, int J, bool RES>
 __device__ __forceinline__ void norm_row_wave_wide(const NormArgs<uint16_t> &a, int row,
                                                    uint4 *vlds) {
@@ -278,13 +347,19 @@ __device__ __forceinline__ void norm_row_wave_wide(const NormArgs<uint16_t> &a, 
   const int lane = threadIdx.x & 63;
   const size_t base = (size_t)row * H;
   uint4 xin[C], rin[C], gin[C];
+  // gamma first (cache-resident: it returns first), then x and the residual
 #pragma unroll
   for (int c = 0; c < C; ++c) {
     const int e = (512 * c + 8 * lane < H) ? 512 * c + 8 * lane : 0; // clamped, unconditional
+    gin[c] = *reinterpret_cast<const uint4 *>(a.gamma + e);
+  }
+  issue_point();
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+    const int e = (512 * c + 8 * lane < H) ? 512 * c + 8 * lane : 0;
     xin[c] = ld_nt(reinterpret_cast<const uint4 *>(a.x + base + e));
     if constexpr (RES)
       rin[c] = ld_nt(reinterpret_cast<const uint4 *>(a.residual + base + e));
-    gin[c] = *reinterpret_cast<const uint4 *>(a.gamma + e);
   }
   // v = B(x + r), packed, into x and LDS.
   uint4 vw[C];
@@ -301,38 +376,69 @@ __device__ __forceinline__ void norm_row_wave_wide(const NormArgs<uint16_t> &a, 
     } else {
       vw[c] = xin[c];
     }
-    if (512 * c + 8 * lane < H) {
-      if constexpr (RES)
+    if constexpr (RES)
+      if (512 * c + 8 * lane < H)
         st_nt(reinterpret_cast<uint4 *>(a.x + base + 512 * c + 8 * lane), vw[c]);
-      vlds[64 * c + lane] = vw[c];
+  }
+  // gamma is used only after the sum, past the rarely taken branch below; without this
+  // use the compiler sinks its loads behind that branch, a memory round trip per row
+  // (0.4 us per config-1 chunk).
+#pragma unroll
+  for (int c = 0; c < C; ++c)
+    pin(gin[c]);
+  // The order-free sum over the lane's valid pieces (the clamped pieces past H repeat
+  // elements 0..7 and are left out).
+  // Eight independent fp64 chains (a single one is a 32-deep dependent chain that the
+  // wave waits on).
+  double acc[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k)
+    acc[k] = 0.0;
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+    if (512 * c + 8 * lane < H) {
+      const uint32_t vv[4] = {vw[c].x, vw[c].y, vw[c].z, vw[c].w};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        acc[2 * k] = sq64(lo16(vv[k]), acc[2 * k]);
+        acc[2 * k + 1] = sq64(hi16(vv[k]), acc[2 * k + 1]);
+      }
     }
   }
-  __syncthreads();
-  // The reference's per-thread sums: lane l owns threads K l .. K l + K - 1, i.e. the K / 2
-  // words K l / 2 + (VT / 2) j of the packed row.
-  const uint32_t *vwords = reinterpret_cast<const uint32_t *>(vlds);
-  float s[K], e[K];
+  const double lane_sum = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
+  float total;
+  if (!certified_sum(wave_sum64(lane_sum), sumsq_margin(J, C + 3 + 6), total)) {
+    // Rare (wave-uniform): the reference's per-thread sums and tree.  v crosses LDS so
+    // that lane l can read the words of threads K l .. K l + K - 1, i.e. the K / 2 words
+    // K l / 2 + (VT / 2) j of the packed row.
 #pragma unroll
-  for (int k = 0; k < K; ++k) {
-    s[k] = 0.f;
-    e[k] = 0.f;
-  }
+    for (int c = 0; c < C; ++c)
+      if (512 * c + 8 * lane < H)
+        vlds[64 * c + lane] = vw[c];
+    __syncthreads();
+    const uint32_t *vwords = reinterpret_cast<const uint32_t *>(vlds);
+    float s[K], e[K];
 #pragma unroll
-  for (int j = 0; j < J; ++j) {
-#pragma unroll
-    for (int w = 0; w < K / 2; ++w) {
-      const uint32_t word = vwords[(K / 2) * lane + w + (VT / 2) * j];
-      const float v0 = lo16(word), v1 = hi16(word);
-      acc_pos(v0 * v0, s[2 * w], e[2 * w]);
-      acc_pos(v1 * v1, s[2 * w + 1], e[2 * w + 1]);
+    for (int k = 0; k < K; ++k) {
+      s[k] = 0.f;
+      e[k] = 0.f;
     }
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+#pragma unroll
+      for (int w = 0; w < K / 2; ++w) {
+        const uint32_t word = vwords[(K / 2) * lane + w + (VT / 2) * j];
+        const float v0 = lo16(word), v1 = hi16(word);
+        acc_pos(v0 * v0, s[2 * w], e[2 * w]);
+        acc_pos(v1 * v1, s[2 * w + 1], e[2 * w + 1]);
+      }
+    }
+    warp_tree<K>(s, e);
+    float S = s[0], E = e[0];
+    partials_tree<WARPS, LPW>(S, E);
+    total = __shfl(S + E, 0, 64);
+    __syncthreads(); // the image is free again for the caller
   }
-  warp_tree<K>(s, e);
-  float S = s[0], E = e[0];
-  partials_tree<WARPS, LPW>(S, E);
-  // lane 0's total through ds_bpermute: a v_readlane here measured 0.8% slower on the
-  // quantized chunk chains (13.76 -> 13.89 us, q8_0)
-  const float total = __shfl(S + E, 0, 64);
   const float variance = total / (float)H;
   const float inv = 1.f / sqrtf(variance + a.eps);
   if (a.stats && lane == 0) {
@@ -363,11 +469,10 @@ __device__ __forceinline__ void norm_row_wave_wide(const NormArgs<uint16_t> &a, 
 
 // One row per wave: all loads of the row, then compute and stores.  WIDE (BF16 rows): the
 // 16-byte layout of norm_row_wave_wide, with `lds` (VT * J / 8 uint4 of LDS owned by the
-// caller); otherwise every access is in the reference's thread-ownership layout.  Alone
-// (padra_ResidualPostNorm) the wide form is faster (2048 x 2048: 7.3 -> 7.0 us); inside the
-// fused chain, where the Q/K waves follow, it measured slower (12.75 -> 13.15 us), so the
-// chain keeps the ownership layout.
-template <int VT, int J, class T, bool RES, bool WIDE = true, bool GATHER = false>
+// caller, for the rare ordered replay); otherwise every access is in the reference's
+// thread-ownership layout, and FAST selects the sum (norm_compute).
+template <int VT, int J, class T, bool RES, bool WIDE = true, bool GATHER = false,
+          bool FAST = true>
 __device__ __forceinline__ void norm_row_wave(const NormArgs<T> &a, int row, uint4 *lds) {
   if (row >= a.rows)
     return; // wave-uniform
@@ -384,7 +489,7 @@ __device__ __forceinline__ void norm_row_wave(const NormArgs<T> &a, int row, uin
     norm_load<VT, J, T, RES>(a, row, in);
   }
   norm_load_gamma<VT, J>(a.gamma, gr);
-  norm_compute<VT, J, T, RES>(a, row, in, gr);
+  norm_compute<VT, J, T, RES, FAST>(a, row, in, gr);
 }
 
 } // namespace padra

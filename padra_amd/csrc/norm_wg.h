@@ -14,8 +14,10 @@
 namespace padra {
 
 // Row `row` by the calling workgroup (blockDim.x == 256).  Lanes t >= VT take part in the
-// barrier only.  GATHER: x is the embedding row of the row's token (norm_load_gather's
-// rule: an invalid token raises the flag and reads x as it is).
+// barriers only.  The sum of squares is the order-free fp64 sum when its fp32 rounding is
+// certain to equal the reference's (sumsq_margin, common.h); otherwise the reference's
+// tree runs as described above.  GATHER: x is the embedding row of the row's token
+// (norm_load_gather's rule: an invalid token raises the flag and reads x as it is).
 template <int VT, int J, bool GATHER>
 __device__ __forceinline__ void norm_row_wg(const NormArgs<uint16_t> &a, int row,
                                             float (*partials)[2]) {
@@ -26,8 +28,8 @@ __device__ __forceinline__ void norm_row_wg(const NormArgs<uint16_t> &a, int row
   const bool act = t < VT; // wave-uniform
   const size_t off = (size_t)row * H + (act ? t : 0);
   float v[J];
-  float s = 0.f, e = 0.f;
-  // The norm weights first: independent of the row, they are in flight during the tree.
+  double acc = 0.0;
+  // The norm weights first: independent of the row, they are in flight during the sums.
   uint16_t gw[J];
 #pragma unroll
   for (int j = 0; j < J; ++j)
@@ -54,34 +56,56 @@ __device__ __forceinline__ void norm_row_wg(const NormArgs<uint16_t> &a, int row
     for (int j = 0; j < J; ++j) {
       v[j] = B(__uint_as_float((uint32_t)xx[j] << 16) + __uint_as_float((uint32_t)rr[j] << 16));
       vb[j] = (uint16_t)(__float_as_uint(v[j]) >> 16);
-      acc_pos(v[j] * v[j], s, e);
+      acc = sq64(v[j], acc);
     }
 #pragma unroll
     for (int j = 0; j < J; ++j)
       a.x[off + VT * j] = vb[j];
-    warp_tree_lanes(s, e);
-    const int lane = t & 63;
-    if ((lane & 31) == 0) {
-      partials[t >> 5][0] = s;
-      partials[t >> 5][1] = e;
-    }
+  }
+#pragma unroll
+  for (int j = 0; j < J; ++j)
+    pin((uint32_t)gw[j]); // the weight loads stay ahead of the rarely taken branch below
+  // The order-free sum (sumsq_margin): per wave, then the four wave totals through LDS.
+  double *wave_totals = reinterpret_cast<double *>(partials);
+  {
+    const double w = wave_sum64(acc);
+    if ((t & 63) == 0)
+      wave_totals[t >> 6] = w;
   }
   __syncthreads();
+  const double s64 = (wave_totals[0] + wave_totals[1]) + (wave_totals[2] + wave_totals[3]);
+  float total;
+  if (!certified_sum(s64, sumsq_margin(J, J + 8), total)) {
+    // Rare (workgroup-uniform: every wave read the same totals): the reference's tree.
+    __syncthreads(); // the totals are read before the partials overwrite them
+    if (act) {
+      float s = 0.f, e = 0.f;
+#pragma unroll
+      for (int j = 0; j < J; ++j)
+        acc_pos(v[j] * v[j], s, e);
+      warp_tree_lanes(s, e);
+      if ((t & 31) == 0) {
+        partials[t >> 5][0] = s;
+        partials[t >> 5][1] = e;
+      }
+    }
+    __syncthreads();
+    // The warp partials' tree: partial w folds partial w + D for D = WARPS/2, ..., 1.
+    float ps[WARPS], pe[WARPS];
+#pragma unroll
+    for (int w = 0; w < WARPS; ++w) {
+      ps[w] = partials[w][0];
+      pe[w] = partials[w][1];
+    }
+#pragma unroll
+    for (int d = WARPS / 2; d >= 1; d /= 2)
+#pragma unroll
+      for (int w = 0; w < d; ++w)
+        fold(ps[w + d], pe[w + d], ps[w], pe[w]);
+    total = ps[0] + pe[0];
+  }
   if (!act)
     return;
-  // The warp partials' tree: partial w folds partial w + D for D = WARPS/2, ..., 1.
-  float ps[WARPS], pe[WARPS];
-#pragma unroll
-  for (int w = 0; w < WARPS; ++w) {
-    ps[w] = partials[w][0];
-    pe[w] = partials[w][1];
-  }
-#pragma unroll
-  for (int d = WARPS / 2; d >= 1; d /= 2)
-#pragma unroll
-    for (int w = 0; w < d; ++w)
-      fold(ps[w + d], pe[w + d], ps[w], pe[w]);
-  const float total = ps[0] + pe[0];
   const float variance = total / (float)H;
   const float inv = 1.f / sqrtf(variance + a.eps);
   if (a.stats && t == 0) {

@@ -217,16 +217,20 @@ template <class T> __device__ __forceinline__ void head_store(T *p, float v) {
 __device__ __forceinline__ bool head_norm_rope(float x0, float x1, float w0, float w1, float c,
                                                float sn, float eps, float &lo, float &hi) {
   constexpr int D = 128;
-  float s0 = x0 * x0, e0 = 0.f, s1 = x1 * x1, e1 = 0.f;
-  warp_tree_lanes(s0, e0);
-  warp_tree_lanes(s1, e1);
-  fold(s1, e1, s0, e0); // lane 0: w0 + w2; lane 32: w1 + w3
-  float S = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s0), 0));
-  float E = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e0), 0));
-  const float s2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s0), 32));
-  const float e2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e0), 32));
-  fold(s2, e2, S, E);
-  const float sum = S + E;
+  // The order-free sum (sumsq_margin), or (rarely; wave-uniform) the reference's tree.
+  float sum;
+  if (!certified_sum(wave_sum64(sq64_rn(x1, sq64_rn(x0, 0.0))), sumsq_margin(1, 8), sum)) {
+    float s0 = x0 * x0, e0 = 0.f, s1 = x1 * x1, e1 = 0.f;
+    warp_tree_lanes(s0, e0);
+    warp_tree_lanes(s1, e1);
+    fold(s1, e1, s0, e0); // lane 0: w0 + w2; lane 32: w1 + w3
+    float S = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s0), 0));
+    float E = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e0), 0));
+    const float s2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s0), 32));
+    const float e2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e0), 32));
+    fold(s2, e2, S, E);
+    sum = S + E;
+  }
   const float inv = 1.f / sqrtf(sum / (float)D + eps);
   const float an = B(B(x0 * inv) * w0), bn = B(B(x1 * inv) * w1);
   lo = B(B(an * c) + B((-bn) * sn));

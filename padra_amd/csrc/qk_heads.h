@@ -7,7 +7,7 @@
 // block has 128 threads, one feature each; warp w (features 32w..32w+31) reduces its
 // squares with a shuffle-down tree and the four warp partials reduce as
 // ((w0 + w2) + (w1 + w3)).  A lane holding warp w's 32 features runs that warp's whole
-// tree in-lane (warp_sumsq32).  The first tree level adds two squares with zero error
+// tree in-lane (warp_tree_node).  The first tree level adds two squares with zero error
 // terms; it is written out directly (its error fold is an exact no-op).
 #pragma once
 #include <type_traits>
@@ -32,27 +32,24 @@ template <class T> struct QKArgs {
 };
 
 // Compensated sum of squares of one warp's 32 features, in the reference tree order
-// (shuffle-down levels 16, 8, 4, 2, 1 of inference.cu:111-119).
-__device__ __forceinline__ void warp_sumsq32(const float (&x)[32], float &S, float &E) {
-  float s[16], e[16];
-#pragma unroll
-  for (int f = 0; f < 16; ++f) {
-    const float a2 = x[f] * x[f], b2 = x[f + 16] * x[f + 16];
-    s[f] = a2 + b2;
-    e[f] = (fmaxf(a2, b2) - s[f]) + fminf(a2, b2);
+// (shuffle-down levels 16, 8, 4, 2, 1 of inference.cu:111-119): after level d, slot f < d
+// holds slot f of level 2d folded with slot f + d of level 2d, and level 16 pairs features
+// f and f + 16.  Evaluated depth first (slot f of level d from its two children), so that
+// at most one partial per level is live: the tree is the rarely taken branch of the Q/K
+// waves, and a breadth-first form (16 partials at once) set the kernel's register count.
+template <int F, int D, class X>
+__device__ __forceinline__ void warp_tree_node(const X &x, float &s, float &e) {
+  if constexpr (D == 16) {
+    const float a = x.get(F), b = x.get(F + 16);
+    const float a2 = a * a, b2 = b * b;
+    s = a2 + b2;
+    e = (fmaxf(a2, b2) - s) + fminf(a2, b2);
+  } else {
+    float s2, e2;
+    warp_tree_node<F, 2 * D>(x, s, e);
+    warp_tree_node<F + D, 2 * D>(x, s2, e2);
+    fold(s2, e2, s, e);
   }
-#pragma unroll
-  for (int f = 0; f < 8; ++f)
-    fold(s[f + 8], e[f + 8], s[f], e[f]);
-#pragma unroll
-  for (int f = 0; f < 4; ++f)
-    fold(s[f + 4], e[f + 4], s[f], e[f]);
-#pragma unroll
-  for (int f = 0; f < 2; ++f)
-    fold(s[f + 2], e[f + 2], s[f], e[f]);
-  fold(s[1], e[1], s[0], e[0]);
-  S = s[0];
-  E = e[0];
 }
 
 template <class T>
@@ -151,6 +148,30 @@ struct Bf8 {
   }
 };
 
+// The same tree evaluated breadth first (16 partials at once): the form the tree-only
+// waves use (it schedules better there).
+__device__ __forceinline__ void warp_sumsq32(const float (&x)[32], float &S, float &E) {
+  float s[16], e[16];
+#pragma unroll
+  for (int f = 0; f < 16; ++f) {
+    const float a2 = x[f] * x[f], b2 = x[f + 16] * x[f + 16];
+    s[f] = a2 + b2;
+    e[f] = (fmaxf(a2, b2) - s[f]) + fminf(a2, b2);
+  }
+#pragma unroll
+  for (int f = 0; f < 8; ++f)
+    fold(s[f + 8], e[f + 8], s[f], e[f]);
+#pragma unroll
+  for (int f = 0; f < 4; ++f)
+    fold(s[f + 4], e[f + 4], s[f], e[f]);
+#pragma unroll
+  for (int f = 0; f < 2; ++f)
+    fold(s[f + 2], e[f + 2], s[f], e[f]);
+  fold(s[1], e[1], s[0], e[0]);
+  S = s[0];
+  E = e[0];
+}
+
 template <class X>
 __device__ __forceinline__ void group_sumsq(const X &x, float &S, float &E) {
   float v[32];
@@ -159,7 +180,10 @@ __device__ __forceinline__ void group_sumsq(const X &x, float &S, float &E) {
     v[i] = x.get(i);
   warp_sumsq32(v, S, E);
 }
-
+template <class X>
+__device__ __forceinline__ void group_sumsq_df(const X &x, float &S, float &E) {
+  warp_tree_node<0, 1>(x, S, E);
+}
 // The source row of head vector hv of the flat index space (q heads, k heads, v heads).
 template <class A>
 __device__ __forceinline__ auto head_src(const A &a, unsigned hv, unsigned nq, unsigned nk) {

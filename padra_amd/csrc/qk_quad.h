@@ -307,7 +307,9 @@ template <class T> __device__ __forceinline__ int quad_piece_slot(int owner, int
 // FMT: -1 (no cache), PADRA_KV_BF16, or a quantized cache format.
 // `stage`: quad_image_slots<T>() uint4 of LDS (the block's transposition image), owned by
 // the caller.
-template <class T, int FMT>
+// FAST: the order-free sum of squares (sumsq_margin, common.h) with the tree as fallback;
+// measured slower with a quantized cache and on fp32 activations, which keep the tree.
+template <class T, int FMT, bool FAST = (FMT <= PADRA_KV_BF16 && std::is_same<T, uint16_t>::value)>
 __device__ __forceinline__ void qk_heads_wave_quad(const QKArgs<T> &a, long long wave,
                                                    uint4 *stage) {
   constexpr int D = 128;
@@ -453,16 +455,36 @@ __device__ __forceinline__ void qk_heads_wave_quad(const QKArgs<T> &a, long long
   uint32_t out[16];
   const bool qk = live && ok && role < 2;
   if (qk) {
-    float S, E;
-    group_sumsq(x, S, E);
-    // (w0 + w2) at g = 0 and (w1 + w3) at g = 1, then their sum at g = 0.
-    {
+    // FAST: the order-free sum over the quad (sumsq_margin), with the reference's tree as
+    // its rarely taken (quad-uniform) fallback; otherwise the tree alone.  The tree: warp
+    // g's in lane g, then (w0 + w2) at g = 0 and (w1 + w3) at g = 1, then their sum at
+    // g = 0.
+    float sum;
+    auto tree = [&](auto depth_first) {
+      float S, E;
+      if constexpr (decltype(depth_first)::value)
+        group_sumsq_df(x, S, E);
+      else
+        group_sumsq(x, S, E);
       const float s2 = fquad_xor2(S), e2 = fquad_xor2(E);
       fold(s2, e2, S, E);
       const float s1 = fquad_xor1(S), e1 = fquad_xor1(E);
       fold(s1, e1, S, E);
+      return fquad_first(S + E);
+    };
+    if constexpr (FAST) {
+      double a4[4] = {0.0, 0.0, 0.0, 0.0}; // independent fp64 chains
+#pragma unroll
+      for (int f = 0; f < 32; ++f)
+        a4[f & 3] = F32 ? sq64_rn(x.get(f), a4[f & 3]) : sq64(x.get(f), a4[f & 3]);
+      double acc = (a4[0] + a4[1]) + (a4[2] + a4[3]);
+      acc = acc + lane_xor<2>(acc);
+      acc = acc + lane_xor<1>(acc);
+      if (!certified_sum(acc, sumsq_margin(1, 12), sum))
+        sum = tree(std::true_type{});
+    } else {
+      sum = tree(std::false_type{});
     }
-    const float sum = fquad_first(S + E);
     const float inv = 1.f / sqrtf(sum / (float)D + a.eps);
     // Normalized group: A = B(B(x * inv) * w) (qk_rope_store_exact.cuh:39), as floats.
     float an[32];
