@@ -95,6 +95,11 @@ template <int J, class T> __global__ __launch_bounds__(64) void k_norm_fp8(NormF
   norm_fp8_row_wave<J, T>(a, blockIdx.x);
 }
 
+// Residual-norm rows per wave in the chain (BF16 or no cache).  Two rows per wave (1,024
+// norm waves, so that with the Q/K waves the grid fits one round of 4 waves per SIMD)
+// measured slower: 13.21 -> 13.30 us on the config-1 chunk.
+constexpr int kChainRows = 1;
+
 // Residual-norm waves first, then the Q/K waves.  Measured on MI355X for a 2048-token
 // chunk, this order is 10% faster than spreading the norm rows evenly over the grid
 // (Bresenham interleave) or over its first half: the early grid streams the four norm
@@ -107,15 +112,22 @@ __global__ __launch_bounds__(64) void k_chain(NormArgs<T> n, QKArgs<T> q, long l
                                               long long waves) {
   // The order-free sums of squares (sumsq_margin, common.h) with a BF16 or no cache; the
   // reference trees alone with a quantized cache or fp32 activations, where the order-free
-  // form measured slower (rotated q8_0: 13.56 -> 14.59 us, q8: 13.10 -> 13.86 us).
-  constexpr bool FAST = FMT <= PADRA_KV_BF16 && std::is_same<T, uint16_t>::value;
+  // form measured slower (config-1 chunk, inputs cold in HBM: rotated q8_0 14.12 -> 14.35
+  // us; q8 and unrotated q8_0 within 1%; with inputs partly served by the Infinity Cache:
+  // rotated q8_0 13.56 -> 14.59 us, q8 13.10 -> 13.86 us).
+    constexpr bool FAST = FMT <= PADRA_KV_BF16 && std::is_same<T, uint16_t>::value;
   // the Q/K waves' image, or a BF16 row of the norm waves (the rare ordered-sum replay)
   constexpr int SLOTS = quad_image_slots_fmt<T, FMT>() > VT * J / 8 ? quad_image_slots_fmt<T, FMT>()
                                                                     : VT * J / 8;
   __shared__ uint4 lds[SLOTS];
   const long long b = blockIdx.x;
   if (b < norm_waves)
-    norm_row_wave<VT, J, T, true, FAST && !GATHER, GATHER, FAST>(n, (int)b, lds);
+  {
+    if constexpr (FAST && !GATHER)
+      norm_row_wave_wide<VT, J, true, kChainRows>(n, (int)b * kChainRows, lds);
+    else
+      norm_row_wave<VT, J, T, true, false, GATHER, FAST>(n, (int)b, lds);
+  }
   else if (b < waves) {
     // Quantized caches: the K waves (K norm + RoPE, then the K and V encodings: the
     // heaviest waves) are dispatched before the Q waves instead of last, so they do not
@@ -582,7 +594,8 @@ int chain(hipStream_t s, const uint16_t *gather, int vocab, const int32_t *ids, 
           }
           return launched();
         }
-        const long long norm_waves = tokens;
+        constexpr bool FAST = FMT <= PADRA_KV_BF16 && !G;
+        const long long norm_waves = FAST ? (tokens + kChainRows - 1) / kChainRows : tokens;
         const long long waves = norm_waves + qk_wave_count<FMT>(tokens, q_heads, kv_heads);
         hipLaunchKernelGGL((k_chain<VT, J, FMT, G>), dim3((unsigned)waves), dim3(64), 0, s, n,
                            a, norm_waves, waves);

@@ -340,13 +340,20 @@ __device__ __forceinline__ void norm_compute(const NormArgs<T> &a, int row,
 // elements t + VT j, summed in j order) and tree, sends v = B(x + r) across LDS once so
 // that each lane can read the words of its K threads.
 template <int VT, int J, bool RES>
-__device__ __forceinline__ void norm_row_wave_wide(const NormArgs<uint16_t> &a, int row,
+__device__ __forceinline__ void norm_wide_finish(const NormArgs<uint16_t> &a, int row,
+                                                 const uint4 (&xin)[(VT * J + 511) / 512],
+                                                 const uint4 (&rin)[(VT * J + 511) / 512],
+                                                 const uint4 (&gin)[(VT * J + 511) / 512],
+                                                 uint4 *vlds);
+
+// R consecutive rows per wave (row0 .. row0 + R - 1; rows past a.rows are skipped): the
+// gamma pieces once, then every row's loads, then each row's arithmetic and stores.
+template <int VT, int J, bool RES, int R = 1>
+__device__ __forceinline__ void norm_row_wave_wide(const NormArgs<uint16_t> &a, int row0,
                                                    uint4 *vlds) {
-  constexpr int K = VT / 64, H = VT * J, C = (H + 511) / 512, LPW = 32 / K, WARPS = VT / 32;
-  constexpr bool CHECK_Y = VT == 256 || !RES;
+  constexpr int H = VT * J, C = (H + 511) / 512;
   const int lane = threadIdx.x & 63;
-  const size_t base = (size_t)row * H;
-  uint4 xin[C], rin[C], gin[C];
+  uint4 xin[R][C], rin[R][C], gin[C];
   // gamma first (cache-resident: it returns first), then x and the residual
 #pragma unroll
   for (int c = 0; c < C; ++c) {
@@ -355,12 +362,32 @@ __device__ __forceinline__ void norm_row_wave_wide(const NormArgs<uint16_t> &a, 
   }
   issue_point();
 #pragma unroll
-  for (int c = 0; c < C; ++c) {
-    const int e = (512 * c + 8 * lane < H) ? 512 * c + 8 * lane : 0;
-    xin[c] = ld_nt(reinterpret_cast<const uint4 *>(a.x + base + e));
-    if constexpr (RES)
-      rin[c] = ld_nt(reinterpret_cast<const uint4 *>(a.residual + base + e));
+  for (int r = 0; r < R; ++r) {
+    const size_t base = (size_t)min(row0 + r, a.rows - 1) * H;
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      const int e = (512 * c + 8 * lane < H) ? 512 * c + 8 * lane : 0;
+      xin[r][c] = ld_nt(reinterpret_cast<const uint4 *>(a.x + base + e));
+      if constexpr (RES)
+        rin[r][c] = ld_nt(reinterpret_cast<const uint4 *>(a.residual + base + e));
+    }
   }
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+    if (row0 + r < a.rows) // wave-uniform
+      norm_wide_finish<VT, J, RES>(a, row0 + r, xin[r], rin[r], gin, vlds);
+}
+
+template <int VT, int J, bool RES>
+__device__ __forceinline__ void norm_wide_finish(const NormArgs<uint16_t> &a, int row,
+                                                 const uint4 (&xin)[(VT * J + 511) / 512],
+                                                 const uint4 (&rin)[(VT * J + 511) / 512],
+                                                 const uint4 (&gin)[(VT * J + 511) / 512],
+                                                 uint4 *vlds) {
+  constexpr int K = VT / 64, H = VT * J, C = (H + 511) / 512, LPW = 32 / K, WARPS = VT / 32;
+  constexpr bool CHECK_Y = VT == 256 || !RES;
+  const int lane = threadIdx.x & 63;
+  const size_t base = (size_t)row * H;
   // v = B(x + r), packed, into x and LDS.
   uint4 vw[C];
 #pragma unroll
