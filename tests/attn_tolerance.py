@@ -1,7 +1,39 @@
-"""The decode attention tolerance of the GPU tests (BF16 outputs against the oracle)."""
+"""The decode attention tolerance of the GPU tests: a per-element bound derived from the
+inputs, for BF16 outputs against the oracle.
+
+Both sides compute one sequence's attention the same way (the reference's 32-key tiles
+and online softmax per split, BF16 probabilities in the P.V product for BF16 and q8 caches,
+fp32 ones in the denominator, the per-head merge) and differ only in the order of fp32
+additions and in exp/log (CUDA's against the host libm on the oracle's side, HIP's on the
+GPU).  For output (h, d), with P_k the exact softmax weight of key k (float64) and v_kd the
+value the kernel multiplies:
+
+  1. score: |ds_k| <= 2 * 130 * 2^-24 * scale * sum_i |q_i k_ki| (two fp32 dot products of
+     128 exact products, each within gamma_128 of the exact sum, plus the scale rounding);
+     the running maximum moves by at most the largest ds of its tile and the ones before;
+     exp adds 2^-20 relative on each side.  So each probability's unrounded value differs
+     by a relative delta_k = ds_k + dm_k + 2^-20 between the two sides.
+  2. BF16 probability (BF16 and q8 caches): the two roundings of values delta_k apart
+     either agree or differ by one BF16 ulp, and they can differ only when a BF16 rounding
+     midpoint lies in [p_k (1 - delta_k), p_k (1 + delta_k)] (flip_k).  A flip moves output
+     (h, d) by at most P_k * ulp(p_k) / p_k * |v_kd|.
+  3. everything else is relative to mag_hd = sum_k P_k |v_kd|: the unrounded probabilities
+     (numerator and denominator), the rescale factors and the merge weights move it by at
+     most 4 max(delta_k); the fp32 sums of the P.V products and of the denominators by
+     4 gamma_n, n the keys of a split (each side within gamma_n of the exact sum); q8_0's
+     BF16 hi + lo split of the fp32 factor p * v_scale by 2^-16.
+  4. the final BF16 rounding of each side: one ulp of the larger result.
+
+bound_hd = 1.05 * (sum_k flip_k P_k ulp(p_k)/p_k |v_kd| + (4 max delta + 4 gamma_n + 2^-16)
+mag_hd) + ulp(max(|got|, |want|)).
+"""
+from __future__ import annotations
+
 import numpy as np
 
 from padra_amd import synth
+
+SCALE = 0.08838834764831845
 
 
 def ulp_diff(got_bits, want_bits):
@@ -12,15 +44,117 @@ def ulp_diff(got_bits, want_bits):
     return np.abs(ordered(got_bits) - ordered(want_bits))
 
 
-def attn_close(got_bits, want_bits):
-    """Per element: within 1 BF16 ulp of the oracle, or within 2^-10 of the head's largest
-    |output|.  The second bound covers near-cancelling sums, where a BF16 probability that
-    rounds the other way (the score's fp32 sum order differs) moves the output by a
-    fraction of one term (2^-8 x p x |v|), not of the small result: p ~ 0.015 against
-    |v| ~ 2 moves an output of 0.003 by 4 ulps.  Over 82k outputs per format (40 local-ring
-    sequences x 16 heads, 6 / 12 / 16 splits) the largest such move was 2^-10.9 of the head
-    maximum.  Returns (mask, ulp distances)."""
+def _bf16_ulp(x):
+    """BF16 ulp of |x| (float64 array; 2^-133 for zero and subnormals)."""
+    a = np.abs(np.asarray(x, np.float64))
+    e = np.floor(np.log2(np.maximum(a, 2.0**-126)))
+    return 2.0 ** (e - 7)
+
+
+def _bf16_round(x):
+    return synth.bf16_to_f32(synth.bf16_bits(np.asarray(x, np.float32))).astype(np.float64)
+
+
+def _window(position, local, cap):
+    n = min(position + 1, 1024) if local else position + 1
+    first = position + 1 - n
+    return (first + np.arange(n)) % cap
+
+
+def _f32(bits):
+    """BF16 bits to float32 values (a view, no per-element rounding work)."""
+    return (np.ascontiguousarray(bits, np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def _head_bound(s, a, vabs, splits, unit, bf16_probs):
+    """One query head: s [n] scaled scores (float64), a [n] scale * sum |q_i k_i|, vabs
+    [n][128] |the values the kernel multiplies|; `splits` the split count used over tiles of
+    `unit` keys (32, or q8_0's 128); the running maximum steps every 32 keys.  Returns the
+    bound of items 1-3 (without the final ulp) for the head's 128 outputs."""
+    n = s.shape[0]
+    tiles = (n + unit - 1) // unit
+    ds = 2 * 130 * 2.0**-24 * a + 2.0**-24 * np.abs(s)
+    gamma = (unit * ((tiles + splits - 1) // splits) + 64) * 2.0**-24
+    lse = np.log(np.sum(np.exp(s - s.max()))) + s.max()
+    P = np.exp(s - lse)
+    mag = P @ vabs
+    # per 32-key tile: its maximum score and largest ds; then the running values within each
+    # split (a split starts its running maximum afresh)
+    n32 = (n + 31) // 32
+    pad = n32 * 32 - n
+    tmax = np.pad(s, (0, pad), constant_values=-np.inf).reshape(n32, 32).max(axis=1)
+    tds = np.pad(ds, (0, pad)).reshape(n32, 32).max(axis=1)
+    tsplit = np.minimum(((np.arange(n32) * 32 // unit) * splits) // max(tiles, 1), splits - 1)
+    m_run = np.empty(n32)
+    d_run = np.empty(n32)
+    for sp in np.unique(tsplit):
+        sel = np.nonzero(tsplit == sp)[0]
+        m_run[sel] = np.maximum.accumulate(tmax[sel])
+        d_run[sel] = np.maximum.accumulate(tds[sel])
+    t32 = np.arange(n) // 32
+    delta = ds + d_run[t32] + 2.0**-20
+    term = (4 * float(delta.max()) + 4 * gamma + 2.0**-16) * mag
+    if bf16_probs:
+        p = np.exp(s - m_run[t32])
+        flip = _bf16_round(p * (1 - delta)) != _bf16_round(p * (1 + delta))
+        if flip.any():
+            r = _bf16_ulp(p[flip]) / p[flip]
+            term = term + (P[flip] * r) @ vabs[flip]
+    return 1.05 * term
+
+
+def _bound(q64, k32, v32, hkv, splits, unit, bf16_probs):
+    """q64 [hq][128] (float64), k32 / v32 [n][hkv*128] (float32) in window order."""
+    hq = q64.shape[0]
+    g = hq // hkv
+    out = np.zeros((hq, 128))
+    for kv in range(hkv):
+        kh = k32[:, kv * 128:(kv + 1) * 128].astype(np.float64)
+        vabs = np.abs(v32[:, kv * 128:(kv + 1) * 128]).astype(np.float64)
+        heads = q64[kv * g:(kv + 1) * g]
+        S = kh @ heads.T * SCALE
+        A = np.abs(kh) @ np.abs(heads).T * SCALE
+        for j in range(g):
+            out[kv * g + j] = _head_bound(S[:, j], A[:, j], vabs, splits, unit, bf16_probs)
+    return out
+
+
+def bound_bf16(q, kc, vc, position, local, splits, hkv=4):
+    """Bound for a BF16 cache (or a q8 cache's decoded rows, kv_q8::Decode): q [hq][128],
+    kc / vc [cap][hkv*128] BF16 bits; `splits` the count the oracle reports it ran."""
+    rows = _window(int(position), local, kc.shape[0])
+    return _bound(_f32(q).astype(np.float64), _f32(kc[rows]), _f32(vc[rows]), hkv, splits, 32,
+                  True)
+
+
+def bound_q8_0(q, rows_k, rows_v, position, local, splits, hkv=4):
+    """Bound for a q8_0 cache (rotated v2 rows [cap][544]): scores from the query's int8
+    block codes and the key codes, values v = d_b * code in the rotated domain, as the
+    kernel multiplies them (fp32 probabilities: no BF16 flips)."""
+    from oracle import oracle
+    hq, features = q.shape[0], hkv * 128
+    nd = 2 * (features // 32)
+    rows = _window(int(position), local, rows_k.shape[0])
+    qx = np.stack([oracle.hadamard(_f32(q[h]), np.float32(SCALE)) for h in range(hq)])
+    qd = np.abs(qx.reshape(hq, 4, 32)).max(axis=2).astype(np.float32) / np.float32(127)
+    inv = np.where(qd == 0, np.float32(0), np.float32(1) / np.where(qd == 0, 1, qd))
+    t = qx.reshape(hq, 4, 32) * inv[:, :, None]
+    qc = np.clip(np.sign(t) * np.floor(np.abs(t) + np.float32(0.5)), -127, 127)
+    qv = (qc * qd[:, :, None]).reshape(hq, 128).astype(np.float64)
+
+    def decode(r):
+        d = r[:, :nd].copy().view(np.float16).astype(np.float32).reshape(len(r), hkv, 4)
+        c = r[:, nd:nd + features].view(np.int8).astype(np.float32).reshape(len(r), hkv, 4, 32)
+        return (c * d[..., None]).reshape(len(r), features)
+    # the query's coding is the same on both sides; the slack covers P from float codes
+    return 1.5 * _bound(qv, decode(rows_k[rows]), decode(rows_v[rows]), hkv, splits, 128, False)
+
+
+def attn_close(got_bits, want_bits, bound):
+    """Per element: |got - want| <= bound (from bound_bf16 / bound_q8_0) + one BF16 ulp of
+    the larger of the two.  Returns (mask, ulp distances)."""
     d = ulp_diff(got_bits, want_bits)
-    g, w = synth.bf16_to_f32(got_bits), synth.bf16_to_f32(want_bits)
-    head_max = np.abs(w).max(axis=-1, keepdims=True)
-    return (d <= 1) | (np.abs(g - w) <= 2.0**-10 * head_max), d
+    g = synth.bf16_to_f32(got_bits).astype(np.float64)
+    w = synth.bf16_to_f32(want_bits).astype(np.float64)
+    tol = bound + _bf16_ulp(np.maximum(np.abs(g), np.abs(w)))
+    return (np.abs(g - w) <= tol) | (d == 0), d

@@ -8,7 +8,7 @@ import torch
 
 from padra_amd import abi, ops, synth
 
-from attn_tolerance import attn_close as _attn_close
+from attn_tolerance import attn_close as _attn_close, bound_bf16, bound_q8_0
 
 pytestmark = pytest.mark.gpu
 
@@ -493,10 +493,11 @@ def test_decode_attention(oracle, hq, local, splits):
     got = host16(out)
     worst = 0
     for s in range(seqs):
-        want, _, wbad = oracle.decode_attention(q[s], kc[s], vc[s], positions[s], local=local,
-                                                splits=splits)
+        want, used, wbad = oracle.decode_attention(q[s], kc[s], vc[s], positions[s],
+                                                   local=local, splits=splits)
         assert not wbad
-        close, d = _attn_close(got[s], want)
+        close, d = _attn_close(got[s], want,
+                               bound_bf16(q[s], kc[s], vc[s], positions[s], local, used))
         assert close.all(), s
         worst = max(worst, int(d.max()))
         if d.max() > 1:
@@ -530,8 +531,9 @@ def test_decode_attention_f32_and_invalid(oracle):
     got = out.cpu().numpy()
     assert np.all(got[2] == 7.0)
     for s in range(2):
-        want, _, _ = oracle.decode_attention(q[s], kc[s], vc[s], positions[s])
-        assert _attn_close(synth.bf16_bits(got[s]), want)[0].all()
+        want, used, _ = oracle.decode_attention(q[s], kc[s], vc[s], positions[s])
+        assert _attn_close(synth.bf16_bits(got[s]), want,
+                           bound_bf16(q[s], kc[s], vc[s], positions[s], False, used))[0].all()
 
 
 
@@ -598,7 +600,11 @@ def test_decode_attention_tuned_splits(oracle, fmt):
         # for q8_0)
         tile = 128 if fmt == abi.KV_Q8_0 else 32
         assert not wbad and wsplits == min(used, (min(positions[s] + 1, cap) + tile - 1) // tile)
-        close, d = _attn_close(got[s], want)
+        if fmt == abi.KV_Q8_0:
+            b = bound_q8_0(q[s], rk[s], rv[s], positions[s], True, wsplits)
+        else:
+            b = bound_bf16(q[s], kc[s], vc[s], positions[s], True, wsplits)
+        close, d = _attn_close(got[s], want, b)
         worst = max(worst, int(d.max()))
         assert close.all(), (s, int(d.max()))
     print(f"  max BF16 ulp difference {worst}", flush=True)
@@ -636,9 +642,11 @@ def test_decode_attention_q8_0(oracle, hq, local):
     got = host16(out)
     worst = 0
     for s in range(seqs):
-        want, _, wbad = oracle.decode_attention_q8_0(q[s], rk[s], rv[s], positions[s], local=local)
+        want, used, wbad = oracle.decode_attention_q8_0(q[s], rk[s], rv[s], positions[s],
+                                                        local=local)
         assert not wbad
-        close, d = _attn_close(got[s], want)
+        close, d = _attn_close(got[s], want,
+                               bound_q8_0(q[s], rk[s], rv[s], positions[s], local, used))
         worst = max(worst, int(d.max()))
         assert close.all(), (s, int(d.max()))
     print(f"  max BF16 ulp difference {worst}", flush=True)
@@ -679,9 +687,10 @@ def test_decode_attention_q8(oracle, hq, local):
     assert bad.item() == 0
     got = host16(out)
     for s in range(seqs):
-        want, _, wbad = oracle.decode_attention(q[s], dk[s], dv[s], positions[s], local=local)
+        want, used, wbad = oracle.decode_attention(q[s], dk[s], dv[s], positions[s], local=local)
         assert not wbad
-        close, d = _attn_close(got[s], want)
+        close, d = _attn_close(got[s], want,
+                               bound_bf16(q[s], dk[s], dv[s], positions[s], local, used))
         assert close.all(), (s, int(d.max()))
     # a -128 code inside the window raises the flag: in the window's first tile (whole,
     # for a window of 32 keys or more) and at the current position
@@ -869,9 +878,11 @@ def test_decode_attention_q8_scales(oracle):
         dv = synth.bf16_bits(codes_v.reshape(seqs, cap, hkv, 128).astype(np.float32) *
                              scales[..., 1:2]).reshape(seqs, cap, -1)
     for s in range(seqs):
-        want, _, wbad = oracle.decode_attention(q[s], dk[s], dv[s], positions[s])
+        want, used, wbad = oracle.decode_attention(q[s], dk[s], dv[s], positions[s])
         assert not wbad
-        close, d = _attn_close(got[s], want)
+        with np.errstate(over="ignore", invalid="ignore"):
+            b = bound_bf16(q[s], dk[s], dv[s], positions[s], False, used)
+        close, d = _attn_close(got[s], want, b)
         assert close.all(), (s, int(d.max()))
     # code 127 at scale 3e36 rounds to a BF16 infinity
     codes_v[1, 17, 3] = 127

@@ -225,7 +225,7 @@ def test_config4_attention_full(oracle, fmt):
     (a window of every row) and 0, in one launch (the split waves ordered by window
     length); four sequences checked against the oracle within the attention tolerance
     (tests/attn_tolerance.py), the others only for a raised flag."""
-    from attn_tolerance import attn_close
+    from attn_tolerance import attn_close, bound_bf16, bound_q8_0
     print(f"[case] config4 attention full fmt={fmt}", flush=True)
     seqs, hq, hkv, cap = 64, 16, 4, 131072
     rng = np.random.default_rng(410 + fmt)
@@ -272,7 +272,8 @@ def test_config4_attention_full(oracle, fmt):
             n = int(positions[s]) + 1
             rk[:n] = kc[window].cpu().numpy().view(np.uint8)
             rv[:n] = vc[window].cpu().numpy().view(np.uint8)
-            want, _, wbad = oracle.decode_attention_q8_0(q[s], rk, rv, positions[s])
+            want, used, wbad = oracle.decode_attention_q8_0(q[s], rk, rv, positions[s])
+            b = bound_q8_0(q[s], rk, rv, positions[s], False, used)
         else:
             n = int(positions[s]) + 1
             dk = np.zeros((cap, hkv * 128), np.uint16)
@@ -286,9 +287,10 @@ def test_config4_attention_full(oracle, fmt):
                 cv = vc[window].cpu().numpy().reshape(n, hkv, 128).astype(np.float32)
                 dk[:n] = synth.bf16_bits(ck * scl[:, :, 0:1]).reshape(n, -1)
                 dv[:n] = synth.bf16_bits(cv * scl[:, :, 1:2]).reshape(n, -1)
-            want, _, wbad = oracle.decode_attention(q[s], dk, dv, positions[s])
+            want, used, wbad = oracle.decode_attention(q[s], dk, dv, positions[s])
+            b = bound_bf16(q[s], dk, dv, positions[s], False, used)
         assert not wbad
-        close, d = attn_close(got[s], want)
+        close, d = attn_close(got[s], want, b)
         assert close.all(), (s, int(d.max()))
     del kc, vc, sc
     torch.cuda.empty_cache()
