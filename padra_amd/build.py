@@ -46,6 +46,23 @@ def command(out: str = OUT, asan: bool = False) -> list[str]:
            [os.path.join(HERE, s) for s in SOURCES]
 
 
+CALLER_SRC = os.path.join(ROOT, "tests", "cpp", "padra_caller.cpp")
+CALLER_OUT = os.path.join(ROOT, "tests", "cpp", "padra_caller")
+
+
+def build_caller(lib: str = OUT) -> str:
+    """The C++20 test program that calls the library through include/padra_hip.h only
+    (tests/test_gpu_cpp_caller.py runs it): host code, linked against libpadra_hip.so with
+    an rpath to the package directory."""
+    cmd = [hipcc(), "-std=c++20", "-O2", "-Wall", "-I", os.path.join(ROOT, "include"),
+           CALLER_SRC, "-L", os.path.dirname(lib), "-lpadra_hip",
+           "-Wl,-rpath," + os.path.dirname(lib), "-o", CALLER_OUT]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError("hipcc failed (C++ caller):\n" + res.stdout + res.stderr)
+    return CALLER_OUT
+
+
 def build(out: str = OUT, verbose: bool = False, asan: bool = False) -> str:
     if asan:
         out = ASAN_OUT
@@ -63,3 +80,5 @@ def build(out: str = OUT, verbose: bool = False, asan: bool = False) -> str:
 
 if __name__ == "__main__":
     print(build(verbose=True, asan="--asan" in sys.argv[1:]))
+    if "--asan" not in sys.argv[1:]:
+        print(build_caller())
