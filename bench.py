@@ -57,6 +57,9 @@ def parse():
     ap.add_argument("--replays", type=int, default=11,
                     help="timed graph replays of the headline workload, each from restored "
                          "inputs; ms_per_step is their median")
+    ap.add_argument("--positions", choices=("prefill", "base"), default="prefill",
+                    help="headline positions from the chunk's device PrefillState (default) "
+                         "or host-known (base + t)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-configs", action="store_true",
                     help="skip the config 0/3/4 measurements (headline only)")
@@ -870,7 +873,8 @@ def main():
     formats = args.formats.split(",")
     results = {}
     for fmt in formats:
-        sets = [ChainSet(torch, host, table, fmt) for _ in range(args.sets)]
+        sets = [ChainSet(torch, host, table, fmt, base_positions=args.positions == "base")
+                for _ in range(args.sets)]
         spread = time_graph_fresh(torch, sets, args.steps, args.warmup, args.replays)
         ms = float(np.median(spread))
         for st in sets:
