@@ -60,6 +60,9 @@ def parse():
     ap.add_argument("--positions", choices=("prefill", "base"), default="prefill",
                     help="headline positions from the chunk's device PrefillState (default) "
                          "or host-known (base + t)")
+    ap.add_argument("--no-compare", action="store_true",
+                    help="skip the 8-set (Infinity-Cache-assisted) comparison leg, so that a "
+                         "profiled run's kernel averages are of cold launches")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-configs", action="store_true",
                     help="skip the config 0/3/4 measurements (headline only)")
@@ -882,9 +885,11 @@ def main():
         eager = time_eager(torch, sets, min(args.steps, 50))
         # The earlier rounds' method, for comparison only: 8 sets rotating with no restore,
         # about 490 MB touched per cycle, partly served by the 256 MB Infinity Cache.
-        for st in sets:
-            st.restore()
-        warm8 = time_graph(torch, sets[:8], args.steps, args.warmup)
+        warm8 = None
+        if not args.no_compare:
+            for st in sets:
+                st.restore()
+            warm8 = time_graph(torch, sets[:8], args.steps, args.warmup)
         nbytes = chain_bytes(fmt) * TOKENS
         results[fmt] = {"ms": ms, "eager_ms": eager, "bytes": nbytes, "warm8_ms": warm8,
                         "gbs": nbytes / (ms * 1e-3) / 1e9, "spread": spread}
@@ -930,7 +935,8 @@ def main():
                          "torch_copy_64MB_gbs": round(ceiling, 1)},
         "formats": {f: {"gbs": round(r["gbs"], 2), "us_per_launch": round(r["ms"] * 1e3, 3),
                         "eager_us_per_launch": round(r["eager_ms"] * 1e3, 3),
-                        "cache_assisted_8_sets_us_per_launch": round(r["warm8_ms"] * 1e3, 3),
+                        "cache_assisted_8_sets_us_per_launch":
+                            None if r["warm8_ms"] is None else round(r["warm8_ms"] * 1e3, 3),
                         "replays_us_p10_median_p90": [
                             round(float(np.percentile(r["spread"], q)) * 1e3, 3)
                             for q in (10, 50, 90)],

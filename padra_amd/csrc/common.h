@@ -233,9 +233,13 @@ __device__ __forceinline__ void st_wt(uint2 *p, uint2 v) {
   const u32x2_t t = {v.x, v.y};
   asm volatile("global_store_dwordx2 %0, %1, off sc1" : : "v"(p), "v"(t) : "memory");
 }
+// A store of more than 8 bytes reads its data VGPRs one cycle after it issues, so a VALU
+// write to them needs one wait state in between.  The compiler inserts it after its own
+// stores but cannot see into an asm block, so the block carries the s_nop itself; without
+// it a following VALU write reused the data registers and 16 lanes stored stale words.
 __device__ __forceinline__ void st_wt(uint4 *p, uint4 v) {
   const u32x4_t t = {v.x, v.y, v.z, v.w};
-  asm volatile("global_store_dwordx4 %0, %1, off sc1" : : "v"(p), "v"(t) : "memory");
+  asm volatile("global_store_dwordx4 %0, %1, off sc1\n\ts_nop 0" : : "v"(p), "v"(t) : "memory");
 }
 // Non-temporal (WT false) or written-through (WT true) streaming store.
 template <bool WT, class P, class V> __device__ __forceinline__ void st_stream(P *p, V v) {
