@@ -161,6 +161,7 @@ def time_graph_fresh(torch, sets, steps, warmup, replays=11, restore="stream"):
             s.restore(restore)
         torch.cuda.synchronize()
         with torch.cuda.stream(stream):
+            lead_in(torch)
             start.record(stream)
             graph.replay()
             end.record(stream)
@@ -187,6 +188,7 @@ def time_graph(torch, sets, steps, warmup, replays=None):
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     with torch.cuda.stream(stream):
         torch.cuda.synchronize()
+        lead_in(torch)
         start.record(stream)
         graph.replay()
         end.record(stream)
@@ -195,12 +197,23 @@ def time_graph(torch, sets, steps, warmup, replays=None):
     if replays is not None:
         for _ in range(9):
             with torch.cuda.stream(stream):
+                lead_in(torch)
                 start.record(stream)
                 graph.replay()
                 end.record(stream)
             torch.cuda.synchronize()
             replays.append(start.elapsed_time(end) / steps)
     return ms
+
+
+def lead_in(torch, cycles=2_000_000):
+    """An untimed spin kernel on the current stream just before a start event: while it
+    runs, the host submits the event, the graph and the end event, so the timed region
+    does not hold the host's submission of the graph to an idle GPU.  (Config-1 BF16 chunk
+    at K = 20: 12.93-12.95 us per launch with it, 12.96-13.06 without; at K = 200 12.52-12.58
+    either way.  The rest of the K = 20 excess is a fixed cost of about 7 us per replay,
+    not per launch.)"""
+    torch.cuda._sleep(cycles)
 
 
 def warm_graph(torch, graph, seconds=0.2, most=400):
@@ -327,8 +340,19 @@ def cpu_baseline(host, seconds, threads):
     }
 
 
-def graph_time(torch, step, steps, warmup=3):
-    """Average ms per call of step(i), captured `steps` times in one HIP graph."""
+COLD_BYTES = 1.5e9  # distinct bytes per graph replay: about six times the Infinity Cache
+
+
+def cold_sets(nbytes, least=4):
+    """Buffer sets for a kernel moving `nbytes` per launch so that one replay of a graph
+    rotating over them touches COLD_BYTES: its inputs then come from HBM, not from the
+    256 MB Infinity Cache, as the streaming copy it is compared with does."""
+    return max(least, -(-int(COLD_BYTES) // int(nbytes)))
+
+
+def graph_time(torch, step, steps, warmup=3, replays=5):
+    """Median over `replays` timed replays of the ms per call of step(i), captured `steps`
+    times in one HIP graph."""
     for i in range(warmup):
         step(i)
     torch.cuda.synchronize()
@@ -341,15 +365,19 @@ def graph_time(torch, step, steps, warmup=3):
     torch.cuda.synchronize()
     warm_graph(torch, graph)
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    with torch.cuda.stream(stream):
-        start.record(stream)
-        graph.replay()
-        end.record(stream)
-    torch.cuda.synchronize()
-    return start.elapsed_time(end) / steps
+    out = []
+    for _ in range(replays):
+        with torch.cuda.stream(stream):
+            lead_in(torch)
+            start.record(stream)
+            graph.replay()
+            end.record(stream)
+        torch.cuda.synchronize()
+        out.append(start.elapsed_time(end) / steps)
+    return float(np.median(out))
 
 
-def bench_swiglu(torch, steps, sets=4):
+def bench_swiglu(torch, steps):
     """Config 3: SwiGLU over 2048 tokens x top-8 = 16384 expert-permuted rows of 1024."""
     from padra_amd import ops, synth
     d = synth.swiglu_inputs(tokens=2048, top_k=8, width=1024, experts=64, sigma=2.0, seed=0)
@@ -357,11 +385,12 @@ def bench_swiglu(torch, steps, sets=4):
     ops.SiluTableBuild(table)
     bad = torch.zeros(1, dtype=torch.int32, device="cuda")
     dev = lambda a: torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).cuda()
+    nbytes = 6 * d["gate"].size
+    sets = cold_sets(nbytes)
     bufs = [(dev(d["gate"]), dev(d["up"]), torch.empty(d["gate"].shape, dtype=torch.int16,
                                                          device="cuda")) for _ in range(sets)]
     ms = graph_time(torch, lambda i: ops.SwiGLU(bufs[i % sets][0], bufs[i % sets][1],
-                                                bufs[i % sets][2], table, bad), steps)
-    nbytes = 6 * d["gate"].size
+                                                bufs[i % sets][2], table, bad), max(steps, sets))
     if bad.item():
         raise SystemExit("device error flag set in the SwiGLU benchmark")
     return {"workload": "config3: SwiGLU 16384 rows x 1024, expert-permuted (64 experts)",
@@ -371,7 +400,7 @@ def bench_swiglu(torch, steps, sets=4):
             "rows_per_s": round(d["gate"].shape[0] / (ms * 1e-3), 1)}
 
 
-def bench_f32_layer(torch, steps, sets=8):
+def bench_f32_layer(torch, steps):
     """The config-1 chunk in the reference's own activation form (fp32 buffers holding
     BF16-exact values, PADRA_ACT_F32): launched as the reference launches it (the residual
     + RMSNorm, then the Q/K norm + RoPE + BF16 KV store, each timed alone), and through
@@ -383,6 +412,10 @@ def bench_f32_layer(torch, steps, sets=8):
     table = torch.from_numpy(ops.RopeTable(TOKENS, D, 1e6).view(torch.int16).numpy()).cuda()
     g, qn, kn = b16(host["gamma"]), b16(host["qn"]), b16(host["kn"])
     bad = torch.zeros(1, dtype=torch.int32, device="cuda")
+    norm_bytes = TOKENS * HIDDEN * 4 * 4
+    qk_bytes = TOKENS * (((HQ + 2 * HKV) + (HQ + HKV)) * D * 4 + 2 * HKV * D * 2 + 2 * D)
+    sets = cold_sets(min(norm_bytes, qk_bytes))
+    steps = max(steps, sets)
     bufs = []
     for _ in range(sets):
         x = f32(host["x"])
@@ -399,8 +432,6 @@ def bench_f32_layer(torch, steps, sets=8):
         bufs[i % sets][6], bad), steps)
     if bad.item():
         raise SystemExit("device error flag set in the fp32-activation benchmark")
-    norm_bytes = TOKENS * HIDDEN * 4 * 4
-    qk_bytes = TOKENS * (((HQ + 2 * HKV) + (HQ + HKV)) * D * 4 + 2 * HKV * D * 2 + 2 * D)
     rate = lambda b, ms: round(b / (ms * 1e-3) / 1e9, 2)
     return {"workload": "config1 chunk with fp32 activations: residual+RMSNorm, then "
                         "QK-norm+RoPE+BF16 KV store (two entry points, and the one chain "
@@ -415,7 +446,7 @@ def bench_f32_layer(torch, steps, sets=8):
             "frac": round((norm_bytes + qk_bytes) / ((norm_ms + qk_ms) * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
 
 
-def bench_chain_sizes(torch, sizes=(2048, 4096, 8192, 16384), steps=50, sets=4):
+def bench_chain_sizes(torch, sizes=(2048, 4096, 8192, 16384), steps=50):
     """The BF16 chain at several token counts, each beside a streaming copy of the same bytes
     timed the same way: how much of a launch is its fixed cost and how fast the chain
     streams once the launch is large.  Host-known positions (PADRA_POS_BASE) at every
@@ -425,15 +456,16 @@ def bench_chain_sizes(torch, sizes=(2048, 4096, 8192, 16384), steps=50, sets=4):
     table = torch.from_numpy(ops.RopeTable(max(sizes), D, 1e6).view(torch.int16).numpy()).cuda()
     out = {}
     for t in sizes:
+        nbytes = chain_bytes("bf16") * t
+        sets = cold_sets(nbytes)
         chain_sets = [ChainSet(torch, host, table, "bf16", tokens=t, base_positions=True)
                       for _ in range(sets)]
-        ms = time_graph(torch, chain_sets, steps, 5)
+        ms = time_graph(torch, chain_sets, max(steps, sets), 5)
         if any(int(c.bad.item()) for c in chain_sets):
             raise SystemExit(f"device error flag set in the chain at {t} tokens")
         del chain_sets
         torch.cuda.empty_cache()
-        nbytes = chain_bytes("bf16") * t
-        _, copy_ms = stream_copy_ceiling(torch, nbytes, steps=steps, sets=sets)
+        _, copy_ms = stream_copy_ceiling(torch, nbytes, steps=max(steps, sets), sets=sets)
         out[str(t)] = {"us_per_launch": round(ms * 1e3, 3), "bytes_per_launch": nbytes,
                        "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
                        "frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
@@ -442,7 +474,7 @@ def bench_chain_sizes(torch, sizes=(2048, 4096, 8192, 16384), steps=50, sets=4):
     return out
 
 
-def bench_norm_fp8(torch, steps, sets=8):
+def bench_norm_fp8(torch, steps):
     """The input RMSNorm with its FP8 E4M3 row encoding (the QKV GEMM's input) over the
     config-1 chunk: 2048 rows of 2048; reads x, writes normalized (BF16) and codes."""
     from padra_amd import ops, synth
@@ -450,6 +482,10 @@ def bench_norm_fp8(torch, steps, sets=8):
     dev = lambda a: torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).cuda()
     g = dev(host["gamma"])
     bad = torch.zeros(1, dtype=torch.int32, device="cuda")
+    nbytes = TOKENS * (HIDDEN * (2 + 2 + 1) + 4)
+    norm_bytes = TOKENS * HIDDEN * 2 * 2
+    sets = cold_sets(norm_bytes)
+    steps = max(steps, sets)
     bufs = []
     for _ in range(sets):
         x = dev(host["x"])
@@ -465,8 +501,6 @@ def bench_norm_fp8(torch, steps, sets=8):
                                                                bufs[i % sets][1], g, bad), steps)
     if bad.item():
         raise SystemExit("device error flag set in the FP8 norm benchmark")
-    nbytes = TOKENS * (HIDDEN * (2 + 2 + 1) + 4)
-    norm_bytes = TOKENS * HIDDEN * 2 * 2
     return {"workload": "RMSNorm + FP8 E4M3 row encoding, 2048 rows x 2048 (BF16 in/out)",
             "us_per_launch": round(ms * 1e3, 3), "bytes_per_launch": nbytes,
             "gbs": round(nbytes / (ms * 1e-3) / 1e9, 2),
@@ -476,19 +510,21 @@ def bench_norm_fp8(torch, steps, sets=8):
                           "frac": round(norm_bytes / (norm_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}}
 
 
-def bench_kv_neighbours(torch, steps=100, sets=4):
+def bench_kv_neighbours(torch, steps=100):
     """The cache writers and readers next to the chain, on the config-1/2 chunk (2048
     tokens, 4 KV heads of 128): the store-only encode of a chunk buffer (padra_KVStore,
     cap = 2048), its commit into a 131072-row ring (padra_KVCommit), the q8_0 decode of a
     1024-row local ring's prefix (padra_KvQ8_0DequantizePrefix), the in-place K rotation
     of the chunk's K rows (padra_RotateRows) and the 1024-row local-ring snapshot
-    (padra_KVCheckpointCapture).  Bytes: what each reads and writes once."""
+    (padra_KVCheckpointCapture).  Bytes: what each reads and writes once.  Each kernel
+    rotates over cold_sets(its bytes) sets of its own buffers; the commits go to four
+    rings, each set into its own 2048-row range of one of them (its own PrefillState)."""
     from padra_amd import abi, ops, synth
     T, F = TOKENS, HKV * D
     host = synth.chain_inputs(T, HIDDEN, HQ, HKV, D, outliers=True, seed=0)
     dev = lambda a: torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).cuda()
     bad = torch.zeros(1, dtype=torch.int32, device="cuda")
-    k, v = dev(host["k"]), dev(host["v"])
+    hk, hv = dev(host["k"]), dev(host["v"])
     row_bytes = {abi.KV_BF16: 2 * F, abi.KV_Q8: F, abi.KV_Q8_0: ops.q8_0_row_bytes(F)}
 
     def planes(fmt, rows):
@@ -503,62 +539,69 @@ def bench_kv_neighbours(torch, steps=100, sets=4):
         return (torch.zeros((rows, rb), dtype=torch.uint8, device="cuda"),
                 torch.zeros((rows, rb), dtype=torch.uint8, device="cuda"), None)
 
-    def entry(name, ms, nbytes):
-        return name, {"us_per_launch": round(ms * 1e3, 3), "bytes_per_launch": nbytes,
-                      "gbs": round(nbytes / (ms * 1e-3) / 1e9, 2),
-                      "frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+    def prefill_state(base, tokens):
+        return torch.tensor([base, base, tokens, CAPACITY, base, 1, 1, 1], dtype=torch.int32,
+                            device="cuda")
+
+    def timed(name, nbytes, make, launch):
+        sets = cold_sets(nbytes)
+        bufs = [make(j) for j in range(sets)]
+        ms = graph_time(torch, lambda i: launch(bufs[i % sets]), max(steps, sets))
+        del bufs
+        torch.cuda.empty_cache()
+        out[name] = {"us_per_launch": round(ms * 1e3, 3), "bytes_per_launch": nbytes,
+                     "gbs": round(nbytes / (ms * 1e-3) / 1e9, 2),
+                     "frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                     "buffer_sets": sets}
 
     out = {}
     names = {abi.KV_BF16: "bf16", abi.KV_Q8: "q8", abi.KV_Q8_0: "q8_0"}
-    state = torch.tensor([0, 0, T, CAPACITY, 0, 1, 1, 1], dtype=torch.int32, device="cuda")
+    rings_per_fmt = 4
     for fmt in (abi.KV_BF16, abi.KV_Q8, abi.KV_Q8_0):
         scale_bytes = T * HKV * 8 if fmt == abi.KV_Q8 else 0
-        chunks = [planes(fmt, T) for _ in range(sets)]
-        rings = [planes(fmt, CAPACITY) for _ in range(sets)]
-        ms = graph_time(torch, lambda i: ops.KVStore(
-            k, v, ops.positions_base(0),
-            ops.kv_cache(fmt, *chunks[i % sets][:2], T, scales=chunks[i % sets][2]), bad), steps)
-        name, e = entry(f"store_{names[fmt]}", ms, 2 * T * F * 2 + 2 * T * row_bytes[fmt] + scale_bytes)
-        out[name] = e
-        ms = graph_time(torch, lambda i: ops.KVCommit(
-            ops.kv_cache(fmt, *chunks[i % sets][:2], T, scales=chunks[i % sets][2]),
-            ops.kv_cache(fmt, *rings[i % sets][:2], CAPACITY, scales=rings[i % sets][2]),
-            ops.positions_prefill(state, maximum=CAPACITY), T, HKV, bad), steps)
-        name, e = entry(f"commit_{names[fmt]}", ms, 2 * (2 * T * row_bytes[fmt] + scale_bytes))
-        out[name] = e
+        timed(f"store_{names[fmt]}", 2 * T * F * 2 + 2 * T * row_bytes[fmt] + scale_bytes,
+              lambda j: (hk.clone(), hv.clone(), planes(fmt, T)),
+              lambda b: ops.KVStore(b[0], b[1], ops.positions_base(0),
+                                    ops.kv_cache(fmt, *b[2][:2], T, scales=b[2][2]), bad))
+        rings = [planes(fmt, CAPACITY) for _ in range(rings_per_fmt)]
+        timed(f"commit_{names[fmt]}", 2 * (2 * T * row_bytes[fmt] + scale_bytes),
+              lambda j: (planes(fmt, T), rings[j % rings_per_fmt],
+                         prefill_state((j // rings_per_fmt) * T % CAPACITY, T)),
+              lambda b: ops.KVCommit(
+                  ops.kv_cache(fmt, *b[0][:2], T, scales=b[0][2]),
+                  ops.kv_cache(fmt, *b[1][:2], CAPACITY, scales=b[1][2]),
+                  ops.positions_prefill(b[2], maximum=CAPACITY), T, HKV, bad))
         del rings
+
     # q8_0 prefix decode of a 1024-row local ring whose chunk starts at base 4096
-    ring_state = torch.tensor([4096, 4096, T, CAPACITY, 4096, 1, 1, 1], dtype=torch.int32,
-                              device="cuda")
-    rk, rv, _ = planes(abi.KV_Q8_0, 1024)
-    rk.view(torch.int16)[:, :16].fill_(0x2400)
-    rv.view(torch.int16)[:, :16].fill_(0x2400)
-    ok = torch.empty((1024, F), dtype=torch.int16, device="cuda")
-    ov = torch.empty_like(ok)
-    ms = graph_time(torch, lambda i: ops.KvQ8_0DequantizePrefix(
-        rk, rv, ok, ov, ops.positions_prefill(ring_state, maximum=CAPACITY), T, bad), steps)
-    name, e = entry("q8_0_dequantize_prefix_1024", ms,
-                    2 * 1024 * row_bytes[abi.KV_Q8_0] + 2 * 1024 * F * 2)
-    out[name] = e
-    kr = [dev(host["k"]) for _ in range(sets)]
-    ms = graph_time(torch, lambda i: ops.RotateRows(kr[i % sets], bad), steps)
-    name, e = entry("rotate_rows_k", ms, 2 * T * F * 2)
-    out[name] = e
+    def prefix_bufs(j):
+        rk, rv, _ = planes(abi.KV_Q8_0, 1024)
+        rk.view(torch.int16)[:, :16].fill_(0x2400)
+        rv.view(torch.int16)[:, :16].fill_(0x2400)
+        ok = torch.empty((1024, F), dtype=torch.int16, device="cuda")
+        return rk, rv, ok, torch.empty_like(ok)
+    ring_state = prefill_state(4096, T)
+    timed("q8_0_dequantize_prefix_1024", 2 * 1024 * row_bytes[abi.KV_Q8_0] + 2 * 1024 * F * 2,
+          prefix_bufs,
+          lambda b: ops.KvQ8_0DequantizePrefix(*b, ops.positions_prefill(ring_state, maximum=CAPACITY),
+                                               T, bad))
+    timed("rotate_rows_k", 2 * T * F * 2, lambda j: hk.clone(), lambda b: ops.RotateRows(b, bad))
     # snapshot of a 1024-row BF16 local ring before the chunk at base 700, anchor 1250
     snap_state = torch.tensor([700, 700, 600, CAPACITY, 700, 1, 1, 1], dtype=torch.int32,
                               device="cuda")
-    old, cur, sv = planes(abi.KV_BF16, 1024), planes(abi.KV_BF16, 600), planes(abi.KV_BF16, 1024)
-    ms = graph_time(torch, lambda i: ops.KVCheckpointCapture(
-        ops.kv_cache(abi.KV_BF16, old[0], old[1], 1024), ops.kv_cache(abi.KV_BF16, cur[0], cur[1], 600),
-        ops.kv_cache(abi.KV_BF16, sv[0], sv[1], 1024),
-        ops.positions_prefill(snap_state, maximum=CAPACITY), 600, 1250, bad), steps)
-    name, e = entry("checkpoint_capture_bf16_1024", ms, 2 * 2 * 1024 * F * 2)
-    out[name] = e
+    timed("checkpoint_capture_bf16_1024", 2 * 2 * 1024 * F * 2,
+          lambda j: (planes(abi.KV_BF16, 1024), planes(abi.KV_BF16, 600), planes(abi.KV_BF16, 1024)),
+          lambda b: ops.KVCheckpointCapture(
+              ops.kv_cache(abi.KV_BF16, b[0][0], b[0][1], 1024),
+              ops.kv_cache(abi.KV_BF16, b[1][0], b[1][1], 600),
+              ops.kv_cache(abi.KV_BF16, b[2][0], b[2][1], 1024),
+              ops.positions_prefill(snap_state, maximum=CAPACITY), 600, 1250, bad))
     torch.cuda.synchronize()
     if bad.item():
         raise SystemExit("device error flag set in the cache neighbour benchmarks")
     for name, e in out.items():
-        gbs, cms = stream_copy_ceiling(torch, e["bytes_per_launch"], steps=steps)
+        gbs, cms = stream_copy_ceiling(torch, e["bytes_per_launch"],
+                                       steps=max(steps, e["buffer_sets"]), sets=e["buffer_sets"])
         e["copy_us"] = round(cms * 1e3, 3)
         e["frac_of_copy"] = round(e["gbs"] / gbs, 4)
     return {"workload": "cache neighbours of the 2048-token chunk: store-only encode, commit "
@@ -566,7 +609,7 @@ def bench_kv_neighbours(torch, steps=100, sets=4):
                         "snapshot", **out}
 
 
-def bench_combine_norm(torch, steps, sets=8):
+def bench_combine_norm(torch, steps):
     """The step after the expert down projection over the config-1 chunk: the ordered BF16
     combine of 8 expert rows into the residual, the RMSNorm and its FP8 encoding; 2048 rows
     of 2048.  Reads down (8 rows) and x, writes x, normalized and codes."""
@@ -578,6 +621,8 @@ def bench_combine_norm(torch, steps, sets=8):
     dev = lambda a: torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).cuda()
     g = dev(host["gamma"])
     bad = torch.zeros(1, dtype=torch.int32, device="cuda")
+    nbytes = TOKENS * (HIDDEN * (8 * 2 + 2 + 2 + 2 + 1) + 8 * 4 + 4)
+    sets = cold_sets(nbytes)
     bufs = []
     for _ in range(sets):
         x = dev(host["x"])
@@ -589,10 +634,9 @@ def bench_combine_norm(torch, steps, sets=8):
         x, down, y, packed, scales = bufs[i % sets]
         ops.CombineNorm(x, down, w, y, g, bad, packed=packed, scales=scales)
 
-    ms = graph_time(torch, step, steps)
+    ms = graph_time(torch, step, max(steps, sets))
     if bad.item():
         raise SystemExit("device error flag set in the combine + norm benchmark")
-    nbytes = TOKENS * (HIDDEN * (8 * 2 + 2 + 2 + 2 + 1) + 8 * 4 + 4)
     return {"workload": "expert combine (8 rows) + residual + RMSNorm + FP8, 2048 rows x 2048",
             "us_per_launch": round(ms * 1e3, 3), "bytes_per_launch": nbytes,
             "gbs": round(nbytes / (ms * 1e-3) / 1e9, 2),
@@ -993,7 +1037,8 @@ def main():
             for part in key.split("."):
                 entry = entry[part]
             nbytes = entry.get("bytes_per_launch") or (entry["norm_bytes"] + entry["qk_bytes"])
-            gbs, ms = stream_copy_ceiling(torch, nbytes, steps=100)
+            sets = cold_sets(nbytes)
+            gbs, ms = stream_copy_ceiling(torch, nbytes, steps=max(100, sets), sets=sets)
             entry["copy_us"] = round(ms * 1e3, 3)
             entry["frac_of_copy"] = round(entry["gbs"] / gbs, 4)
             if "fused_gbs" in entry:
