@@ -92,7 +92,12 @@ __global__ void k_zero_u64(unsigned long long *p, int n) {
 }
 
 template <int J, class T> __global__ __launch_bounds__(64) void k_norm_fp8(NormFP8Args<T> a) {
-  norm_fp8_row_wave<J, T>(a, blockIdx.x);
+  if constexpr (std::is_same<T, uint16_t>::value) {
+    __shared__ uint4 lds[128 * J / 8]; // the row, for the rare ordered replay
+    norm_fp8_row_wide<J>(a, blockIdx.x, lds);
+  } else {
+    norm_fp8_row_wave<J, T>(a, blockIdx.x);
+  }
 }
 
 // Residual-norm rows per wave in the chain (BF16 or no cache).  Two rows per wave (1,024

@@ -368,7 +368,7 @@ def test_combine(oracle, residual, act):
     assert bool(bad.item()) == want_bad
 
 
-@pytest.mark.parametrize("hidden,rows", [(2048, 67), (2304, 67), (2048, 2048)])
+@pytest.mark.parametrize("hidden,rows", [(2048, 67), (2304, 67), (4608, 67), (1024, 5), (2048, 2048)])
 @pytest.mark.parametrize("fp8", [True, False])
 def test_combine_norm(oracle, hidden, rows, fp8):
     """Combine + RMSNorm (+ FP8) against the oracle bit for bit; 2048 x 2048 is the size the

@@ -6,7 +6,7 @@ fp64 sum replays the reference's ordered tree for them.  They are mixed with ord
 rows and heads in one launch, so waves that take the fallback and waves that do not run
 side by side, and every output is compared with the oracle bit for bit.  The launch
 shapes covered: the residual norm (a wave per row; a workgroup per row for the 256-thread
-tree at few rows), the FP8 norm, the Q/K launch (four lanes per head; a wave per head),
+tree at few rows), the FP8 norm, the expert combine + norm, the Q/K launch (four lanes per head; a wave per head),
 and the fused chain in each of its shapes.
 """
 import numpy as np
@@ -97,6 +97,38 @@ def test_fallback_norm_fp8(oracle):
     assert np.array_equal(host16(y), want_y)
     assert np.array_equal(packed.cpu().numpy(), want_codes)
     assert np.array_equal(scales.cpu().numpy(), want_scales)
+
+
+@pytest.mark.parametrize("hidden", [2048, 2304, 4608])
+@pytest.mark.parametrize("fp8", [True, False])
+def test_fallback_combine_norm(oracle, hidden, fp8):
+    """Expert combine + norm (+ FP8), four waves per row: every other row's expert rows are
+    zero, so its combined row is x, a row next to an fp32 midpoint."""
+    print(f"[case] fallback combine norm hidden={hidden} fp8={fp8}", flush=True)
+    rows = 40
+    d = tie_inputs(rows, hidden=hidden, seed=hidden + fp8)
+    rng = np.random.default_rng(hidden)
+    down = synth.bf16_bits((rng.standard_normal((rows, 8, hidden)) * 0.5).astype(np.float32))
+    down[0::2] = 0
+    w = rng.dirichlet(np.ones(8), rows).astype(np.float32)
+    want_x, want_y, want_p, want_s, want_st, want_bad = oracle.combine_norm(
+        d["x"], down, w, d["gamma"], fp8=fp8)
+    assert not want_bad
+    x = dev(d["x"])
+    y = torch.empty_like(x)
+    packed = torch.zeros((rows, hidden), dtype=torch.uint8, device="cuda") if fp8 else None
+    scales = torch.zeros(rows, dtype=torch.float32, device="cuda") if fp8 else None
+    st = torch.empty(2, dtype=torch.float32, device="cuda")
+    bad = flag()
+    ops.CombineNorm(x, dev(down), torch.from_numpy(w).cuda(), y, dev(d["gamma"]), bad,
+                    packed=packed, scales=scales, statistics=st)
+    torch.cuda.synchronize()
+    assert not bad.item()
+    assert np.array_equal(host16(x), want_x) and np.array_equal(host16(y), want_y)
+    assert np.array_equal(st.cpu().numpy(), want_st)
+    if fp8:
+        assert np.array_equal(packed.cpu().numpy(), want_p)
+        assert np.array_equal(scales.cpu().numpy(), want_s)
 
 
 @pytest.mark.parametrize("tokens", [24, 400])

@@ -125,7 +125,8 @@ def test_residual_norm_nonfinite_sets_bad():
 # ---- RMSNorm + FP8 E4M3 row encoding ---------------------------------------------------------
 
 @pytest.mark.parametrize("hidden,rows", [(2048, 1), (2048, 37), (2048, 512), (2048, 2048),
-                                         (2304, 1), (2304, 37), (2304, 512)])
+                                         (2304, 1), (2304, 37), (2304, 512), (1024, 9),
+                                         (1152, 9), (4096, 9), (4608, 9)])
 @pytest.mark.parametrize("act", ["bf16", "f32"])
 def test_norm_fp8(oracle, hidden, rows, act):
     print(f"[case] norm fp8 hidden={hidden} rows={rows} act={act}", flush=True)
