@@ -102,7 +102,8 @@ template <int J, class T> __global__ __launch_bounds__(64) void k_norm_fp8(NormF
 
 // Residual-norm rows per wave in the chain (BF16 or no cache).  Two rows per wave (1,024
 // norm waves, so that with the Q/K waves the grid fits one round of 4 waves per SIMD)
-// measured slower: 13.21 -> 13.30 us on the config-1 chunk.
+// measured slower on the config-1 chunk: 13.21 -> 13.30 us, and with the inputs restored
+// clean in HBM before each timed replay 12.55 -> 12.70 us.
 constexpr int kChainRows = 1;
 
 // Residual-norm waves first, then the Q/K waves.  Measured on MI355X for a 2048-token
