@@ -204,6 +204,8 @@ template <int J>
 __device__ __forceinline__ void norm_fp8_row_wide(const NormFP8Args<uint16_t> &a, int row,
                                                   uint4 *vlds) {
   constexpr int VT = 128, K = 2, H = VT * J, C = (H + 511) / 512;
+  if (row >= a.rows)
+    return; // wave-uniform
   const int lane = threadIdx.x & 63;
   const size_t base = (size_t)row * H;
   uint4 xin[C], gin[C];
