@@ -91,9 +91,10 @@ __global__ __launch_bounds__(256) void k_combine(T *x, const T *down, const floa
 // Waves per row of the combine + norm kernel.  The row's 36 sixteen-byte loads per lane
 // (8 expert rows and x, four 512-column chunks at H = 2048) do not fit one wave's registers
 // at once, so one wave per row loaded them in dependent rounds; four waves, one chunk
-// each, put them all in flight: 2048 x 2048 with FP8, 21.1 -> 19.3 us.  Finishing the
-// norm in every wave (each storing a quarter of the row after the same reductions)
-// measured slower (22.6 us), so wave 0 finishes the row alone.
+// each, put them all in flight: 2048 x 2048 with FP8, 21.1 -> 19.3 us.  With the ordered
+// tree, finishing the norm in every wave (each storing a quarter of the row after the same
+// reductions) measured slower (22.6 us), so for fp32 rows wave 0 finishes the row alone;
+// BF16 rows take k_combine_norm_wide, whose order-free sum makes every wave's finish cheap.
 constexpr int kCombineWaves = 4;
 
 // Combine + RMSNorm (+ FP8): W waves per row.  The combine runs in the natural layout
