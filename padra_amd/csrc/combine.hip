@@ -452,16 +452,16 @@ extern "C" int padra_CombineNorm(void *stream, void *x, const void *down, const 
           hipLaunchKernelGGL((k_combine_norm_wide<j.value, false, kCombineWaves>), dim3(rows),
                              dim3(64 * kCombineWaves), 0, s, static_cast<uint16_t *>(x),
                              static_cast<const uint16_t *>(down), weights, a);
-        return launched("CombineNorm");
+      } else {
+        if (packed)
+          hipLaunchKernelGGL((k_combine_norm<j.value, T, true, kCombineWaves>), dim3(rows),
+                             dim3(64 * kCombineWaves), 0, s,
+                             static_cast<T *>(x), static_cast<const T *>(down), weights, a);
+        else
+          hipLaunchKernelGGL((k_combine_norm<j.value, T, false, kCombineWaves>), dim3(rows),
+                             dim3(64 * kCombineWaves), 0, s,
+                             static_cast<T *>(x), static_cast<const T *>(down), weights, a);
       }
-      if (packed)
-        hipLaunchKernelGGL((k_combine_norm<j.value, T, true, kCombineWaves>), dim3(rows),
-                           dim3(64 * kCombineWaves), 0, s,
-                           static_cast<T *>(x), static_cast<const T *>(down), weights, a);
-      else
-        hipLaunchKernelGGL((k_combine_norm<j.value, T, false, kCombineWaves>), dim3(rows),
-                           dim3(64 * kCombineWaves), 0, s,
-                           static_cast<T *>(x), static_cast<const T *>(down), weights, a);
       return launched("CombineNorm");
     });
   };
