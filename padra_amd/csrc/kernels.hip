@@ -11,6 +11,7 @@
 
 #include "norm_fp8.h"
 #include "norm_rows.h"
+#include "padra_hip_diag.h"
 #include "norm_wg.h"
 #include "qk_head.h"
 #include "qk_quad.h"

@@ -1,4 +1,5 @@
-"""The C-ABI library loads, exports every entry point include/padra_hip.h declares, and
+"""The C-ABI library loads, exports every entry point include/padra_hip.h (the drop-in
+surface) and include/padra_hip_diag.h (self-checks, the benchmark's copy) declare, and
 rejects bad host arguments with a status before any GPU work (CPU-only tests)."""
 import ctypes
 import os
@@ -12,18 +13,21 @@ from padra_amd import abi, ops, synth
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 
-def declared():
-    text = open(os.path.join(ROOT, "include", "padra_hip.h")).read()
+def declared(header="padra_hip.h"):
+    text = open(os.path.join(ROOT, "include", header)).read()
     return sorted(set(re.findall(r"\b(padra_[A-Za-z0-9_]+)\s*\(", text)))
 
 
 def test_library_exports_every_declaration():
     lib = abi.lib()
     names = declared()
+    diag = declared("padra_hip_diag.h")
     assert len(names) >= 4
-    for name in names:
+    assert diag == ["padra_CheckFP8Paths", "padra_CheckQ8Path", "padra_StreamCopy"]
+    assert not set(diag) & set(names)  # the drop-in header carries no diagnostics
+    for name in names + diag:
         assert hasattr(lib, name), name
-    assert set(names) <= set(abi.SIGNATURES)
+    assert set(names + diag) <= set(abi.SIGNATURES)
 
 
 def test_static_workspace_size_matches_header():
