@@ -996,6 +996,8 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": traffic_from_profiles(formats[0]),
+                     "traffic_source": "profiles/chain_config1_traffic.json: rocprofv3 --pmc "
+                                       "request counts of this kernel (profiles/chain_config1.md)",
                      "kernel": chain_kernel(formats[0]), "bytes_per_launch": head["bytes"]},
         "copy_ceiling_gbs": round(stream_gbs, 1),
         "copy_ceiling": {"kernel": "padra_StreamCopy", "bytes_per_launch": 2 * (head["bytes"] // 2 // 16 * 16),
