@@ -1258,6 +1258,7 @@ KERNEL_ROLES = {
     "k_qk": "Q/K norm + RoPE + store (fp32 activations)",
     "k_norm_fp8": "RMSNorm + FP8 E4M3",
     "k_combine_norm": "expert combine + residual + RMSNorm + FP8",
+    "k_combine_norm_wide": "expert combine + residual + RMSNorm + FP8 (BF16 rows)",
     "k_attn_mx": "decode attention split (BF16 / q8 cache)",
     "k_attn_merge": "decode attention merge",
     "k_q8_0_query": "decode attention, q8_0 query coding",
